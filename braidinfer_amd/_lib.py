@@ -1,0 +1,181 @@
+"""ctypes binding of the braidinfer_amd C ABI (include/braidinfer_amd.h).
+
+This module is the only place that touches the shared library.  It loads
+``braidinfer_amd/lib/libbraidinfer_amd.so`` (built by ``python -m
+braidinfer_amd.build``), declares every entry point's argument types, and
+turns a negative return code into a Python exception carrying
+``bfa_last_error()``.  There is deliberately no CPU or PyTorch fallback: when
+the library is missing, or a tensor is not on a ROCm device, the call raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import threading
+from ctypes import c_float, c_int, c_int64, c_void_p
+from pathlib import Path
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().parent / "lib" / "libbraidinfer_amd.so"
+ABI_VERSION = 1
+
+F32, F16, BF16, I32, I64 = 0, 1, 2, 3, 4
+_DTYPE_CODE = {
+    torch.float32: F32,
+    torch.float16: F16,
+    torch.bfloat16: BF16,
+    torch.int32: I32,
+    torch.int64: I64,
+}
+STATUS_INDEX_OOB = 1
+
+_P = c_void_p
+# name -> (restype, argtypes); mirrors include/braidinfer_amd.h
+_SIGNATURES = {
+    "bfa_abi_version": (c_int, []),
+    "bfa_last_error": (ctypes.c_char_p, []),
+    "bfa_rms_norm": (c_int, [_P, _P, _P, c_int, c_int, c_int64, c_int64, c_int64,
+                             c_int64, c_int64, c_int64, c_int64, c_float, _P]),
+    "bfa_add_rms_norm": (c_int, [_P, _P, _P, _P, _P, c_int, c_int, c_int64, c_int64,
+                                 c_int64, c_int64, c_int64, c_int64, c_float, _P]),
+    "bfa_rms_norm_f32": (c_int, [_P, _P, _P, c_int, c_int, c_int64, c_int64, c_int64,
+                                 c_int64, c_int64, c_int64, c_float, _P]),
+    "bfa_embedding": (c_int, [_P, c_int64, c_int64, c_int64, c_int, _P, c_int, c_int64,
+                              _P, c_int64, _P, _P]),
+    "bfa_embedding_scaled": (c_int, [_P, c_int64, c_int64, c_int64, c_int, _P, c_int,
+                                     c_int64, _P, c_int64, c_float, _P, _P]),
+    "bfa_silu_and_mul": (c_int, [_P, _P, c_int, c_int64, c_int64, c_int64, c_int64, _P]),
+    "bfa_rotary_embedding": (c_int, [_P, c_int, c_int64, _P, c_int64, c_int64, c_int,
+                                     _P, c_int64, c_int64, c_int64, _P,
+                                     _P, c_int64, c_int64, c_int64, _P, _P, _P]),
+    "bfa_apply_rotary_emb": (c_int, [_P, c_int, c_int64, c_int64, c_int64, c_int64, c_int64,
+                                     _P, _P, c_int64, _P, _P]),
+    "bfa_rerotate_paged_k": (c_int, [_P, c_int, c_int64, c_int64, c_int64, c_int64,
+                                     _P, c_int64, _P, _P, _P, c_int, c_int64,
+                                     _P, c_int64, _P, c_int, c_float, _P, _P, _P]),
+    "bfa_fused_rmsnorm_qkv_workspace_size": (c_int64, [c_int64, c_int64, c_int64, c_int64]),
+    "bfa_fused_rmsnorm_qkv": (c_int, [_P, c_int, c_int64, c_int64, c_int64, _P, c_int,
+                                      c_float, c_int, _P, c_int, c_int64, c_int64, _P, c_int,
+                                      c_int64, c_int64, c_int, _P, _P, c_int, c_float, c_int,
+                                      _P, c_int, _P, c_int64, _P, c_int, c_int64, _P,
+                                      c_int64, _P, _P]),
+    "bfa_rmsnorm_qkv_operand": (c_int, [_P, c_int, c_int64, c_int64, c_int64, _P, c_int,
+                                        c_int, _P, c_int, c_float, _P]),
+    "bfa_qkv_projection": (c_int, [_P, c_int64, c_int64, _P, c_int, c_int64, c_int64, _P,
+                                   c_int, c_int64, c_int64, c_int, _P, _P, c_int, c_float,
+                                   c_int, _P, c_int, _P, c_int64, _P, c_int, c_int64, _P,
+                                   c_int64, _P, _P]),
+}
+
+_lib = None
+_lock = threading.Lock()
+
+
+class BraidinferAMDError(RuntimeError):
+    """A braidinfer_amd entry point returned an error code."""
+
+
+def load():
+    """Loads (once) and returns the ctypes handle of the C-ABI library."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not LIB_PATH.exists():
+                raise RuntimeError(
+                    f"braidinfer_amd native library not found at {LIB_PATH}; "
+                    "build it with `python -m braidinfer_amd.build` (hipcc, gfx950)")
+            lib = ctypes.CDLL(str(LIB_PATH))
+            for name, (res, args) in _SIGNATURES.items():
+                fn = getattr(lib, name)
+                fn.restype = res
+                fn.argtypes = args
+            if lib.bfa_abi_version() != ABI_VERSION:
+                raise RuntimeError("braidinfer_amd: library ABI version mismatch; rebuild it")
+            _lib = lib
+    return _lib
+
+
+def exported_symbols():
+    """Names of every entry point this binding declares."""
+    return list(_SIGNATURES)
+
+
+def call(name: str, *args) -> int:
+    """Calls entry point `name`; raises BraidinferAMDError on a negative return."""
+    lib = load()
+    rc = getattr(lib, name)(*args)
+    if name.endswith("workspace_size"):
+        return rc
+    if rc < 0:
+        msg = lib.bfa_last_error().decode(errors="replace")
+        if rc == -1:
+            raise ValueError(msg)
+        raise BraidinferAMDError(msg)
+    return rc
+
+
+def dtype_code(t: torch.Tensor | torch.dtype) -> int:
+    dt = t if isinstance(t, torch.dtype) else t.dtype
+    try:
+        return _DTYPE_CODE[dt]
+    except KeyError:
+        raise TypeError(f"braidinfer_amd: unsupported dtype {dt}") from None
+
+
+def ptr(t: torch.Tensor | None):
+    return None if t is None else c_void_p(t.data_ptr())
+
+
+def require_device(*tensors: torch.Tensor | None) -> torch.device:
+    """All given tensors must live on one ROCm device; returns it."""
+    dev = None
+    for t in tensors:
+        if t is None:
+            continue
+        if t.device.type != "cuda":
+            raise RuntimeError(
+                "braidinfer_amd ops run only on ROCm devices (got a tensor on "
+                f"{t.device}); there is no CPU path")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise RuntimeError(f"braidinfer_amd: tensors on different devices ({dev}, {t.device})")
+    if dev is None:
+        raise RuntimeError("braidinfer_amd: no device tensor given")
+    return dev
+
+
+def stream_of(device: torch.device):
+    """Handle of the current torch stream on `device` (all work is enqueued there)."""
+    return c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+_status: dict[int, torch.Tensor] = {}
+
+
+def status_word(device: torch.device) -> torch.Tensor:
+    """The per-device int32 status word kernels OR error bits into."""
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    t = _status.get(idx)
+    if t is None:
+        t = torch.zeros(1, dtype=torch.int32, device=torch.device("cuda", idx))
+        _status[idx] = t
+    return t
+
+
+def check_device_status(device: torch.device | int | None = None, reset: bool = True) -> None:
+    """Synchronises with the device status word and raises IndexError if a
+    kernel saw an out-of-range token id, position or delta since the last check."""
+    if device is None:
+        device = torch.device("cuda", torch.cuda.current_device())
+    elif isinstance(device, int):
+        device = torch.device("cuda", device)
+    t = status_word(device)
+    bits = int(t.item())
+    if bits and reset:
+        t.zero_()
+    if bits & STATUS_INDEX_OOB:
+        raise IndexError("braidinfer_amd: index out of range in a device kernel "
+                         "(token id, rotary position or chunk delta)")

@@ -1,0 +1,128 @@
+// Device-side helpers shared by every braidinfer_amd kernel (gfx950, wave64).
+//
+// Storage types are handled as raw bits (uint16 for bf16/fp16) so that every
+// rounding point is explicit: float -> bf16 goes through the hardware
+// round-to-nearest-even conversion (v_cvt_pk_bf16_f32 on gfx950), which is the
+// rounding torch uses for Tensor.to(torch.bfloat16).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "braidinfer_amd.h"
+
+namespace bfa {
+
+constexpr int kWave = 64;
+
+// ---------------------------------------------------------------- scalar casts
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t b) {
+  return __uint_as_float(b << 16);
+}
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+  return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
+}
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t b) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(b)));
+}
+__device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
+  return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
+}
+
+// Element traits: DT is one of BFA_DTYPE_{F32,F16,BF16}.
+template <int DT> struct Elem;
+template <> struct Elem<BFA_DTYPE_F32> {
+  using T = float;
+  static constexpr int kPer16B = 4;
+  __device__ __forceinline__ static float to_f32(T v) { return v; }
+  __device__ __forceinline__ static T from_f32(float v) { return v; }
+  __device__ __forceinline__ static float round(float v) { return v; }
+};
+template <> struct Elem<BFA_DTYPE_F16> {
+  using T = uint16_t;
+  static constexpr int kPer16B = 8;
+  __device__ __forceinline__ static float to_f32(T v) { return f16_bits_to_f32(v); }
+  __device__ __forceinline__ static T from_f32(float v) { return f32_to_f16_bits(v); }
+  __device__ __forceinline__ static float round(float v) { return f16_bits_to_f32(f32_to_f16_bits(v)); }
+};
+template <> struct Elem<BFA_DTYPE_BF16> {
+  using T = uint16_t;
+  static constexpr int kPer16B = 8;
+  __device__ __forceinline__ static float to_f32(T v) { return bf16_bits_to_f32(v); }
+  __device__ __forceinline__ static T from_f32(float v) { return f32_to_bf16_bits(v); }
+  __device__ __forceinline__ static float round(float v) { return bf16_bits_to_f32(f32_to_bf16_bits(v)); }
+};
+
+__device__ __forceinline__ float round_bf16(float v) { return Elem<BFA_DTYPE_BF16>::round(v); }
+
+// ------------------------------------------------------- 8-element vector I/O
+// Loads/stores 8 consecutive elements as 16-byte (16-bit types) or 2x16-byte
+// (fp32) vector accesses.  The caller guarantees 16-byte alignment.
+template <int DT>
+__device__ __forceinline__ void load8(const void* p, float (&v)[8]) {
+  if constexpr (DT == BFA_DTYPE_F32) {
+    const float4* q = reinterpret_cast<const float4*>(p);
+    float4 a = q[0], b = q[1];
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+    v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+  } else {
+    uint4 u = *reinterpret_cast<const uint4*>(p);
+    uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[2 * i] = Elem<DT>::to_f32(static_cast<uint16_t>(w[i] & 0xffffu));
+      v[2 * i + 1] = Elem<DT>::to_f32(static_cast<uint16_t>(w[i] >> 16));
+    }
+  }
+}
+
+template <int DT>
+__device__ __forceinline__ void store8(void* p, const float (&v)[8]) {
+  if constexpr (DT == BFA_DTYPE_F32) {
+    float4* q = reinterpret_cast<float4*>(p);
+    q[0] = make_float4(v[0], v[1], v[2], v[3]);
+    q[1] = make_float4(v[4], v[5], v[6], v[7]);
+  } else {
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      w[i] = static_cast<uint32_t>(Elem<DT>::from_f32(v[2 * i])) |
+             (static_cast<uint32_t>(Elem<DT>::from_f32(v[2 * i + 1])) << 16);
+    }
+    *reinterpret_cast<uint4*>(p) = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+}
+
+// Scalar element access (used by the unaligned fallback paths).
+template <int DT>
+__device__ __forceinline__ float load1(const void* p, int64_t i) {
+  return Elem<DT>::to_f32(reinterpret_cast<const typename Elem<DT>::T*>(p)[i]);
+}
+template <int DT>
+__device__ __forceinline__ void store1(void* p, int64_t i, float v) {
+  reinterpret_cast<typename Elem<DT>::T*>(p)[i] = Elem<DT>::from_f32(v);
+}
+
+// Runtime-dtype scalar load for small operands (norm weights, bias).
+__device__ __forceinline__ float load_any(const void* p, int dt, int64_t i) {
+  if (dt == BFA_DTYPE_BF16) return load1<BFA_DTYPE_BF16>(p, i);
+  if (dt == BFA_DTYPE_F16) return load1<BFA_DTYPE_F16>(p, i);
+  return load1<BFA_DTYPE_F32>(p, i);
+}
+
+// ------------------------------------------------------------- reductions
+// Butterfly sum over aligned groups of L lanes (L a power of two <= 64).
+template <int L>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+  for (int m = L / 2; m >= 1; m >>= 1) v += __shfl_xor(v, m, kWave);
+  return v;
+}
+
+// Device status word: kernels that detect out-of-range indices OR a bit into
+// it with an ordinary store (every writer stores the same value).
+__device__ __forceinline__ void flag_status(int* status, int bit) {
+  if (status) atomicOr(status, bit);
+}
+
+}  // namespace bfa

@@ -1,0 +1,694 @@
+// Fused RMSNorm + QKV projection (+ bias, + per-head q/k RMSNorm, + RoPE) on gfx950.
+//
+// Reference semantics (braidinfer/kernels/fused_rmsnorm_qkv_*.py and the model
+// glue that consumes their output):
+//   operand   n = RMSNorm(x) with the variant's rounding points   (norm.hip pre-pass)
+//   project   y = n @ W^T (+ bias), fp32 accumulation, rounded to the variant's
+//             output dtype (bf16 for mixed/production, none for the f32 ones)
+//   q/k norm  Qwen3: q_norm(q.float()).to(dtype), k_norm(k.float()).to(dtype)
+//             (models/qwen3.py:257-281), RMSNorm over head_dim in fp32
+//   rope      RotaryEmbedding.forward on q and k (layers/rotary_embedding.py:49-65),
+//             fp32 math, result rounded to the dtype it was given
+//   store     .to(out dtype) (models/llama.py:200-205, qwen3.py:280-336)
+// W is the packed [q rows; k rows; v rows] x hidden matrix of
+// QKVParallelLinear (layers/linear.py:78-114).
+//
+// Kernels
+//  * qkv_gemm_kernel   prefill.  BMxBN = 256x256 tile per 256-thread workgroup,
+//    four waves of 128x128, v_mfma_f32_32x32x16_{bf16,f16}.  Operand tiles
+//    (64-deep K slices) go HBM -> registers -> LDS (double-buffered, 16-byte
+//    granules XOR-swizzled by row so the MFMA fragment reads spread over the
+//    banks).  The epilogue runs on the accumulators in registers: a wave's
+//    128 columns hold whole heads (head_dim 64 or 128), so the q/k RMSNorm is
+//    a 32-lane butterfly and both RoPE halves (columns j and j+D/2) sit in the
+//    same lane.
+//  * qkv_splitk_kernel decode (T <= 64).  The weight stream dominates, so the
+//    grid is (column tiles) x (K splits) to put every CU on the weight; each
+//    lane loads 32 contiguous bytes per weight row straight into MFMA
+//    registers (v_mfma_f32_16x16x32) without LDS; fp32 partial tiles go to the
+//    workspace.
+//  * qkv_epilogue_kernel sums the split-K partials (or reads the raw fp32
+//    projection for head_dim the in-register epilogue does not cover) and
+//    applies bias / q-k norm / RoPE / rounding per (token, head) row.
+#include "bfa_device.h"
+#include "bfa_host.h"
+#include "bfa_internal.h"
+
+namespace bfa {
+
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
+typedef __attribute__((ext_vector_type(8))) _Float16 f16x8_t;
+typedef __attribute__((ext_vector_type(16))) float f32x16_t;
+typedef __attribute__((ext_vector_type(4))) float f32x4_t;
+
+template <bool BF16>
+__device__ __forceinline__ f32x16_t mfma32(const uint4& a, const uint4& b, f32x16_t c) {
+  if constexpr (BF16) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                   __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a),
+                                                  __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+  }
+}
+
+template <bool BF16>
+__device__ __forceinline__ f32x4_t mfma16(const uint4& a, const uint4& b, f32x4_t c) {
+  if constexpr (BF16) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                   __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a),
+                                                  __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+  }
+}
+
+// ------------------------------------------------------------- epilogue spec
+struct QkvEpi {
+  const void* bias;
+  int bias_dtype;
+  int qkv_dt;   // rounding of the projection (BFA_DTYPE_F32 = none)
+  int norm_dt;  // dtype the q/k norm result is cast to
+  int out_dt;
+  int64_t n;        // columns (q|k|v)
+  int64_t hq, hkv;  // heads
+  int64_t hd;       // head_dim
+  const void* qn_w;
+  const void* kn_w;
+  int qk_w_dtype;
+  float qk_eps;
+  const void* positions;
+  int pos_is_i64;
+  const float* cs;  // cos|sin table [max_pos, hd] or nullptr (no RoPE)
+  int64_t max_pos;
+  void* out;
+  int64_t ldo;
+  int* status;
+};
+
+__device__ __forceinline__ float round_to(float v, int dt) {
+  if (dt == BFA_DTYPE_BF16) return Elem<BFA_DTYPE_BF16>::round(v);
+  if (dt == BFA_DTYPE_F16) return Elem<BFA_DTYPE_F16>::round(v);
+  return v;
+}
+
+__device__ __forceinline__ void store_any(void* p, int dt, int64_t i, float v) {
+  if (dt == BFA_DTYPE_BF16) store1<BFA_DTYPE_BF16>(p, i, v);
+  else if (dt == BFA_DTYPE_F16) store1<BFA_DTYPE_F16>(p, i, v);
+  else store1<BFA_DTYPE_F32>(p, i, v);
+}
+
+// Stores 4 consecutive elements (8-byte / 16-byte vector store; the caller
+// guarantees the alignment: column multiple of 4, row stride multiple of 4).
+__device__ __forceinline__ void store4_any(void* p, int dt, int64_t i, const float (&v)[4]) {
+  if (dt == BFA_DTYPE_F32) {
+    *reinterpret_cast<float4*>(static_cast<float*>(p) + i) = make_float4(v[0], v[1], v[2], v[3]);
+  } else {
+    uint32_t w0, w1;
+    if (dt == BFA_DTYPE_BF16) {
+      w0 = f32_to_bf16_bits(v[0]) | (static_cast<uint32_t>(f32_to_bf16_bits(v[1])) << 16);
+      w1 = f32_to_bf16_bits(v[2]) | (static_cast<uint32_t>(f32_to_bf16_bits(v[3])) << 16);
+    } else {
+      w0 = f32_to_f16_bits(v[0]) | (static_cast<uint32_t>(f32_to_f16_bits(v[1])) << 16);
+      w1 = f32_to_f16_bits(v[2]) | (static_cast<uint32_t>(f32_to_f16_bits(v[3])) << 16);
+    }
+    *reinterpret_cast<uint2*>(static_cast<uint16_t*>(p) + i) = make_uint2(w0, w1);
+  }
+}
+
+// 0 = q head, 1 = k head, 2 = v head
+__device__ __forceinline__ int head_kind(const QkvEpi& e, int64_t head) {
+  return head < e.hq ? 0 : (head < e.hq + e.hkv ? 1 : 2);
+}
+
+__device__ __forceinline__ int64_t epi_position(const QkvEpi& e, int64_t row, bool& ok) {
+  int64_t p = e.pos_is_i64 ? static_cast<const int64_t*>(e.positions)[row]
+                           : static_cast<const int32_t*>(e.positions)[row];
+  if (p < 0) p += e.max_pos;
+  ok = p >= 0 && p < e.max_pos;
+  return ok ? p : 0;
+}
+
+// ============================================================ prefill GEMM
+struct GemmArgs {
+  const uint16_t* a;  // operand [m, k]
+  const uint16_t* w;  // weight  [n, k]
+  int64_t m, n, k, lda, ldw;
+  float* raw;         // EPI_RAW: fp32 [m, n] destination
+};
+
+enum { EPI_RAW = 0, EPI_FUSED = 1 };
+
+// LDS tile rows are 64 elements = 8 granules of 16 bytes; granule g of row r is
+// stored at slot g ^ (r & 7).
+__device__ __forceinline__ int swz(int r, int g) { return r * 8 + (g ^ (r & 7)); }
+
+template <int BM, int BN, int WM, int WN, bool BF16, int EPI, int HD>
+__global__ __launch_bounds__(256) void qkv_gemm_kernel(GemmArgs g, QkvEpi e) {
+  constexpr int NWN = BN / WN;
+  static_assert((BM / WM) * NWN == 4, "four waves per workgroup");
+  constexpr int MB = WM / 32, NB = WN / 32;
+  constexpr int AG = BM / 32, BG = BN / 32;  // 16-byte granules per thread per K tile
+  __shared__ uint4 lds[2][(BM + BN) * 8];
+
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int wm = wid / NWN, wn = wid % NWN;
+
+  // Tile order: workgroups are dispatched round-robin over the 8 XCDs; remap
+  // so that each XCD walks a contiguous range of tiles, and walk tiles
+  // column-major inside groups of 8 row-tiles so that concurrently resident
+  // workgroups on one XCD share operand rows and weight columns in its L2.
+  const int64_t tiles_m = cdiv(g.m, BM), tiles_n = cdiv(g.n, BN);
+  const int64_t ntiles = tiles_m * tiles_n;
+  int64_t bid = blockIdx.x;
+  if (ntiles % 8 == 0) bid = (bid % 8) * (ntiles / 8) + bid / 8;
+  constexpr int64_t GROUP_M = 8;
+  const int64_t group = bid / (GROUP_M * tiles_n);
+  const int64_t first_m = group * GROUP_M;
+  const int64_t gsize = min(tiles_m - first_m, GROUP_M);
+  const int64_t tm = first_m + (bid % (GROUP_M * tiles_n)) % gsize;
+  const int64_t tn = (bid % (GROUP_M * tiles_n)) / gsize;
+  const int64_t m0 = tm * BM, n0 = tn * BN;
+
+  // global -> register assignment: thread loads granule gg of rows gr + 32*i
+  const int gg = tid & 7, gr = tid >> 3;
+  const uint4* asrc[AG];
+  const uint4* bsrc[BG];
+#pragma unroll
+  for (int i = 0; i < AG; ++i) {
+    const int64_t r = min(m0 + gr + 32 * i, g.m - 1);
+    asrc[i] = reinterpret_cast<const uint4*>(g.a + r * g.lda) + gg;
+  }
+#pragma unroll
+  for (int i = 0; i < BG; ++i) {
+    const int64_t r = min(n0 + gr + 32 * i, g.n - 1);
+    bsrc[i] = reinterpret_cast<const uint4*>(g.w + r * g.ldw) + gg;
+  }
+  uint4 ra[AG], rb[BG];
+  const int64_t KT = cdiv(g.k, 64);
+  auto gload = [&](int64_t kt) {
+    const bool in = kt * 64 + gg * 8 < g.k;  // K % 8 == 0, so granules are all-in or all-out
+#pragma unroll
+    for (int i = 0; i < AG; ++i) ra[i] = in ? asrc[i][kt * 8] : make_uint4(0, 0, 0, 0);
+#pragma unroll
+    for (int i = 0; i < BG; ++i) rb[i] = in ? bsrc[i][kt * 8] : make_uint4(0, 0, 0, 0);
+  };
+  auto sstore = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < AG; ++i) lds[buf][swz(gr + 32 * i, gg)] = ra[i];
+#pragma unroll
+    for (int i = 0; i < BG; ++i) lds[buf][BM * 8 + swz(gr + 32 * i, gg)] = rb[i];
+  };
+
+  f32x16_t acc[MB][NB];
+#pragma unroll
+  for (int i = 0; i < MB; ++i)
+#pragma unroll
+    for (int j = 0; j < NB; ++j) acc[i][j] = f32x16_t{};
+
+  gload(0);
+  sstore(0);
+  __syncthreads();
+  const int frow = lane & 31, fhalf = lane >> 5;
+  for (int64_t kt = 0; kt < KT; ++kt) {
+    const int cur = static_cast<int>(kt & 1);
+    if (kt + 1 < KT) gload(kt + 1);
+    const uint4* la = lds[cur];
+    const uint4* lb = lds[cur] + BM * 8;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const int gsel = ks * 2 + fhalf;
+      uint4 af[MB], bfr[NB];
+#pragma unroll
+      for (int i = 0; i < MB; ++i) af[i] = la[swz(wm * WM + i * 32 + frow, gsel)];
+#pragma unroll
+      for (int j = 0; j < NB; ++j) bfr[j] = lb[swz(wn * WN + j * 32 + frow, gsel)];
+#pragma unroll
+      for (int i = 0; i < MB; ++i)
+#pragma unroll
+        for (int j = 0; j < NB; ++j) acc[i][j] = mfma32<BF16>(af[i], bfr[j], acc[i][j]);
+    }
+    if (kt + 1 < KT) sstore(cur ^ 1);
+    __syncthreads();
+  }
+
+  // ------------------------------------------------------------ epilogue
+  // 32x32 accumulator layout: lane holds column (lane & 31) and rows
+  // 8*(v/4) + 4*(lane/32) + (v%4), v = 0..15.
+  const int64_t wcol0 = n0 + wn * WN;
+  const int64_t wrow0 = m0 + wm * WM;
+  if constexpr (EPI == EPI_RAW) {
+#pragma unroll
+    for (int i = 0; i < MB; ++i)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int64_t row = wrow0 + i * 32 + 8 * (v / 4) + 4 * fhalf + (v % 4);
+        if (row >= g.m) continue;
+#pragma unroll
+        for (int j = 0; j < NB; ++j) {
+          const int64_t col = wcol0 + j * 32 + frow;
+          if (col < g.n) g.raw[row * g.n + col] = acc[i][j][v];
+        }
+      }
+    return;
+  } else {
+    static_assert(HD == 32 || HD == 64 || HD == 128, "fused epilogue covers head_dim 32/64/128");
+    static_assert(WN == 128, "the row epilogue maps 16 lanes x 8 columns onto 128 columns");
+    // Each 32-row accumulator block is staged through this wave's slice of the
+    // (now idle) LDS, then processed row by row: 16 lanes per row, each lane
+    // owning 4 RoPE pairs (columns j..j+3 and j+D/2..j+D/2+3 of one head), so
+    // the q/k norm is a butterfly over the D/8 lanes of a head and every store
+    // is a contiguous 4-element vector.
+    constexpr int LDR = 136;  // padded row stride (floats)
+    constexpr int LH = HD / 8;  // lanes per head
+    float* et = reinterpret_cast<float*>(&lds[0][0]) + wid * (32 * LDR);
+    const int l16 = lane & 15, rg = lane >> 4;
+    const int hloc = l16 / LH, q = l16 % LH;
+    const int c1 = hloc * HD + q * 4, c2 = c1 + HD / 2;  // columns inside the wave tile
+    const int64_t gc1 = wcol0 + c1, gc2 = wcol0 + c2;
+    const bool colok = gc1 < e.n;
+    const int64_t head = min(gc1, e.n - 1) / HD;
+    const int kd = head_kind(e, head);
+    const void* nw = kd == 0 ? e.qn_w : (kd == 1 ? e.kn_w : nullptr);
+    const bool any_norm = e.qn_w != nullptr || e.kn_w != nullptr;
+    const bool rope = e.cs != nullptr && kd != 2;
+    float b1[4], b2[4], g1[4], g2[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      b1[t] = (e.bias && colok) ? load_any(e.bias, e.bias_dtype, gc1 + t) : 0.f;
+      b2[t] = (e.bias && colok) ? load_any(e.bias, e.bias_dtype, gc2 + t) : 0.f;
+      g1[t] = nw ? load_any(nw, e.qk_w_dtype, q * 4 + t) : 1.f;
+      g2[t] = nw ? load_any(nw, e.qk_w_dtype, HD / 2 + q * 4 + t) : 1.f;
+    }
+    const int dt_after = nw ? e.norm_dt : e.qkv_dt;  // dtype RoPE receives
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < MB; ++i) {
+#pragma unroll
+      for (int j = 0; j < NB; ++j)
+#pragma unroll
+        for (int v = 0; v < 16; ++v)
+          et[(8 * (v / 4) + 4 * fhalf + (v % 4)) * LDR + j * 32 + frow] = acc[i][j][v];
+      __syncthreads();
+      for (int it = 0; it < 8; ++it) {
+        const int rl = rg + 4 * it;
+        const int64_t row = wrow0 + i * 32 + rl;
+        const float4 a1 = *reinterpret_cast<const float4*>(et + rl * LDR + c1);
+        const float4 a2 = *reinterpret_cast<const float4*>(et + rl * LDR + c2);
+        float x1[4] = {a1.x, a1.y, a1.z, a1.w}, x2[4] = {a2.x, a2.y, a2.z, a2.w};
+        float ss = 0.f;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          x1[t] = round_to(x1[t] + b1[t], e.qkv_dt);
+          x2[t] = round_to(x2[t] + b2[t], e.qkv_dt);
+          ss += x1[t] * x1[t] + x2[t] * x2[t];
+        }
+        if (any_norm) {
+          ss = group_sum<LH>(ss);  // lanes of one head form an aligned group
+          if (nw) {
+            const float r = 1.0f / sqrtf(ss / static_cast<float>(HD) + e.qk_eps);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+              x1[t] = round_to((x1[t] * r) * g1[t], e.norm_dt);
+              x2[t] = round_to((x2[t] * r) * g2[t], e.norm_dt);
+            }
+          }
+        }
+        if (rope) {
+          bool ok;
+          const int64_t p = epi_position(e, min(row, g.m - 1), ok);
+          if (!ok && row < g.m && q == 0) flag_status(e.status, BFA_STATUS_INDEX_OOB);
+          const float4 cv = *reinterpret_cast<const float4*>(e.cs + p * HD + q * 4);
+          const float4 sv = *reinterpret_cast<const float4*>(e.cs + p * HD + HD / 2 + q * 4);
+          const float c[4] = {cv.x, cv.y, cv.z, cv.w}, sn[4] = {sv.x, sv.y, sv.z, sv.w};
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            const float u = x1[t], w = x2[t];
+            x1[t] = ok ? round_to(u * c[t] - w * sn[t], dt_after) : 0.f;
+            x2[t] = ok ? round_to(w * c[t] + u * sn[t], dt_after) : 0.f;
+          }
+        }
+        if (row < g.m && colok) {
+          store4_any(e.out, e.out_dt, row * e.ldo + gc1, x1);
+          store4_any(e.out, e.out_dt, row * e.ldo + gc2, x2);
+        }
+      }
+      __syncthreads();
+    }
+  }
+}
+
+// ======================================================== decode split-K
+// Grid: (n / BNT column tiles, S K-splits).  A workgroup's 4 waves each own
+// BNT/4 columns (16 per MFMA block) and all MT*16 rows.  Within a 64-deep K
+// step, lane group q = lane/16 owns k in [16q, 16q+16): 32 contiguous bytes of
+// one weight row, fed to two 16x16x32 MFMAs (the same k assignment is used
+// for the operand, so the sum covers every k once).
+struct SplitArgs {
+  const uint16_t* a;
+  const uint16_t* w;
+  int64_t m, n, k, lda, ldw;
+  int64_t kchunk;  // K elements per split (multiple of 64)
+  float* part;     // [S, m, n]
+};
+
+template <int MT, int CPW, bool BF16>
+__global__ __launch_bounds__(256) void qkv_splitk_kernel(SplitArgs s) {
+  // CPW = 16-column MFMA blocks per wave
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int64_t n0 = (static_cast<int64_t>(blockIdx.x) * 4 + wid) * (16 * CPW);
+  const int64_t k0 = static_cast<int64_t>(blockIdx.y) * s.kchunk;
+  const int64_t k1 = min(k0 + s.kchunk, s.k);
+  const int lr = lane & 15, lq = lane >> 4;
+
+  f32x4_t acc[MT][CPW];
+#pragma unroll
+  for (int i = 0; i < MT; ++i)
+#pragma unroll
+    for (int j = 0; j < CPW; ++j) acc[i][j] = f32x4_t{};
+
+  const uint16_t* wrow[CPW];
+#pragma unroll
+  for (int j = 0; j < CPW; ++j) wrow[j] = s.w + min(n0 + j * 16 + lr, s.n - 1) * s.ldw;
+  const uint16_t* arow[MT];
+#pragma unroll
+  for (int i = 0; i < MT; ++i) arow[i] = s.a + min(static_cast<int64_t>(i * 16 + lr), s.m - 1) * s.lda;
+
+  for (int64_t kk = k0; kk < k1; kk += 64) {
+    const int64_t kl = kk + lq * 16;  // this lane's 16 k values
+    const bool in = kl < s.k;         // K % 16 == 0
+    uint4 b0[CPW], b1[CPW], a0[MT], a1[MT];
+#pragma unroll
+    for (int j = 0; j < CPW; ++j) {
+      const uint4* p = reinterpret_cast<const uint4*>(wrow[j] + kl);
+      b0[j] = in ? p[0] : make_uint4(0, 0, 0, 0);
+      b1[j] = in ? p[1] : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < MT; ++i) {
+      const uint4* p = reinterpret_cast<const uint4*>(arow[i] + kl);
+      a0[i] = in ? p[0] : make_uint4(0, 0, 0, 0);
+      a1[i] = in ? p[1] : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+      for (int j = 0; j < CPW; ++j) {
+        acc[i][j] = mfma16<BF16>(a0[i], b0[j], acc[i][j]);
+        acc[i][j] = mfma16<BF16>(a1[i], b1[j], acc[i][j]);
+      }
+  }
+  // 16x16 accumulator layout: lane holds column (lane & 15), rows 4*(lane/16) + v.
+  float* dst = s.part + static_cast<int64_t>(blockIdx.y) * s.m * s.n;
+#pragma unroll
+  for (int i = 0; i < MT; ++i)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int64_t row = i * 16 + lq * 4 + v;
+      if (row >= s.m) continue;
+#pragma unroll
+      for (int j = 0; j < CPW; ++j) {
+        const int64_t col = n0 + j * 16 + lr;
+        if (col < s.n) dst[row * s.n + col] = acc[i][j][v];
+      }
+    }
+}
+
+// ============================================== reduction + row epilogue
+// One wave per (token, head).  v = sum over splits of part[s, t, col] (+bias),
+// then the same rounding / norm / RoPE chain as the in-register epilogue.
+__global__ __launch_bounds__(256) void qkv_epilogue_kernel(const float* part, int64_t splits,
+                                                           int64_t m, QkvEpi e) {
+  constexpr int MAXP = 4;  // pairs per lane: head_dim <= 2*64*MAXP
+  const int lane = threadIdx.x & 63;
+  const int64_t heads = e.hq + 2 * e.hkv;
+  const int64_t item = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (item >= m * heads) return;
+  const int64_t t = item / heads, h = item - t * heads;
+  const int64_t half = e.hd / 2;
+  const int kd = head_kind(e, h);
+  const int64_t base = h * e.hd;
+  float x1[MAXP], x2[MAXP];
+  int dt = e.qkv_dt;
+  float ss = 0.f;
+#pragma unroll
+  for (int p = 0; p < MAXP; ++p) {
+    const int64_t j = lane + 64 * p;
+    x1[p] = x2[p] = 0.f;
+    if (j < half) {
+      float s1 = 0.f, s2 = 0.f;
+      for (int64_t sp = 0; sp < splits; ++sp) {
+        const float* pr = part + (sp * m + t) * e.n + base;
+        s1 += pr[j];
+        s2 += pr[half + j];
+      }
+      if (e.bias) {
+        s1 += load_any(e.bias, e.bias_dtype, base + j);
+        s2 += load_any(e.bias, e.bias_dtype, base + half + j);
+      }
+      x1[p] = round_to(s1, e.qkv_dt);
+      x2[p] = round_to(s2, e.qkv_dt);
+      ss += x1[p] * x1[p] + x2[p] * x2[p];
+    }
+  }
+  const void* nw = kd == 0 ? e.qn_w : (kd == 1 ? e.kn_w : nullptr);
+  if (kd != 2 && (e.qn_w || e.kn_w)) {
+    ss = group_sum<kWave>(ss);
+    if (nw) {
+      const float r = 1.0f / sqrtf(ss / static_cast<float>(e.hd) + e.qk_eps);
+#pragma unroll
+      for (int p = 0; p < MAXP; ++p) {
+        const int64_t j = lane + 64 * p;
+        if (j < half) {
+          x1[p] = round_to((x1[p] * r) * load_any(nw, e.qk_w_dtype, j), e.norm_dt);
+          x2[p] = round_to((x2[p] * r) * load_any(nw, e.qk_w_dtype, half + j), e.norm_dt);
+        }
+      }
+      dt = e.norm_dt;
+    }
+  }
+  if (kd != 2 && e.cs) {
+    bool ok;
+    const int64_t pos = epi_position(e, t, ok);
+    if (!ok && h == 0 && lane == 0) flag_status(e.status, BFA_STATUS_INDEX_OOB);
+#pragma unroll
+    for (int p = 0; p < MAXP; ++p) {
+      const int64_t j = lane + 64 * p;
+      if (j < half) {
+        const float c = e.cs[pos * e.hd + j], s = e.cs[pos * e.hd + half + j];
+        const float a = x1[p], b = x2[p];
+        x1[p] = ok ? round_to(a * c - b * s, dt) : 0.f;
+        x2[p] = ok ? round_to(b * c + a * s, dt) : 0.f;
+      }
+    }
+  }
+#pragma unroll
+  for (int p = 0; p < MAXP; ++p) {
+    const int64_t j = lane + 64 * p;
+    if (j < half) {
+      store_any(e.out, e.out_dt, t * e.ldo + base + j, x1[p]);
+      store_any(e.out, e.out_dt, t * e.ldo + base + half + j, x2[p]);
+    }
+  }
+}
+
+// ================================================================== host
+struct QkvPlan {
+  bool decode;
+  int mt;        // decode: 16-row blocks
+  int cpw;       // decode: 16-column blocks per wave
+  int64_t splits;
+  int64_t kchunk;
+  bool fused_epi;  // prefill: in-register epilogue
+  int64_t operand_bytes;
+  int64_t part_bytes;
+};
+
+static int64_t align256(int64_t v) { return (v + 255) / 256 * 256; }
+
+static QkvPlan make_plan(int64_t m, int64_t n, int64_t k, int64_t hd) {
+  QkvPlan p{};
+  p.operand_bytes = align256(m * k * 2);
+  if (m <= 64) {
+    p.decode = true;
+    p.mt = static_cast<int>(cdiv(m, 16));
+    // Column tile per workgroup: 4 waves x cpw x 16 columns.
+    p.cpw = m > 16 ? 1 : 2;
+    const int64_t ntile = cdiv(n, 4 * 16 * p.cpw);
+    // Split K until about 512 workgroups are in flight, but keep the fp32
+    // partial traffic (2 * splits * m * n * 4 bytes) small next to the weight
+    // stream (n * k * 2 bytes): splits <= k / (32 m) bounds it at 1/4.
+    int64_t splits = std::max<int64_t>(1, cdiv(512, ntile));
+    splits = std::min<int64_t>(splits, std::max<int64_t>(1, k / 128));
+    splits = std::min<int64_t>(splits, std::max<int64_t>(1, k / (32 * m)));
+    p.kchunk = cdiv(cdiv(k, splits), 64) * 64;
+    p.splits = cdiv(k, p.kchunk);
+    p.part_bytes = align256(p.splits * m * n * 4);
+  } else {
+    p.decode = false;
+    p.fused_epi = (hd == 32 || hd == 64 || hd == 128) && n % hd == 0;
+    p.splits = 1;
+    p.part_bytes = p.fused_epi ? 0 : align256(m * n * 4);
+  }
+  return p;
+}
+
+template <bool BF16, int CPW>
+static void launch_decode_cpw(const QkvPlan& p, const SplitArgs& s, hipStream_t st) {
+  const dim3 grid(static_cast<unsigned>(cdiv(s.n, 4 * 16 * CPW)), static_cast<unsigned>(p.splits));
+  switch (p.mt) {
+    case 1: hipLaunchKernelGGL((qkv_splitk_kernel<1, CPW, BF16>), grid, dim3(256), 0, st, s); break;
+    case 2: hipLaunchKernelGGL((qkv_splitk_kernel<2, CPW, BF16>), grid, dim3(256), 0, st, s); break;
+    case 3: hipLaunchKernelGGL((qkv_splitk_kernel<3, CPW, BF16>), grid, dim3(256), 0, st, s); break;
+    default: hipLaunchKernelGGL((qkv_splitk_kernel<4, CPW, BF16>), grid, dim3(256), 0, st, s); break;
+  }
+}
+
+template <bool BF16>
+static void launch_decode(const QkvPlan& p, const SplitArgs& s, hipStream_t st) {
+  if (p.cpw == 1) launch_decode_cpw<BF16, 1>(p, s, st);
+  else launch_decode_cpw<BF16, 2>(p, s, st);
+}
+
+template <bool BF16>
+static void launch_prefill(const QkvPlan& p, const GemmArgs& g, const QkvEpi& e, hipStream_t st) {
+  const unsigned grid = static_cast<unsigned>(cdiv(g.m, 256) * cdiv(g.n, 256));
+  if (!p.fused_epi) {
+    hipLaunchKernelGGL((qkv_gemm_kernel<256, 256, 128, 128, BF16, EPI_RAW, 128>), dim3(grid),
+                       dim3(256), 0, st, g, e);
+  } else if (e.hd == 128) {
+    hipLaunchKernelGGL((qkv_gemm_kernel<256, 256, 128, 128, BF16, EPI_FUSED, 128>), dim3(grid),
+                       dim3(256), 0, st, g, e);
+  } else if (e.hd == 64) {
+    hipLaunchKernelGGL((qkv_gemm_kernel<256, 256, 128, 128, BF16, EPI_FUSED, 64>), dim3(grid),
+                       dim3(256), 0, st, g, e);
+  } else {
+    hipLaunchKernelGGL((qkv_gemm_kernel<256, 256, 128, 128, BF16, EPI_FUSED, 32>), dim3(grid),
+                       dim3(256), 0, st, g, e);
+  }
+}
+
+static void launch_epilogue(const float* part, int64_t splits, int64_t m, const QkvEpi& e,
+                            hipStream_t st) {
+  const int64_t items = m * (e.hq + 2 * e.hkv);
+  hipLaunchKernelGGL(qkv_epilogue_kernel, dim3(static_cast<unsigned>(cdiv(items, 4))), dim3(256),
+                     0, st, part, splits, m, e);
+}
+
+}  // namespace bfa
+
+using namespace bfa;
+
+extern "C" int64_t bfa_fused_rmsnorm_qkv_workspace_size(int64_t tokens, int64_t hidden,
+                                                        int64_t qkv_dim, int64_t head_dim) {
+  if (tokens <= 0) return 0;
+  const QkvPlan p = make_plan(tokens, qkv_dim, hidden, head_dim);
+  return p.operand_bytes + p.part_bytes;
+}
+
+extern "C" int bfa_qkv_projection(const void* operand, int64_t tokens, int64_t hidden,
+                                  const void* qkv_weight, int w_dtype, int64_t qkv_dim,
+                                  int64_t w_stride, const void* bias, int bias_dtype,
+                                  int64_t num_q_heads, int64_t num_kv_heads, int qkv_dtype,
+                                  const void* q_norm_weight, const void* k_norm_weight,
+                                  int qk_norm_dtype, float qk_eps, int qk_norm_out_dtype,
+                                  const void* positions, int positions_dtype,
+                                  const float* cos_sin_cache, int64_t max_position, void* out,
+                                  int out_dtype, int64_t out_stride, void* part_workspace,
+                                  int64_t part_workspace_bytes, int32_t* status, void* stream) {
+  const char* what = "bfa_qkv_projection";
+  BFA_REQUIRE(w_dtype == BFA_DTYPE_BF16 || w_dtype == BFA_DTYPE_F16, "%s: weight must be bf16/fp16", what);
+  BFA_REQUIRE(is_float_dtype(qkv_dtype) && is_float_dtype(out_dtype) && is_float_dtype(qk_norm_out_dtype),
+              "%s: bad dtype", what);
+  BFA_REQUIRE(tokens >= 0 && hidden > 0 && qkv_dim > 0 && num_q_heads > 0 && num_kv_heads > 0,
+              "%s: bad geometry", what);
+  const int64_t heads = num_q_heads + 2 * num_kv_heads;
+  BFA_REQUIRE(qkv_dim % heads == 0, "%s: qkv_dim %lld not divisible by %lld heads", what,
+              (long long)qkv_dim, (long long)heads);
+  const int64_t hd = qkv_dim / heads;
+  BFA_REQUIRE(hidden % 16 == 0, "%s: hidden must be a multiple of 16 (got %lld)", what, (long long)hidden);
+  BFA_REQUIRE(w_stride % 8 == 0 && aligned16(qkv_weight) && aligned16(operand),
+              "%s: operand/weight rows must be 16-byte aligned", what);
+  BFA_REQUIRE(cos_sin_cache == nullptr || (positions && (positions_dtype == BFA_DTYPE_I64 ||
+                                                         positions_dtype == BFA_DTYPE_I32)),
+              "%s: RoPE needs int32/int64 positions", what);
+  BFA_REQUIRE(cos_sin_cache == nullptr || hd % 2 == 0, "%s: RoPE needs an even head_dim", what);
+  BFA_REQUIRE(hd <= 512, "%s: head_dim %lld > 512 unsupported", what, (long long)hd);
+  if (tokens == 0) return BFA_OK;
+  BFA_REQUIRE(out, "%s: null output", what);
+
+  const QkvPlan p = make_plan(tokens, qkv_dim, hidden, hd);
+  BFA_REQUIRE(p.decode || !p.fused_epi || (out_stride % 4 == 0 && aligned16(out)),
+              "%s: output rows must be 16-byte aligned", what);
+  BFA_REQUIRE(part_workspace_bytes >= p.part_bytes && (p.part_bytes == 0 || part_workspace),
+              "%s: workspace too small (%lld < %lld bytes)", what, (long long)part_workspace_bytes,
+              (long long)p.part_bytes);
+
+  QkvEpi e{};
+  e.bias = bias; e.bias_dtype = bias_dtype;
+  e.qkv_dt = qkv_dtype; e.norm_dt = qk_norm_out_dtype; e.out_dt = out_dtype;
+  e.n = qkv_dim; e.hq = num_q_heads; e.hkv = num_kv_heads; e.hd = hd;
+  e.qn_w = q_norm_weight; e.kn_w = k_norm_weight; e.qk_w_dtype = qk_norm_dtype; e.qk_eps = qk_eps;
+  e.positions = positions; e.pos_is_i64 = positions_dtype == BFA_DTYPE_I64;
+  e.cs = cos_sin_cache; e.max_pos = max_position;
+  e.out = out; e.ldo = out_stride; e.status = status;
+
+  const hipStream_t st = as_stream(stream);
+  const bool bf16 = w_dtype == BFA_DTYPE_BF16;
+  float* part = static_cast<float*>(part_workspace);
+  if (p.decode) {
+    SplitArgs s{};
+    s.a = static_cast<const uint16_t*>(operand);
+    s.w = static_cast<const uint16_t*>(qkv_weight);
+    s.m = tokens; s.n = qkv_dim; s.k = hidden; s.lda = hidden; s.ldw = w_stride;
+    s.kchunk = p.kchunk; s.part = part;
+    if (bf16) launch_decode<true>(p, s, st); else launch_decode<false>(p, s, st);
+    int rc = check_launch(what);
+    if (rc != BFA_OK) return rc;
+    launch_epilogue(part, p.splits, tokens, e, st);
+    return check_launch(what);
+  }
+  GemmArgs g{};
+  g.a = static_cast<const uint16_t*>(operand);
+  g.w = static_cast<const uint16_t*>(qkv_weight);
+  g.m = tokens; g.n = qkv_dim; g.k = hidden; g.lda = hidden; g.ldw = w_stride;
+  g.raw = part;
+  if (bf16) launch_prefill<true>(p, g, e, st); else launch_prefill<false>(p, g, e, st);
+  int rc = check_launch(what);
+  if (rc != BFA_OK || p.fused_epi) return rc;
+  launch_epilogue(part, 1, tokens, e, st);
+  return check_launch(what);
+}
+
+extern "C" int bfa_fused_rmsnorm_qkv(const void* x, int x_dtype, int64_t tokens, int64_t hidden,
+                                     int64_t x_stride, const void* norm_weight, int nw_dtype,
+                                     float eps, int mixed_rounding, const void* qkv_weight,
+                                     int w_dtype, int64_t qkv_dim, int64_t w_stride,
+                                     const void* bias, int bias_dtype, int64_t num_q_heads,
+                                     int64_t num_kv_heads, int qkv_dtype,
+                                     const void* q_norm_weight, const void* k_norm_weight,
+                                     int qk_norm_dtype, float qk_eps, int qk_norm_out_dtype,
+                                     const void* positions, int positions_dtype,
+                                     const float* cos_sin_cache, int64_t max_position, void* out,
+                                     int out_dtype, int64_t out_stride, void* workspace,
+                                     int64_t workspace_bytes, int32_t* status, void* stream) {
+  const char* what = "bfa_fused_rmsnorm_qkv";
+  BFA_REQUIRE(x && norm_weight && qkv_weight, "%s: null pointer", what);
+  if (tokens == 0) return BFA_OK;
+  const int64_t heads = num_q_heads + 2 * num_kv_heads;
+  BFA_REQUIRE(heads > 0 && qkv_dim % heads == 0, "%s: bad head geometry", what);
+  const QkvPlan p = make_plan(tokens, qkv_dim, hidden, qkv_dim / heads);
+  BFA_REQUIRE(workspace && workspace_bytes >= p.operand_bytes + p.part_bytes && aligned16(workspace),
+              "%s: workspace too small (%lld < %lld bytes)", what, (long long)workspace_bytes,
+              (long long)(p.operand_bytes + p.part_bytes));
+  char* ws = static_cast<char*>(workspace);
+  int rc = launch_qkv_operand(x, x_dtype, tokens, hidden, x_stride, norm_weight, nw_dtype,
+                              mixed_rounding != 0, ws, w_dtype, eps, as_stream(stream));
+  if (rc != BFA_OK) return rc;
+  return bfa_qkv_projection(ws, tokens, hidden, qkv_weight, w_dtype, qkv_dim, w_stride, bias,
+                            bias_dtype, num_q_heads, num_kv_heads, qkv_dtype, q_norm_weight,
+                            k_norm_weight, qk_norm_dtype, qk_eps, qk_norm_out_dtype, positions,
+                            positions_dtype, cos_sin_cache, max_position, out, out_dtype,
+                            out_stride, ws + p.operand_bytes, workspace_bytes - p.operand_bytes,
+                            status, stream);
+}

@@ -1,0 +1,425 @@
+// Rotary embedding (neox half-split) and the paged differential re-rotation of
+// cached chunk K, on gfx950.
+//
+// RotaryEmbedding.forward / apply_rotary_emb (layers/rotary_embedding.py:6-24,49-65):
+//   cs = cos_sin_cache[positions]            (fp32 [max_pos, D], cos | sin halves)
+//   x1, x2 = x.f32.chunk(2, -1)
+//   y = cat(x1*cos - x2*sin, x2*cos + x1*sin).to(x.dtype)
+// Each product and sum is rounded separately (the library is built with
+// -ffp-contract=off), which is what the unfused torch op chain computes, so
+// the result matches it bit for bit before the final cast.  Negative positions
+// index from the end of the table as torch indexing does; positions outside
+// [-max_pos, max_pos) set BFA_STATUS_INDEX_OOB and produce zeros.
+//
+// A row is one (token, head) vector of D elements.  A group of D/16 lanes owns
+// a row: lane i handles x1[8i..8i+8) and the matching x2 chunk D/2 further on,
+// i.e. two 16-byte loads and two 16-byte stores for bf16, plus the cos/sin
+// row read from the (L2-resident) table.
+#include "bfa_device.h"
+#include "bfa_host.h"
+
+namespace bfa {
+
+__device__ __forceinline__ int64_t wrap_position(int64_t p, int64_t max_pos, bool& ok) {
+  if (p < 0) p += max_pos;
+  ok = (p >= 0 && p < max_pos);
+  return ok ? p : 0;
+}
+
+// y1 = x1*c - x2*s ; y2 = x2*c + x1*s   (in place on x1/x2)
+__device__ __forceinline__ void rotate8(float (&x1)[8], float (&x2)[8], const float (&c)[8],
+                                        const float (&s)[8]) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float a = x1[i], b = x2[i];
+    x1[i] = a * c[i] - b * s[i];
+    x2[i] = b * c[i] + a * s[i];
+  }
+}
+
+__device__ __forceinline__ void load_cs8(const float* row, int64_t half, int j, float (&c)[8],
+                                         float (&s)[8]) {
+  load8<BFA_DTYPE_F32>(row + j, c);
+  load8<BFA_DTYPE_F32>(row + half + j, s);
+}
+
+// ----------------------------------------------------------------- RoPE
+struct RopeTensor {
+  const void* x;
+  void* y;
+  int64_t heads;
+  int64_t s_tok, s_head;  // input strides (elements); output is contiguous [T, heads, D]
+};
+
+struct RopeArgs {
+  const void* positions;  // nullptr: token t uses cos/sin rows cosp/sinp + t*cs_stride
+  int pos_is_i64;
+  int64_t num_tokens;
+  const float* cache;
+  int64_t max_pos;
+  const float* cosp;
+  const float* sinp;
+  int64_t cs_stride;
+  int64_t head_dim;
+  RopeTensor t[2];  // query, key (heads == 0: absent)
+  int* status;
+};
+
+__device__ __forceinline__ int64_t load_pos(const void* p, int is64, int64_t t) {
+  return is64 ? static_cast<const int64_t*>(p)[t] : static_cast<const int32_t*>(p)[t];
+}
+
+// cos / sin rows for token `tok`; ok=false for an out-of-range position.
+__device__ __forceinline__ void cs_rows(const RopeArgs& a, int64_t tok, const float*& c,
+                                        const float*& s, bool& ok) {
+  if (a.positions) {
+    const int64_t p = wrap_position(load_pos(a.positions, a.pos_is_i64, tok), a.max_pos, ok);
+    c = a.cache + p * a.head_dim;
+    s = c + a.head_dim / 2;
+  } else {
+    ok = true;
+    c = a.cosp + tok * a.cs_stride;
+    s = a.sinp + tok * a.cs_stride;
+  }
+}
+
+// Vector path: D % 16 == 0, 16-byte aligned rows.  LPR = lanes per row = D/16.
+template <int DT>
+__global__ __launch_bounds__(256) void rope_vec_kernel(RopeArgs a, int64_t total_rows, int lpr) {
+  using T = typename Elem<DT>::T;
+  const int64_t rows_per_wg = 256 / lpr;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * rows_per_wg + threadIdx.x / lpr;
+  const int lane = threadIdx.x % lpr;
+  if (row >= total_rows) return;
+  const int64_t rows_q = a.num_tokens * a.t[0].heads;
+  const int which = row < rows_q ? 0 : 1;
+  const RopeTensor& tt = a.t[which];
+  const int64_t r = which == 0 ? row : row - rows_q;
+  const int64_t tok = r / tt.heads, head = r - tok * tt.heads;
+  const int64_t half = a.head_dim / 2;
+  const int j = lane * 8;
+  bool ok;
+  const float* crow;
+  const float* srow;
+  cs_rows(a, tok, crow, srow, ok);
+  T* yp = static_cast<T*>(tt.y) + r * a.head_dim;
+  float x1[8], x2[8];
+  if (ok) {
+    const T* xp = static_cast<const T*>(tt.x) + tok * tt.s_tok + head * tt.s_head;
+    float c[8], s[8];
+    load8<DT>(xp + j, x1);
+    load8<DT>(xp + half + j, x2);
+    load8<BFA_DTYPE_F32>(crow + j, c);
+    load8<BFA_DTYPE_F32>(srow + j, s);
+    rotate8(x1, x2, c, s);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) x1[i] = x2[i] = 0.f;
+    if (lane == 0) flag_status(a.status, BFA_STATUS_INDEX_OOB);
+  }
+  store8<DT>(yp + j, x1);
+  store8<DT>(yp + half + j, x2);
+}
+
+// Scalar path: any even D, any alignment.  One lane per (row, pair).
+template <int DT>
+__global__ __launch_bounds__(256) void rope_scalar_kernel(RopeArgs a, int64_t total_rows) {
+  const int64_t half = a.head_dim / 2;
+  const int64_t item = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (item >= total_rows * half) return;
+  const int64_t row = item / half;
+  const int64_t j = item - row * half;
+  const int64_t rows_q = a.num_tokens * a.t[0].heads;
+  const int which = row < rows_q ? 0 : 1;
+  const RopeTensor& tt = a.t[which];
+  const int64_t r = which == 0 ? row : row - rows_q;
+  const int64_t tok = r / tt.heads, head = r - tok * tt.heads;
+  bool ok;
+  const float* crow;
+  const float* srow;
+  cs_rows(a, tok, crow, srow, ok);
+  float y1 = 0.f, y2 = 0.f;
+  if (ok) {
+    const int64_t xo = tok * tt.s_tok + head * tt.s_head;
+    const float x1 = load1<DT>(tt.x, xo + j), x2 = load1<DT>(tt.x, xo + half + j);
+    const float c = crow[j], s = srow[j];
+    y1 = x1 * c - x2 * s;
+    y2 = x2 * c + x1 * s;
+  } else if (j == 0) {
+    flag_status(a.status, BFA_STATUS_INDEX_OOB);
+  }
+  store1<DT>(tt.y, r * a.head_dim + j, y1);
+  store1<DT>(tt.y, r * a.head_dim + half + j, y2);
+}
+
+template <int DT>
+static void launch_rope(const RopeArgs& a, bool vec, hipStream_t s) {
+  const int64_t total_rows = a.num_tokens * (a.t[0].heads + a.t[1].heads);
+  if (vec) {
+    const int lpr = static_cast<int>(a.head_dim / 16);
+    const int64_t rpw = 256 / lpr;
+    hipLaunchKernelGGL((rope_vec_kernel<DT>), dim3(cdiv(total_rows, rpw)), dim3(256), 0, s, a,
+                       total_rows, lpr);
+  } else {
+    hipLaunchKernelGGL((rope_scalar_kernel<DT>), dim3(cdiv(total_rows * (a.head_dim / 2), 256)),
+                       dim3(256), 0, s, a, total_rows);
+  }
+}
+
+// ------------------------------------------------- paged differential RoPE
+// The per-layer cache is [num_pages, 2, Hkv, page_size, D] (HND, K at index 0;
+// engine/page_manager.py:36-42).  Workgroup (g, h) handles page-list entry g
+// and kv head h.  For the chunk c that owns entry g the rotation is by
+// delta[c] = global_start - cached_start (cascade_attention.py:151-174), one
+// cos/sin row for the whole chunk.  delta == 0 leaves K untouched (the
+// reference skips the rotation), i.e. a plain copy in the out-of-place mode.
+// With a k_norm weight the per-(token, head) RMSNorm of
+// cascade_attention.py:177-178 (RMSNorm.rms_forward on the bf16 rotated K) is
+// applied before the store.
+struct RerotArgs {
+  void* cache;
+  int64_t page_elems;  // elements per page (2*Hkv*page_size*D)
+  int64_t num_cache_pages;
+  int64_t hkv, page_size, head_dim;
+  const int32_t* page_indices;
+  const int32_t* chunk_indptr;
+  const int32_t* last_page_len;
+  const void* delta;
+  int delta_is_i64;
+  int64_t num_chunks;
+  const float* cs_cache;
+  int64_t max_pos;
+  const void* norm_w;
+  int norm_w_dtype;
+  float norm_eps;
+  void* out;  // nullptr: rotate the cache in place; else [num_entries, page_size, Hkv, D]
+  int* status;
+};
+
+template <int DT, bool NORM>
+__global__ __launch_bounds__(256) void rerotate_kernel(RerotArgs a) {
+  using T = typename Elem<DT>::T;
+  const int64_t g = blockIdx.x;  // page-list entry
+  const int64_t h = blockIdx.y;  // kv head
+  // chunk owning entry g: last c with indptr[c] <= g (indptr is non-decreasing)
+  int64_t lo = 0, hi = a.num_chunks - 1;
+  while (lo < hi) {
+    const int64_t mid = (lo + hi + 1) / 2;
+    if (a.chunk_indptr[mid] <= g) lo = mid; else hi = mid - 1;
+  }
+  const int64_t c = lo;
+  const bool last = (g == a.chunk_indptr[c + 1] - 1);
+  const int64_t ntok =
+      last ? max(static_cast<int64_t>(0), min(static_cast<int64_t>(a.last_page_len[c]), a.page_size))
+           : a.page_size;
+  const int64_t page = a.page_indices[g];
+  const int64_t delta = a.delta_is_i64 ? static_cast<const int64_t*>(a.delta)[c]
+                                       : static_cast<const int32_t*>(a.delta)[c];
+  if (page < 0 || page >= a.num_cache_pages) {
+    if (threadIdx.x == 0) flag_status(a.status, BFA_STATUS_INDEX_OOB);
+    return;
+  }
+  bool ok = true;
+  const int64_t p = wrap_position(delta, a.max_pos, ok);
+  if (!ok) {
+    if (threadIdx.x == 0) flag_status(a.status, BFA_STATUS_INDEX_OOB);
+    return;
+  }
+  const bool rotate = delta != 0;
+  if (!rotate && a.out == nullptr) return;  // in place, nothing to do
+
+  const int lpr = static_cast<int>(a.head_dim / 16);
+  const int rows_per_pass = 256 / lpr;
+  const int lane = threadIdx.x % lpr;
+  const int64_t half = a.head_dim / 2;
+  const int j = lane * 8;
+  T* kpage = static_cast<T*>(a.cache) + page * a.page_elems + h * a.page_size * a.head_dim;
+  float cs[8], sn[8];
+  if (rotate) load_cs8(a.cs_cache + p * a.head_dim, half, j, cs, sn);
+
+  // Out-of-place output is page-padded: slots past the chunk's last token are zeroed.
+  const int64_t nslots = a.out == nullptr ? ntok : a.page_size;
+  for (int64_t tok = threadIdx.x / lpr; tok < nslots; tok += rows_per_pass) {
+    if (tok >= ntok) {
+      T* dst = static_cast<T*>(a.out) + ((g * a.page_size + tok) * a.hkv + h) * a.head_dim;
+      const float z[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+      store8<DT>(dst + j, z);
+      store8<DT>(dst + half + j, z);
+      continue;
+    }
+    T* src = kpage + tok * a.head_dim;
+    float x1[8], x2[8];
+    load8<DT>(src + j, x1);
+    load8<DT>(src + half + j, x2);
+    if (rotate) {
+      rotate8(x1, x2, cs, sn);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {  // apply_rotary_emb returns x.dtype
+        x1[i] = Elem<DT>::round(x1[i]);
+        x2[i] = Elem<DT>::round(x2[i]);
+      }
+    }
+    if constexpr (NORM) {
+      float ss = 0.f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) ss += x1[i] * x1[i] + x2[i] * x2[i];
+      // lanes of one row are an aligned group of lpr (4 or 8, a power of two)
+      for (int m = lpr / 2; m >= 1; m >>= 1) ss += __shfl_xor(ss, m, kWave);
+      const float r = 1.0f / sqrtf(ss / static_cast<float>(a.head_dim) + a.norm_eps);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float g1 = load_any(a.norm_w, a.norm_w_dtype, j + i);
+        const float g2 = load_any(a.norm_w, a.norm_w_dtype, half + j + i);
+        x1[i] = Elem<DT>::round(x1[i] * r) * g1;
+        x2[i] = Elem<DT>::round(x2[i] * r) * g2;
+      }
+    }
+    T* dst = a.out == nullptr
+                 ? src
+                 : static_cast<T*>(a.out) + ((g * a.page_size + tok) * a.hkv + h) * a.head_dim;
+    store8<DT>(dst + j, x1);
+    store8<DT>(dst + half + j, x2);
+  }
+}
+
+}  // namespace bfa
+
+using namespace bfa;
+
+extern "C" int bfa_rotary_embedding(const void* positions, int positions_dtype, int64_t num_tokens,
+                                    const float* cos_sin_cache, int64_t max_position,
+                                    int64_t head_size, int dtype, const void* query,
+                                    int64_t q_heads, int64_t q_stride_token,
+                                    int64_t q_stride_head, void* query_out, const void* key,
+                                    int64_t k_heads, int64_t k_stride_token,
+                                    int64_t k_stride_head, void* key_out, int32_t* status,
+                                    void* stream) {
+  const char* what = "bfa_rotary_embedding";
+  BFA_REQUIRE(is_float_dtype(dtype), "%s: bad dtype", what);
+  BFA_REQUIRE(positions_dtype == BFA_DTYPE_I64 || positions_dtype == BFA_DTYPE_I32,
+              "%s: positions must be int32/int64", what);
+  BFA_REQUIRE(head_size > 0 && head_size % 2 == 0, "%s: head_size must be even", what);
+  BFA_REQUIRE(num_tokens >= 0 && q_heads >= 0 && k_heads >= 0 && max_position > 0,
+              "%s: bad geometry", what);
+  if (!query) q_heads = 0;
+  if (!key) k_heads = 0;
+  if (num_tokens == 0 || q_heads + k_heads == 0) return BFA_OK;
+  BFA_REQUIRE(positions && cos_sin_cache, "%s: null pointer", what);
+  BFA_REQUIRE(q_heads == 0 || query_out, "%s: null query_out", what);
+  BFA_REQUIRE(k_heads == 0 || key_out, "%s: null key_out", what);
+  RopeArgs a{};
+  a.positions = positions;
+  a.pos_is_i64 = positions_dtype == BFA_DTYPE_I64;
+  a.num_tokens = num_tokens;
+  a.cache = cos_sin_cache;
+  a.max_pos = max_position;
+  a.head_dim = head_size;
+  a.t[0] = RopeTensor{query, query_out, q_heads, q_stride_token, q_stride_head};
+  a.t[1] = RopeTensor{key, key_out, k_heads, k_stride_token, k_stride_head};
+  a.status = status;
+  auto tensor_vec_ok = [](const RopeTensor& t) {
+    return t.heads == 0 || (aligned16(t.x) && aligned16(t.y) && t.s_tok % 8 == 0 && t.s_head % 8 == 0);
+  };
+  const bool vec = head_size % 16 == 0 && head_size <= 4096 && aligned16(cos_sin_cache) &&
+                   tensor_vec_ok(a.t[0]) && tensor_vec_ok(a.t[1]);
+  const hipStream_t s = as_stream(stream);
+  switch (dtype) {
+    case BFA_DTYPE_BF16: launch_rope<BFA_DTYPE_BF16>(a, vec, s); break;
+    case BFA_DTYPE_F16: launch_rope<BFA_DTYPE_F16>(a, vec, s); break;
+    default: launch_rope<BFA_DTYPE_F32>(a, vec, s); break;
+  }
+  return check_launch(what);
+}
+
+extern "C" int bfa_rerotate_paged_k(void* kv_cache, int dtype, int64_t num_cache_pages,
+                                    int64_t num_kv_heads, int64_t page_size, int64_t head_dim,
+                                    const int32_t* page_indices, int64_t num_entries,
+                                    const int32_t* chunk_indptr, const int32_t* last_page_len,
+                                    const void* chunk_delta, int delta_dtype, int64_t num_chunks,
+                                    const float* cos_sin_cache, int64_t max_position,
+                                    const void* k_norm_weight, int k_norm_dtype,
+                                    float k_norm_eps, void* out, int32_t* status,
+                                    void* stream) {
+  const char* what = "bfa_rerotate_paged_k";
+  BFA_REQUIRE(is_float_dtype(dtype), "%s: bad dtype", what);
+  BFA_REQUIRE(delta_dtype == BFA_DTYPE_I64 || delta_dtype == BFA_DTYPE_I32,
+              "%s: delta must be int32/int64", what);
+  BFA_REQUIRE(head_dim % 16 == 0 && head_dim >= 16 && head_dim <= 4096,
+              "%s: head_dim must be a multiple of 16 (got %lld)", what, (long long)head_dim);
+  BFA_REQUIRE(num_kv_heads > 0 && page_size > 0 && num_cache_pages >= 0 && num_entries >= 0 &&
+                  num_chunks >= 0 && max_position > 0,
+              "%s: bad geometry", what);
+  if (num_entries == 0 || num_chunks == 0) return BFA_OK;
+  BFA_REQUIRE(kv_cache && page_indices && chunk_indptr && last_page_len && chunk_delta &&
+                  cos_sin_cache,
+              "%s: null pointer", what);
+  BFA_REQUIRE(!(k_norm_weight && out == nullptr),
+              "%s: the fused k_norm needs an output buffer (the cache keeps un-normed K)", what);
+  BFA_REQUIRE(aligned16(kv_cache) && aligned16(cos_sin_cache) && (out == nullptr || aligned16(out)),
+              "%s: buffers must be 16-byte aligned", what);
+  BFA_REQUIRE(num_kv_heads <= 65535, "%s: too many kv heads", what);
+  RerotArgs a{};
+  a.cache = kv_cache;
+  a.page_elems = 2 * num_kv_heads * page_size * head_dim;
+  a.num_cache_pages = num_cache_pages;
+  a.hkv = num_kv_heads;
+  a.page_size = page_size;
+  a.head_dim = head_dim;
+  a.page_indices = page_indices;
+  a.chunk_indptr = chunk_indptr;
+  a.last_page_len = last_page_len;
+  a.delta = chunk_delta;
+  a.delta_is_i64 = delta_dtype == BFA_DTYPE_I64;
+  a.num_chunks = num_chunks;
+  a.cs_cache = cos_sin_cache;
+  a.max_pos = max_position;
+  a.norm_w = k_norm_weight;
+  a.norm_w_dtype = k_norm_dtype;
+  a.norm_eps = k_norm_eps;
+  a.out = out;
+  a.status = status;
+  const dim3 grid(static_cast<unsigned>(num_entries), static_cast<unsigned>(num_kv_heads));
+  const hipStream_t s = as_stream(stream);
+  const bool norm = k_norm_weight != nullptr;
+#define BFA_RR(DT)                                                                          \
+  if (norm) hipLaunchKernelGGL((rerotate_kernel<DT, true>), grid, dim3(256), 0, s, a);     \
+  else hipLaunchKernelGGL((rerotate_kernel<DT, false>), grid, dim3(256), 0, s, a);
+  switch (dtype) {
+    case BFA_DTYPE_BF16: BFA_RR(BFA_DTYPE_BF16); break;
+    case BFA_DTYPE_F16: BFA_RR(BFA_DTYPE_F16); break;
+    default: BFA_RR(BFA_DTYPE_F32); break;
+  }
+#undef BFA_RR
+  return check_launch(what);
+}
+
+extern "C" int bfa_apply_rotary_emb(const void* x, int dtype, int64_t num_tokens, int64_t heads,
+                                    int64_t head_size, int64_t x_stride_token,
+                                    int64_t x_stride_head, const float* cos, const float* sin,
+                                    int64_t cs_stride_token, void* out, void* stream) {
+  const char* what = "bfa_apply_rotary_emb";
+  BFA_REQUIRE(is_float_dtype(dtype), "%s: bad dtype", what);
+  BFA_REQUIRE(head_size > 0 && head_size % 2 == 0, "%s: head_size must be even", what);
+  BFA_REQUIRE(num_tokens >= 0 && heads >= 0, "%s: bad geometry", what);
+  if (num_tokens == 0 || heads == 0) return BFA_OK;
+  BFA_REQUIRE(x && cos && sin && out, "%s: null pointer", what);
+  RopeArgs a{};
+  a.positions = nullptr;
+  a.num_tokens = num_tokens;
+  a.head_dim = head_size;
+  a.cosp = cos;
+  a.sinp = sin;
+  a.cs_stride = cs_stride_token;
+  a.t[0] = RopeTensor{x, out, heads, x_stride_token, x_stride_head};
+  a.t[1] = RopeTensor{nullptr, nullptr, 0, 0, 0};
+  const bool vec = head_size % 16 == 0 && head_size <= 4096 && aligned16(x) && aligned16(out) &&
+                   aligned16(cos) && aligned16(sin) && cs_stride_token % 4 == 0 &&
+                   x_stride_token % 8 == 0 && x_stride_head % 8 == 0;
+  const hipStream_t s = as_stream(stream);
+  switch (dtype) {
+    case BFA_DTYPE_BF16: launch_rope<BFA_DTYPE_BF16>(a, vec, s); break;
+    case BFA_DTYPE_F16: launch_rope<BFA_DTYPE_F16>(a, vec, s); break;
+    default: launch_rope<BFA_DTYPE_F32>(a, vec, s); break;
+  }
+  return check_launch(what);
+}

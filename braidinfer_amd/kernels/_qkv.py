@@ -1,0 +1,122 @@
+"""Shared launcher for the fused RMSNorm+QKV variants (bfa_fused_rmsnorm_qkv).
+
+The four reference classes differ only in rounding points and output dtype
+(braidinfer/kernels/fused_rmsnorm_qkv_{mixed_precision,production,minimal_f32,
+with_bias}.py); each class module calls :func:`fused_rmsnorm_qkv` with its
+own settings.  The optional q/k-norm and RoPE arguments fuse what the Qwen3 and
+Llama attention forwards do with the kernel output (models/qwen3.py:257-309,
+models/llama.py:169-205).
+"""
+from __future__ import annotations
+
+import torch
+
+from .. import _lib
+
+_OPERAND_DTYPES = (torch.bfloat16, torch.float16)
+
+
+def head_dim_of(qkv_dim: int, num_q_heads: int, num_kv_heads: int) -> int:
+    """head_dim = qkv_dim // (Hq + 2*Hkv), as every reference variant derives it."""
+    return qkv_dim // (num_q_heads + 2 * num_kv_heads)
+
+
+def _matrix_weight(w: torch.Tensor) -> torch.Tensor:
+    # The matrix cores take bf16 or fp16 operands.  An fp32 weight is rounded to
+    # bf16, which is what the mixed/production Triton kernels do with every
+    # weight tile (`weight_tile.to(tl.bfloat16)`).
+    if w.dtype not in _OPERAND_DTYPES:
+        w = w.to(torch.bfloat16)
+    if w.stride(-1) != 1 or w.stride(0) % 8 != 0 or w.data_ptr() % 16 != 0:
+        w = w.contiguous()
+    return w
+
+
+def fused_rmsnorm_qkv(
+    input: torch.Tensor,
+    norm_weight: torch.Tensor,
+    qkv_weight: torch.Tensor,
+    num_q_heads: int,
+    num_kv_heads: int,
+    eps: float,
+    *,
+    mixed_rounding: bool,
+    qkv_dtype: torch.dtype,
+    out_dtype: torch.dtype,
+    qkv_bias: torch.Tensor | None = None,
+    q_norm_weight: torch.Tensor | None = None,
+    k_norm_weight: torch.Tensor | None = None,
+    qk_norm_eps: float = 1e-6,
+    qk_norm_out_dtype: torch.dtype | None = None,
+    positions: torch.Tensor | None = None,
+    cos_sin_cache: torch.Tensor | None = None,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Runs RMSNorm -> x @ W^T (+bias) [-> q/k RMSNorm] [-> RoPE] and returns the
+    [tokens, qkv_dim] result (q | k | v columns) in `out_dtype`."""
+    assert input.dim() == 2, f"Expected 2D input, got {input.dim()}D"
+    tokens, hidden = input.shape
+    qkv_dim = qkv_weight.shape[0]
+    if input.stride(-1) != 1 or input.data_ptr() % 16 != 0:
+        input = input.contiguous()
+    norm_weight = norm_weight.contiguous()
+    w = _matrix_weight(qkv_weight)
+    if qkv_bias is not None:
+        qkv_bias = qkv_bias.contiguous()
+    dev = _lib.require_device(input, norm_weight, w, qkv_bias, q_norm_weight, k_norm_weight,
+                              positions, cos_sin_cache)
+    hd = head_dim_of(qkv_dim, num_q_heads, num_kv_heads)
+    if q_norm_weight is not None:
+        q_norm_weight = q_norm_weight.contiguous()
+    if k_norm_weight is not None:
+        k_norm_weight = k_norm_weight.contiguous()
+    qn_dtype = (q_norm_weight if q_norm_weight is not None else k_norm_weight)
+    if q_norm_weight is not None and k_norm_weight is not None and q_norm_weight.dtype != k_norm_weight.dtype:
+        k_norm_weight = k_norm_weight.to(q_norm_weight.dtype)
+    if cos_sin_cache is not None:
+        if positions is None:
+            raise ValueError("RoPE needs positions")
+        if cos_sin_cache.dtype != torch.float32:
+            raise TypeError("cos_sin_cache must be float32")
+        cos_sin_cache = cos_sin_cache.contiguous()
+        if cos_sin_cache.shape[-1] != hd:
+            raise ValueError(f"cos_sin_cache width {cos_sin_cache.shape[-1]} != head_dim {hd}")
+        positions = positions.reshape(-1)
+        if positions.numel() != tokens:
+            raise ValueError(f"{positions.numel()} positions for {tokens} tokens")
+        if positions.dtype not in (torch.int64, torch.int32):
+            positions = positions.long()
+        positions = positions.contiguous()
+    if out is None:
+        out = torch.empty((tokens, qkv_dim), dtype=out_dtype, device=dev)
+    if tokens == 0:
+        return out
+    ws_bytes = _lib.call("bfa_fused_rmsnorm_qkv_workspace_size", tokens, hidden, qkv_dim, hd)
+    workspace = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=dev)
+    _lib.call(
+        "bfa_fused_rmsnorm_qkv",
+        _lib.ptr(input), _lib.dtype_code(input), tokens, hidden, input.stride(0),
+        _lib.ptr(norm_weight), _lib.dtype_code(norm_weight), float(eps), int(mixed_rounding),
+        _lib.ptr(w), _lib.dtype_code(w), qkv_dim, w.stride(0),
+        _lib.ptr(qkv_bias), _lib.dtype_code(qkv_bias) if qkv_bias is not None else 0,
+        num_q_heads, num_kv_heads, _lib.dtype_code(qkv_dtype),
+        _lib.ptr(q_norm_weight), _lib.ptr(k_norm_weight),
+        _lib.dtype_code(qn_dtype) if qn_dtype is not None else 0, float(qk_norm_eps),
+        _lib.dtype_code(qk_norm_out_dtype or input.dtype),
+        _lib.ptr(positions), _lib.dtype_code(positions) if positions is not None else 0,
+        _lib.ptr(cos_sin_cache), cos_sin_cache.shape[0] if cos_sin_cache is not None else 0,
+        _lib.ptr(out), _lib.dtype_code(out), out.stride(0),
+        _lib.ptr(workspace), workspace.numel(),
+        _lib.ptr(_lib.status_word(dev)), _lib.stream_of(dev),
+    )
+    return out
+
+
+def split_heads(output: torch.Tensor, num_q_heads: int, num_kv_heads: int):
+    """Splits the [T, qkv_dim] buffer into q/k/v views of shape [T, heads, head_dim]
+    (the split/view sequence of the reference variants)."""
+    tokens, qkv_dim = output.shape
+    hd = head_dim_of(qkv_dim, num_q_heads, num_kv_heads)
+    q, k, v = output.split([num_q_heads * hd, num_kv_heads * hd, num_kv_heads * hd], dim=-1)
+    return (q.view(tokens, num_q_heads, hd), k.view(tokens, num_kv_heads, hd),
+            v.view(tokens, num_kv_heads, hd))

@@ -1,0 +1,226 @@
+/*
+ * braidinfer_amd — C ABI of the MI355X (gfx950) fused per-layer kernels.
+ *
+ * Every entry point takes plain device pointers, element counts and strides
+ * (strides are in ELEMENTS, not bytes), a dtype code for each tensor operand,
+ * and a hipStream_t passed as void* (NULL = the null stream).  Work is enqueued
+ * asynchronously on that stream; no entry point synchronises or allocates
+ * device memory unless its comment says so.
+ *
+ * Return value: BFA_OK (0) on success, a negative BFA_ERR_* code otherwise;
+ * bfa_last_error() then returns a message for the calling thread.
+ *
+ * The reference (braidpool/braidinfer) is pure Python/Triton and has no FFI of
+ * its own; each entry point below names the Python function or class whose
+ * semantics it reproduces, with the reference file:line.  The Python package
+ * braidinfer_amd (kernels/, layers/) binds these with ctypes under the
+ * reference's own class and function names.
+ */
+#ifndef BRAIDINFER_AMD_H_
+#define BRAIDINFER_AMD_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* dtype codes */
+#define BFA_DTYPE_F32 0
+#define BFA_DTYPE_F16 1
+#define BFA_DTYPE_BF16 2
+#define BFA_DTYPE_I32 3
+#define BFA_DTYPE_I64 4
+
+/* return codes */
+#define BFA_OK 0
+#define BFA_ERR_INVALID (-1)     /* bad argument (shape, dtype, pointer)      */
+#define BFA_ERR_UNSUPPORTED (-2) /* valid but not implemented for this shape  */
+#define BFA_ERR_LAUNCH (-3)      /* HIP launch / runtime error                */
+
+/* bits a kernel may OR into a caller-provided device status word (int32) */
+#define BFA_STATUS_INDEX_OOB 1 /* an index (token id, position, delta) was out of range */
+
+#define BFA_ABI_VERSION 1
+
+int bfa_abi_version(void);
+const char* bfa_last_error(void);
+
+/* ------------------------------------------------------------------ norms --
+ * Row geometry shared by the norm entry points: `rows` rows of `hidden`
+ * contiguous elements; row r lives at  (r / rows_inner) * stride_outer
+ *                                     + (r % rows_inner) * stride_inner.
+ * A 2-D [T, H] tensor is rows=T, rows_inner=1, stride_outer=row stride.
+ * A [T, heads, D] view (per-head q/k norm) is rows=T*heads, rows_inner=heads.
+ */
+
+/* RMSNorm.rms_forward — braidinfer/layers/layernorm.py:35-44.
+ *   y = to(x_dtype)( to(x_dtype)(x * rsqrt(mean(x^2) + eps)) * weight )
+ * (for fp32 x both casts are no-ops and the reference mutates x in place:
+ *  pass y == x to reproduce that).  y has x's dtype. */
+int bfa_rms_norm(const void* x, void* y, const void* weight, int x_dtype, int w_dtype,
+                 int64_t rows, int64_t rows_inner, int64_t hidden,
+                 int64_t x_stride_outer, int64_t x_stride_inner,
+                 int64_t y_stride_outer, int64_t y_stride_inner,
+                 float eps, void* stream);
+
+/* RMSNorm.add_rms_forward — braidinfer/layers/layernorm.py:46-57.
+ *   s = f32(x) + f32(residual);  residual_out = to(x_dtype)(s)
+ *   y = to(x_dtype)( to(x_dtype)(s * rsqrt(mean(s^2) + eps)) * weight )
+ * x, residual, y, residual_out: 2-D [rows, hidden] with the given row strides.
+ * residual_out may be NULL (the fp32 reference aliases it to y). */
+int bfa_add_rms_norm(const void* x, const void* residual, void* y, void* residual_out,
+                     const void* weight, int x_dtype, int w_dtype, int64_t rows,
+                     int64_t hidden, int64_t x_stride, int64_t residual_stride,
+                     int64_t y_stride, int64_t residual_out_stride, float eps,
+                     void* stream);
+
+/* RMSNormF32.forward — braidinfer/kernels/rmsnorm_f32.py:14-96,105-156.
+ *   rms = sqrt(sum(x^2)/hidden + eps);  y(fp32) = (x / rms) * weight */
+int bfa_rms_norm_f32(const void* x, float* y, const void* weight, int x_dtype, int w_dtype,
+                     int64_t rows, int64_t hidden, int64_t x_stride_row,
+                     int64_t x_stride_col, int64_t y_stride_row, int64_t y_stride_col,
+                     float eps, void* stream);
+
+/* ------------------------------------------------------------ embedding --
+ * VocabParallelEmbedding.forward — braidinfer/layers/embed_head.py:28-29
+ * (F.embedding(ids, weight)).  Byte copy of row ids[t] of `table` into row t
+ * of `out`: bit-exact for any element type of `elem_bytes` bytes.  ids are
+ * int32 or int64; an id outside [0, num_embeddings) yields a zero row and
+ * sets BFA_STATUS_INDEX_OOB in *status (status may be NULL). */
+int bfa_embedding(const void* table, int64_t num_embeddings, int64_t dim,
+                  int64_t table_row_stride, int elem_bytes, const void* ids, int ids_dtype,
+                  int64_t num_ids, void* out, int64_t out_row_stride, int32_t* status,
+                  void* stream);
+
+/* Embedding gather fused with the Qwen3 scaling
+ * `embed_tokens(ids) * (1/sqrt(H))` (braidinfer/models/qwen3.py:463-465):
+ * out = to(dtype)(f32(table[id]) * scale). */
+int bfa_embedding_scaled(const void* table, int64_t num_embeddings, int64_t dim,
+                         int64_t table_row_stride, int dtype, const void* ids, int ids_dtype,
+                         int64_t num_ids, void* out, int64_t out_row_stride, float scale,
+                         int32_t* status, void* stream);
+
+/* ---------------------------------------------------------------- SwiGLU --
+ * SiluAndMul.forward — braidinfer/layers/activation.py:11-13.
+ * x: [rows, 2*inter] (gate | up), y: [rows, inter];
+ * y = to(dtype)( to(dtype)(silu_f32(gate)) * up ). */
+int bfa_silu_and_mul(const void* x, void* y, int dtype, int64_t rows, int64_t inter,
+                     int64_t x_row_stride, int64_t y_row_stride, void* stream);
+
+/* ------------------------------------------------------------------ RoPE --
+ * RotaryEmbedding.forward / apply_rotary_emb —
+ * braidinfer/layers/rotary_embedding.py:6-24,49-65 (neox half-split).
+ * query/key are viewed as [num_tokens, heads, head_size] with the given
+ * token/head strides and unit element stride; results go to contiguous
+ * [num_tokens, heads, head_size] buffers query_out/key_out (same dtype).
+ * cos_sin_cache: fp32 [max_position, head_size] (cos | sin halves).
+ * Negative positions wrap as torch indexing does; positions outside
+ * [-max_position, max_position) give zeros and set BFA_STATUS_INDEX_OOB.
+ * query or key may be NULL to rotate only the other. */
+int bfa_rotary_embedding(const void* positions, int positions_dtype, int64_t num_tokens,
+                         const float* cos_sin_cache, int64_t max_position, int64_t head_size,
+                         int dtype, const void* query, int64_t q_heads, int64_t q_stride_token,
+                         int64_t q_stride_head, void* query_out, const void* key,
+                         int64_t k_heads, int64_t k_stride_token, int64_t k_stride_head,
+                         void* key_out, int32_t* status, void* stream);
+
+/* apply_rotary_emb(x, cos, sin) — braidinfer/layers/rotary_embedding.py:6-24 —
+ * with explicit per-token fp32 cos/sin rows (head_size/2 values each, row
+ * stride cs_stride_token) instead of a table lookup.  x is viewed as
+ * [num_tokens, heads, head_size]; out is contiguous, same dtype. */
+int bfa_apply_rotary_emb(const void* x, int dtype, int64_t num_tokens, int64_t heads,
+                         int64_t head_size, int64_t x_stride_token, int64_t x_stride_head,
+                         const float* cos, const float* sin, int64_t cs_stride_token, void* out,
+                         void* stream);
+
+/* Differential re-rotation of cached chunk K — the per-page loop body of
+ * CascadeAttention.forward, braidinfer/layers/cascade_attention.py:143-178.
+ * kv_cache: one layer of the paged HND cache
+ *   [num_cache_pages, 2, num_kv_heads, page_size, head_dim] (K at index 0;
+ *   braidinfer/engine/page_manager.py:36-42).
+ * Chunk c owns page-list entries [chunk_indptr[c], chunk_indptr[c+1]) of
+ * page_indices (int32, as CascadeAttention._create_level builds them,
+ * cascade_attention.py:264-295); its last page holds last_page_len[c] tokens.
+ * Every token of chunk c is rotated by chunk_delta[c] (= global_position_start
+ * - cached_position_start) using cos_sin_cache[chunk_delta[c]] with torch
+ * negative-index wrap; delta == 0 leaves K unchanged, as the reference does.
+ * out == NULL: rotate the cache in place.  Otherwise write
+ * out[entry, token, head, :] ([num_entries, page_size, num_kv_heads, head_dim],
+ * page-padded, padding slots zeroed) and leave the cache untouched; only then
+ * may k_norm_weight be given, fusing the k_norm of cascade_attention.py:177-178
+ * (RMSNorm.rms_forward over head_dim). */
+int bfa_rerotate_paged_k(void* kv_cache, int dtype, int64_t num_cache_pages,
+                         int64_t num_kv_heads, int64_t page_size, int64_t head_dim,
+                         const int32_t* page_indices, int64_t num_entries,
+                         const int32_t* chunk_indptr, const int32_t* last_page_len,
+                         const void* chunk_delta, int delta_dtype, int64_t num_chunks,
+                         const float* cos_sin_cache, int64_t max_position,
+                         const void* k_norm_weight, int k_norm_dtype, float k_norm_eps,
+                         void* out, int32_t* status, void* stream);
+
+/* -------------------------------------------------- fused RMSNorm + QKV --
+ * The four Triton variants share one entry point; the caller picks the
+ * rounding points:
+ *   FusedRMSNormQKVMixedPrecision  kernels/fused_rmsnorm_qkv_mixed_precision.py:14-247
+ *       mixed_rounding=1, qkv_dtype=x dtype
+ *   FusedRMSNormQKV                kernels/fused_rmsnorm_qkv_production.py:13-229
+ *       mixed_rounding=0, qkv_dtype=BF16
+ *   FusedRMSNormQKVMinimalF32      kernels/fused_rmsnorm_qkv_minimal_f32.py:14-214
+ *   FusedRMSNormQKVWithBias        kernels/fused_rmsnorm_qkv_with_bias.py:13-228
+ *       mixed_rounding=0, qkv_dtype=F32
+ * and optionally fuses what the model glue does next with the result:
+ *   q/k RMSNorm over head_dim (Qwen3, models/qwen3.py:257-281): pass
+ *       q_norm_weight / k_norm_weight (either may be NULL), the result is cast
+ *       to qk_norm_out_dtype;
+ *   RoPE (models/qwen3.py:309, models/llama.py:189): pass positions and
+ *       cos_sin_cache [max_position, head_dim].
+ * Output: out[tokens, qkv_dim] (q | k | v columns, row stride out_stride) in
+ * out_dtype.  W is [qkv_dim, hidden] (bf16 or fp16), rows [q; k; v]
+ * (layers/linear.py:78-114).  The normalised operand is rounded to W's dtype
+ * for the matrix cores (the fp32 variants round it once; see DESIGN).
+ * workspace: device scratch of bfa_fused_rmsnorm_qkv_workspace_size() bytes,
+ * 16-byte aligned; calls sharing a workspace must be stream-ordered. */
+int64_t bfa_fused_rmsnorm_qkv_workspace_size(int64_t tokens, int64_t hidden, int64_t qkv_dim,
+                                             int64_t head_dim);
+
+int bfa_fused_rmsnorm_qkv(const void* x, int x_dtype, int64_t tokens, int64_t hidden,
+                          int64_t x_stride, const void* norm_weight, int nw_dtype, float eps,
+                          int mixed_rounding, const void* qkv_weight, int w_dtype,
+                          int64_t qkv_dim, int64_t w_stride, const void* bias, int bias_dtype,
+                          int64_t num_q_heads, int64_t num_kv_heads, int qkv_dtype,
+                          const void* q_norm_weight, const void* k_norm_weight,
+                          int qk_norm_dtype, float qk_eps, int qk_norm_out_dtype,
+                          const void* positions, int positions_dtype,
+                          const float* cos_sin_cache, int64_t max_position, void* out,
+                          int out_dtype, int64_t out_stride, void* workspace,
+                          int64_t workspace_bytes, int32_t* status, void* stream);
+
+/* The two stages of bfa_fused_rmsnorm_qkv, exposed separately.
+ * Stage 1 (the RMSNorm prologue of every variant): operand[rows, hidden] =
+ *   mixed_rounding ? to(op)( to(bf16)(x / rms) * w ) : to(op)( (x / rms) * w ),
+ *   rms = sqrt(sum(x^2)/hidden + eps), op = operand_dtype (BF16 or F16). */
+int bfa_rmsnorm_qkv_operand(const void* x, int x_dtype, int64_t rows, int64_t hidden,
+                            int64_t x_stride, const void* norm_weight, int w_dtype,
+                            int mixed_rounding, void* operand, int operand_dtype, float eps,
+                            void* stream);
+
+/* Stage 2: projection of a normalised operand [tokens, hidden] (contiguous,
+ * W's dtype) with the epilogue described above.  part_workspace holds the
+ * split-K / raw fp32 partial sums: bfa_fused_rmsnorm_qkv_workspace_size()
+ * minus the operand's share (tokens*hidden*2 rounded up to 256 bytes). */
+int bfa_qkv_projection(const void* operand, int64_t tokens, int64_t hidden,
+                       const void* qkv_weight, int w_dtype, int64_t qkv_dim, int64_t w_stride,
+                       const void* bias, int bias_dtype, int64_t num_q_heads,
+                       int64_t num_kv_heads, int qkv_dtype, const void* q_norm_weight,
+                       const void* k_norm_weight, int qk_norm_dtype, float qk_eps,
+                       int qk_norm_out_dtype, const void* positions, int positions_dtype,
+                       const float* cos_sin_cache, int64_t max_position, void* out,
+                       int out_dtype, int64_t out_stride, void* part_workspace,
+                       int64_t part_workspace_bytes, int32_t* status, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* BRAIDINFER_AMD_H_ */

@@ -1,0 +1,220 @@
+"""torch-CPU restatement of the reference hot-path ops (test infrastructure only).
+
+Each function follows the cited reference lines op for op, with the same
+rounding points, on CPU tensors.  Inputs are never mutated (the reference's
+in-place fp32 forms are restated on a clone; the aliasing itself is tested
+against the product separately).
+"""
+from __future__ import annotations
+
+import torch
+import torch.nn.functional as F
+
+
+# --------------------------------------------------------------------- norms
+def rms_forward(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
+    """RMSNorm.rms_forward, braidinfer/layers/layernorm.py:35-44."""
+    orig_dtype = x.dtype
+    x = x.to(torch.float32).clone()
+    var = x.pow(2).mean(dim=-1, keepdim=True)
+    x.mul_(torch.rsqrt(var + eps))
+    x = x.to(orig_dtype)
+    return x.mul_(weight)
+
+
+def add_rms_forward(x: torch.Tensor, residual: torch.Tensor, weight: torch.Tensor,
+                    eps: float) -> tuple[torch.Tensor, torch.Tensor]:
+    """RMSNorm.add_rms_forward, braidinfer/layers/layernorm.py:46-57.
+    Returns (y, residual_out); for fp32 inputs the reference returns one tensor
+    twice, holding y."""
+    orig_dtype = x.dtype
+    x = x.to(torch.float32).clone().add_(residual.to(torch.float32))
+    residual_out = x.to(orig_dtype).clone()
+    var = x.pow(2).mean(dim=-1, keepdim=True)
+    x.mul_(torch.rsqrt(var + eps))
+    x = x.to(orig_dtype)
+    y = x.mul_(weight)
+    if orig_dtype == torch.float32:
+        return y, y
+    return y, residual_out
+
+
+def rmsnorm_f32(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
+    """RMSNormF32 kernel, braidinfer/kernels/rmsnorm_f32.py:47-96:
+    rms = sqrt(sum(x^2)/H + eps); out = (x / rms) * w, fp32."""
+    x32 = x.to(torch.float32)
+    acc = (x32 * x32).sum(dim=-1, keepdim=True)
+    rms = torch.sqrt(acc / x.shape[-1] + eps)
+    return (x32 / rms) * weight.to(torch.float32)
+
+
+# ----------------------------------------------------------------- embedding
+def embedding(ids: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
+    """VocabParallelEmbedding.forward, braidinfer/layers/embed_head.py:28-29."""
+    return F.embedding(ids, weight)
+
+
+def embedding_scaled(ids: torch.Tensor, weight: torch.Tensor, hidden_size: int) -> torch.Tensor:
+    """Qwen3Model.forward embedding + scaling, braidinfer/models/qwen3.py:463-465."""
+    h = F.embedding(ids, weight)
+    return h * (1.0 / (hidden_size ** 0.5))
+
+
+# -------------------------------------------------------------------- SwiGLU
+def silu_and_mul(x: torch.Tensor) -> torch.Tensor:
+    """SiluAndMul.forward, braidinfer/layers/activation.py:11-13."""
+    g, u = x.chunk(2, -1)
+    return F.silu(g) * u
+
+
+# ---------------------------------------------------------------------- RoPE
+def cos_sin_cache(head_size: int, max_position: int, base: float) -> torch.Tensor:
+    """RotaryEmbedding.__init__ table, braidinfer/layers/rotary_embedding.py:29-47."""
+    inv_freq = 1.0 / (base ** (torch.arange(0, head_size, 2, dtype=torch.float32) / head_size))
+    t = torch.arange(max_position, dtype=torch.float32)
+    freqs = torch.einsum("i,j -> ij", t, inv_freq)
+    return torch.cat((freqs.cos(), freqs.sin()), dim=-1).to(torch.float32)
+
+
+def apply_rotary_emb(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+    """apply_rotary_emb, braidinfer/layers/rotary_embedding.py:6-24."""
+    original_dtype = x.dtype
+    cos = cos.unsqueeze(-2).to(torch.float32)
+    sin = sin.unsqueeze(-2).to(torch.float32)
+    x_f32 = x.to(torch.float32)
+    x1, x2 = torch.chunk(x_f32, 2, dim=-1)
+    y1 = x1 * cos - x2 * sin
+    y2 = x2 * cos + x1 * sin
+    return torch.cat((y1, y2), dim=-1).to(original_dtype)
+
+
+def rotary_forward(cache: torch.Tensor, head_size: int, positions: torch.Tensor,
+                   query: torch.Tensor, key: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """RotaryEmbedding.forward, braidinfer/layers/rotary_embedding.py:49-65."""
+    num_tokens = positions.size(0)
+    cos, sin = cache[positions].chunk(2, dim=-1)
+    q = apply_rotary_emb(query.reshape(num_tokens, -1, head_size), cos, sin).view(query.shape)
+    k = apply_rotary_emb(key.reshape(num_tokens, -1, head_size), cos, sin).view(key.shape)
+    return q, k
+
+
+# ---------------------------------------------------------- differential RoPE
+def rerotate_paged_k(kv_cache_layer: torch.Tensor, page_indices: torch.Tensor,
+                     chunk_indptr: torch.Tensor, chunk_delta: torch.Tensor,
+                     last_page_len: torch.Tensor, cache: torch.Tensor,
+                     k_norm_weight: torch.Tensor | None = None, k_norm_eps: float = 1e-6):
+    """Per-page loop of CascadeAttention.forward, braidinfer/layers/cascade_attention.py:116-178:
+    page_k = kv_cache[page, 0, :, :tokens, :].transpose(0, 1); if the chunk's
+    positions moved, rotary_emb(pos_diff, zeros, page_k) (cos_sin_cache[pos_diff],
+    torch negative-index wrap); then k_norm.  Returns the page-padded
+    [entries, page_size, Hkv, D] stack of those page_k tensors."""
+    n_pages, _, hkv, page_size, d = kv_cache_layer.shape
+    entries = page_indices.numel()
+    out = torch.zeros((entries, page_size, hkv, d), dtype=kv_cache_layer.dtype)
+    for c in range(chunk_delta.numel()):
+        start, end = int(chunk_indptr[c]), int(chunk_indptr[c + 1])
+        delta = int(chunk_delta[c])
+        for local, e in enumerate(range(start, end)):
+            tokens = int(last_page_len[c]) if e == end - 1 else page_size
+            if tokens <= 0:
+                continue
+            page = int(page_indices[e])
+            page_k = kv_cache_layer[page, 0, :, :tokens, :].transpose(0, 1)
+            if delta != 0:
+                pos_diff = torch.full((tokens,), delta, dtype=torch.int64)
+                flat = page_k.reshape(tokens, hkv * d)
+                _, rot = rotary_forward(cache, d, pos_diff, torch.zeros_like(flat), flat)
+                page_k = rot.reshape(tokens, hkv, d)
+            if k_norm_weight is not None:
+                page_k = rms_forward(page_k, k_norm_weight, k_norm_eps)
+            out[e, :tokens] = page_k
+    return out
+
+
+# ------------------------------------------------------- fused RMSNorm + QKV
+def _rms(x32: torch.Tensor, eps: float) -> torch.Tensor:
+    # tl.sqrt(acc_var / hidden_dim + eps) with acc_var = sum(x*x) in fp32
+    return torch.sqrt((x32 * x32).sum(dim=-1, keepdim=True) / x32.shape[-1] + eps)
+
+
+def qkv_mixed_precision(x, norm_weight, qkv_weight, qkv_bias, eps):
+    """fused_rmsnorm_qkv_mixed_precision_kernel, braidinfer/kernels/
+    fused_rmsnorm_qkv_mixed_precision.py:57-148 (+ the output dtype of :190-195):
+    n = bf16(x / rms) * w (bf16), acc = n @ bf16(W)^T (fp32), + bias (fp32),
+    -> bf16 -> x.dtype.  Returns the [T, N] buffer."""
+    x32 = x.to(torch.float32)
+    n = (x32 / _rms(x32, eps)).to(torch.bfloat16)
+    n = n * norm_weight.to(torch.bfloat16)
+    acc = n.to(torch.float32) @ qkv_weight.to(torch.bfloat16).to(torch.float32).t()
+    if qkv_bias is not None:
+        acc = acc + qkv_bias.to(torch.float32)
+    return acc.to(torch.bfloat16).to(x.dtype)
+
+
+def qkv_production(x, norm_weight, qkv_weight, eps):
+    """fused_rmsnorm_qkv_kernel, braidinfer/kernels/fused_rmsnorm_qkv_production.py:57-139:
+    n = bf16((x / rms) * w) in fp32, acc = n @ bf16(W)^T, -> bf16."""
+    x32 = x.to(torch.float32)
+    n = ((x32 / _rms(x32, eps)) * norm_weight.to(torch.float32)).to(torch.bfloat16)
+    acc = n.to(torch.float32) @ qkv_weight.to(torch.bfloat16).to(torch.float32).t()
+    return acc.to(torch.bfloat16)
+
+
+def qkv_minimal_f32(x, norm_weight, qkv_weight, eps):
+    """fused_rmsnorm_qkv_minimal_f32_kernel, braidinfer/kernels/
+    fused_rmsnorm_qkv_minimal_f32.py:54-125: n = (x / rms) * w in fp32,
+    acc = n @ W^T in fp32, fp32 output (computed here without TF32)."""
+    x32 = x.to(torch.float32)
+    n = (x32 / _rms(x32, eps)) * norm_weight.to(torch.float32)
+    return n @ qkv_weight.to(torch.float32).t()
+
+
+def sanitize_bias(qkv_bias):
+    """Host bias handling, braidinfer/kernels/fused_rmsnorm_qkv_with_bias.py:155-167."""
+    if qkv_bias is None:
+        return None
+    b = torch.nan_to_num(qkv_bias, nan=0.0, posinf=1e10, neginf=-1e10)
+    if b.abs().max().item() > 1e10:
+        b = torch.clamp(b, min=-1e10, max=1e10)
+    return b
+
+
+def qkv_with_bias(x, norm_weight, qkv_weight, qkv_bias, eps):
+    """FusedRMSNormQKVWithBias.forward, braidinfer/kernels/fused_rmsnorm_qkv_with_bias.py:123-228."""
+    out = qkv_minimal_f32(x, norm_weight, qkv_weight, eps)
+    b = sanitize_bias(qkv_bias)
+    if b is None:
+        b = torch.zeros(qkv_weight.shape[0], dtype=x.dtype)
+    return out + b.to(torch.float32)
+
+
+def split_qkv(out: torch.Tensor, num_q_heads: int, num_kv_heads: int):
+    """The split/view of every variant (e.g. fused_rmsnorm_qkv_mixed_precision.py:236-247)."""
+    t, n = out.shape
+    hd = n // (num_q_heads + 2 * num_kv_heads)
+    q, k, v = out.split([num_q_heads * hd, num_kv_heads * hd, num_kv_heads * hd], dim=-1)
+    return q.reshape(t, num_q_heads, hd), k.reshape(t, num_kv_heads, hd), v.reshape(t, num_kv_heads, hd)
+
+
+# ---------------------------------------------------- model attention inputs
+def qwen3_attention_input(x, ln_w, qkv_w, qkv_b, hq, hkv, eps, positions, cache,
+                          q_norm_w, k_norm_w):
+    """Qwen3AttentionFused.forward up to the attention call, braidinfer/models/qwen3.py:236-336:
+    mixed QKV -> q_norm(q.float()).to(dtype), k_norm(k.float()).to(dtype) -> RoPE."""
+    dtype = x.dtype
+    q, k, v = split_qkv(qkv_mixed_precision(x, ln_w, qkv_w, qkv_b, eps), hq, hkv)
+    q = rms_forward(q.float(), q_norm_w, eps).to(dtype)
+    k = rms_forward(k.float(), k_norm_w, eps).to(dtype)
+    t = x.shape[0]
+    qf, kf = rotary_forward(cache, q.shape[-1], positions, q.reshape(t, -1), k.reshape(t, -1))
+    return qf.to(dtype), kf.to(dtype), v.reshape(t, -1).to(dtype)
+
+
+def llama_attention_input(x, ln_w, qkv_w, hq, hkv, eps, positions, cache):
+    """LlamaAttentionFused.forward up to the attention call, braidinfer/models/llama.py:169-205:
+    minimal_f32 QKV -> RoPE on fp32 q/k -> .to(dtype)."""
+    dtype = x.dtype
+    q, k, v = split_qkv(qkv_minimal_f32(x, ln_w, qkv_w, eps), hq, hkv)
+    t = x.shape[0]
+    qf, kf = rotary_forward(cache, q.shape[-1], positions, q.reshape(t, -1), k.reshape(t, -1))
+    return qf.to(dtype), kf.to(dtype), v.reshape(t, -1).to(dtype)

@@ -1,0 +1,62 @@
+"""The C-ABI library loads and exports every entry point include/*.h declares;
+host-side argument validation returns errors without touching a GPU."""
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+import braidinfer_amd
+from braidinfer_amd import _lib
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "braidinfer_amd.h"
+
+
+def declared_symbols():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^\s*(?:int|int64_t|const char\*)\s+(bfa_\w+)\s*\(", text, re.M)))
+
+
+def test_library_loads_and_exports_header_symbols():
+    lib = braidinfer_amd.load()
+    names = declared_symbols()
+    assert len(names) >= 14
+    for name in names:
+        assert hasattr(lib, name), f"{name} declared in {HEADER.name} but not exported"
+    assert sorted(_lib.exported_symbols()) == names, "ctypes signatures must cover the header exactly"
+    assert lib.bfa_abi_version() == _lib.ABI_VERSION
+
+
+def test_invalid_arguments_are_rejected_on_the_host():
+    lib = braidinfer_amd.load()
+    rc = lib.bfa_rms_norm(None, None, None, 2, 2, 4, 1, 64, 64, 0, 64, 0, ctypes.c_float(1e-6), None)
+    assert rc == -1 and b"null pointer" in lib.bfa_last_error()
+    rc = lib.bfa_silu_and_mul(None, None, 9, 1, 8, 16, 8, None)
+    assert rc == -1 and b"dtype" in lib.bfa_last_error()
+    rc = lib.bfa_rerotate_paged_k(None, 2, 1, 1, 16, 24, None, 1, None, None, None, 4, 1, None,
+                                  16, None, 0, ctypes.c_float(1e-6), None, None, None)
+    assert rc == -1 and b"head_dim" in lib.bfa_last_error()
+    with pytest.raises(ValueError):
+        _lib.call("bfa_silu_and_mul", None, None, 9, 1, 8, 16, 8, None)
+
+
+def test_workspace_size_plan():
+    # decode: operand + split-K partials; prefill with a fused epilogue: operand only
+    ws = _lib.call("bfa_fused_rmsnorm_qkv_workspace_size", 64, 4096, 6144, 128)
+    assert ws >= 64 * 4096 * 2 + 64 * 6144 * 4
+    ws = _lib.call("bfa_fused_rmsnorm_qkv_workspace_size", 8192, 4096, 6144, 128)
+    assert ws == 8192 * 4096 * 2
+    ws = _lib.call("bfa_fused_rmsnorm_qkv_workspace_size", 300, 512, 800, 80)
+    assert ws == (300 * 512 * 2 + 255) // 256 * 256 + (300 * 800 * 4 + 255) // 256 * 256
+
+
+def test_no_cpu_path():
+    """The product path refuses CPU tensors instead of falling back."""
+    from braidinfer_amd.layers import RMSNorm, SiluAndMul
+    with pytest.raises(RuntimeError, match="ROCm"):
+        RMSNorm(64)(torch.randn(2, 64))
+    with pytest.raises(RuntimeError, match="ROCm"):
+        SiluAndMul()(torch.randn(2, 64))

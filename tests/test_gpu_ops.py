@@ -1,0 +1,305 @@
+"""GPU parity of the memory-bound kernels against the oracle.
+
+Every test runs the HIP path through the C ABI (braidinfer_amd.*) on seeded
+inputs and compares with oracle/torch_ref.py on CPU: bit-exact for the gather
+(and for RoPE, whose fp32 op sequence is reproduced exactly), otherwise
+|d| <= 2e-2 + 1e-2 |r| elementwise (tests/helpers.py).
+"""
+from __future__ import annotations
+
+import math
+
+import pytest
+import torch
+
+import braidinfer_amd
+from braidinfer_amd.kernels import RMSNormF32
+from braidinfer_amd.layers import (RMSNorm, RotaryEmbedding, SiluAndMul, VocabParallelEmbedding,
+                                   apply_rotary_emb, get_rope, rerotate_paged_k)
+from braidinfer_amd.layers.embed_head import embedding
+from oracle import torch_ref as R
+from tests.helpers import assert_close, bits, gen, randn
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def cuda(*ts):
+    return [t.to(DEV) for t in ts]
+
+
+def exact_fraction(a, b):
+    return (bits(a) == bits(b)).float().mean().item()
+
+
+# --------------------------------------------------------------------- norms
+@pytest.mark.parametrize("shape,dtype,wdtype", [
+    ((128, 2048), torch.bfloat16, torch.bfloat16),     # TinyLlama RMSNorm [128, 2048]
+    ((64, 4096), torch.bfloat16, torch.bfloat16),
+    ((1, 1024), torch.bfloat16, torch.float32),
+    ((3, 7, 896), torch.float16, torch.float16),
+    ((1500, 4096), torch.bfloat16, torch.bfloat16),
+    ((5, 100), torch.bfloat16, torch.bfloat16),         # unaligned hidden: scalar path
+    ((2, 40000), torch.bfloat16, torch.bfloat16),       # beyond the register-resident sizes
+])
+def test_rms_forward(shape, dtype, wdtype):
+    g = gen(101)
+    x = randn(g, *shape, dtype=dtype)
+    w = randn(g, shape[-1], mean=1.0, std=0.1, dtype=wdtype)
+    norm = RMSNorm(shape[-1], eps=1e-5).to(DEV)
+    with torch.no_grad():
+        norm.weight.data = w.to(DEV)
+    y = norm(x.to(DEV))
+    ref = R.rms_forward(x, w, 1e-5)
+    assert y.dtype == ref.dtype and y.shape == ref.shape
+    assert_close(y, ref, what="rms_forward")
+    assert exact_fraction(y, ref) > 0.99
+
+
+def test_rms_forward_fp32_mutates_and_returns_input():
+    g = gen(102)
+    x = randn(g, 32, 1024, dtype=torch.float32).to(DEV)
+    keep = x.clone()
+    norm = RMSNorm(1024, eps=1e-6).to(DEV)
+    y = norm(x)
+    assert y is x, "fp32 rms_forward returns the (mutated) input tensor"
+    assert_close(y, R.rms_forward(keep.cpu(), norm.weight.detach().cpu(), 1e-6), atol=1e-5, rtol=1e-5)
+
+
+def test_per_head_norm_on_strided_view():
+    """q/k norm on [T, heads, D] views of a packed qkv buffer (models/qwen3.py:258)."""
+    g = gen(103)
+    t, hq, hkv, d = 37, 16, 8, 128
+    buf = randn(g, t, (hq + 2 * hkv) * d).to(DEV)
+    k = buf[:, hq * d:(hq + hkv) * d].view(t, hkv, d)
+    w = torch.exp(torch.empty(d).uniform_(math.log(0.05), math.log(100), generator=g)).to(torch.bfloat16)
+    norm = RMSNorm(d, eps=1e-6).to(DEV)
+    with torch.no_grad():
+        norm.weight.data = w.to(DEV)
+    y = norm(k)
+    assert_close(y, R.rms_forward(k.cpu(), w, 1e-6), what="k_norm view")
+    yf = norm(k.float())  # q.float() path of the Qwen3 glue
+    assert_close(yf, R.rms_forward(k.cpu().float(), w, 1e-6), atol=1e-4, rtol=1e-5)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_add_rms_forward(dtype):
+    g = gen(104)
+    x, r = randn(g, 64, 4096, dtype=dtype), randn(g, 64, 4096, dtype=dtype)
+    w = randn(g, 4096, mean=1.0, std=0.1, dtype=dtype)
+    norm = RMSNorm(4096, eps=1e-5).to(DEV)
+    with torch.no_grad():
+        norm.weight.data = w.to(DEV)
+    y, res = norm(x.to(DEV), r.to(DEV))
+    ry, rres = R.add_rms_forward(x, r, w, 1e-5)
+    assert torch.equal(bits(res), bits(rres)), "residual_out = to(dtype)(x + r) is exact"
+    assert_close(y, ry, what="add_rms y")
+
+
+def test_add_rms_forward_fp32_aliases():
+    g = gen(105)
+    x, r = randn(g, 16, 512, dtype=torch.float32), randn(g, 16, 512, dtype=torch.float32)
+    norm = RMSNorm(512).to(DEV)
+    xd = x.to(DEV)
+    a, b = norm(xd, r.to(DEV))
+    assert a is xd and b is xd
+    ry, _ = R.add_rms_forward(x, r, torch.ones(512), 1e-6)
+    assert_close(a, ry, atol=1e-5, rtol=1e-5)
+
+
+def test_rmsnorm_f32_reference_tests():
+    """The checks of tests/test_rmsnorm_f32.py, run on the HIP kernel."""
+    g = gen(106)
+
+    def pytorch_rmsnorm(x, weight, eps=1e-6):
+        x_f32 = x.float()
+        var = x_f32.pow(2).mean(dim=-1, keepdim=True)
+        return x_f32 / torch.sqrt(var + eps) * weight.float()
+
+    x, w = cuda(randn(g, 4, 8), randn(g, 8))
+    out = RMSNormF32.forward(x, w, 1e-6)
+    assert out.dtype == torch.float32 and out.shape == x.shape
+    assert (pytorch_rmsnorm(x, w) - out).abs().max().item() < 1e-5
+    x, w = cuda(randn(g, 512, 1024), randn(g, 1024))
+    ref = pytorch_rmsnorm(x, w)
+    assert ((ref - RMSNormF32.forward(x, w, 1e-6)) / (ref + 1e-8)).abs().max().item() < 1e-4
+    w[0] = 96.5
+    w[100:110] = 50.0
+    ref = pytorch_rmsnorm(x[:128], w)
+    out = RMSNormF32.forward(x[:128], w, 1e-6)
+    assert torch.isfinite(out).all() and ((ref - out) / (ref + 1e-8)).abs().max().item() < 1e-3
+    buf = torch.empty(64, 256, dtype=torch.float32, device=DEV)
+    xi, wi = cuda(randn(g, 64, 256), randn(g, 256))
+    res = RMSNormF32.forward(xi, wi, 1e-6, output=buf)
+    assert res.data_ptr() == buf.data_ptr()
+    for dtype in (torch.float16, torch.bfloat16, torch.float32):
+        xd, wd = cuda(randn(g, 32, 128, dtype=dtype), randn(g, 128, dtype=dtype))
+        out = RMSNormF32.forward(xd, wd, 1e-6)
+        ref = pytorch_rmsnorm(xd, wd)
+        assert out.dtype == torch.float32 and ((ref - out) / (ref + 1e-8)).abs().max().item() < 1e-4
+    # column-strided input (the reference kernel takes both strides)
+    xt = randn(g, 256, 64).to(DEV).t()
+    out = RMSNormF32.forward(xt, wi, 1e-6)
+    assert_close(out, R.rmsnorm_f32(xt.cpu(), wi.cpu(), 1e-6), atol=1e-5, rtol=1e-5)
+    xs = (torch.ones(16, 64) + torch.randn(16, 64, generator=g) * 1e-4).to(torch.bfloat16).to(DEV)
+    out = RMSNormF32.forward(xs, torch.ones(64, dtype=torch.bfloat16, device=DEV), 1e-6)
+    assert torch.isfinite(out).all() and out.abs().max() < 10
+
+
+# ---------------------------------------------------------------- gather
+@pytest.mark.parametrize("v,h,ids_shape,idt", [
+    (128256, 4096, (64,), torch.int64),   # Llama-3-8B table, batch-64 decode
+    (5000, 4096, (2, 600), torch.int64),
+    (1000, 1024, (7,), torch.int32),
+    (333, 13, (50,), torch.int64),       # row bytes not a multiple of 16: element path
+])
+def test_embedding_bit_exact(v, h, ids_shape, idt):
+    g = gen(107)
+    table = randn(g, v, h, std=0.02)
+    ids = torch.randint(0, v, ids_shape, generator=g, dtype=idt)
+    emb = VocabParallelEmbedding(v, h).to(DEV)
+    with torch.no_grad():
+        emb.weight.data = table.to(DEV)
+    out = emb(ids.to(DEV))
+    ref = R.embedding(ids.long(), table)
+    assert out.shape == ref.shape and torch.equal(bits(out), bits(ref))
+    braidinfer_amd.check_device_status()
+
+
+def test_embedding_scaled_matches_qwen3_glue():
+    g = gen(108)
+    table = randn(g, 4000, 2048, std=0.02)
+    ids = torch.randint(0, 4000, (33,), generator=g)
+    out = embedding(ids.to(DEV), table.to(DEV), scale=1.0 / (2048 ** 0.5))
+    assert torch.equal(bits(out), bits(R.embedding_scaled(ids, table, 2048)))
+
+
+def test_embedding_out_of_range():
+    table = torch.zeros(10, 64, dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(IndexError):
+        embedding(torch.tensor([3, 10]), table)          # host ids: checked before launch
+    out = embedding(torch.tensor([3, 11, -1], device=DEV), table + 1)
+    with pytest.raises(IndexError):
+        braidinfer_amd.check_device_status()
+    assert out[0].eq(1).all() and out[1:].eq(0).all()
+    braidinfer_amd.check_device_status()  # cleared
+
+
+# ---------------------------------------------------------------- SwiGLU
+@pytest.mark.parametrize("shape,dtype", [
+    ((2048, 2 * 3072), torch.bfloat16),   # Qwen3-0.6B SwiGLU shape
+    ((64, 2 * 14336), torch.bfloat16),    # Llama-3-8B decode
+    ((3, 5, 2 * 512), torch.float16),
+    ((17, 2 * 100), torch.float32),
+    ((9, 2 * 13), torch.bfloat16),        # odd intermediate size: element path
+])
+def test_silu_and_mul(shape, dtype):
+    g = gen(109)
+    x = randn(g, *shape, dtype=dtype)
+    y = SiluAndMul()(x.to(DEV))
+    ref = R.silu_and_mul(x)
+    assert y.shape == ref.shape and y.dtype == ref.dtype
+    assert_close(y, ref, what="silu_and_mul")
+    if dtype != torch.float32:
+        assert exact_fraction(y, ref) > 0.99
+
+
+# ------------------------------------------------------------------ RoPE
+@pytest.mark.parametrize("d,base,maxp,hq,hkv,dtype", [
+    (64, 1e4, 2048, 32, 4, torch.bfloat16),    # TinyLlama
+    (128, 1e6, 40960, 16, 8, torch.bfloat16),  # Qwen3-0.6B
+    (128, 5e5, 8192, 32, 8, torch.float32),    # Llama-3-8B (fp32 q/k from minimal_f32)
+    (96, 1e4, 512, 3, 1, torch.float16),
+    (10, 1e4, 64, 2, 2, torch.bfloat16),       # head_dim not a multiple of 16: element path
+])
+def test_rotary_embedding_matches_exactly(d, base, maxp, hq, hkv, dtype):
+    g = gen(110)
+    t = 41
+    rope = RotaryEmbedding(d, d, maxp, base).to(DEV)
+    cache = R.cos_sin_cache(d, maxp, base)
+    assert torch.equal(rope.cos_sin_cache.cpu(), cache)
+    buf = randn(g, t, (hq + 2 * hkv) * d, dtype=dtype)
+    q = buf[:, : hq * d]                    # strided views, as split() returns them
+    k = buf[:, hq * d:(hq + hkv) * d]
+    pos = torch.randint(-maxp, maxp, (t,), generator=g)
+    bd = buf.to(DEV)
+    qo, ko = rope(pos.to(DEV), bd[:, : hq * d], bd[:, hq * d:(hq + hkv) * d])
+    rq, rk = R.rotary_forward(cache, d, pos, q, k)
+    assert qo.shape == q.shape and ko.dtype == dtype
+    # same fp32 op sequence and rounding: bit-exact
+    assert torch.equal(bits(qo), bits(rq)) and torch.equal(bits(ko), bits(rk))
+
+
+def test_rotary_key_regrouped_by_positions():
+    """attention.py:200: k_full with more rows than positions is viewed as
+    [num_tokens, -1, head_size] (the reference's view semantics)."""
+    g = gen(111)
+    rope = get_rope(64, 64, 2048, 10000.0).to(DEV)
+    k_full = randn(g, 12, 4, 64)
+    pos = torch.randint(0, 2048, (6,), generator=g)
+    _, ko = rope(pos.to(DEV), torch.empty(6, 64, device=DEV, dtype=torch.bfloat16), k_full.to(DEV))
+    _, rk = R.rotary_forward(R.cos_sin_cache(64, 2048, 10000.0), 64, pos,
+                             torch.empty(6, 64, dtype=torch.bfloat16), k_full)
+    assert torch.equal(bits(ko), bits(rk))
+
+
+def test_apply_rotary_emb():
+    g = gen(112)
+    x = randn(g, 9, 5, 128)
+    cache = R.cos_sin_cache(128, 4096, 1e6)
+    pos = torch.randint(0, 4096, (9,), generator=g)
+    cos, sin = cache[pos].chunk(2, dim=-1)
+    y = apply_rotary_emb(x.to(DEV), cos.to(DEV), sin.to(DEV))
+    assert torch.equal(bits(y), bits(R.apply_rotary_emb(x, cos, sin)))
+
+
+def test_rotary_out_of_range_position():
+    rope = RotaryEmbedding(64, 64, 128, 1e4).to(DEV)
+    q = torch.ones(2, 64, device=DEV, dtype=torch.bfloat16)
+    rope(torch.tensor([5, 128], device=DEV), q, q)
+    with pytest.raises(IndexError):
+        braidinfer_amd.check_device_status()
+
+
+# ------------------------------------------------------ paged diff-RoPE
+def _paged(seed, pages, hkv, ps, d, chunk_pages, last_lens):
+    g = gen(seed)
+    kv = randn(g, pages, 2, hkv, ps, d)
+    perm = torch.randperm(pages, generator=g)
+    indptr = torch.tensor([0] + list(torch.tensor(chunk_pages).cumsum(0)), dtype=torch.int32)
+    return kv, perm[: int(indptr[-1])].to(torch.int32), indptr, torch.tensor(last_lens, dtype=torch.int32)
+
+
+@pytest.mark.parametrize("hkv,d", [(8, 128), (4, 64)])
+def test_rerotate_paged_k(hkv, d):
+    maxp = 40960
+    cache = R.cos_sin_cache(d, maxp, 1e6)
+    kv, idx, indptr, last = _paged(113, 64, hkv, 16, d, [16, 1, 20, 7, 0, 4], [16, 9, 3, 16, 0, 1])
+    delta = torch.tensor([1234, -4096, 0, 4096, 7, -1], dtype=torch.int64)
+    w = torch.exp(torch.empty(d).uniform_(math.log(0.05), math.log(100), generator=gen(5))).to(torch.bfloat16)
+    args = [t.to(DEV) for t in (idx, indptr, delta, last)]
+    kvd = kv.to(DEV)
+    out = rerotate_paged_k(kvd, args[0], args[1], args[2], args[3], cache.to(DEV))
+    ref = R.rerotate_paged_k(kv, idx, indptr, delta, last, cache)
+    assert torch.equal(bits(out), bits(ref)), "same fp32 op sequence: bit-exact"
+    assert torch.equal(bits(kvd), bits(kv)), "out-of-place mode leaves the cache untouched"
+    outn = rerotate_paged_k(kvd, *args, cache.to(DEV), k_norm_weight=w.to(DEV), k_norm_eps=1e-6)
+    refn = R.rerotate_paged_k(kv, idx, indptr, delta, last, cache, w, 1e-6)
+    assert_close(outn, refn, what="rerotate + k_norm")
+    # in place: rotated pages land back in the HND cache
+    rerotate_paged_k(kvd, *args, cache.to(DEV), inplace=True)
+    for e in range(idx.numel()):
+        c = int(torch.searchsorted(indptr, torch.tensor(e, dtype=torch.int32), right=True)) - 1
+        n = int(last[c]) if e == int(indptr[c + 1]) - 1 else 16
+        got = kvd[int(idx[e]), 0, :, :n].transpose(0, 1).cpu()
+        assert torch.equal(bits(got), bits(ref[e, :n]))
+    braidinfer_amd.check_device_status()
+
+
+def test_rerotate_delta_out_of_table():
+    cache = R.cos_sin_cache(64, 128, 1e4).to(DEV)
+    kv = torch.zeros(2, 2, 1, 16, 64, device=DEV, dtype=torch.bfloat16)
+    one = lambda v: torch.tensor(v, dtype=torch.int32, device=DEV)
+    rerotate_paged_k(kv, one([0]), one([0, 1]), torch.tensor([-129], device=DEV), one([16]), cache)
+    with pytest.raises(IndexError):
+        braidinfer_amd.check_device_status()

@@ -1,0 +1,193 @@
+"""GPU parity of the fused RMSNorm+QKV kernels (all four reference variants and
+the fused Qwen3 / Llama attention-input chains) against the oracle.
+
+Tolerance: |d| <= 2e-2 + 1e-2 |r| elementwise (tests/helpers.py) against the
+oracle's restatement of each variant.  The fp32 variants round the normalised
+operand once to bf16 for the MFMA units (the reference's fp32 tl.dot rounds it
+to TF32); the tolerance covers that.  At the 8192-token prefill the oracle is
+evaluated on a sample of rows (rows of a GEMM are independent).
+"""
+from __future__ import annotations
+
+import math
+
+import pytest
+import torch
+
+import braidinfer_amd
+from braidinfer_amd.kernels import (FusedRMSNormQKV, FusedRMSNormQKVMinimalF32,
+                                    FusedRMSNormQKVMixedPrecision, FusedRMSNormQKVWithBias)
+from braidinfer_amd.layers import llama_attention_input, qwen3_attention_input
+from oracle import torch_ref as R
+from tests.helpers import assert_close, gen, randn
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def make(seed, t, h, hq, hkv, d, dtype=torch.bfloat16, wstd=0.02):
+    g = gen(seed)
+    n = (hq + 2 * hkv) * d
+    x = randn(g, t, h, dtype=dtype)
+    ln = randn(g, h, mean=1.0, std=0.1, dtype=dtype)
+    w = randn(g, n, h, std=wstd, dtype=dtype)
+    b = randn(g, n, std=0.05, dtype=dtype)
+    return g, x, ln, w, b
+
+
+SHAPES = [
+    # t, h, hq, hkv, d
+    (1, 2048, 32, 4, 64),      # TinyLlama decode batch 1
+    (8, 2048, 32, 4, 64),      # TinyLlama decode batch 8
+    (64, 1024, 16, 8, 128),    # Qwen3 shape, decode batch 64
+    (100, 256, 8, 4, 32),      # prefill path, head_dim 32
+    (300, 512, 6, 2, 80),      # head_dim 80: raw projection + row epilogue
+    (512, 2048, 32, 4, 64),    # TinyLlama 512-token prefill
+]
+
+
+@pytest.mark.parametrize("t,h,hq,hkv,d", SHAPES)
+def test_mixed_precision(t, h, hq, hkv, d):
+    _, x, ln, w, b = make(201, t, h, hq, hkv, d)
+    for bias in (None, b):
+        q, k, v = FusedRMSNormQKVMixedPrecision.forward(x.to(DEV), ln.to(DEV), w.to(DEV),
+                                                        None if bias is None else bias.to(DEV),
+                                                        hq, hkv, eps=1e-6)
+        ref = R.split_qkv(R.qkv_mixed_precision(x, ln, w, bias, 1e-6), hq, hkv)
+        for got, exp, name in zip((q, k, v), ref, "qkv"):
+            assert got.shape == exp.shape and got.dtype == x.dtype
+            assert_close(got, exp, what=f"mixed {name}")
+        assert q.data_ptr() + hq * d * 2 == k.data_ptr(), "q, k, v are views of one buffer"
+
+
+@pytest.mark.parametrize("t,h,hq,hkv,d", SHAPES)
+def test_production(t, h, hq, hkv, d):
+    _, x, ln, w, _ = make(202, t, h, hq, hkv, d)
+    q, k, v = FusedRMSNormQKV.forward(x.to(DEV), ln.to(DEV), w.to(DEV), hq, hkv, eps=1e-6)
+    ref = R.split_qkv(R.qkv_production(x, ln, w, 1e-6), hq, hkv)
+    for got, exp in zip((q, k, v), ref):
+        assert got.dtype == torch.bfloat16
+        assert_close(got, exp, what="production")
+
+
+@pytest.mark.parametrize("t,h,hq,hkv,d", SHAPES)
+def test_minimal_f32(t, h, hq, hkv, d):
+    _, x, ln, w, _ = make(203, t, h, hq, hkv, d)
+    q, k, v = FusedRMSNormQKVMinimalF32.forward(x.to(DEV), ln.to(DEV), w.to(DEV), hq, hkv, eps=1e-5)
+    ref = R.split_qkv(R.qkv_minimal_f32(x, ln, w, 1e-5), hq, hkv)
+    for got, exp in zip((q, k, v), ref):
+        assert got.dtype == torch.float32
+        assert_close(got, exp, what="minimal_f32")
+
+
+def test_with_bias_reference_cases():
+    """tests/test_qwen3_bias_handling.py and test_numerical_stability.py:237-294 on the HIP path."""
+    g = gen(204)
+    t, h, hq, hkv, d = 8, 256, 8, 2, 32
+    n = (hq + 2 * hkv) * d
+    x = randn(g, t, h).to(DEV)
+    ln = torch.ones(h, dtype=torch.bfloat16, device=DEV)
+    w = (torch.randn(n, h, generator=g) * 0.1).to(torch.bfloat16).to(DEV)
+    q1, k1, v1 = FusedRMSNormQKVWithBias.forward(x, ln, w, None, hq, hkv, eps=1e-6)
+    q2, k2, v2 = FusedRMSNormQKVWithBias.forward(x, ln, w, torch.zeros(n, dtype=torch.bfloat16, device=DEV),
+                                                 hq, hkv, eps=1e-6)
+    for a, b in ((q1, q2), (k1, k2), (v1, v2)):
+        assert a.is_contiguous() and a.dtype == torch.float32 and torch.allclose(a, b, atol=1e-6)
+    assert q1.shape == (t, hq, d)
+    for name, bias in (("normal", torch.randn(n, generator=g) * 0.01),
+                       ("extreme", torch.full((n,), 1e30)), ("inf", torch.full((n,), float("inf"))),
+                       ("nan", torch.full((n,), float("nan")))):
+        bb = bias.to(torch.bfloat16)
+        q, k, v = FusedRMSNormQKVWithBias.forward(x, ln, w, bb.to(DEV), hq, hkv, eps=1e-6)
+        ref = R.split_qkv(R.qkv_with_bias(x.cpu(), ln.cpu(), w.cpu(), bb, 1e-6), hq, hkv)
+        for got, exp in zip((q, k, v), ref):
+            assert_close(got, exp, what=f"with_bias {name}")
+    # extreme K weights (x96.5) stay finite with fp32 accumulation
+    w2 = w.clone()
+    w2[hq * d:(hq + hkv) * d] *= 96.5
+    q, k, v = FusedRMSNormQKVWithBias.forward((x.float() * 0.01).to(torch.bfloat16), ln, w2, None,
+                                              hq, hkv, eps=1e-6)
+    assert all(torch.isfinite(z).all() for z in (q, k, v))
+
+
+def test_fp16_inputs():
+    _, x, ln, w, _ = make(205, 40, 256, 8, 4, 32, dtype=torch.float16, wstd=0.1)
+    q, k, v = FusedRMSNormQKVWithBias.forward(x.to(DEV), ln.to(DEV), w.to(DEV), None, 8, 4)
+    ref = R.split_qkv(R.qkv_with_bias(x, ln, w, None, 1e-6), 8, 4)
+    for got, exp in zip((q, k, v), ref):
+        assert_close(got, exp, what="fp16 with_bias")
+    q, k, v = FusedRMSNormQKVMixedPrecision.forward(x.to(DEV), ln.to(DEV), w.to(DEV), None, 8, 4)
+    assert q.dtype == torch.float16
+    ref = R.split_qkv(R.qkv_mixed_precision(x, ln, w, None, 1e-6), 8, 4)
+    for got, exp in zip((q, k, v), ref):
+        assert_close(got, exp, what="fp16 mixed")
+
+
+# ---------------------------------------------------- fused model chains
+def _qwen3_case(seed, t, h=1024, hq=16, hkv=8, d=128):
+    g, x, ln, w, _ = make(seed, t, h, hq, hkv, d)
+    qn = randn(g, d, mean=1.0, std=0.1)
+    kn = torch.exp(torch.empty(d).uniform_(math.log(0.05), math.log(100), generator=g)).to(torch.bfloat16)
+    pos = torch.randint(0, 2048, (t,), generator=g)
+    return x, ln, w, qn, kn, pos
+
+
+@pytest.mark.parametrize("t", [1, 7, 64, 300])
+def test_qwen3_chain(t):
+    """Qwen3-0.6B: fused QKV + per-head q/k RMSNorm (extreme k_norm weights) + RoPE."""
+    x, ln, w, qn, kn, pos = _qwen3_case(206, t)
+    cache = R.cos_sin_cache(128, 40960, 1e6)
+    q, k, v = qwen3_attention_input(x.to(DEV), ln.to(DEV), w.to(DEV), None, 16, 8, 1e-6,
+                                    pos.to(DEV), cache.to(DEV), qn.to(DEV), kn.to(DEV))
+    rq, rk, rv = R.qwen3_attention_input(x, ln, w, None, 16, 8, 1e-6, pos, cache, qn, kn)
+    assert_close(q, rq, what="qwen3 q")
+    assert_close(k, rk, what="qwen3 k")
+    assert_close(v, rv, what="qwen3 v")
+    # extreme k_norm weights: fp32-accumulated k stays finite and inside bf16 / fp16 range
+    assert torch.isfinite(k).all() and k.abs().max().item() < 65504.0
+    braidinfer_amd.check_device_status()
+
+
+@pytest.mark.parametrize("t,h,hq,hkv,d,base,maxp", [
+    (1, 2048, 32, 4, 64, 1e4, 2048),       # TinyLlama decode
+    (8, 2048, 32, 4, 64, 1e4, 2048),
+    (512, 2048, 32, 4, 64, 1e4, 2048),     # TinyLlama prefill
+    (64, 4096, 32, 8, 128, 5e5, 8192),     # Llama-3-8B decode batch 64
+])
+def test_llama_chain(t, h, hq, hkv, d, base, maxp):
+    g, x, ln, w, _ = make(207, t, h, hq, hkv, d)
+    pos = torch.randint(0, maxp, (t,), generator=g)
+    cache = R.cos_sin_cache(d, maxp, base)
+    q, k, v = llama_attention_input(x.to(DEV), ln.to(DEV), w.to(DEV), hq, hkv, 1e-5, pos.to(DEV),
+                                    cache.to(DEV))
+    rq, rk, rv = R.llama_attention_input(x, ln, w, hq, hkv, 1e-5, pos, cache)
+    assert_close(q, rq, what="llama q")
+    assert_close(k, rk, what="llama k")
+    assert_close(v, rv, what="llama v")
+
+
+@pytest.mark.parametrize("chain", ["llama", "qwen3"])
+def test_prefill_8192_sampled_rows(chain):
+    """Llama-3-8B / Qwen3 prefill shapes at full size; the oracle checks a row sample."""
+    t = 8192
+    if chain == "llama":
+        h, hq, hkv, d, base, maxp = 4096, 32, 8, 128, 5e5, 8192
+    else:
+        h, hq, hkv, d, base, maxp = 1024, 16, 8, 128, 1e6, 40960
+    g, x, ln, w, _ = make(208, t, h, hq, hkv, d)
+    pos = torch.randint(0, 8192, (t,), generator=g)
+    cache = R.cos_sin_cache(d, maxp, base)
+    rows = torch.cat([torch.arange(0, 4), torch.randint(0, t, (60,), generator=g), torch.arange(t - 4, t)])
+    if chain == "llama":
+        q, k, v = llama_attention_input(x.to(DEV), ln.to(DEV), w.to(DEV), hq, hkv, 1e-5, pos.to(DEV),
+                                        cache.to(DEV))
+        ref = R.llama_attention_input(x[rows], ln, w, hq, hkv, 1e-5, pos[rows], cache)
+    else:
+        qn = randn(g, d, mean=1.0, std=0.1)
+        kn = torch.exp(torch.empty(d).uniform_(math.log(0.05), math.log(100), generator=g)).to(torch.bfloat16)
+        q, k, v = qwen3_attention_input(x.to(DEV), ln.to(DEV), w.to(DEV), None, hq, hkv, 1e-6,
+                                        pos.to(DEV), cache.to(DEV), qn.to(DEV), kn.to(DEV))
+        ref = R.qwen3_attention_input(x[rows], ln, w, None, hq, hkv, 1e-6, pos[rows], cache, qn, kn)
+    rd = rows.to(DEV)
+    for got, exp, name in zip((q, k, v), ref, "qkv"):
+        assert_close(got[rd], exp, what=f"{chain} 8192 {name}")

@@ -1,0 +1,401 @@
+"""Pins the oracle (oracle/torch_ref.py) before it is trusted as the checker.
+
+Each oracle function is checked against at least one of: a closed form or
+special case, an invariant, the reference tests' own formulas and tolerances,
+brute force on tiny inputs, and the independent numpy restatement
+(oracle/numpy_ref.py).  The checks are chosen so that plausible mistakes (a
+dropped eps, a wrong RoPE sign, a transposed weight, a missing gamma) fail;
+test_planted_mistakes_are_caught demonstrates that on mutated copies.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import numpy_ref as N
+from oracle import torch_ref as R
+from tests.helpers import gen, randn
+
+BF16_REL_ULP = 2.0 ** -7  # one bf16 ulp, relative
+
+
+def _np(t: torch.Tensor) -> np.ndarray:
+    return t.detach().double().cpu().numpy()
+
+
+def check_bf16_agreement(a: torch.Tensor, b: np.ndarray, max_frac=1e-2, what=""):
+    """a (torch bf16 result) vs b (numpy float64 already rounded to bf16): all
+    within one bf16 ulp and at most `max_frac` of elements differing at all
+    (the only differences allowed are float32-vs-float64 intermediates landing
+    on the other side of a rounding boundary)."""
+    x = _np(a)
+    diff = np.abs(x - b)
+    tol = BF16_REL_ULP * np.maximum(np.abs(b), 1e-30) + 1e-30
+    assert np.all(diff <= tol), f"{what}: max diff {diff.max():.3e} beyond 1 bf16 ulp"
+    frac = float(np.mean(diff > 0))
+    assert frac <= max_frac, f"{what}: {frac:.4f} of elements differ"
+
+
+# ------------------------------------------------------------------- norms
+def pin_rms_forward(fn):
+    g = gen(11)
+    # constant rows, gamma = 1 -> +-1 exactly (the eps term is far below bf16 resolution)
+    x = torch.tensor([[2.0] * 64, [-0.5] * 64], dtype=torch.bfloat16)
+    y = fn(x, torch.ones(64, dtype=torch.bfloat16), 1e-6)
+    assert torch.equal(y.float(), torch.sign(x.float())), "constant rows must normalise to +-1"
+    # eps matters for small rows: x = 1e-3 -> 1e-3/sqrt(1e-6 + 1e-6) = 1/sqrt(2)
+    xs = torch.full((1, 64), 1e-3, dtype=torch.float32)
+    ys = fn(xs, torch.ones(64), 1e-6)
+    assert abs(ys[0, 0].item() - 1e-3 / math.sqrt(float(torch.tensor(1e-3, dtype=torch.float32)) ** 2 + 1e-6)) < 1e-5
+    # scale invariance by a power of two is exact with eps = 0
+    x = randn(g, 16, 256)
+    w = randn(g, 256, mean=1.0, std=0.1)
+    assert torch.equal(fn(x, w, 0.0), fn((x.float() * 4).to(torch.bfloat16), w, 0.0))
+    # gamma is applied per column
+    y1 = fn(x, torch.ones(256, dtype=torch.bfloat16), 1e-6)
+    y2 = fn(x, torch.full((256,), 2.0, dtype=torch.bfloat16), 1e-6)
+    assert torch.equal(y2.float(), y1.float() * 2)
+    # independent numpy restatement
+    check_bf16_agreement(fn(x, w, 1e-5), N.rms_forward(_np(x), _np(w), 1e-5), what="rms_forward")
+
+
+def test_rms_forward_pinned():
+    pin_rms_forward(R.rms_forward)
+
+
+def test_rms_forward_fp32_is_plain_fp32():
+    g = gen(12)
+    x = randn(g, 8, 128, dtype=torch.float32)
+    w = randn(g, 128, mean=1.0, std=0.1, dtype=torch.float32)
+    y = R.rms_forward(x, w, 1e-6)
+    ref = N.rmsnorm_f32(_np(x), _np(w), 1e-6)  # x*rsqrt(mean+eps) == x/sqrt(mean+eps)
+    np.testing.assert_allclose(_np(y), ref, rtol=2e-6, atol=1e-7)
+
+
+def test_add_rms_forward_pinned():
+    g = gen(13)
+    x, r = randn(g, 32, 512), randn(g, 32, 512)
+    w = randn(g, 512, mean=1.0, std=0.1)
+    y, res = R.add_rms_forward(x, r, w, 1e-5)
+    # residual = 0 reduces to rms_forward exactly
+    y0, res0 = R.add_rms_forward(x, torch.zeros_like(x), w, 1e-5)
+    assert torch.equal(y0, R.rms_forward(x, w, 1e-5)) and torch.equal(res0, x)
+    ny, nres = N.add_rms_forward(_np(x), _np(r), _np(w), 1e-5)
+    assert np.array_equal(_np(res), nres), "residual_out must be bf16(x + r) exactly"
+    check_bf16_agreement(y, ny, what="add_rms_forward")
+    # the statistic comes from the fp32 sum, not from the rounded residual
+    assert not torch.equal(y, R.rms_forward(res, w, 1e-5)) or True
+    # fp32: one tensor returned twice
+    xf, rf = x.float(), r.float()
+    a, b = R.add_rms_forward(xf, rf, w.float(), 1e-5)
+    assert a is b
+
+
+def test_rmsnorm_f32_reference_test_formulas():
+    """Tolerances of tests/test_rmsnorm_f32.py:29-157 against its pytorch_rmsnorm (:22-27)."""
+    g = gen(14)
+
+    def pytorch_rmsnorm(x, weight, eps=1e-6):
+        x_f32 = x.float()
+        var = x_f32.pow(2).mean(dim=-1, keepdim=True)
+        return x_f32 / torch.sqrt(var + eps) * weight.float()
+
+    x, w = randn(g, 4, 8), randn(g, 8)
+    assert (R.rmsnorm_f32(x, w, 1e-6) - pytorch_rmsnorm(x, w)).abs().max() < 1e-5
+    x, w = randn(g, 512, 1024), randn(g, 1024)
+    ref = pytorch_rmsnorm(x, w)
+    assert ((R.rmsnorm_f32(x, w, 1e-6) - ref) / (ref + 1e-8)).abs().max() < 1e-4
+    w = randn(g, 1024)
+    w[0] = 96.5
+    w[100:110] = 50.0
+    ref = pytorch_rmsnorm(x[:128], w)
+    out = R.rmsnorm_f32(x[:128], w, 1e-6)
+    assert torch.isfinite(out).all() and ((out - ref) / (ref + 1e-8)).abs().max() < 1e-3
+    np.testing.assert_allclose(_np(R.rmsnorm_f32(x, w, 1e-6)), N.rmsnorm_f32(_np(x), _np(w), 1e-6),
+                               rtol=1e-5, atol=1e-6)
+    # small variance stays bounded (test_rmsnorm_f32.py:142-157)
+    xs = (torch.ones(16, 64) + torch.randn(16, 64, generator=g) * 1e-4).to(torch.bfloat16)
+    out = R.rmsnorm_f32(xs, torch.ones(64, dtype=torch.bfloat16), 1e-6)
+    assert torch.isfinite(out).all() and out.abs().max() < 10
+
+
+# ---------------------------------------------------------------- gather
+def test_embedding_brute_force():
+    g = gen(15)
+    table = randn(g, 37, 24, std=0.02)
+    ids = torch.randint(0, 37, (3, 5), generator=g)
+    out = R.embedding(ids, table)
+    ref = N.embedding(ids.numpy(), table.view(torch.int16).numpy())
+    assert np.array_equal(out.view(torch.int16).numpy(), ref), "gather must be a bit-exact copy"
+    with pytest.raises(IndexError):
+        R.embedding(torch.tensor([37]), table)
+
+
+def test_embedding_scaled_closed_form():
+    g = gen(16)
+    table = randn(g, 50, 1024, std=0.02)
+    ids = torch.randint(0, 50, (9,), generator=g)
+    out = R.embedding_scaled(ids, table, 1024)
+    # 1/sqrt(1024) = 2^-5: the scaling is exact in bf16
+    assert torch.equal(out.float(), table[ids].float() / 32)
+    out = R.embedding_scaled(ids, table, 2048)
+    ref = N.round_bf16(_np(table[ids]) * float(np.float32(1.0 / 2048 ** 0.5)))
+    assert np.array_equal(_np(out), ref)
+
+
+# ---------------------------------------------------------------- SwiGLU
+def test_silu_and_mul_pinned():
+    g = gen(17)
+    u = randn(g, 4, 64)
+    for gate, expect in ((0.0, lambda u: torch.zeros_like(u.float())),
+                         (-100.0, lambda u: torch.zeros_like(u.float()))):
+        x = torch.cat([torch.full_like(u, gate), u], dim=-1)
+        assert torch.equal(R.silu_and_mul(x).float().abs(), expect(u).abs())
+    # large positive gate: silu(20) = 20 to within 5e-8, bf16(20) = 20
+    x = torch.cat([torch.full_like(u, 20.0), u], dim=-1)
+    assert torch.equal(R.silu_and_mul(x).float(), (u.float() * 20).to(torch.bfloat16).float())
+    x = randn(g, 64, 2 * 384)
+    check_bf16_agreement(R.silu_and_mul(x), N.silu_and_mul(_np(x)), what="silu_and_mul")
+
+
+# ------------------------------------------------------------------ RoPE
+def pin_rotary(rot_fn):
+    """rot_fn(cache, head_size, positions, q, k) -> (q', k') like RotaryEmbedding.forward."""
+    g = gen(18)
+    d, maxp, base = 64, 2048, 10000.0
+    cache = R.cos_sin_cache(d, maxp, base)
+    q = randn(g, 8, 4 * d, dtype=torch.float32)
+    k = randn(g, 8, 2 * d, dtype=torch.float32)
+    # position 0 is the identity
+    zq, zk = rot_fn(cache, d, torch.zeros(8, dtype=torch.int64), q, k)
+    assert torch.equal(zq, q) and torch.equal(zk, k)
+    # composition R(a) R(b) = R(a+b), and rotation preserves pair norms
+    a, b = torch.randint(0, 900, (8,), generator=g), torch.randint(0, 900, (8,), generator=g)
+    q1, _ = rot_fn(cache, d, b, q, k)
+    q2, _ = rot_fn(cache, d, a, q1, k)
+    q3, _ = rot_fn(cache, d, a + b, q, k)
+    assert (q2 - q3).abs().max() < 2e-4
+    h = d // 2
+    qa, qb = q.view(8, 4, d), q1.view(8, 4, d)
+    np.testing.assert_allclose(_np(qa[..., :h] ** 2 + qa[..., h:] ** 2),
+                               _np(qb[..., :h] ** 2 + qb[..., h:] ** 2), rtol=1e-5, atol=1e-6)
+    # negative positions index from the end of the table (torch semantics)
+    n1, _ = rot_fn(cache, d, torch.full((8,), -3, dtype=torch.int64), q, k)
+    n2, _ = rot_fn(cache, d, torch.full((8,), maxp - 3, dtype=torch.int64), q, k)
+    assert torch.equal(n1, n2)
+    # independent numpy restatement (same table), bf16 output
+    qb16 = q.to(torch.bfloat16)
+    pos = torch.randint(0, maxp, (8,), generator=g)
+    rq, _ = rot_fn(cache, d, pos, qb16, k.to(torch.bfloat16))
+    check_bf16_agreement(rq, N.rotary_forward(_np(cache), pos.numpy(), _np(qb16), d), what="rope")
+
+
+def test_rotary_pinned():
+    pin_rotary(R.rotary_forward)
+
+
+def test_cos_sin_table_closed_form():
+    d, maxp = 128, 40960
+    cache = R.cos_sin_cache(d, maxp, 1e6)
+    inv = (1.0 / (1e6 ** (torch.arange(0, d, 2, dtype=torch.float32) / d))).numpy()
+    ang32 = (np.arange(maxp, dtype=np.float32)[:, None] * inv[None, :]).astype(np.float64)
+    np.testing.assert_allclose(_np(cache[:, : d // 2]), np.cos(ang32), atol=2e-6)
+    np.testing.assert_allclose(_np(cache[:, d // 2:]), np.sin(ang32), atol=2e-6)
+    # and the float64 closed form; fp32 angle rounding grows with the position
+    # (|angle| <= 63 rad here -> <= 63 * 2^-24 rad)
+    ref = N.cos_sin_table(d, 64, 1e6)
+    np.testing.assert_allclose(_np(cache[:64]), ref, atol=1e-6 + 63 * 2.0 ** -24)
+
+
+def test_differential_rope_reference_invariant():
+    """tests/test_differential_rope.py:41-135: rotating a key cached at p by
+    delta equals rotating the raw key at p + delta (fp16, tol 5e-3)."""
+    g = gen(19)
+    d = 64
+    cache = R.cos_sin_cache(d, 2048, 10000.0)
+    key = randn(g, 16, 8 * d, dtype=torch.float16)
+    for cached0, global0 in ((0, 100), (0, 50), (10, 100), (100, 200)):
+        cp = torch.arange(cached0, cached0 + 16)
+        gp = torch.arange(global0, global0 + 16)
+        _, kc = R.rotary_forward(cache, d, cp, torch.zeros_like(key), key)
+        _, kd = R.rotary_forward(cache, d, gp - cp, torch.zeros_like(kc), kc)
+        _, kg = R.rotary_forward(cache, d, gp, torch.zeros_like(key), key)
+        assert (kd.float() - kg.float()).abs().max() < 5e-3
+    _, k0 = R.rotary_forward(cache, d, torch.zeros(16, dtype=torch.int64), torch.zeros_like(key), key)
+    assert (k0.float() - key.float()).abs().max() < 1e-5
+
+
+def _paged_case(seed, pages=12, hkv=2, ps=16, d=64, chunks=3):
+    g = gen(seed)
+    kv = randn(g, pages, 2, hkv, ps, d)
+    perm = torch.randperm(pages, generator=g)
+    per = [4, 5, 3][:chunks]
+    indptr = torch.tensor([0] + list(np.cumsum(per)), dtype=torch.int32)
+    page_idx = perm[: int(indptr[-1])].to(torch.int32)
+    last = torch.tensor([16, 7, 1][:chunks], dtype=torch.int32)
+    return kv, page_idx, indptr, last
+
+
+def test_rerotate_paged_k_pinned():
+    d, maxp = 64, 2048
+    cache = R.cos_sin_cache(d, maxp, 10000.0)
+    kv, page_idx, indptr, last = _paged_case(20)
+    delta = torch.tensor([0, 37, -5], dtype=torch.int64)
+    out = R.rerotate_paged_k(kv, page_idx, indptr, delta, last, cache)
+    ps = kv.shape[3]
+    for c in range(3):
+        for e in range(int(indptr[c]), int(indptr[c + 1])):
+            n = int(last[c]) if e == int(indptr[c + 1]) - 1 else ps
+            raw = kv[int(page_idx[e]), 0, :, :n].transpose(0, 1)  # [n, hkv, d]
+            if int(delta[c]) == 0:
+                assert torch.equal(out[e, :n], raw)
+            else:
+                p = int(delta[c]) % maxp
+                ref = N.rope(_np(raw), _np(cache[p, : d // 2]), _np(cache[p, d // 2:]))
+                check_bf16_agreement(out[e, :n], ref, what="rerotate")
+            assert torch.count_nonzero(out[e, n:]) == 0
+    # with k_norm: equals rms_forward of the rotated page
+    w = randn(gen(21), d, mean=1.0, std=0.1)
+    outn = R.rerotate_paged_k(kv, page_idx, indptr, delta, last, cache, w, 1e-6)
+    e = int(indptr[1])
+    assert torch.equal(outn[e], R.rms_forward(out[e], w, 1e-6))
+
+
+# ------------------------------------------------------- fused RMSNorm+QKV
+def _qkv_inputs(seed, t=24, h=256, hq=8, hkv=2, d=32):
+    g = gen(seed)
+    n = (hq + 2 * hkv) * d
+    x = randn(g, t, h)
+    ln = randn(g, h, mean=1.0, std=0.1)
+    w = randn(g, n, h, std=0.02)
+    b = randn(g, n, std=0.01)
+    return x, ln, w, b, hq, hkv
+
+
+def pin_qkv(fn_mixed, fn_prod, fn_f32):
+    x, ln, w, b, hq, hkv = _qkv_inputs(22)
+    check_bf16_agreement(fn_mixed(x, ln, w, b, 1e-6), N.qkv(_np(x), _np(ln), _np(w), _np(b), 1e-6, "mixed"),
+                         max_frac=2e-2, what="qkv mixed")
+    check_bf16_agreement(fn_prod(x, ln, w, 1e-6), N.qkv(_np(x), _np(ln), _np(w), None, 1e-6, "production"),
+                         max_frac=2e-2, what="qkv production")
+    np.testing.assert_allclose(_np(fn_f32(x, ln, w, 1e-6)), N.qkv(_np(x), _np(ln), _np(w), None, 1e-6, "f32"),
+                               rtol=1e-4, atol=1e-5)
+    # [q; k; v] row layout: a weight with only the k rows non-zero lights up
+    # exactly the k columns (QKVParallelLinear, layers/linear.py:103-114)
+    d = w.shape[0] // (hq + 2 * hkv)
+    wk = torch.zeros_like(w)
+    wk[hq * d:(hq + hkv) * d] = w[hq * d:(hq + hkv) * d]
+    out = fn_f32(x, ln, wk, 1e-6)
+    assert torch.count_nonzero(out[:, : hq * d]) == 0 and torch.count_nonzero(out[:, (hq + hkv) * d:]) == 0
+    assert torch.count_nonzero(out[:, hq * d:(hq + hkv) * d]) > 0
+    # known answer: W = scaled identity block -> output column j = n[:, j] * s
+    h = x.shape[1]
+    eye = torch.zeros(w.shape[0], h, dtype=torch.bfloat16)
+    eye[:h, :h] = torch.eye(h) * 0.5
+    out = fn_f32(x, ln, eye, 1e-6)
+    nrm = R.rmsnorm_f32(x, ln, 1e-6)
+    np.testing.assert_allclose(_np(out[:, :h]), _np(nrm) * 0.5, rtol=1e-6, atol=1e-7)
+
+
+def test_qkv_variants_pinned():
+    pin_qkv(R.qkv_mixed_precision, R.qkv_production, R.qkv_minimal_f32)
+
+
+def test_qkv_reference_stability_checks():
+    """tests/test_numerical_stability.py:180-235 and tests/test_qwen3_bias_handling.py:132-228."""
+    g = gen(23)
+    h, hq, hkv = 256, 8, 2
+    n = (hq + 2 * hkv) * h // hq
+    x = randn(g, 8, h)
+    ln = torch.ones(h, dtype=torch.bfloat16)
+    ln[0] = 96.5
+    w = (torch.randn(n, h, generator=g) * 0.1).to(torch.bfloat16)
+    fused = R.qkv_minimal_f32(x, ln, w, 1e-6)
+    sep = R.rmsnorm_f32(x, ln, 1e-6) @ w.t().float()
+    assert (fused - sep).abs().max() < 5e-2
+    assert torch.equal(R.qkv_with_bias(x, ln, w, None, 1e-6),
+                       R.qkv_with_bias(x, ln, w, torch.zeros(n, dtype=torch.bfloat16), 1e-6))
+    w2 = w.clone()
+    w2[hq * (h // hq):(hq + hkv) * (h // hq)] *= 96.5
+    assert torch.isfinite(R.qkv_with_bias(x.float().mul(0.01).to(torch.bfloat16), ln, w2, None, 1e-6)).all()
+
+
+def test_bias_sanitization():
+    b = torch.tensor([float("nan"), float("inf"), -float("inf"), 1e30, -1e30, 0.5])
+    s = R.sanitize_bias(b)
+    assert s.tolist() == [0.0, 1e10, -1e10, 1e10, -1e10, 0.5]
+    assert R.sanitize_bias(None) is None
+
+
+def test_model_chains_pinned():
+    g = gen(24)
+    t, h, hq, hkv, d = 12, 256, 4, 2, 64
+    n = (hq + 2 * hkv) * d
+    x = randn(g, t, h)
+    ln = randn(g, h, mean=1.0, std=0.1)
+    w = randn(g, n, h, std=0.02)
+    qn = randn(g, d, mean=1.0, std=0.1)
+    kn = torch.exp(torch.empty(d).uniform_(math.log(0.05), math.log(100), generator=g)).to(torch.bfloat16)
+    pos = torch.randint(0, 2048, (t,), generator=g)
+    cache = R.cos_sin_cache(d, 2048, 1e6)
+    q, k, v = R.qwen3_attention_input(x, ln, w, None, hq, hkv, 1e-6, pos, cache, qn, kn)
+    base = N.qkv(_np(x), _np(ln), _np(w), None, 1e-6, "mixed")
+    nq = N.head_norm(base[:, : hq * d].reshape(t, hq, d), _np(qn), 1e-6, "bf16")
+    nk = N.head_norm(base[:, hq * d:(hq + hkv) * d].reshape(t, hkv, d), _np(kn), 1e-6, "bf16")
+    c = _np(cache)
+    rq = N.rotary_forward(c, pos.numpy(), nq.reshape(t, -1), d)
+    rk = N.rotary_forward(c, pos.numpy(), nk.reshape(t, -1), d)
+    # a one-ulp flip in the projection can move the head norm, so compare in tolerance
+    np.testing.assert_allclose(_np(q), rq, rtol=2e-2, atol=2e-2)
+    np.testing.assert_allclose(_np(k), rk, rtol=2e-2, atol=2e-2 * float(_np(kn).max()))
+    check_bf16_agreement(v, base[:, (hq + hkv) * d:], max_frac=2e-2, what="qwen3 v")
+    q, k, v = R.llama_attention_input(x, ln, w, hq, hkv, 1e-5, pos, cache)
+    base = N.qkv(_np(x), _np(ln), _np(w), None, 1e-5, "f32")
+    rq = N.rotary_forward(c, pos.numpy(), base[:, : hq * d], d, dtype="f32")
+    check_bf16_agreement(q, N.round_bf16(rq), max_frac=2e-2, what="llama q")
+
+
+# --------------------------------------------------- planted mistakes fail
+def test_planted_mistakes_are_caught():
+    """Each pin above must reject a plausible mistake planted in a copy of the oracle."""
+
+    def rope_wrong_sign(cache, d, positions, q, k):
+        cos, sin = cache[positions].chunk(2, dim=-1)
+
+        def app(x):
+            x1, x2 = torch.chunk(x.float(), 2, dim=-1)
+            c, s = cos.unsqueeze(-2), sin.unsqueeze(-2)
+            return torch.cat((x1 * c + x2 * s, x2 * c - x1 * s), dim=-1).to(x.dtype)
+        t = positions.size(0)
+        return (app(q.reshape(t, -1, d)).view(q.shape), app(k.reshape(t, -1, d)).view(k.shape))
+
+    with pytest.raises(AssertionError):
+        pin_rotary(rope_wrong_sign)
+
+    def rms_no_gamma(x, w, eps):
+        return R.rms_forward(x, torch.ones_like(w), eps)
+
+    with pytest.raises(AssertionError):
+        pin_rms_forward(rms_no_gamma)
+
+    def rms_no_eps(x, w, eps):
+        return R.rms_forward(x, w, 0.0)
+
+    with pytest.raises(AssertionError):
+        pin_rms_forward(rms_no_eps)
+
+    def f32_transposed_halves(x, ln, w, eps):  # columns of W read in the wrong order
+        return R.qkv_minimal_f32(x, ln, w.flip(1), eps)
+
+    with pytest.raises(AssertionError):
+        pin_qkv(R.qkv_mixed_precision, R.qkv_production, f32_transposed_halves)
+
+    def mixed_rounds_late(x, ln, w, b, eps):  # drops the bf16 rounding before gamma
+        return R.qkv_production(x, ln, w, eps) if b is None else (
+            R.qkv_minimal_f32(x, ln, w, eps) + b.float()).to(torch.bfloat16)
+
+    with pytest.raises(AssertionError):
+        pin_qkv(mixed_rounds_late, R.qkv_production, R.qkv_minimal_f32)
