@@ -1,0 +1,336 @@
+"""Benchmark: Llama-3-8B per-layer fused chain on one MI355X.
+
+One step = one decoder layer's hot-path chain on synthetic inputs already
+resident in HBM:
+    residual-add + RMSNorm        [T, 4096]
+    fused RMSNorm + QKV + RoPE    [T, 4096] x [6144, 4096]^T, theta 5e5, bf16 out
+    SiLU * mul (SwiGLU)           [T, 2 x 14336] -> [T, 14336]
+(the GEMMs between them -- o_proj, gate_up, down -- are not part of this
+path).  The headline line is the 8192-token prefill (the QKV projection is
+matrix-core bound there); the batch-64 decode chain and the per-forward
+embedding gather are reported in the same JSON line.
+
+    python bench.py [--steps K] [--warmup W] [--tokens T] [--no-cpu]
+
+Prints one JSON line.  `value` is microseconds per layer (lower is better),
+measured with HIP events around K back-to-back chain steps on the current
+stream.  `roofline` is for the dominant kernel (the QKV projection at
+8192 tokens): its algorithmic FLOPs / its own average event-timed duration
+against the 2.5 PFLOP/s dense-bf16 peak.  `cpu_baseline` times the oracle's
+torch-CPU restatement of the same chain on a bounded token sample and scales
+it linearly to T tokens.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import torch
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+from braidinfer_amd import _lib  # noqa: E402
+from braidinfer_amd.kernels._qkv import fused_rmsnorm_qkv  # noqa: E402
+from braidinfer_amd.layers import RMSNorm, SiluAndMul  # noqa: E402
+from braidinfer_amd.layers.embed_head import embedding  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+
+# Llama-3-8B layer
+H, HQ, HKV, D, INTER, VOCAB = 4096, 32, 8, 128, 14336, 128256
+N = (HQ + 2 * HKV) * D
+THETA, MAXPOS, EPS = 5e5, 8192, 1e-5
+
+
+def rope_table(d, maxp, base):
+    inv_freq = 1.0 / (base ** (torch.arange(0, d, 2, dtype=torch.float32) / d))
+    t = torch.arange(maxp, dtype=torch.float32)
+    freqs = torch.einsum("i,j -> ij", t, inv_freq)
+    return torch.cat((freqs.cos(), freqs.sin()), dim=-1)
+
+
+class Chain:
+    """Synthetic inputs of one layer at T tokens (seed 5, drawn on the CPU)."""
+
+    def __init__(self, t: int, dev: torch.device, seed: int = 5):
+        g = torch.Generator().manual_seed(seed)
+        bf = torch.bfloat16
+
+        def randn(*shape, std=1.0, mean=0.0):
+            return (torch.randn(*shape, generator=g) * std + mean).to(bf).to(dev)
+
+        self.t = t
+        self.x = randn(t, H)
+        self.residual = randn(t, H)
+        self.norm = RMSNorm(H, eps=EPS).to(dev)
+        with torch.no_grad():
+            self.norm.weight.data = randn(H, std=0.1, mean=1.0)
+        self.hidden = randn(t, H)
+        self.ln_w = randn(H, std=0.1, mean=1.0)
+        self.w_qkv = randn(N, H, std=0.02)
+        self.positions = torch.randint(0, MAXPOS, (t,), generator=g).to(dev)
+        self.cache = rope_table(D, MAXPOS, THETA).to(dev)
+        self.gate_up = randn(t, 2 * INTER)
+        self.silu = SiluAndMul()
+        self.out_qkv = torch.empty(t, N, dtype=bf, device=dev)
+        self.ids = torch.randint(0, VOCAB, (t,), generator=g).to(dev)
+
+    def qkv(self):
+        return fused_rmsnorm_qkv(self.hidden, self.ln_w, self.w_qkv, HQ, HKV, EPS,
+                                 mixed_rounding=False, qkv_dtype=torch.float32,
+                                 out_dtype=torch.bfloat16, positions=self.positions,
+                                 cos_sin_cache=self.cache, out=self.out_qkv)
+
+    def step(self):
+        self.norm(self.x, self.residual)
+        self.qkv()
+        self.silu(self.gate_up)
+
+
+class QkvStages:
+    """Calls the two stages of the fused QKV op directly through the C ABI, so
+    each kernel can be timed on its own: the RMSNorm operand pre-pass and the
+    MFMA projection with the fused RoPE epilogue."""
+
+    def __init__(self, c: Chain, dev):
+        self.c = c
+        self.dev = dev
+        ws = _lib.call("bfa_fused_rmsnorm_qkv_workspace_size", c.t, H, N, D)
+        self.op_bytes = (c.t * H * 2 + 255) // 256 * 256
+        self.ws = torch.empty(max(ws, 16), dtype=torch.uint8, device=dev)
+        self.status = _lib.status_word(dev)
+
+    def operand(self):
+        c = self.c
+        _lib.call("bfa_rmsnorm_qkv_operand", _lib.ptr(c.hidden), _lib.BF16, c.t, H, H,
+                  _lib.ptr(c.ln_w), _lib.BF16, 0, _lib.ptr(self.ws), _lib.BF16, EPS,
+                  _lib.stream_of(self.dev))
+
+    def projection(self):
+        c = self.c
+        part = self.ws.data_ptr() + self.op_bytes
+        _lib.call("bfa_qkv_projection", _lib.ptr(self.ws), c.t, H, _lib.ptr(c.w_qkv), _lib.BF16, N, H,
+                  None, 0, HQ, HKV, _lib.F32, None, None, 0, 0.0, _lib.BF16,
+                  _lib.ptr(c.positions), _lib.I64, _lib.ptr(c.cache), MAXPOS,
+                  _lib.ptr(c.out_qkv), _lib.BF16, N, _lib.c_void_p(part),
+                  self.ws.numel() - self.op_bytes, _lib.ptr(self.status), _lib.stream_of(self.dev))
+
+
+def time_fn(fn, iters: int, warmup: int = 3) -> float:
+    """Average milliseconds per call, HIP events on the current stream."""
+    for _ in range(warmup):
+        fn()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    s.record()
+    for _ in range(iters):
+        fn()
+    e.record()
+    torch.cuda.synchronize()
+    return s.elapsed_time(e) / iters
+
+
+def kernel_table(c: Chain, dev, iters: int) -> dict:
+    """Per-kernel event timing with algorithmic bytes / FLOPs and roofline fractions."""
+    t = c.t
+    st = QkvStages(c, dev)
+    rows = {}
+
+    def add(name, fn, nbytes, flops=0.0):
+        ms = time_fn(fn, iters)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        row = {"us": round(ms * 1e3, 3), "bytes": int(nbytes), "gbs": round(gbs, 1),
+               "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
+        if flops:
+            tf = flops / (ms * 1e-3) / 1e12
+            row.update({"flops": flops, "tflops": round(tf, 1), "mfma_frac": round(tf / BF16_PEAK_TFLOPS, 4)})
+        rows[name] = row
+
+    add("add_rms_norm", lambda: c.norm(c.x, c.residual), 4 * t * H * 2 + H * 2)
+    add("qkv_operand_prepass", st.operand, 2 * t * H * 2 + H * 2)
+    add("qkv_projection_rope", st.projection,
+        t * H * 2 + N * H * 2 + t * N * 2 + t * 8 + t * D * 4, 2.0 * t * H * N)
+    add("fused_rmsnorm_qkv_rope", c.qkv,
+        t * H * 2 + H * 2 + N * H * 2 + t * N * 2 + t * 8 + t * D * 4, 2.0 * t * H * N)
+    add("silu_and_mul", lambda: c.silu(c.gate_up), 3 * t * INTER * 2)
+    table = torch.empty(VOCAB, H, dtype=torch.bfloat16, device=dev).normal_(0, 0.02)
+    add("embedding_gather", lambda: embedding(c.ids, table), 2 * t * H * 2 + 8 * t)
+    del table
+    return rows
+
+
+def time_cold(fn, iters: int, flush: torch.Tensor) -> float:
+    """Average milliseconds per call with the 256 MB Infinity Cache flushed
+    (512 MB written) before each call; each call is bracketed by its own events."""
+    fn()
+    pairs = []
+    for _ in range(iters):
+        flush.zero_()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        fn()
+        e.record()
+        pairs.append((s, e))
+    torch.cuda.synchronize()
+    return sum(s.elapsed_time(e) for s, e in pairs) / iters
+
+
+def cold_decode_table(dev, t: int, iters: int) -> dict:
+    """Decode-shape kernels streaming their operands from HBM (cache flushed)."""
+    c = Chain(t, dev)
+    flush = torch.empty(512 * 2**20 // 4, dtype=torch.float32, device=dev)
+    out = {}
+    for name, fn, nbytes in (
+        ("add_rms_norm", lambda: c.norm(c.x, c.residual), 4 * t * H * 2 + H * 2),
+        ("fused_rmsnorm_qkv_rope", c.qkv,
+         t * H * 2 + H * 2 + N * H * 2 + t * N * 2 + t * 8 + t * D * 4),
+        ("silu_and_mul", lambda: c.silu(c.gate_up), 3 * t * INTER * 2),
+    ):
+        ms = time_cold(fn, iters, flush)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        out[name] = {"us": round(ms * 1e3, 3), "gbs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
+    del c, flush
+    return out
+
+
+def chain_us(c: Chain, steps: int, warmup: int) -> float:
+    for _ in range(warmup):
+        c.step()
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(steps):
+        c.step()
+    e.record()
+    torch.cuda.synchronize()
+    return s.elapsed_time(e) / steps * 1e3
+
+
+def cpu_baseline(t_full: int, budget_s: float = 12.0) -> dict:
+    """The oracle's torch-CPU restatement of the same chain on a token sample,
+    scaled linearly to t_full tokens (rows of every op are independent)."""
+    from oracle import torch_ref as R
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    ts = 256
+    g = torch.Generator().manual_seed(5)
+    bf = torch.bfloat16
+    x = torch.randn(ts, H, generator=g).to(bf)
+    res = torch.randn(ts, H, generator=g).to(bf)
+    w = (torch.randn(H, generator=g) * 0.1 + 1).to(bf)
+    wq = (torch.randn(N, H, generator=g) * 0.02).to(bf)
+    pos = torch.randint(0, MAXPOS, (ts,), generator=g)
+    cache = rope_table(D, MAXPOS, THETA)
+    gu = torch.randn(ts, 2 * INTER, generator=g).to(bf)
+
+    def step():
+        R.add_rms_forward(x, res, w, EPS)
+        R.llama_attention_input(x, w, wq, HQ, HKV, EPS, pos, cache)
+        R.silu_and_mul(gu)
+
+    step()
+    times = []
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < budget_s and len(times) < 30:
+        s = time.perf_counter()
+        step()
+        times.append(time.perf_counter() - s)
+    times.sort()
+    med = times[len(times) // 2]
+    return {"value": round(med * 1e6 * t_full / ts, 1), "unit": "us/layer", "cores": threads,
+            "kind": "port",
+            "sample": f"oracle torch-CPU chain (add_rms_forward, llama attention input: minimal_f32 "
+                      f"QKV + RoPE, silu_and_mul) at {ts} tokens, median of {len(times)} runs, "
+                      f"scaled x{t_full / ts:g} to {t_full} tokens; torch {torch.__version__}"}
+
+
+def read_traffic(name: str):
+    """HBM bytes per launch measured with rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE),
+    recorded in profiles/<name>.txt as a `traffic_bytes: N` line."""
+    p = ROOT / "profiles" / f"{name}.txt"
+    if not p.exists():
+        return None
+    for line in p.read_text().splitlines():
+        if line.startswith("traffic_bytes:"):
+            return int(float(line.split(":", 1)[1]))
+    return None
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--tokens", type=int, default=8192)
+    ap.add_argument("--decode-tokens", type=int, default=64)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-cold", action="store_true", help="skip the cold-cache decode table")
+    args = ap.parse_args(argv)
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus > 1 or world > 1:
+        print("bench.py: this path is measured on one GPU only (the fused per-layer kernels "
+              "shard by tokens or heads with no exchange); --gpus > 1 is not supported",
+              file=sys.stderr)
+        return 2
+    if not torch.cuda.is_available():
+        print("bench.py: no ROCm GPU visible", file=sys.stderr)
+        return 1
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    _lib.load()
+
+    prefill = Chain(args.tokens, dev)
+    us = chain_us(prefill, args.steps, args.warmup)
+    kp = kernel_table(prefill, dev, max(10, args.steps))
+    proj = kp["qkv_projection_rope"]
+    del prefill
+    torch.cuda.empty_cache()
+
+    decode = Chain(args.decode_tokens, dev)
+    us_dec = chain_us(decode, max(args.steps, 100), args.warmup)
+    kd = kernel_table(decode, dev, max(50, args.steps))
+    del decode
+    torch.cuda.empty_cache()
+    cold = None if args.no_cold else cold_decode_table(dev, args.decode_tokens, 48)
+    _lib.check_device_status(dev)
+
+    line = {
+        "metric": "us/layer + % HBM / % MFMA peak, fused norm+QKV+RoPE+SwiGLU, 1 MI355X",
+        "value": round(us, 2),
+        "unit": "us/layer",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(us / 1e3, 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) activations, N(0,0.02) weights, Llama-3-8B shapes)",
+        "config": {"workload": f"Llama-3-8B layer chain, {args.tokens}-token prefill: add+RMSNorm "
+                               f"[{args.tokens},4096] -> fused RMSNorm+QKV(4096->6144)+RoPE(theta 5e5) "
+                               f"-> SiLU*mul [{args.tokens},2x14336]",
+                   "tokens": args.tokens, "hidden": H, "q_heads": HQ, "kv_heads": HKV,
+                   "head_dim": D, "intermediate": INTER},
+        "roofline": {"bound": "mfma", "kernel": "qkv_projection_rope",
+                     "achieved": proj["tflops"], "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": proj["mfma_frac"],
+                     "traffic": read_traffic(f"traffic_qkv_projection_llama3_8b_t{args.tokens}")},
+        "kernels_prefill": kp,
+        "decode": {"tokens": args.decode_tokens, "us_per_layer": round(us_dec, 2),
+                   "kernels_warm": kd, "kernels_cold": cold},
+    }
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline(args.tokens)
+    print(json.dumps(line))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
