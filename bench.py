@@ -262,6 +262,19 @@ def read_traffic(name: str):
     return None
 
 
+def profile_one(kernel: str, tokens: int, steps: int, dev) -> int:
+    """Runs one kernel `steps` times on the chain's inputs; prints its event-timed average."""
+    c = Chain(tokens, dev)
+    st = QkvStages(c, dev)
+    table = torch.empty(VOCAB, H, dtype=torch.bfloat16, device=dev) if kernel == "embedding" else None
+    fn = {"qkv_projection": st.projection, "qkv_operand": st.operand,
+          "add_rms_norm": lambda: c.norm(c.x, c.residual), "silu_and_mul": lambda: c.silu(c.gate_up),
+          "embedding": lambda: embedding(c.ids, table)}[kernel]
+    ms = time_fn(fn, steps)
+    print(json.dumps({"kernel": kernel, "tokens": tokens, "calls": steps, "us": round(ms * 1e3, 3)}))
+    return 0
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -271,6 +284,9 @@ def main(argv=None) -> int:
     ap.add_argument("--decode-tokens", type=int, default=64)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-cold", action="store_true", help="skip the cold-cache decode table")
+    ap.add_argument("--kernel", choices=["qkv_projection", "qkv_operand", "add_rms_norm",
+                                         "silu_and_mul", "embedding"],
+                    help="only run this kernel --steps times at --tokens (for profilers)")
     args = ap.parse_args(argv)
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus > 1 or world > 1:
@@ -284,6 +300,8 @@ def main(argv=None) -> int:
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
     _lib.load()
+    if args.kernel:
+        return profile_one(args.kernel, args.tokens, args.steps, dev)
 
     prefill = Chain(args.tokens, dev)
     us = chain_us(prefill, args.steps, args.warmup)

@@ -143,15 +143,101 @@ enum { EPI_RAW = 0, EPI_FUSED = 1 };
 // stored at slot g ^ (r & 7).
 __device__ __forceinline__ int swz(int r, int g) { return r * 8 + (g ^ (r & 7)); }
 
-template <int BM, int BN, int WM, int WN, bool BF16, int EPI, int HD>
+// Loads the MFMA fragments of K sub-step ks (16 deep) from an LDS tile buffer.
+template <int MB, int NB, int BM, int WM, int WN>
+__device__ __forceinline__ void load_frags(const uint4* buf, int ks, int wm, int wn, int frow,
+                                           int fhalf, uint4 (&af)[MB], uint4 (&bf)[NB]) {
+  const int gsel = ks * 2 + fhalf;
+#pragma unroll
+  for (int i = 0; i < MB; ++i) af[i] = buf[swz(wm * WM + i * 32 + frow, gsel)];
+#pragma unroll
+  for (int j = 0; j < NB; ++j) bf[j] = buf[BM * 8 + swz(wn * WN + j * 32 + frow, gsel)];
+}
+
+template <int MB, int NB, bool BF16>
+__device__ __forceinline__ void mfma_block(f32x16_t (&acc)[MB][NB], const uint4 (&af)[MB],
+                                           const uint4 (&bf)[NB]) {
+#pragma unroll
+  for (int i = 0; i < MB; ++i)
+#pragma unroll
+    for (int j = 0; j < NB; ++j) acc[i][j] = mfma32<BF16>(af[i], bf[j], acc[i][j]);
+}
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+// LDS byte address of a __shared__ pointer, as a wave-uniform SGPR value.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return __builtin_amdgcn_readfirstlane(
+      static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const lds_void_t*)p)));
+}
+
+// Asynchronous 16-byte-per-lane copy global -> LDS (global_load_lds_dwordx4):
+// lane i's 16 bytes at base + voff land at LDS byte m0 + 16*i.  Issued as
+// inline assembly so the compiler does not serialise consecutive copies; the
+// caller waits (wait_vmem) and barriers before the LDS is read.
+__device__ __forceinline__ void dma16(const void* base, uint32_t voff, uint32_t m0) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(__builtin_amdgcn_readfirstlane(m0)),
+               "v"(voff), "s"(base)
+               : "memory");
+}
+
+__device__ __forceinline__ void wait_vmem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// First three 16-deep K sub-steps of a tile (fragments of sub-step 0 are in
+// fa0/fb0 on entry; sub-step 3's are left in fa1/fb1 for the caller).
+template <int MB, int NB, int BM, int WM, int WN, bool BF16>
+__device__ __forceinline__ void compute3(const uint4* cur, int wm, int wn, int frow, int fhalf,
+                                         f32x16_t (&acc)[MB][NB], uint4 (&fa0)[MB], uint4 (&fb0)[NB],
+                                         uint4 (&fa1)[MB], uint4 (&fb1)[NB]) {
+  load_frags<MB, NB, BM, WM, WN>(cur, 1, wm, wn, frow, fhalf, fa1, fb1);
+  mfma_block<MB, NB, BF16>(acc, fa0, fb0);
+  load_frags<MB, NB, BM, WM, WN>(cur, 2, wm, wn, frow, fhalf, fa0, fb0);
+  mfma_block<MB, NB, BF16>(acc, fa1, fb1);
+  load_frags<MB, NB, BM, WM, WN>(cur, 3, wm, wn, frow, fhalf, fa1, fb1);
+  mfma_block<MB, NB, BF16>(acc, fa0, fb0);
+}
+
+// Tile loads: thread (gr, gg) fetches granule gg of rows gr + 32 i of the
+// operand and weight tiles for K tile kt (MASKED: zero past K, K % 8 == 0).
+// Row addresses are 32-bit element offsets from the uniform matrix bases.
+template <int AG, int BG, bool NOMASK>
+__device__ __forceinline__ void tile_load(const uint16_t* a, const uint16_t* w,
+                                          const uint32_t (&aoff)[AG], const uint32_t (&boff)[BG],
+                                          int64_t kt, int gg, int64_t k, uint4 (&ra)[AG],
+                                          uint4 (&rb)[BG]) {
+  const bool in = NOMASK || kt * 64 + gg * 8 < k;
+  const uint16_t* ak = a + kt * 64;
+  const uint16_t* wk = w + kt * 64;
+#pragma unroll
+  for (int i = 0; i < AG; ++i)
+    ra[i] = in ? *reinterpret_cast<const uint4*>(ak + aoff[i]) : make_uint4(0, 0, 0, 0);
+#pragma unroll
+  for (int i = 0; i < BG; ++i)
+    rb[i] = in ? *reinterpret_cast<const uint4*>(wk + boff[i]) : make_uint4(0, 0, 0, 0);
+}
+
+template <int AG, int BG, int BM>
+__device__ __forceinline__ void tile_store(uint4* buf, int gr, int gg, const uint4 (&ra)[AG],
+                                           const uint4 (&rb)[BG]) {
+#pragma unroll
+  for (int i = 0; i < AG; ++i) buf[swz(gr + 32 * i, gg)] = ra[i];
+#pragma unroll
+  for (int i = 0; i < BG; ++i) buf[BM * 8 + swz(gr + 32 * i, gg)] = rb[i];
+}
+
+// DIRECT: tiles go HBM -> LDS by DMA (K % 64 == 0, 16-byte aligned rows,
+// byte offsets below 4 GiB); otherwise HBM -> registers -> LDS with K masking.
+template <int BM, int BN, int WM, int WN, bool BF16, int EPI, int HD, bool DIRECT>
 __global__ __launch_bounds__(256) void qkv_gemm_kernel(GemmArgs g, QkvEpi e) {
   constexpr int NWN = BN / WN;
   static_assert((BM / WM) * NWN == 4, "four waves per workgroup");
   constexpr int MB = WM / 32, NB = WN / 32;
   constexpr int AG = BM / 32, BG = BN / 32;  // 16-byte granules per thread per K tile
-  __shared__ uint4 lds[2][(BM + BN) * 8];
+  __shared__ uint4 lds0[(BM + BN) * 8];
+  __shared__ uint4 lds1[(BM + BN) * 8];
 
-  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
   const int wm = wid / NWN, wn = wid % NWN;
 
   // Tile order: workgroups are dispatched round-robin over the 8 XCDs; remap
@@ -169,36 +255,8 @@ __global__ __launch_bounds__(256) void qkv_gemm_kernel(GemmArgs g, QkvEpi e) {
   const int64_t tm = first_m + (bid % (GROUP_M * tiles_n)) % gsize;
   const int64_t tn = (bid % (GROUP_M * tiles_n)) / gsize;
   const int64_t m0 = tm * BM, n0 = tn * BN;
-
-  // global -> register assignment: thread loads granule gg of rows gr + 32*i
-  const int gg = tid & 7, gr = tid >> 3;
-  const uint4* asrc[AG];
-  const uint4* bsrc[BG];
-#pragma unroll
-  for (int i = 0; i < AG; ++i) {
-    const int64_t r = min(m0 + gr + 32 * i, g.m - 1);
-    asrc[i] = reinterpret_cast<const uint4*>(g.a + r * g.lda) + gg;
-  }
-#pragma unroll
-  for (int i = 0; i < BG; ++i) {
-    const int64_t r = min(n0 + gr + 32 * i, g.n - 1);
-    bsrc[i] = reinterpret_cast<const uint4*>(g.w + r * g.ldw) + gg;
-  }
-  uint4 ra[AG], rb[BG];
   const int64_t KT = cdiv(g.k, 64);
-  auto gload = [&](int64_t kt) {
-    const bool in = kt * 64 + gg * 8 < g.k;  // K % 8 == 0, so granules are all-in or all-out
-#pragma unroll
-    for (int i = 0; i < AG; ++i) ra[i] = in ? asrc[i][kt * 8] : make_uint4(0, 0, 0, 0);
-#pragma unroll
-    for (int i = 0; i < BG; ++i) rb[i] = in ? bsrc[i][kt * 8] : make_uint4(0, 0, 0, 0);
-  };
-  auto sstore = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < AG; ++i) lds[buf][swz(gr + 32 * i, gg)] = ra[i];
-#pragma unroll
-    for (int i = 0; i < BG; ++i) lds[buf][BM * 8 + swz(gr + 32 * i, gg)] = rb[i];
-  };
+  const int frow = lane & 31, fhalf = lane >> 5;
 
   f32x16_t acc[MB][NB];
 #pragma unroll
@@ -206,30 +264,99 @@ __global__ __launch_bounds__(256) void qkv_gemm_kernel(GemmArgs g, QkvEpi e) {
 #pragma unroll
     for (int j = 0; j < NB; ++j) acc[i][j] = f32x16_t{};
 
-  gload(0);
-  sstore(0);
-  __syncthreads();
-  const int frow = lane & 31, fhalf = lane >> 5;
-  for (int64_t kt = 0; kt < KT; ++kt) {
-    const int cur = static_cast<int>(kt & 1);
-    if (kt + 1 < KT) gload(kt + 1);
-    const uint4* la = lds[cur];
-    const uint4* lb = lds[cur] + BM * 8;
+  // global -> register -> LDS (any K that is a multiple of 8).  The next
+  // tile's loads are issued before this tile's MFMAs and stored to the other
+  // LDS buffer after them; MFMA fragments are double-buffered across the four
+  // 16-deep K sub-steps so every ds_read overlaps the previous sub-step's MFMAs.
+  if constexpr (DIRECT) {
+    // Each wave fills 1 KiB blocks of 8 tile rows (block b = 4 i + wid): lane l
+    // lands at physical slot l % 8 of row l / 8 and therefore fetches logical
+    // granule (l % 8) ^ (l / 8), which realises the XOR swizzle of swz().
+    const int lrow = lane >> 3, lgran = (lane & 7) ^ (lane >> 3);
+    uint32_t aoff[AG], boff[BG];
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      const int gsel = ks * 2 + fhalf;
-      uint4 af[MB], bfr[NB];
+    for (int i = 0; i < AG; ++i)
+      aoff[i] = static_cast<uint32_t>((min(m0 + (i * 4 + wid) * 8 + lrow, g.m - 1) * g.lda + lgran * 8) * 2);
 #pragma unroll
-      for (int i = 0; i < MB; ++i) af[i] = la[swz(wm * WM + i * 32 + frow, gsel)];
+    for (int i = 0; i < BG; ++i)
+      boff[i] = static_cast<uint32_t>((min(n0 + (i * 4 + wid) * 8 + lrow, g.n - 1) * g.ldw + lgran * 8) * 2);
+    const uint32_t l0 = lds_addr(lds0) + wid * 1024, l1 = lds_addr(lds1) + wid * 1024;
+    auto issue = [&](int64_t kt, uint32_t lbase) {
+      const uint16_t* ak = g.a + kt * 64;
+      const uint16_t* wk = g.w + kt * 64;
 #pragma unroll
-      for (int j = 0; j < NB; ++j) bfr[j] = lb[swz(wn * WN + j * 32 + frow, gsel)];
+      for (int i = 0; i < AG; ++i) dma16(ak, aoff[i], lbase + i * 4096);
 #pragma unroll
-      for (int i = 0; i < MB; ++i)
-#pragma unroll
-        for (int j = 0; j < NB; ++j) acc[i][j] = mfma32<BF16>(af[i], bfr[j], acc[i][j]);
-    }
-    if (kt + 1 < KT) sstore(cur ^ 1);
+      for (int i = 0; i < BG; ++i) dma16(wk, boff[i], lbase + BM * 128 + i * 4096);
+    };
+    uint4 fa0[MB], fb0[NB], fa1[MB], fb1[NB];
+    issue(0, l0);
+    wait_vmem();
     __syncthreads();
+    load_frags<MB, NB, BM, WM, WN>(lds0, 0, wm, wn, frow, fhalf, fa0, fb0);
+    int64_t kt = 0;
+    for (; kt + 2 <= KT; kt += 2) {
+      issue(kt + 1, l1);
+      compute3<MB, NB, BM, WM, WN, BF16>(lds0, wm, wn, frow, fhalf, acc, fa0, fb0, fa1, fb1);
+      mfma_block<MB, NB, BF16>(acc, fa1, fb1);
+      wait_vmem();
+      __syncthreads();
+      load_frags<MB, NB, BM, WM, WN>(lds1, 0, wm, wn, frow, fhalf, fa0, fb0);
+      if (kt + 2 < KT) issue(kt + 2, l0);
+      compute3<MB, NB, BM, WM, WN, BF16>(lds1, wm, wn, frow, fhalf, acc, fa0, fb0, fa1, fb1);
+      mfma_block<MB, NB, BF16>(acc, fa1, fb1);
+      wait_vmem();
+      __syncthreads();
+      if (kt + 2 < KT) load_frags<MB, NB, BM, WM, WN>(lds0, 0, wm, wn, frow, fhalf, fa0, fb0);
+    }
+    if (kt < KT) {  // odd tile count: the last tile is in lds0
+      compute3<MB, NB, BM, WM, WN, BF16>(lds0, wm, wn, frow, fhalf, acc, fa0, fb0, fa1, fb1);
+      mfma_block<MB, NB, BF16>(acc, fa1, fb1);
+      __syncthreads();
+    }
+  } else {
+    const int gg = tid & 7, gr = tid >> 3;
+    uint32_t aoff[AG], boff[BG];
+  #pragma unroll
+    for (int i = 0; i < AG; ++i)
+      aoff[i] = static_cast<uint32_t>(min(m0 + gr + 32 * i, g.m - 1) * g.lda + gg * 8);
+  #pragma unroll
+    for (int i = 0; i < BG; ++i)
+      boff[i] = static_cast<uint32_t>(min(n0 + gr + 32 * i, g.n - 1) * g.ldw + gg * 8);
+    uint4 ra[AG], rb[BG];
+    // Two register sets keep the loads of tiles kt+1 and kt+2 in flight while
+    // tile kt is multiplied (the K loop is unrolled by two so the sets are
+    // static): misses that go to the Infinity Cache get ~2 tiles of MFMA time.
+    uint4 ra2[AG], rb2[BG];
+    uint4 fa0[MB], fb0[NB], fa1[MB], fb1[NB];
+    tile_load<AG, BG, false>(g.a, g.w, aoff, boff, 0, gg, g.k, ra, rb);
+    tile_store<AG, BG, BM>(lds0, gr, gg, ra, rb);
+    if (KT > 1) tile_load<AG, BG, false>(g.a, g.w, aoff, boff, 1, gg, g.k, ra, rb);
+    if (KT > 2) tile_load<AG, BG, false>(g.a, g.w, aoff, boff, 2, gg, g.k, ra2, rb2);
+    __syncthreads();
+    load_frags<MB, NB, BM, WM, WN>(lds0, 0, wm, wn, frow, fhalf, fa0, fb0);
+    int64_t kt = 0;
+    for (; kt + 2 <= KT; kt += 2) {
+      // tile kt from lds0; set 1 holds tile kt+1, set 2 holds tile kt+2
+      compute3<MB, NB, BM, WM, WN, BF16>(lds0, wm, wn, frow, fhalf, acc, fa0, fb0, fa1, fb1);
+      tile_store<AG, BG, BM>(lds1, gr, gg, ra, rb);
+      mfma_block<MB, NB, BF16>(acc, fa1, fb1);
+      __syncthreads();
+      if (kt + 3 < KT) tile_load<AG, BG, false>(g.a, g.w, aoff, boff, kt + 3, gg, g.k, ra, rb);
+      load_frags<MB, NB, BM, WM, WN>(lds1, 0, wm, wn, frow, fhalf, fa0, fb0);
+      // tile kt+1 from lds1; set 2 holds tile kt+2, set 1 holds tile kt+3
+      compute3<MB, NB, BM, WM, WN, BF16>(lds1, wm, wn, frow, fhalf, acc, fa0, fb0, fa1, fb1);
+      if (kt + 2 < KT) tile_store<AG, BG, BM>(lds0, gr, gg, ra2, rb2);
+      mfma_block<MB, NB, BF16>(acc, fa1, fb1);
+      __syncthreads();
+      if (kt + 4 < KT) tile_load<AG, BG, false>(g.a, g.w, aoff, boff, kt + 4, gg, g.k, ra2, rb2);
+      if (kt + 2 < KT) load_frags<MB, NB, BM, WM, WN>(lds0, 0, wm, wn, frow, fhalf, fa0, fb0);
+    }
+    if (kt < KT) {  // odd tile count: the last tile is in lds0
+      compute3<MB, NB, BM, WM, WN, BF16>(lds0, wm, wn, frow, fhalf, acc, fa0, fb0, fa1, fb1);
+      mfma_block<MB, NB, BF16>(acc, fa1, fb1);
+      __syncthreads();
+    }
   }
 
   // ------------------------------------------------------------ epilogue
@@ -261,7 +388,8 @@ __global__ __launch_bounds__(256) void qkv_gemm_kernel(GemmArgs g, QkvEpi e) {
     // is a contiguous 4-element vector.
     constexpr int LDR = 136;  // padded row stride (floats)
     constexpr int LH = HD / 8;  // lanes per head
-    float* et = reinterpret_cast<float*>(&lds[0][0]) + wid * (32 * LDR);
+    float* et = reinterpret_cast<float*>(wid < 2 ? lds0 : lds1) + (wid & 1) * (32 * LDR);
+    static_assert(2 * 32 * LDR * 4 <= (BM + BN) * 8 * 16, "epilogue staging fits one buffer");
     const int l16 = lane & 15, rg = lane >> 4;
     const int hloc = l16 / LH, q = l16 % LH;
     const int c1 = hloc * HD + q * 4, c2 = c1 + HD / 2;  // columns inside the wave tile
@@ -550,22 +678,31 @@ static void launch_decode(const QkvPlan& p, const SplitArgs& s, hipStream_t st) 
   else launch_decode_cpw<BF16, 2>(p, s, st);
 }
 
-template <bool BF16>
-static void launch_prefill(const QkvPlan& p, const GemmArgs& g, const QkvEpi& e, hipStream_t st) {
+template <bool BF16, bool DIRECT>
+static void launch_prefill_t(const QkvPlan& p, const GemmArgs& g, const QkvEpi& e, hipStream_t st) {
   const unsigned grid = static_cast<unsigned>(cdiv(g.m, 256) * cdiv(g.n, 256));
   if (!p.fused_epi) {
-    hipLaunchKernelGGL((qkv_gemm_kernel<256, 256, 128, 128, BF16, EPI_RAW, 128>), dim3(grid),
+    hipLaunchKernelGGL((qkv_gemm_kernel<256, 256, 128, 128, BF16, EPI_RAW, 128, DIRECT>), dim3(grid),
                        dim3(256), 0, st, g, e);
   } else if (e.hd == 128) {
-    hipLaunchKernelGGL((qkv_gemm_kernel<256, 256, 128, 128, BF16, EPI_FUSED, 128>), dim3(grid),
-                       dim3(256), 0, st, g, e);
+    hipLaunchKernelGGL((qkv_gemm_kernel<256, 256, 128, 128, BF16, EPI_FUSED, 128, DIRECT>),
+                       dim3(grid), dim3(256), 0, st, g, e);
   } else if (e.hd == 64) {
-    hipLaunchKernelGGL((qkv_gemm_kernel<256, 256, 128, 128, BF16, EPI_FUSED, 64>), dim3(grid),
-                       dim3(256), 0, st, g, e);
+    hipLaunchKernelGGL((qkv_gemm_kernel<256, 256, 128, 128, BF16, EPI_FUSED, 64, DIRECT>),
+                       dim3(grid), dim3(256), 0, st, g, e);
   } else {
-    hipLaunchKernelGGL((qkv_gemm_kernel<256, 256, 128, 128, BF16, EPI_FUSED, 32>), dim3(grid),
-                       dim3(256), 0, st, g, e);
+    hipLaunchKernelGGL((qkv_gemm_kernel<256, 256, 128, 128, BF16, EPI_FUSED, 32, DIRECT>),
+                       dim3(grid), dim3(256), 0, st, g, e);
   }
+}
+
+template <bool BF16>
+static void launch_prefill(const QkvPlan& p, const GemmArgs& g, const QkvEpi& e, hipStream_t st) {
+  const bool dma = g.k % 64 == 0 && g.lda % 8 == 0 && g.ldw % 8 == 0 && aligned16(g.a) &&
+                   aligned16(g.w) && g.m * g.lda * 2 < (int64_t(1) << 32) &&
+                   g.n * g.ldw * 2 < (int64_t(1) << 32);
+  if (dma) launch_prefill_t<BF16, true>(p, g, e, st);
+  else launch_prefill_t<BF16, false>(p, g, e, st);
 }
 
 static void launch_epilogue(const float* part, int64_t splits, int64_t m, const QkvEpi& e,
