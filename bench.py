@@ -12,9 +12,11 @@ embedding gather are reported in the same JSON line.
 
     python bench.py [--steps K] [--warmup W] [--tokens T] [--no-cpu]
 
-Prints one JSON line.  `value` is microseconds per layer (lower is better),
-measured with HIP events around K back-to-back chain steps on the current
-stream.  `roofline` is for the dominant kernel (the QKV projection at
+Prints one JSON line.  `value` is microseconds per layer (lower is better):
+K chain steps captured into one HIP graph and replayed between HIP events,
+i.e. the GPU time of the three kernels back to back without Python launch
+gaps; `eager_us_per_layer` is the same chain launched eagerly.  Per-kernel
+rows are graph-replayed too.  `roofline` is for the dominant kernel (the QKV projection at
 8192 tokens): its algorithmic FLOPs / its own average event-timed duration
 against the 2.5 PFLOP/s dense-bf16 peak.  `cpu_baseline` times the oracle's
 torch-CPU restatement of the same chain on a bounded token sample and scales
@@ -143,7 +145,7 @@ def kernel_table(c: Chain, dev, iters: int) -> dict:
     rows = {}
 
     def add(name, fn, nbytes, flops=0.0):
-        ms = time_fn(fn, iters)
+        ms = time_graph(fn, iters)
         gbs = nbytes / (ms * 1e-3) / 1e9
         row = {"us": round(ms * 1e3, 3), "bytes": int(nbytes), "gbs": round(gbs, 1),
                "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
@@ -165,13 +167,41 @@ def kernel_table(c: Chain, dev, iters: int) -> dict:
     return rows
 
 
+def time_graph(fn, iters: int, reps: int = 20) -> float:
+    """Average milliseconds per call of `fn` captured `reps` times into one HIP
+    graph and replayed: the GPU time of the kernels without Python launch gaps."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(3):
+            fn()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(reps):
+            fn()
+    graph.replay()
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    n = max(1, iters // reps)
+    s.record()
+    for _ in range(n):
+        graph.replay()
+    e.record()
+    torch.cuda.synchronize()
+    return s.elapsed_time(e) / (n * reps)
+
+
 def time_cold(fn, iters: int, flush: torch.Tensor) -> float:
     """Average milliseconds per call with the 256 MB Infinity Cache flushed
-    (512 MB written) before each call; each call is bracketed by its own events."""
+    before each call by reading a 512 MB buffer (a read leaves no dirty lines
+    whose write-back would overlap the timed call); each call is bracketed by
+    its own events."""
     fn()
+    sink = torch.empty((), device=flush.device)
     pairs = []
     for _ in range(iters):
-        flush.zero_()
+        torch.sum(flush, dim=0, out=sink)
         s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         s.record()
         fn()
@@ -197,6 +227,10 @@ def cold_decode_table(dev, t: int, iters: int) -> dict:
         out[name] = {"us": round(ms * 1e3, 3), "gbs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
     del c, flush
     return out
+
+
+def chain_graph_us(c: Chain, steps: int) -> float:
+    return time_graph(c.step, steps) * 1e3
 
 
 def chain_us(c: Chain, steps: int, warmup: int) -> float:
@@ -304,14 +338,16 @@ def main(argv=None) -> int:
         return profile_one(args.kernel, args.tokens, args.steps, dev)
 
     prefill = Chain(args.tokens, dev)
-    us = chain_us(prefill, args.steps, args.warmup)
+    us_eager = chain_us(prefill, args.steps, args.warmup)
+    us = chain_graph_us(prefill, args.steps)
     kp = kernel_table(prefill, dev, max(10, args.steps))
     proj = kp["qkv_projection_rope"]
     del prefill
     torch.cuda.empty_cache()
 
     decode = Chain(args.decode_tokens, dev)
-    us_dec = chain_us(decode, max(args.steps, 100), args.warmup)
+    us_dec_eager = chain_us(decode, max(args.steps, 100), args.warmup)
+    us_dec = chain_graph_us(decode, max(args.steps, 100))
     kd = kernel_table(decode, dev, max(50, args.steps))
     del decode
     torch.cuda.empty_cache()
@@ -341,7 +377,9 @@ def main(argv=None) -> int:
                      "frac": proj["mfma_frac"],
                      "traffic": read_traffic(f"traffic_qkv_projection_llama3_8b_t{args.tokens}")},
         "kernels_prefill": kp,
+        "eager_us_per_layer": round(us_eager, 2),
         "decode": {"tokens": args.decode_tokens, "us_per_layer": round(us_dec, 2),
+                   "eager_us_per_layer": round(us_dec_eager, 2),
                    "kernels_warm": kd, "kernels_cold": cold},
     }
     if not args.no_cpu:

@@ -542,6 +542,148 @@ __global__ __launch_bounds__(256) void qkv_splitk_kernel(SplitArgs s) {
     }
 }
 
+// ============================================================= decode
+// T <= 64 tokens.  Pure weight streaming: a workgroup (4 waves) owns 32*4 = 128
+// output columns and a K slice of KC_MAX or fewer, and issues its whole slice
+// at once.  The operand rows go by DMA into LDS (16-byte granules XOR-swizzled
+// by row so the 16-row MFMA fragment reads are conflict-free).  The weight rows
+// go to registers laid out 8 lanes per row, so each load instruction covers 8
+// full 128-byte lines (the MFMA fragment layout, 16 rows x 64 bytes per
+// instruction, streams about 1.2x slower at this shape); each 64-deep K segment is
+// then turned into B fragments through a 4 KiB wave-private LDS area and fed to
+// 16x16x32 MFMAs.  The split writes an fp32 partial tile.  (Nontemporal weight
+// loads stream faster back to back but slow the kernel by a third once the
+// reduction kernel has read the partial tiles in between, so they are not used.)
+struct DecodeArgs {
+  const uint16_t* a;  // operand [m, k] (row stride k)
+  const uint16_t* w;  // weight [n, k]
+  int64_t m, n, k, ldw;
+  float* part;        // [splits, m, n]
+};
+
+constexpr int KC_MAX = 512;  // deepest K slice per split (8 segments of 64)
+
+typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
+
+// 16-byte weight load returned through a plain vector value: loading straight
+// into the uint4 array member makes the compiler keep the whole array in scratch.
+__device__ __forceinline__ uint4 load16(const uint16_t* p) {
+  const u32x4_t t = *reinterpret_cast<const u32x4_t*>(p);
+  return make_uint4(t.x, t.y, t.z, t.w);
+}
+
+// staging slot of (row r, granule g) in a 32-row x 8-granule block: rows r and
+// r+8 share bank groups, so the granule is XORed with r/2 -- conflict-free for
+// the 8-lanes-per-row writes and for the 16-rows-per-granule fragment reads.
+__device__ __forceinline__ int wslot(int r, int g) { return r * 8 + (g ^ ((r >> 1) & 7)); }
+
+// KS: 64-deep K segments per split (every split has exactly KS; the host picks
+// KS dividing k / 64), fixed at compile time so the weight loads carry no
+// branches and each segment waits only for its own four loads.
+template <int MT, int KS, bool BF16>
+__global__ __launch_bounds__(256) void qkv_decode_kernel(DecodeArgs d) {
+  static_assert(KS >= 1 && KS * 64 <= KC_MAX, "segments per split");
+  constexpr int GPR = KC_MAX / 8;      // 16-byte granules per LDS operand row (row pitch 1 KiB)
+  __shared__ uint4 abuf[64 * GPR];     // 64 rows x KC_MAX bf16 = 64 KiB
+  __shared__ uint4 wst[4][32 * 8];     // per wave: 32 weight rows x 64 bf16 = 4 KiB
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * 128 + wid * 32;
+  const int64_t k0 = static_cast<int64_t>(blockIdx.y) * (KS * 64);
+  const int lr = lane & 15, lq = lane >> 4;
+  constexpr int gpr = KS * 8;  // granules per operand row actually used
+
+  // 1. operand slice -> LDS, one 1 KiB DMA per row (KC_MAX = 512 bf16): lane i
+  //    fills physical granule slot i of row r, which holds logical granule
+  //    G = (i & ~15) | ((i & 15) ^ (r & 15)); lanes with G past the slice are
+  //    masked off.
+  {
+    static_assert(GPR == 64, "one wave-wide DMA per operand row");
+    const uint32_t lbase = lds_addr(abuf);
+    const uint16_t* abase = d.a + k0;
+    for (int row = wid; row < d.m; row += 4) {
+      const int g = (lane & ~15) | ((lane & 15) ^ (row & 15));
+      if (g < gpr) {
+        dma16(abase, static_cast<uint32_t>((static_cast<int64_t>(row) * d.k + g * 8) * 2),
+              lbase + row * 1024);
+      }
+    }
+  }
+  // 2. weight slice -> registers: lane holds row 8i + lane/8, granule lane%8 of
+  //    every 64-deep segment (rows past n re-read row n-1; those columns are
+  //    never stored)
+  uint4 wr[KS][4];
+  const int wrow_l = lane >> 3, wg_l = lane & 7;
+  {
+    const uint16_t* wrow[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) wrow[i] = d.w + min(n0 + i * 8 + wrow_l, d.n - 1) * d.ldw + k0 + wg_l * 8;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) wr[ks][i] = load16(wrow[i] + ks * 64);
+  }
+  // the operand DMAs were issued before the 4 * KS weight loads and loads
+  // complete in order: vmcnt(4 KS) means the DMAs have landed
+  // (gfx9 s_waitcnt encoding: vmcnt[3:0], expcnt[6:4], lgkmcnt[11:8], vmcnt[5:4] in [15:14])
+  constexpr int kVm = 4 * KS;
+  __builtin_amdgcn_s_waitcnt((kVm & 15) | (7 << 4) | (15 << 8) | ((kVm >> 4) << 14));
+  __syncthreads();
+
+  // 3. per segment: registers -> staging -> B fragments, then MFMAs.  The
+  //    staging area is private to the wave and LDS executes a wave's accesses
+  //    in order, so only compiler ordering is needed between the phases.
+  f32x4_t acc[MT][2];
+#pragma unroll
+  for (int i = 0; i < MT; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = f32x4_t{};
+  uint4* ws = wst[wid];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+    {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) ws[wslot(i * 8 + wrow_l, wg_l)] = wr[ks][i];
+      asm volatile("" ::: "memory");
+      uint4 wf[2][2], af[MT][2];
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) wf[j][h] = ws[wslot(j * 16 + lr, h * 4 + lq)];
+#pragma unroll
+      for (int i = 0; i < MT; ++i) {
+        const int row = i * 16 + lr;
+        const int g0 = ks * 8 + lq, g1 = g0 + 4;  // this lane's two logical granules
+        af[i][0] = abuf[row * GPR + ((g0 & ~15) | ((g0 & 15) ^ (row & 15)))];
+        af[i][1] = abuf[row * GPR + ((g1 & ~15) | ((g1 & 15) ^ (row & 15)))];
+      }
+      asm volatile("" ::: "memory");
+#pragma unroll
+      for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          acc[i][j] = mfma16<BF16>(af[i][0], wf[j][0], acc[i][j]);
+          acc[i][j] = mfma16<BF16>(af[i][1], wf[j][1], acc[i][j]);
+        }
+    }
+  }
+  // 4. partial tile: 16x16 layout, lane holds column (lane & 15), rows 4*(lane/16) + v
+  float* dst = d.part + static_cast<int64_t>(blockIdx.y) * d.m * d.n;
+#pragma unroll
+  for (int i = 0; i < MT; ++i)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int64_t row = i * 16 + lq * 4 + v;
+      if (row >= d.m) continue;
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int64_t col = n0 + j * 16 + lr;
+        if (col < d.n) dst[row * d.n + col] = acc[i][j][v];
+      }
+    }
+}
+
 // ============================================== reduction + row epilogue
 // One wave per (token, head).  v = sum over splits of part[s, t, col] (+bias),
 // then the same rounding / norm / RoPE chain as the in-register epilogue.
@@ -564,11 +706,23 @@ __global__ __launch_bounds__(256) void qkv_epilogue_kernel(const float* part, in
     const int64_t j = lane + 64 * p;
     x1[p] = x2[p] = 0.f;
     if (j < half) {
+      // issue the loads of all splits before summing (latency, not bandwidth, bound)
       float s1 = 0.f, s2 = 0.f;
-      for (int64_t sp = 0; sp < splits; ++sp) {
-        const float* pr = part + (sp * m + t) * e.n + base;
-        s1 += pr[j];
-        s2 += pr[half + j];
+      const float* pr = part + t * e.n + base;
+      const int64_t stride = m * e.n;
+      for (int64_t sp0 = 0; sp0 < splits; sp0 += 8) {
+        float v1[8], v2[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const bool in = sp0 + u < splits;
+          v1[u] = in ? pr[(sp0 + u) * stride + j] : 0.f;
+          v2[u] = in ? pr[(sp0 + u) * stride + half + j] : 0.f;
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          s1 += v1[u];
+          s2 += v2[u];
+        }
       }
       if (e.bias) {
         s1 += load_any(e.bias, e.bias_dtype, base + j);
@@ -628,6 +782,8 @@ struct QkvPlan {
   int64_t splits;
   int64_t kchunk;
   bool fused_epi;  // prefill: in-register epilogue
+  bool stream;     // decode: weight-streaming kernel (k % 64 == 0)
+  int ks;          // decode stream: 64-deep K segments per split
   int64_t operand_bytes;
   int64_t part_bytes;
 };
@@ -640,17 +796,33 @@ static QkvPlan make_plan(int64_t m, int64_t n, int64_t k, int64_t hd) {
   if (m <= 64) {
     p.decode = true;
     p.mt = static_cast<int>(cdiv(m, 16));
-    // Column tile per workgroup: 4 waves x cpw x 16 columns.
-    p.cpw = m > 16 ? 1 : 2;
-    const int64_t ntile = cdiv(n, 4 * 16 * p.cpw);
-    // Split K until about 512 workgroups are in flight, but keep the fp32
-    // partial traffic (2 * splits * m * n * 4 bytes) small next to the weight
-    // stream (n * k * 2 bytes): splits <= k / (32 m) bounds it at 1/4.
-    int64_t splits = std::max<int64_t>(1, cdiv(512, ntile));
-    splits = std::min<int64_t>(splits, std::max<int64_t>(1, k / 128));
-    splits = std::min<int64_t>(splits, std::max<int64_t>(1, k / (32 * m)));
-    p.kchunk = cdiv(cdiv(k, splits), 64) * 64;
-    p.splits = cdiv(k, p.kchunk);
+    p.stream = k % 64 == 0;
+    if (p.stream) {
+      // 128 columns per workgroup; K split into equal slices of ks segments (ks
+      // divides k / 64, at most 8): the deepest slice that still gives one
+      // workgroup per CU (256), since every extra split adds an fp32 partial
+      // tile (m x n x 4 bytes) to write and reduce.
+      const int64_t segs = k / 64, ntile = cdiv(n, 128);
+      int ks = 1;
+      for (int c = 8; c >= 1; --c)
+        if (segs % c == 0 && ntile * (segs / c) >= 256) { ks = c; break; }
+      p.ks = ks;
+      p.kchunk = 64 * ks;
+      p.splits = segs / ks;
+      p.cpw = 2;
+    } else {
+      // Column tile per workgroup: 4 waves x cpw x 16 columns.
+      p.cpw = m > 16 ? 1 : 2;
+      const int64_t ntile = cdiv(n, 4 * 16 * p.cpw);
+      // Split K until about 512 workgroups are in flight, but keep the fp32
+      // partial traffic (2 * splits * m * n * 4 bytes) small next to the weight
+      // stream (n * k * 2 bytes): splits <= k / (32 m) bounds it at 1/4.
+      int64_t splits = std::max<int64_t>(1, cdiv(512, ntile));
+      splits = std::min<int64_t>(splits, std::max<int64_t>(1, k / 128));
+      splits = std::min<int64_t>(splits, std::max<int64_t>(1, k / (32 * m)));
+      p.kchunk = cdiv(cdiv(k, splits), 64) * 64;
+      p.splits = cdiv(k, p.kchunk);
+    }
     p.part_bytes = align256(p.splits * m * n * 4);
   } else {
     p.decode = false;
@@ -672,8 +844,35 @@ static void launch_decode_cpw(const QkvPlan& p, const SplitArgs& s, hipStream_t 
   }
 }
 
+template <int MT, bool BF16>
+static void launch_stream(int ks, dim3 grid, const DecodeArgs& d, hipStream_t st) {
+  switch (ks) {
+    case 1: hipLaunchKernelGGL((qkv_decode_kernel<MT, 1, BF16>), grid, dim3(256), 0, st, d); break;
+    case 2: hipLaunchKernelGGL((qkv_decode_kernel<MT, 2, BF16>), grid, dim3(256), 0, st, d); break;
+    case 3: hipLaunchKernelGGL((qkv_decode_kernel<MT, 3, BF16>), grid, dim3(256), 0, st, d); break;
+    case 4: hipLaunchKernelGGL((qkv_decode_kernel<MT, 4, BF16>), grid, dim3(256), 0, st, d); break;
+    case 5: hipLaunchKernelGGL((qkv_decode_kernel<MT, 5, BF16>), grid, dim3(256), 0, st, d); break;
+    case 6: hipLaunchKernelGGL((qkv_decode_kernel<MT, 6, BF16>), grid, dim3(256), 0, st, d); break;
+    case 7: hipLaunchKernelGGL((qkv_decode_kernel<MT, 7, BF16>), grid, dim3(256), 0, st, d); break;
+    default: hipLaunchKernelGGL((qkv_decode_kernel<MT, 8, BF16>), grid, dim3(256), 0, st, d); break;
+  }
+}
+
 template <bool BF16>
 static void launch_decode(const QkvPlan& p, const SplitArgs& s, hipStream_t st) {
+  if (p.stream) {
+    DecodeArgs d{};
+    d.a = s.a; d.w = s.w; d.m = s.m; d.n = s.n; d.k = s.k; d.ldw = s.ldw;
+    d.part = s.part;
+    const dim3 grid(static_cast<unsigned>(cdiv(s.n, 128)), static_cast<unsigned>(p.splits));
+    switch (p.mt) {
+      case 1: launch_stream<1, BF16>(p.ks, grid, d, st); break;
+      case 2: launch_stream<2, BF16>(p.ks, grid, d, st); break;
+      case 3: launch_stream<3, BF16>(p.ks, grid, d, st); break;
+      default: launch_stream<4, BF16>(p.ks, grid, d, st); break;
+    }
+    return;
+  }
   if (p.cpw == 1) launch_decode_cpw<BF16, 1>(p, s, st);
   else launch_decode_cpw<BF16, 2>(p, s, st);
 }
@@ -744,6 +943,8 @@ extern "C" int bfa_qkv_projection(const void* operand, int64_t tokens, int64_t h
               (long long)qkv_dim, (long long)heads);
   const int64_t hd = qkv_dim / heads;
   BFA_REQUIRE(hidden % 16 == 0, "%s: hidden must be a multiple of 16 (got %lld)", what, (long long)hidden);
+  BFA_REQUIRE(w_stride >= hidden, "%s: weight row stride %lld < hidden %lld", what,
+              (long long)w_stride, (long long)hidden);
   BFA_REQUIRE(w_stride % 8 == 0 && aligned16(qkv_weight) && aligned16(operand),
               "%s: operand/weight rows must be 16-byte aligned", what);
   BFA_REQUIRE(cos_sin_cache == nullptr || (positions && (positions_dtype == BFA_DTYPE_I64 ||

@@ -80,6 +80,28 @@ def test_minimal_f32(t, h, hq, hkv, d):
         assert_close(got, exp, what="minimal_f32")
 
 
+@pytest.mark.parametrize("t,heads,h", [
+    (1, 3, 64),        # one 64-deep segment per split
+    (20, 4, 8192),     # 2 segments per split
+    (37, 8, 6144),     # 3
+    (64, 8, 8192),     # 4
+    (5, 16, 5120),     # 5
+    (20, 16, 6144),    # 6
+    (37, 16, 7168),    # 7
+    (64, 16, 8192),    # 8
+])
+def test_decode_split_depths(t, heads, h):
+    """Decode (T <= 64) weight-streaming path: the K slice per split is chosen from
+    k / 64 and the column-tile count; these shapes give every slice depth 1..8 and
+    every 16-token block count 1..4."""
+    hq, hkv, d = heads - 2, 1, 128
+    _, x, ln, w, _ = make(209, t, h, hq, hkv, d)
+    q, k, v = FusedRMSNormQKV.forward(x.to(DEV), ln.to(DEV), w.to(DEV), hq, hkv, eps=1e-6)
+    ref = R.split_qkv(R.qkv_production(x, ln, w, 1e-6), hq, hkv)
+    for got, exp, name in zip((q, k, v), ref, "qkv"):
+        assert_close(got, exp, what=f"decode {name} t={t} h={h}")
+
+
 def test_with_bias_reference_cases():
     """tests/test_qwen3_bias_handling.py and test_numerical_stability.py:237-294 on the HIP path."""
     g = gen(204)
