@@ -301,6 +301,15 @@ def profile_one(kernel: str, tokens: int, steps: int, dev) -> int:
     c = Chain(tokens, dev)
     st = QkvStages(c, dev)
     table = torch.empty(VOCAB, H, dtype=torch.bfloat16, device=dev) if kernel == "embedding" else None
+    if kernel == "copy":
+        # calibration for the HBM byte counters: a 512 MiB device-to-device copy
+        # reads and writes exactly 512 MiB
+        src = torch.empty(256 << 20, dtype=torch.bfloat16, device=dev).normal_()
+        dst = torch.empty_like(src)
+        ms = time_fn(lambda: dst.copy_(src), steps)
+        print(json.dumps({"kernel": "copy", "bytes_read": src.numel() * 2, "bytes_written": dst.numel() * 2,
+                          "calls": steps, "us": round(ms * 1e3, 3)}))
+        return 0
     fn = {"qkv_projection": st.projection, "qkv_operand": st.operand,
           "add_rms_norm": lambda: c.norm(c.x, c.residual), "silu_and_mul": lambda: c.silu(c.gate_up),
           "embedding": lambda: embedding(c.ids, table)}[kernel]
@@ -319,7 +328,7 @@ def main(argv=None) -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-cold", action="store_true", help="skip the cold-cache decode table")
     ap.add_argument("--kernel", choices=["qkv_projection", "qkv_operand", "add_rms_norm",
-                                         "silu_and_mul", "embedding"],
+                                         "silu_and_mul", "embedding", "copy"],
                     help="only run this kernel --steps times at --tokens (for profilers)")
     args = ap.parse_args(argv)
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -337,6 +346,10 @@ def main(argv=None) -> int:
     if args.kernel:
         return profile_one(args.kernel, args.tokens, args.steps, dev)
 
+    def progress(stage: str) -> None:
+        print(f"bench: {stage}", file=sys.stderr, flush=True)
+
+    progress(f"prefill chain, {args.tokens} tokens")
     prefill = Chain(args.tokens, dev)
     us_eager = chain_us(prefill, args.steps, args.warmup)
     us = chain_graph_us(prefill, args.steps)
@@ -345,6 +358,7 @@ def main(argv=None) -> int:
     del prefill
     torch.cuda.empty_cache()
 
+    progress(f"decode chain, {args.decode_tokens} tokens")
     decode = Chain(args.decode_tokens, dev)
     us_dec_eager = chain_us(decode, max(args.steps, 100), args.warmup)
     us_dec = chain_graph_us(decode, max(args.steps, 100))
@@ -383,6 +397,7 @@ def main(argv=None) -> int:
                    "kernels_warm": kd, "kernels_cold": cold},
     }
     if not args.no_cpu:
+        progress("CPU baseline")
         line["cpu_baseline"] = cpu_baseline(args.tokens)
     print(json.dumps(line))
     return 0
