@@ -145,14 +145,7 @@ def kernel_table(c: Chain, dev, iters: int) -> dict:
     rows = {}
 
     def add(name, fn, nbytes, flops=0.0):
-        ms = time_graph(fn, iters)
-        gbs = nbytes / (ms * 1e-3) / 1e9
-        row = {"us": round(ms * 1e3, 3), "bytes": int(nbytes), "gbs": round(gbs, 1),
-               "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
-        if flops:
-            tf = flops / (ms * 1e-3) / 1e12
-            row.update({"flops": flops, "tflops": round(tf, 1), "mfma_frac": round(tf / BF16_PEAK_TFLOPS, 4)})
-        rows[name] = row
+        rows[name] = _roof_row(time_graph(fn, iters), nbytes, flops)
 
     add("add_rms_norm", lambda: c.norm(c.x, c.residual), 4 * t * H * 2 + H * 2)
     add("qkv_operand_prepass", st.operand, 2 * t * H * 2 + H * 2)
@@ -165,6 +158,92 @@ def kernel_table(c: Chain, dev, iters: int) -> dict:
     add("embedding_gather", lambda: embedding(c.ids, table), 2 * t * H * 2 + 8 * t)
     del table
     return rows
+
+
+def _roof_row(ms: float, nbytes: float, flops: float = 0.0) -> dict:
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    row = {"us": round(ms * 1e3, 3), "bytes": int(nbytes), "gbs": round(gbs, 1),
+           "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
+    if flops:
+        tf = flops / (ms * 1e-3) / 1e12
+        row.update({"flops": flops, "tflops": round(tf, 1), "mfma_frac": round(tf / BF16_PEAK_TFLOPS, 4)})
+    return row
+
+
+def config_cases(dev) -> list:
+    """The path's other workloads as (name, fn, algorithmic bytes, FLOPs), inputs
+    drawn per configuration (seeds 1-4, CPU generator, fp32 then bf16):
+      rmsnorm     TinyLlama RMSNorm, x [128, 2048], eps 1e-5
+      tinyllama   fused RMSNorm+QKV(2048 -> 2560, 32/4 heads, D 64)+RoPE(theta 1e4), T 1/8/512
+      qwen3       fused RMSNorm+QKV(1024 -> 4096, 16/8 heads, D 128)+q/k norm+RoPE(theta 1e6), T 1/2048
+      rerotate    paged K [256 pages, 2, 8, 16, 128] in shuffled page order, 16 chunks of
+                  16 pages, delta U[-4096, 4096], theta 1e6, rotated copy out
+      swiglu      SiLU*mul [2048, 2 x 3072]"""
+    from braidinfer_amd.layers import llama_attention_input, qwen3_attention_input, rerotate_paged_k
+    bf = torch.bfloat16
+    cases = []
+
+    def gen(seed):
+        g = torch.Generator().manual_seed(seed)
+
+        def randn(*shape, std=1.0, mean=0.0):
+            return (torch.randn(*shape, generator=g) * std + mean).to(bf).to(dev)
+        return g, randn
+
+    g, randn = gen(1)
+    x = randn(128, 2048)
+    norm = RMSNorm(2048, eps=1e-5).to(dev)
+    with torch.no_grad():
+        norm.weight.data = randn(2048, std=0.1, mean=1.0)
+    cases.append(("rmsnorm_t128_h2048", lambda: norm(x), 2 * 128 * 2048 * 2 + 2048 * 2, 0.0))
+
+    def tiny(t, h=2048, hq=32, hkv=4, d=64):
+        n = (hq + 2 * hkv) * d
+        xt, ln, w = randn(t, h), randn(h, std=0.1, mean=1.0), randn(n, h, std=0.02)
+        pos = torch.randint(0, 2048, (t,), generator=g).to(dev)
+        cache = rope_table(d, 2048, 1e4).to(dev)
+        return (f"tinyllama_qkv_rope_t{t}", lambda: llama_attention_input(xt, ln, w, hq, hkv, 1e-5, pos, cache),
+                t * h * 2 + h * 2 + n * h * 2 + t * n * 2 + t * 8 + t * d * 4, 2.0 * t * h * n)
+
+    g, randn = gen(2)
+    cases += [tiny(t) for t in (1, 8, 512)]
+
+    def qwen(t, h=1024, hq=16, hkv=8, d=128):
+        n = (hq + 2 * hkv) * d
+        xt, w, ln = randn(t, h), randn(n, h, std=0.02), randn(h, std=0.1, mean=1.0)
+        qn = randn(d, std=0.1, mean=1.0)
+        kn = torch.exp(torch.empty(d).uniform_(-2.995732, 4.605170, generator=g)).to(bf).to(dev)
+        pos = torch.randint(0, 2048, (t,), generator=g).to(dev)
+        cache = rope_table(d, 40960, 1e6).to(dev)
+        return (f"qwen3_qkv_qknorm_rope_t{t}",
+                lambda: qwen3_attention_input(xt, ln, w, None, hq, hkv, 1e-6, pos, cache, qn, kn),
+                t * h * 2 + h * 2 + n * h * 2 + t * n * 2 + t * 8 + t * d * 4 + 2 * d * 2, 2.0 * t * h * n)
+
+    g, randn = gen(3)
+    cases += [qwen(t) for t in (1, 2048)]
+
+    g, randn = gen(4)
+    pages, hkv, ps, d = 256, 8, 16, 128
+    kv = randn(pages, 2, hkv, ps, d)
+    page_idx = torch.randperm(pages, generator=g).to(torch.int32).to(dev)
+    indptr = (torch.arange(17, dtype=torch.int32) * 16).to(dev)
+    delta = torch.randint(-4096, 4097, (16,), generator=g).to(dev)
+    last = torch.full((16,), ps, dtype=torch.int32, device=dev)
+    rcache = rope_table(d, 40960, 1e6).to(dev)
+    rout = torch.empty(pages, ps, hkv, d, dtype=bf, device=dev)
+    cases.append(("rerotate_paged_k_4096tok",
+                  lambda: rerotate_paged_k(kv, page_idx, indptr, delta, last, rcache, out=rout),
+                  2 * pages * ps * hkv * d * 2, 0.0))
+    gu = randn(2048, 2 * 3072)
+    silu = SiluAndMul()
+    cases.append(("swiglu_t2048_i3072", lambda: silu(gu), 3 * 2048 * 3072 * 2, 0.0))
+    return cases
+
+
+def config_table(dev, iters: int) -> dict:
+    """Each case of config_cases graph-timed, with its roofline fractions."""
+    return {name: _roof_row(time_graph(fn, iters), nbytes, flops)
+            for name, fn, nbytes, flops in config_cases(dev)}
 
 
 def time_graph(fn, iters: int, reps: int = 20) -> float:
@@ -297,7 +376,13 @@ def read_traffic(name: str):
 
 
 def profile_one(kernel: str, tokens: int, steps: int, dev) -> int:
-    """Runs one kernel `steps` times on the chain's inputs; prints its event-timed average."""
+    """Runs one kernel `steps` times on the chain's inputs (or one case of
+    config_cases by name); prints its event-timed average."""
+    cases = {name: fn for name, fn, _, _ in config_cases(dev)} if kernel.startswith("case:") else {}
+    if cases:
+        ms = time_fn(cases[kernel[5:]], steps)
+        print(json.dumps({"kernel": kernel, "calls": steps, "us": round(ms * 1e3, 3)}))
+        return 0
     c = Chain(tokens, dev)
     st = QkvStages(c, dev)
     table = torch.empty(VOCAB, H, dtype=torch.bfloat16, device=dev) if kernel == "embedding" else None
@@ -327,9 +412,9 @@ def main(argv=None) -> int:
     ap.add_argument("--decode-tokens", type=int, default=64)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-cold", action="store_true", help="skip the cold-cache decode table")
-    ap.add_argument("--kernel", choices=["qkv_projection", "qkv_operand", "add_rms_norm",
-                                         "silu_and_mul", "embedding", "copy"],
-                    help="only run this kernel --steps times at --tokens (for profilers)")
+    ap.add_argument("--kernel", help="only run this kernel --steps times at --tokens (for "
+                    "profilers): qkv_projection, qkv_operand, add_rms_norm, silu_and_mul, "
+                    "embedding, copy, or case:<name> for a case of the configuration table")
     args = ap.parse_args(argv)
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus > 1 or world > 1:
@@ -366,6 +451,8 @@ def main(argv=None) -> int:
     del decode
     torch.cuda.empty_cache()
     cold = None if args.no_cold else cold_decode_table(dev, args.decode_tokens, 48)
+    progress("other configurations")
+    configs = config_table(dev, max(40, args.steps))
     _lib.check_device_status(dev)
 
     line = {
@@ -395,6 +482,7 @@ def main(argv=None) -> int:
         "decode": {"tokens": args.decode_tokens, "us_per_layer": round(us_dec, 2),
                    "eager_us_per_layer": round(us_dec_eager, 2),
                    "kernels_warm": kd, "kernels_cold": cold},
+        "configs": configs,
     }
     if not args.no_cpu:
         progress("CPU baseline")

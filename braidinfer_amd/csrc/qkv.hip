@@ -140,8 +140,11 @@ struct GemmArgs {
 enum { EPI_RAW = 0, EPI_FUSED = 1 };
 
 // LDS tile rows are 64 elements = 8 granules of 16 bytes; granule g of row r is
-// stored at slot g ^ (r & 7).
-__device__ __forceinline__ int swz(int r, int g) { return r * 8 + (g ^ (r & 7)); }
+// stored at slot g ^ ((r / 2) & 7).  A 16-lane phase of a ds_read_b128 fragment
+// load reads one granule of 16 consecutive rows: rows r and r + 1 sit in
+// different halves of a 256-byte bank line and r / 2 spreads the eight pairs
+// over all eight 16-byte slots, so the 16 reads hit 16 distinct bank groups.
+__device__ __forceinline__ int swz(int r, int g) { return r * 8 + (g ^ ((r >> 1) & 7)); }
 
 // Loads the MFMA fragments of K sub-step ks (16 deep) from an LDS tile buffer.
 template <int MB, int NB, int BM, int WM, int WN>
@@ -233,8 +236,12 @@ __global__ __launch_bounds__(256) void qkv_gemm_kernel(GemmArgs g, QkvEpi e) {
   static_assert((BM / WM) * NWN == 4, "four waves per workgroup");
   constexpr int MB = WM / 32, NB = WN / 32;
   constexpr int AG = BM / 32, BG = BN / 32;  // 16-byte granules per thread per K tile
-  __shared__ uint4 lds0[(BM + BN) * 8];
-  __shared__ uint4 lds1[(BM + BN) * 8];
+  // Each buffer holds one 64-deep K tile of both operands, and later the fused
+  // epilogue's staging of two waves' 32-row blocks (row stride LDR floats).
+  constexpr int LDR = 136;
+  constexpr int LDS_U4 = (BM + BN) * 8 > 2 * 32 * LDR / 4 ? (BM + BN) * 8 : 2 * 32 * LDR / 4;
+  __shared__ uint4 lds0[LDS_U4];
+  __shared__ uint4 lds1[LDS_U4];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
@@ -270,9 +277,10 @@ __global__ __launch_bounds__(256) void qkv_gemm_kernel(GemmArgs g, QkvEpi e) {
   // 16-deep K sub-steps so every ds_read overlaps the previous sub-step's MFMAs.
   if constexpr (DIRECT) {
     // Each wave fills 1 KiB blocks of 8 tile rows (block b = 4 i + wid): lane l
-    // lands at physical slot l % 8 of row l / 8 and therefore fetches logical
-    // granule (l % 8) ^ (l / 8), which realises the XOR swizzle of swz().
-    const int lrow = lane >> 3, lgran = (lane & 7) ^ (lane >> 3);
+    // lands at physical slot l % 8 of tile row 8 b + l / 8 and therefore fetches
+    // logical granule (l % 8) ^ ((8 b + l / 8) / 2 % 8) = (l % 8) ^ ((4 (wid % 2)
+    // + l / 16) % 8), which realises the XOR swizzle of swz().
+    const int lrow = lane >> 3, lgran = (lane & 7) ^ ((4 * (wid & 1) + (lane >> 4)) & 7);
     uint32_t aoff[AG], boff[BG];
 #pragma unroll
     for (int i = 0; i < AG; ++i)
@@ -386,10 +394,9 @@ __global__ __launch_bounds__(256) void qkv_gemm_kernel(GemmArgs g, QkvEpi e) {
     // owning 4 RoPE pairs (columns j..j+3 and j+D/2..j+D/2+3 of one head), so
     // the q/k norm is a butterfly over the D/8 lanes of a head and every store
     // is a contiguous 4-element vector.
-    constexpr int LDR = 136;  // padded row stride (floats)
     constexpr int LH = HD / 8;  // lanes per head
     float* et = reinterpret_cast<float*>(wid < 2 ? lds0 : lds1) + (wid & 1) * (32 * LDR);
-    static_assert(2 * 32 * LDR * 4 <= (BM + BN) * 8 * 16, "epilogue staging fits one buffer");
+    static_assert(2 * 32 * LDR * 4 <= LDS_U4 * 16, "epilogue staging fits one buffer");
     const int l16 = lane & 15, rg = lane >> 4;
     const int hloc = l16 / LH, q = l16 % LH;
     const int c1 = hloc * HD + q * 4, c2 = c1 + HD / 2;  // columns inside the wave tile
@@ -782,6 +789,7 @@ struct QkvPlan {
   int64_t splits;
   int64_t kchunk;
   bool fused_epi;  // prefill: in-register epilogue
+  int tile;        // prefill: 256 (256x256, one workgroup per CU) or 128 (128x128, two per CU)
   bool stream;     // decode: weight-streaming kernel (k % 64 == 0)
   int ks;          // decode stream: 64-deep K segments per split
   int64_t operand_bytes;
@@ -827,6 +835,9 @@ static QkvPlan make_plan(int64_t m, int64_t n, int64_t k, int64_t hd) {
   } else {
     p.decode = false;
     p.fused_epi = (hd == 32 || hd == 64 || hd == 128) && n % hd == 0;
+    // 256x256 tiles (the most MFMA work per LDS byte) once they give two
+    // workgroups per CU; below that, 128x128 tiles so that more CUs take part.
+    p.tile = cdiv(m, 256) * cdiv(n, 256) >= 512 ? 256 : 128;
     p.splits = 1;
     p.part_bytes = p.fused_epi ? 0 : align256(m * n * 4);
   }
@@ -877,22 +888,29 @@ static void launch_decode(const QkvPlan& p, const SplitArgs& s, hipStream_t st) 
   else launch_decode_cpw<BF16, 2>(p, s, st);
 }
 
-template <bool BF16, bool DIRECT>
-static void launch_prefill_t(const QkvPlan& p, const GemmArgs& g, const QkvEpi& e, hipStream_t st) {
-  const unsigned grid = static_cast<unsigned>(cdiv(g.m, 256) * cdiv(g.n, 256));
+// BM x BN tile, waves of WM x 128 (the fused epilogue needs 128-column waves).
+template <int BM, int BN, int WM, bool BF16, bool DIRECT>
+static void launch_prefill_tile(const QkvPlan& p, const GemmArgs& g, const QkvEpi& e, hipStream_t st) {
+  const unsigned grid = static_cast<unsigned>(cdiv(g.m, BM) * cdiv(g.n, BN));
   if (!p.fused_epi) {
-    hipLaunchKernelGGL((qkv_gemm_kernel<256, 256, 128, 128, BF16, EPI_RAW, 128, DIRECT>), dim3(grid),
+    hipLaunchKernelGGL((qkv_gemm_kernel<BM, BN, WM, 128, BF16, EPI_RAW, 128, DIRECT>), dim3(grid),
                        dim3(256), 0, st, g, e);
   } else if (e.hd == 128) {
-    hipLaunchKernelGGL((qkv_gemm_kernel<256, 256, 128, 128, BF16, EPI_FUSED, 128, DIRECT>),
+    hipLaunchKernelGGL((qkv_gemm_kernel<BM, BN, WM, 128, BF16, EPI_FUSED, 128, DIRECT>),
                        dim3(grid), dim3(256), 0, st, g, e);
   } else if (e.hd == 64) {
-    hipLaunchKernelGGL((qkv_gemm_kernel<256, 256, 128, 128, BF16, EPI_FUSED, 64, DIRECT>),
+    hipLaunchKernelGGL((qkv_gemm_kernel<BM, BN, WM, 128, BF16, EPI_FUSED, 64, DIRECT>),
                        dim3(grid), dim3(256), 0, st, g, e);
   } else {
-    hipLaunchKernelGGL((qkv_gemm_kernel<256, 256, 128, 128, BF16, EPI_FUSED, 32, DIRECT>),
+    hipLaunchKernelGGL((qkv_gemm_kernel<BM, BN, WM, 128, BF16, EPI_FUSED, 32, DIRECT>),
                        dim3(grid), dim3(256), 0, st, g, e);
   }
+}
+
+template <bool BF16, bool DIRECT>
+static void launch_prefill_t(const QkvPlan& p, const GemmArgs& g, const QkvEpi& e, hipStream_t st) {
+  if (p.tile == 256) launch_prefill_tile<256, 256, 128, BF16, DIRECT>(p, g, e, st);
+  else launch_prefill_tile<128, 128, 32, BF16, DIRECT>(p, g, e, st);
 }
 
 template <bool BF16>

@@ -188,6 +188,19 @@ def test_llama_chain(t, h, hq, hkv, d, base, maxp):
     assert_close(v, rv, what="llama v")
 
 
+def test_prefill_raw_epilogue_256_tiles():
+    """head_dim 80 at 8192 tokens: 256x256 tiles with the raw fp32 store and the
+    row epilogue kernel (the fused epilogue covers head_dim 32/64/128 only)."""
+    t, h, hq, hkv, d = 8192, 256, 48, 4, 80
+    g, x, ln, w, _ = make(210, t, h, hq, hkv, d)
+    rows = torch.cat([torch.arange(0, 4), torch.randint(0, t, (60,), generator=g), torch.arange(t - 4, t)])
+    q, k, v = FusedRMSNormQKV.forward(x.to(DEV), ln.to(DEV), w.to(DEV), hq, hkv, eps=1e-6)
+    ref = R.split_qkv(R.qkv_production(x[rows], ln, w, 1e-6), hq, hkv)
+    rd = rows.to(DEV)
+    for got, exp, name in zip((q, k, v), ref, "qkv"):
+        assert_close(got[rd], exp, what=f"raw 256-tile {name}")
+
+
 @pytest.mark.parametrize("chain", ["llama", "qwen3"])
 def test_prefill_8192_sampled_rows(chain):
     """Llama-3-8B / Qwen3 prefill shapes at full size; the oracle checks a row sample."""
