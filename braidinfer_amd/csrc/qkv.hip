@@ -30,6 +30,8 @@
 //  * qkv_epilogue_kernel sums the split-K partials (or reads the raw fp32
 //    projection for head_dim the in-register epilogue does not cover) and
 //    applies bias / q-k norm / RoPE / rounding per (token, head) row.
+#include <cstdlib>
+
 #include "bfa_device.h"
 #include "bfa_host.h"
 #include "bfa_internal.h"
@@ -186,6 +188,53 @@ __device__ __forceinline__ void dma16(const void* base, uint32_t voff, uint32_t 
 
 __device__ __forceinline__ void wait_vmem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
+// s_waitcnt vmcnt(N) for a compile-time N, other counters untouched
+// (gfx9 encoding: vmcnt[3:0], expcnt[6:4], lgkmcnt[11:8], vmcnt[5:4] in [15:14]).
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+// 32-deep K stages (DMA path): rows of 4 granules of 16 bytes; granule g of row
+// r sits at slot g ^ ((r / 4) & 3), so a 16-lane phase of a fragment read (one
+// granule of 16 consecutive rows) hits 16 distinct bank groups.
+__device__ __forceinline__ int sw32(int r, int g) { return r * 4 + (g ^ ((r >> 2) & 3)); }
+
+template <int MB, int NB, int BM, int WM, int WN>
+__device__ __forceinline__ void load_frags32(const uint4* st, int ks, int wm, int wn, int frow,
+                                             int fhalf, uint4 (&af)[MB], uint4 (&bf)[NB]) {
+  const int gsel = ks * 2 + fhalf;
+#pragma unroll
+  for (int i = 0; i < MB; ++i) af[i] = st[sw32(wm * WM + i * 32 + frow, gsel)];
+#pragma unroll
+  for (int j = 0; j < NB; ++j) bf[j] = st[BM * 4 + sw32(wn * WN + j * 32 + frow, gsel)];
+}
+
+// One 32-deep stage of both operands by DMA: each wave moves 1 KiB blocks of 16
+// rows (block b = 4 i + wid; the wave's block offset is folded into lstage).
+template <int ADPW, int BDPW, int BM>
+__device__ __forceinline__ void issue_stage(const uint16_t* a, const uint16_t* w, int64_t kt,
+                                            const uint32_t (&aoff)[ADPW],
+                                            const uint32_t (&boff)[BDPW], uint32_t lstage) {
+  const uint16_t* ak = a + kt * 32;
+  const uint16_t* wk = w + kt * 32;
+#pragma unroll
+  for (int i = 0; i < ADPW; ++i) dma16(ak, aoff[i], lstage + i * 4096);
+#pragma unroll
+  for (int i = 0; i < BDPW; ++i) dma16(wk, boff[i], lstage + BM * 64 + i * 4096);
+}
+
+// Waits until at most `later` (< NS) stages of DPW DMAs each are still in flight.
+template <int DPW, int NS>
+__device__ __forceinline__ void wait_stages(int64_t later) {
+  static_assert(NS >= 2 && NS <= 4, "cases below cover up to 3 later stages");
+  if (NS > 3 && later >= 3) wait_vm<(NS > 3 ? 3 : 0) * DPW>();
+  else if (NS > 2 && later >= 2) wait_vm<(NS > 2 ? 2 : 0) * DPW>();
+  else if (later >= 1) wait_vm<DPW>();
+  else wait_vm<0>();
+}
+
 // First three 16-deep K sub-steps of a tile (fragments of sub-step 0 are in
 // fa0/fb0 on entry; sub-step 3's are left in fa1/fb1 for the caller).
 template <int MB, int NB, int BM, int WM, int WN, bool BF16>
@@ -230,18 +279,25 @@ __device__ __forceinline__ void tile_store(uint4* buf, int gr, int gg, const uin
 
 // DIRECT: tiles go HBM -> LDS by DMA (K % 64 == 0, 16-byte aligned rows,
 // byte offsets below 4 GiB); otherwise HBM -> registers -> LDS with K masking.
-template <int BM, int BN, int WM, int WN, bool BF16, int EPI, int HD, bool DIRECT>
-__global__ __launch_bounds__(256) void qkv_gemm_kernel(GemmArgs g, QkvEpi e) {
+// Wave tiles of at most 64x128 (128 accumulator registers) are compiled for two
+// waves per SIMD, so two workgroups share a CU.
+template <int BM, int BN, int WM, int WN, bool BF16, int EPI, int HD, bool DIRECT, int NS>
+__global__ __launch_bounds__(256, (WM * WN <= 8192 ? 2 : 1)) void qkv_gemm_kernel(GemmArgs g, QkvEpi e) {
   constexpr int NWN = BN / WN;
   static_assert((BM / WM) * NWN == 4, "four waves per workgroup");
   constexpr int MB = WM / 32, NB = WN / 32;
   constexpr int AG = BM / 32, BG = BN / 32;  // 16-byte granules per thread per K tile
-  // Each buffer holds one 64-deep K tile of both operands, and later the fused
-  // epilogue's staging of two waves' 32-row blocks (row stride LDR floats).
+  // LDS: the DMA path keeps a ring of NS 32-deep stages of both operands; the
+  // register path two 64-deep buffers; afterwards the fused epilogue stages
+  // each wave's 32-row accumulator blocks (row stride LDR floats).
   constexpr int LDR = 136;
-  constexpr int LDS_U4 = (BM + BN) * 8 > 2 * 32 * LDR / 4 ? (BM + BN) * 8 : 2 * 32 * LDR / 4;
-  __shared__ uint4 lds0[LDS_U4];
-  __shared__ uint4 lds1[LDS_U4];
+  constexpr int STAGE_U4 = (BM + BN) * 4;
+  constexpr int EPI_U4 = 4 * 32 * LDR / 4;
+  constexpr int MAIN_U4 = DIRECT ? NS * STAGE_U4 : 2 * (BM + BN) * 8;
+  constexpr int LDS_U4 = MAIN_U4 > EPI_U4 ? MAIN_U4 : EPI_U4;
+  __shared__ uint4 lds[LDS_U4];
+  uint4* const lds0 = lds;
+  uint4* const lds1 = lds + (BM + BN) * 8;
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
@@ -276,52 +332,54 @@ __global__ __launch_bounds__(256) void qkv_gemm_kernel(GemmArgs g, QkvEpi e) {
   // LDS buffer after them; MFMA fragments are double-buffered across the four
   // 16-deep K sub-steps so every ds_read overlaps the previous sub-step's MFMAs.
   if constexpr (DIRECT) {
-    // Each wave fills 1 KiB blocks of 8 tile rows (block b = 4 i + wid): lane l
-    // lands at physical slot l % 8 of tile row 8 b + l / 8 and therefore fetches
-    // logical granule (l % 8) ^ ((8 b + l / 8) / 2 % 8) = (l % 8) ^ ((4 (wid % 2)
-    // + l / 16) % 8), which realises the XOR swizzle of swz().
-    const int lrow = lane >> 3, lgran = (lane & 7) ^ ((4 * (wid & 1) + (lane >> 4)) & 7);
-    uint32_t aoff[AG], boff[BG];
+    // Ring of NS 32-deep stages.  Per step: the second sub-step's fragments are
+    // read while the first sub-step's MFMAs run; then the wave waits for stage
+    // kt+1's DMAs (vmcnt counts only this wave's copies, issued in order, so
+    // `later` stages may stay in flight), and a barrier makes every wave's copies
+    // visible and proves every wave has finished reading stage kt, whose buffer
+    // is refilled with stage kt+NS at once; stage kt+1's first fragments are then
+    // read under the second sub-step's MFMAs.
+    constexpr int ADPW = BM / 64, BDPW = BN / 64;  // 1 KiB blocks per wave per stage
+    constexpr int DPW = ADPW + BDPW;
+    // lane l lands at slot l % 4 of row 16 b + l / 4 and fetches logical granule
+    // (l % 4) ^ ((l / 4 / 4) % 4), which realises sw32().
+    const int lrow = lane >> 2, lgran = (lane & 3) ^ ((lane >> 4) & 3);
+    uint32_t aoff[ADPW], boff[BDPW];
 #pragma unroll
-    for (int i = 0; i < AG; ++i)
-      aoff[i] = static_cast<uint32_t>((min(m0 + (i * 4 + wid) * 8 + lrow, g.m - 1) * g.lda + lgran * 8) * 2);
+    for (int i = 0; i < ADPW; ++i)
+      aoff[i] = static_cast<uint32_t>((min(m0 + (i * 4 + wid) * 16 + lrow, g.m - 1) * g.lda + lgran * 8) * 2);
 #pragma unroll
-    for (int i = 0; i < BG; ++i)
-      boff[i] = static_cast<uint32_t>((min(n0 + (i * 4 + wid) * 8 + lrow, g.n - 1) * g.ldw + lgran * 8) * 2);
-    const uint32_t l0 = lds_addr(lds0) + wid * 1024, l1 = lds_addr(lds1) + wid * 1024;
-    auto issue = [&](int64_t kt, uint32_t lbase) {
-      const uint16_t* ak = g.a + kt * 64;
-      const uint16_t* wk = g.w + kt * 64;
+    for (int i = 0; i < BDPW; ++i)
+      boff[i] = static_cast<uint32_t>((min(n0 + (i * 4 + wid) * 16 + lrow, g.n - 1) * g.ldw + lgran * 8) * 2);
+    const uint32_t lbase = lds_addr(lds) + wid * 1024;
+    constexpr uint32_t SB = STAGE_U4 * 16;  // stage bytes
+    const int64_t nst = g.k / 32;  // 32-deep stages
 #pragma unroll
-      for (int i = 0; i < AG; ++i) dma16(ak, aoff[i], lbase + i * 4096);
-#pragma unroll
-      for (int i = 0; i < BG; ++i) dma16(wk, boff[i], lbase + BM * 128 + i * 4096);
-    };
-    uint4 fa0[MB], fb0[NB], fa1[MB], fb1[NB];
-    issue(0, l0);
-    wait_vmem();
+    for (int st = 0; st < NS; ++st)
+      if (st < nst) issue_stage<ADPW, BDPW, BM>(g.a, g.w, st, aoff, boff, lbase + st * SB);
+    wait_stages<DPW, NS>(min<int64_t>(NS - 1, nst - 1));
     __syncthreads();
-    load_frags<MB, NB, BM, WM, WN>(lds0, 0, wm, wn, frow, fhalf, fa0, fb0);
+    uint4 fa0[MB], fb0[NB], fa1[MB], fb1[NB];
+    load_frags32<MB, NB, BM, WM, WN>(lds, 0, wm, wn, frow, fhalf, fa0, fb0);
+    // The last stage is peeled off so that the loop body has no path that skips
+    // the barrier: the second sub-step's MFMAs then never wait on the next
+    // stage's fragment reads.
     int64_t kt = 0;
-    for (; kt + 2 <= KT; kt += 2) {
-      issue(kt + 1, l1);
-      compute3<MB, NB, BM, WM, WN, BF16>(lds0, wm, wn, frow, fhalf, acc, fa0, fb0, fa1, fb1);
-      mfma_block<MB, NB, BF16>(acc, fa1, fb1);
-      wait_vmem();
+    for (; kt + 1 < nst; ++kt) {
+      const int slot = static_cast<int>(kt % NS);
+      load_frags32<MB, NB, BM, WM, WN>(lds + slot * STAGE_U4, 1, wm, wn, frow, fhalf, fa1, fb1);
+      mfma_block<MB, NB, BF16>(acc, fa0, fb0);
+      wait_stages<DPW, NS>(min<int64_t>(NS - 2, nst - 2 - kt));
       __syncthreads();
-      load_frags<MB, NB, BM, WM, WN>(lds1, 0, wm, wn, frow, fhalf, fa0, fb0);
-      if (kt + 2 < KT) issue(kt + 2, l0);
-      compute3<MB, NB, BM, WM, WN, BF16>(lds1, wm, wn, frow, fhalf, acc, fa0, fb0, fa1, fb1);
+      if (kt + NS < nst) issue_stage<ADPW, BDPW, BM>(g.a, g.w, kt + NS, aoff, boff, lbase + slot * SB);
+      load_frags32<MB, NB, BM, WM, WN>(lds + static_cast<int>((kt + 1) % NS) * STAGE_U4, 0, wm, wn,
+                                       frow, fhalf, fa0, fb0);
       mfma_block<MB, NB, BF16>(acc, fa1, fb1);
-      wait_vmem();
-      __syncthreads();
-      if (kt + 2 < KT) load_frags<MB, NB, BM, WM, WN>(lds0, 0, wm, wn, frow, fhalf, fa0, fb0);
     }
-    if (kt < KT) {  // odd tile count: the last tile is in lds0
-      compute3<MB, NB, BM, WM, WN, BF16>(lds0, wm, wn, frow, fhalf, acc, fa0, fb0, fa1, fb1);
-      mfma_block<MB, NB, BF16>(acc, fa1, fb1);
-      __syncthreads();
-    }
+    load_frags32<MB, NB, BM, WM, WN>(lds + static_cast<int>(kt % NS) * STAGE_U4, 1, wm, wn, frow,
+                                     fhalf, fa1, fb1);
+    mfma_block<MB, NB, BF16>(acc, fa0, fb0);
+    mfma_block<MB, NB, BF16>(acc, fa1, fb1);
   } else {
     const int gg = tid & 7, gr = tid >> 3;
     uint32_t aoff[AG], boff[BG];
@@ -395,8 +453,8 @@ __global__ __launch_bounds__(256) void qkv_gemm_kernel(GemmArgs g, QkvEpi e) {
     // the q/k norm is a butterfly over the D/8 lanes of a head and every store
     // is a contiguous 4-element vector.
     constexpr int LH = HD / 8;  // lanes per head
-    float* et = reinterpret_cast<float*>(wid < 2 ? lds0 : lds1) + (wid & 1) * (32 * LDR);
-    static_assert(2 * 32 * LDR * 4 <= LDS_U4 * 16, "epilogue staging fits one buffer");
+    float* et = reinterpret_cast<float*>(lds) + wid * (32 * LDR);
+    static_assert(EPI_U4 <= LDS_U4, "epilogue staging fits");
     const int l16 = lane & 15, rg = lane >> 4;
     const int hloc = l16 / LH, q = l16 % LH;
     const int c1 = hloc * HD + q * 4, c2 = c1 + HD / 2;  // columns inside the wave tile
@@ -789,7 +847,7 @@ struct QkvPlan {
   int64_t splits;
   int64_t kchunk;
   bool fused_epi;  // prefill: in-register epilogue
-  int tile;        // prefill: 256 (256x256, one workgroup per CU) or 128 (128x128, two per CU)
+  int tile;        // prefill: 256 (256x256 tiles), 1 (128x256) or 128 (128x128)
   bool stream;     // decode: weight-streaming kernel (k % 64 == 0)
   int ks;          // decode stream: 64-deep K segments per split
   int64_t operand_bytes;
@@ -835,9 +893,15 @@ static QkvPlan make_plan(int64_t m, int64_t n, int64_t k, int64_t hd) {
   } else {
     p.decode = false;
     p.fused_epi = (hd == 32 || hd == 64 || hd == 128) && n % hd == 0;
-    // 256x256 tiles (the most MFMA work per LDS byte) once they give two
-    // workgroups per CU; below that, 128x128 tiles so that more CUs take part.
-    p.tile = cdiv(m, 256) * cdiv(n, 256) >= 512 ? 256 : 128;
+    // 128x256 tiles (two workgroups per CU, so one's barriers and LDS waits
+    // are covered by the other's MFMAs) once they give two workgroups per CU;
+    // below that, 128x128 tiles so that more CUs take part.  BFA_QKV_TILE
+    // (256, 1 for 128x256, 128) overrides the choice for measurements.
+    p.tile = cdiv(m, 128) * cdiv(n, 256) >= 512 ? 1 : 128;
+    if (const char* t = getenv("BFA_QKV_TILE")) {
+      const int v = atoi(t);
+      if (v == 256 || v == 1 || v == 128) p.tile = v;
+    }
     p.splits = 1;
     p.part_bytes = p.fused_epi ? 0 : align256(m * n * 4);
   }
@@ -888,29 +952,38 @@ static void launch_decode(const QkvPlan& p, const SplitArgs& s, hipStream_t st) 
   else launch_decode_cpw<BF16, 2>(p, s, st);
 }
 
-// BM x BN tile, waves of WM x 128 (the fused epilogue needs 128-column waves).
-template <int BM, int BN, int WM, bool BF16, bool DIRECT>
+// BM x BN tile, waves of WM x 128 (the fused epilogue needs 128-column waves),
+// NS-stage DMA ring.
+template <int BM, int BN, int WM, int NS, bool BF16, bool DIRECT>
 static void launch_prefill_tile(const QkvPlan& p, const GemmArgs& g, const QkvEpi& e, hipStream_t st) {
   const unsigned grid = static_cast<unsigned>(cdiv(g.m, BM) * cdiv(g.n, BN));
   if (!p.fused_epi) {
-    hipLaunchKernelGGL((qkv_gemm_kernel<BM, BN, WM, 128, BF16, EPI_RAW, 128, DIRECT>), dim3(grid),
+    hipLaunchKernelGGL((qkv_gemm_kernel<BM, BN, WM, 128, BF16, EPI_RAW, 128, DIRECT, NS>), dim3(grid),
                        dim3(256), 0, st, g, e);
   } else if (e.hd == 128) {
-    hipLaunchKernelGGL((qkv_gemm_kernel<BM, BN, WM, 128, BF16, EPI_FUSED, 128, DIRECT>),
+    hipLaunchKernelGGL((qkv_gemm_kernel<BM, BN, WM, 128, BF16, EPI_FUSED, 128, DIRECT, NS>),
                        dim3(grid), dim3(256), 0, st, g, e);
   } else if (e.hd == 64) {
-    hipLaunchKernelGGL((qkv_gemm_kernel<BM, BN, WM, 128, BF16, EPI_FUSED, 64, DIRECT>),
+    hipLaunchKernelGGL((qkv_gemm_kernel<BM, BN, WM, 128, BF16, EPI_FUSED, 64, DIRECT, NS>),
                        dim3(grid), dim3(256), 0, st, g, e);
   } else {
-    hipLaunchKernelGGL((qkv_gemm_kernel<BM, BN, WM, 128, BF16, EPI_FUSED, 32, DIRECT>),
+    hipLaunchKernelGGL((qkv_gemm_kernel<BM, BN, WM, 128, BF16, EPI_FUSED, 32, DIRECT, NS>),
                        dim3(grid), dim3(256), 0, st, g, e);
   }
 }
 
 template <bool BF16, bool DIRECT>
 static void launch_prefill_t(const QkvPlan& p, const GemmArgs& g, const QkvEpi& e, hipStream_t st) {
-  if (p.tile == 256) launch_prefill_tile<256, 256, 128, BF16, DIRECT>(p, g, e, st);
-  else launch_prefill_tile<128, 128, 32, BF16, DIRECT>(p, g, e, st);
+  if (p.tile == 256) {
+    launch_prefill_tile<256, 256, 128, 4, BF16, DIRECT>(p, g, e, st);
+  } else if constexpr (DIRECT) {
+    if (p.tile == 1) launch_prefill_tile<128, 256, 64, 3, BF16, true>(p, g, e, st);
+    else launch_prefill_tile<128, 128, 32, 4, BF16, true>(p, g, e, st);
+  } else {
+    // the register-staged path keeps 128x128 tiles for both (a 128x256 tile
+    // would not fit two waves per SIMD there)
+    launch_prefill_tile<128, 128, 32, 4, BF16, false>(p, g, e, st);
+  }
 }
 
 template <bool BF16>
