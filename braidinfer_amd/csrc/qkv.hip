@@ -211,18 +211,19 @@ __device__ __forceinline__ void load_frags32(const uint4* st, int ks, int wm, in
   for (int j = 0; j < NB; ++j) bf[j] = st[BM * 4 + sw32(wn * WN + j * 32 + frow, gsel)];
 }
 
-// One 32-deep stage of both operands by DMA: each wave moves 1 KiB blocks of 16
-// rows (block b = 4 i + wid; the wave's block offset is folded into lstage).
-template <int ADPW, int BDPW, int BM>
+// One stage (BK deep) of both operands by DMA: each of the NW waves moves 1 KiB
+// blocks (block b = NW i + wid; the wave's own block offset is folded into
+// lstage); the weight blocks follow the BM operand rows of BK * 2 bytes.
+template <int ADPW, int BDPW, int BM, int BK, int NW>
 __device__ __forceinline__ void issue_stage(const uint16_t* a, const uint16_t* w, int64_t kt,
                                             const uint32_t (&aoff)[ADPW],
                                             const uint32_t (&boff)[BDPW], uint32_t lstage) {
-  const uint16_t* ak = a + kt * 32;
-  const uint16_t* wk = w + kt * 32;
+  const uint16_t* ak = a + kt * BK;
+  const uint16_t* wk = w + kt * BK;
 #pragma unroll
-  for (int i = 0; i < ADPW; ++i) dma16(ak, aoff[i], lstage + i * 4096);
+  for (int i = 0; i < ADPW; ++i) dma16(ak, aoff[i], lstage + i * NW * 1024);
 #pragma unroll
-  for (int i = 0; i < BDPW; ++i) dma16(wk, boff[i], lstage + BM * 64 + i * 4096);
+  for (int i = 0; i < BDPW; ++i) dma16(wk, boff[i], lstage + BM * BK * 2 + i * NW * 1024);
 }
 
 // Waits until at most `later` (< NS) stages of DPW DMAs each are still in flight.
@@ -279,21 +280,28 @@ __device__ __forceinline__ void tile_store(uint4* buf, int gr, int gg, const uin
 
 // DIRECT: tiles go HBM -> LDS by DMA (K % 64 == 0, 16-byte aligned rows,
 // byte offsets below 4 GiB); otherwise HBM -> registers -> LDS with K masking.
-// Wave tiles of at most 64x128 (128 accumulator registers) are compiled for two
-// waves per SIMD, so two workgroups share a CU.
-template <int BM, int BN, int WM, int WN, bool BF16, int EPI, int HD, bool DIRECT, int NS>
-__global__ __launch_bounds__(256, (WM * WN <= 8192 ? 2 : 1)) void qkv_gemm_kernel(GemmArgs g, QkvEpi e) {
+// NW = (BM / WM) (BN / WN) waves per workgroup (4 or 8).  Wave tiles of at most
+// 64x128 (128 accumulator registers) are compiled for two waves per SIMD: two
+// 4-wave workgroups, or one 8-wave workgroup, per CU.  BK is the depth of a DMA
+// stage: 32 (ring of NS stages, 16 rows x 64 bytes per copy) or 64 (two
+// buffers, 8 rows x 128 bytes per copy, full cache lines).
+template <int BM, int BN, int WM, int WN, bool BF16, int EPI, int HD, bool DIRECT, int NS, int BK>
+__global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, (WM * WN <= 8192 ? 2 : 1)) void qkv_gemm_kernel(
+    GemmArgs g, QkvEpi e) {
   constexpr int NWN = BN / WN;
-  static_assert((BM / WM) * NWN == 4, "four waves per workgroup");
+  constexpr int NW = (BM / WM) * NWN;
+  static_assert(NW == 4 || NW == 8, "four or eight waves per workgroup");
+  static_assert(DIRECT || NW == 4, "the register-staged path assumes 256 threads");
+  static_assert(BK == 32 || BK == 64, "stage depth");
   constexpr int MB = WM / 32, NB = WN / 32;
   constexpr int AG = BM / 32, BG = BN / 32;  // 16-byte granules per thread per K tile
   // LDS: the DMA path keeps a ring of NS 32-deep stages of both operands; the
   // register path two 64-deep buffers; afterwards the fused epilogue stages
   // each wave's 32-row accumulator blocks (row stride LDR floats).
   constexpr int LDR = 136;
-  constexpr int STAGE_U4 = (BM + BN) * 4;
-  constexpr int EPI_U4 = 4 * 32 * LDR / 4;
-  constexpr int MAIN_U4 = DIRECT ? NS * STAGE_U4 : 2 * (BM + BN) * 8;
+  constexpr int STAGE_U4 = (BM + BN) * BK / 8;
+  constexpr int EPI_U4 = NW * 32 * LDR / 4;
+  constexpr int MAIN_U4 = DIRECT ? (BK == 32 ? NS : 2) * STAGE_U4 : 2 * (BM + BN) * 8;
   constexpr int LDS_U4 = MAIN_U4 > EPI_U4 ? MAIN_U4 : EPI_U4;
   __shared__ uint4 lds[LDS_U4];
   uint4* const lds0 = lds;
@@ -331,7 +339,7 @@ __global__ __launch_bounds__(256, (WM * WN <= 8192 ? 2 : 1)) void qkv_gemm_kerne
   // tile's loads are issued before this tile's MFMAs and stored to the other
   // LDS buffer after them; MFMA fragments are double-buffered across the four
   // 16-deep K sub-steps so every ds_read overlaps the previous sub-step's MFMAs.
-  if constexpr (DIRECT) {
+  if constexpr (DIRECT && BK == 32) {
     // Ring of NS 32-deep stages.  Per step: the second sub-step's fragments are
     // read while the first sub-step's MFMAs run; then the wave waits for stage
     // kt+1's DMAs (vmcnt counts only this wave's copies, issued in order, so
@@ -339,7 +347,7 @@ __global__ __launch_bounds__(256, (WM * WN <= 8192 ? 2 : 1)) void qkv_gemm_kerne
     // visible and proves every wave has finished reading stage kt, whose buffer
     // is refilled with stage kt+NS at once; stage kt+1's first fragments are then
     // read under the second sub-step's MFMAs.
-    constexpr int ADPW = BM / 64, BDPW = BN / 64;  // 1 KiB blocks per wave per stage
+    constexpr int ADPW = BM / 16 / NW, BDPW = BN / 16 / NW;  // 1 KiB blocks per wave per stage
     constexpr int DPW = ADPW + BDPW;
     // lane l lands at slot l % 4 of row 16 b + l / 4 and fetches logical granule
     // (l % 4) ^ ((l / 4 / 4) % 4), which realises sw32().
@@ -347,16 +355,16 @@ __global__ __launch_bounds__(256, (WM * WN <= 8192 ? 2 : 1)) void qkv_gemm_kerne
     uint32_t aoff[ADPW], boff[BDPW];
 #pragma unroll
     for (int i = 0; i < ADPW; ++i)
-      aoff[i] = static_cast<uint32_t>((min(m0 + (i * 4 + wid) * 16 + lrow, g.m - 1) * g.lda + lgran * 8) * 2);
+      aoff[i] = static_cast<uint32_t>((min(m0 + (i * NW + wid) * 16 + lrow, g.m - 1) * g.lda + lgran * 8) * 2);
 #pragma unroll
     for (int i = 0; i < BDPW; ++i)
-      boff[i] = static_cast<uint32_t>((min(n0 + (i * 4 + wid) * 16 + lrow, g.n - 1) * g.ldw + lgran * 8) * 2);
+      boff[i] = static_cast<uint32_t>((min(n0 + (i * NW + wid) * 16 + lrow, g.n - 1) * g.ldw + lgran * 8) * 2);
     const uint32_t lbase = lds_addr(lds) + wid * 1024;
     constexpr uint32_t SB = STAGE_U4 * 16;  // stage bytes
     const int64_t nst = g.k / 32;  // 32-deep stages
 #pragma unroll
     for (int st = 0; st < NS; ++st)
-      if (st < nst) issue_stage<ADPW, BDPW, BM>(g.a, g.w, st, aoff, boff, lbase + st * SB);
+      if (st < nst) issue_stage<ADPW, BDPW, BM, 32, NW>(g.a, g.w, st, aoff, boff, lbase + st * SB);
     wait_stages<DPW, NS>(min<int64_t>(NS - 1, nst - 1));
     __syncthreads();
     uint4 fa0[MB], fb0[NB], fa1[MB], fb1[NB];
@@ -371,7 +379,7 @@ __global__ __launch_bounds__(256, (WM * WN <= 8192 ? 2 : 1)) void qkv_gemm_kerne
       mfma_block<MB, NB, BF16>(acc, fa0, fb0);
       wait_stages<DPW, NS>(min<int64_t>(NS - 2, nst - 2 - kt));
       __syncthreads();
-      if (kt + NS < nst) issue_stage<ADPW, BDPW, BM>(g.a, g.w, kt + NS, aoff, boff, lbase + slot * SB);
+      if (kt + NS < nst) issue_stage<ADPW, BDPW, BM, 32, NW>(g.a, g.w, kt + NS, aoff, boff, lbase + slot * SB);
       load_frags32<MB, NB, BM, WM, WN>(lds + static_cast<int>((kt + 1) % NS) * STAGE_U4, 0, wm, wn,
                                        frow, fhalf, fa0, fb0);
       mfma_block<MB, NB, BF16>(acc, fa1, fb1);
@@ -380,6 +388,47 @@ __global__ __launch_bounds__(256, (WM * WN <= 8192 ? 2 : 1)) void qkv_gemm_kerne
                                      fhalf, fa1, fb1);
     mfma_block<MB, NB, BF16>(acc, fa0, fb0);
     mfma_block<MB, NB, BF16>(acc, fa1, fb1);
+  } else if constexpr (DIRECT) {
+    // Two 64-deep buffers; each copy is 8 rows x 128 bytes.  Lane l lands at
+    // slot l % 8 of tile row 8 b + l / 8 and fetches logical granule
+    // (l % 8) ^ ((8 b + l / 8) / 2 % 8) = (l % 8) ^ ((4 (wid % 2) + l / 16) % 8)
+    // (b = NW i + wid, NW even), which realises swz().  Stage kt+1 is issued as
+    // stage kt's MFMAs start and waited for as they end.
+    constexpr int ADPW = BM / 8 / NW, BDPW = BN / 8 / NW;
+    const int lrow = lane >> 3, lgran = (lane & 7) ^ ((4 * (wid & 1) + (lane >> 4)) & 7);
+    uint32_t aoff[ADPW], boff[BDPW];
+#pragma unroll
+    for (int i = 0; i < ADPW; ++i)
+      aoff[i] = static_cast<uint32_t>((min(m0 + (i * NW + wid) * 8 + lrow, g.m - 1) * g.lda + lgran * 8) * 2);
+#pragma unroll
+    for (int i = 0; i < BDPW; ++i)
+      boff[i] = static_cast<uint32_t>((min(n0 + (i * NW + wid) * 8 + lrow, g.n - 1) * g.ldw + lgran * 8) * 2);
+    const uint32_t l0 = lds_addr(lds0) + wid * 1024, l1 = lds_addr(lds1) + wid * 1024;
+    uint4 fa0[MB], fb0[NB], fa1[MB], fb1[NB];
+    issue_stage<ADPW, BDPW, BM, 64, NW>(g.a, g.w, 0, aoff, boff, l0);
+    wait_vmem();
+    __syncthreads();
+    load_frags<MB, NB, BM, WM, WN>(lds0, 0, wm, wn, frow, fhalf, fa0, fb0);
+    int64_t kt = 0;
+    for (; kt + 2 <= KT; kt += 2) {
+      issue_stage<ADPW, BDPW, BM, 64, NW>(g.a, g.w, kt + 1, aoff, boff, l1);
+      compute3<MB, NB, BM, WM, WN, BF16>(lds0, wm, wn, frow, fhalf, acc, fa0, fb0, fa1, fb1);
+      mfma_block<MB, NB, BF16>(acc, fa1, fb1);
+      wait_vmem();
+      __syncthreads();
+      load_frags<MB, NB, BM, WM, WN>(lds1, 0, wm, wn, frow, fhalf, fa0, fb0);
+      if (kt + 2 < KT) issue_stage<ADPW, BDPW, BM, 64, NW>(g.a, g.w, kt + 2, aoff, boff, l0);
+      compute3<MB, NB, BM, WM, WN, BF16>(lds1, wm, wn, frow, fhalf, acc, fa0, fb0, fa1, fb1);
+      mfma_block<MB, NB, BF16>(acc, fa1, fb1);
+      wait_vmem();
+      __syncthreads();
+      if (kt + 2 < KT) load_frags<MB, NB, BM, WM, WN>(lds0, 0, wm, wn, frow, fhalf, fa0, fb0);
+    }
+    if (kt < KT) {  // odd tile count: the last tile is in lds0
+      compute3<MB, NB, BM, WM, WN, BF16>(lds0, wm, wn, frow, fhalf, acc, fa0, fb0, fa1, fb1);
+      mfma_block<MB, NB, BF16>(acc, fa1, fb1);
+      __syncthreads();
+    }
   } else {
     const int gg = tid & 7, gr = tid >> 3;
     uint32_t aoff[AG], boff[BG];
@@ -847,7 +896,7 @@ struct QkvPlan {
   int64_t splits;
   int64_t kchunk;
   bool fused_epi;  // prefill: in-register epilogue
-  int tile;        // prefill: 256 (256x256 tiles), 1 (128x256) or 128 (128x128)
+  int tile;        // prefill: 256 (256x256, 4 waves), 2 (256x256, 8 waves), 1 (128x256), 128
   bool stream;     // decode: weight-streaming kernel (k % 64 == 0)
   int ks;          // decode stream: 64-deep K segments per split
   int64_t operand_bytes;
@@ -893,14 +942,17 @@ static QkvPlan make_plan(int64_t m, int64_t n, int64_t k, int64_t hd) {
   } else {
     p.decode = false;
     p.fused_epi = (hd == 32 || hd == 64 || hd == 128) && n % hd == 0;
-    // 128x256 tiles (two workgroups per CU, so one's barriers and LDS waits
-    // are covered by the other's MFMAs) once they give two workgroups per CU;
-    // below that, 128x128 tiles so that more CUs take part.  BFA_QKV_TILE
-    // (256, 1 for 128x256, 128) overrides the choice for measurements.
-    p.tile = cdiv(m, 128) * cdiv(n, 256) >= 512 ? 1 : 128;
+    // Largest tile that still fills the CUs: 256x256 with 8 waves (two per
+    // SIMD, full-line 64-deep DMA stages) from one tile per CU; else 128x256
+    // with 4 waves at two workgroups per CU; else 128x128.  BFA_QKV_TILE (2 for
+    // 256x256 with 8 waves, 256 for 256x256 with 4 waves, 1 for 128x256, 128)
+    // overrides the choice for measurements.
+    if (cdiv(m, 256) * cdiv(n, 256) >= 256) p.tile = 2;
+    else if (cdiv(m, 128) * cdiv(n, 256) >= 512) p.tile = 1;
+    else p.tile = 128;
     if (const char* t = getenv("BFA_QKV_TILE")) {
       const int v = atoi(t);
-      if (v == 256 || v == 1 || v == 128) p.tile = v;
+      if (v == 256 || v == 2 || v == 1 || v == 128) p.tile = v;
     }
     p.splits = 1;
     p.part_bytes = p.fused_epi ? 0 : align256(m * n * 4);
@@ -953,36 +1005,39 @@ static void launch_decode(const QkvPlan& p, const SplitArgs& s, hipStream_t st) 
 }
 
 // BM x BN tile, waves of WM x 128 (the fused epilogue needs 128-column waves),
-// NS-stage DMA ring.
-template <int BM, int BN, int WM, int NS, bool BF16, bool DIRECT>
+// BK-deep DMA stages (NS of them when BK = 32).
+template <int BM, int BN, int WM, int NS, int BK, bool BF16, bool DIRECT>
 static void launch_prefill_tile(const QkvPlan& p, const GemmArgs& g, const QkvEpi& e, hipStream_t st) {
   const unsigned grid = static_cast<unsigned>(cdiv(g.m, BM) * cdiv(g.n, BN));
+  const dim3 block((BM / WM) * (BN / 128) * 64);
   if (!p.fused_epi) {
-    hipLaunchKernelGGL((qkv_gemm_kernel<BM, BN, WM, 128, BF16, EPI_RAW, 128, DIRECT, NS>), dim3(grid),
-                       dim3(256), 0, st, g, e);
+    hipLaunchKernelGGL((qkv_gemm_kernel<BM, BN, WM, 128, BF16, EPI_RAW, 128, DIRECT, NS, BK>), dim3(grid),
+                       block, 0, st, g, e);
   } else if (e.hd == 128) {
-    hipLaunchKernelGGL((qkv_gemm_kernel<BM, BN, WM, 128, BF16, EPI_FUSED, 128, DIRECT, NS>),
-                       dim3(grid), dim3(256), 0, st, g, e);
+    hipLaunchKernelGGL((qkv_gemm_kernel<BM, BN, WM, 128, BF16, EPI_FUSED, 128, DIRECT, NS, BK>),
+                       dim3(grid), block, 0, st, g, e);
   } else if (e.hd == 64) {
-    hipLaunchKernelGGL((qkv_gemm_kernel<BM, BN, WM, 128, BF16, EPI_FUSED, 64, DIRECT, NS>),
-                       dim3(grid), dim3(256), 0, st, g, e);
+    hipLaunchKernelGGL((qkv_gemm_kernel<BM, BN, WM, 128, BF16, EPI_FUSED, 64, DIRECT, NS, BK>),
+                       dim3(grid), block, 0, st, g, e);
   } else {
-    hipLaunchKernelGGL((qkv_gemm_kernel<BM, BN, WM, 128, BF16, EPI_FUSED, 32, DIRECT, NS>),
-                       dim3(grid), dim3(256), 0, st, g, e);
+    hipLaunchKernelGGL((qkv_gemm_kernel<BM, BN, WM, 128, BF16, EPI_FUSED, 32, DIRECT, NS, BK>),
+                       dim3(grid), block, 0, st, g, e);
   }
 }
 
 template <bool BF16, bool DIRECT>
 static void launch_prefill_t(const QkvPlan& p, const GemmArgs& g, const QkvEpi& e, hipStream_t st) {
-  if (p.tile == 256) {
-    launch_prefill_tile<256, 256, 128, 4, BF16, DIRECT>(p, g, e, st);
-  } else if constexpr (DIRECT) {
-    if (p.tile == 1) launch_prefill_tile<128, 256, 64, 3, BF16, true>(p, g, e, st);
-    else launch_prefill_tile<128, 128, 32, 4, BF16, true>(p, g, e, st);
+  if constexpr (DIRECT) {
+    switch (p.tile) {
+      case 256: launch_prefill_tile<256, 256, 128, 4, 32, BF16, true>(p, g, e, st); break;
+      case 2: launch_prefill_tile<256, 256, 64, 2, 64, BF16, true>(p, g, e, st); break;
+      case 1: launch_prefill_tile<128, 256, 64, 3, 32, BF16, true>(p, g, e, st); break;
+      default: launch_prefill_tile<128, 128, 32, 4, 32, BF16, true>(p, g, e, st); break;
+    }
   } else {
-    // the register-staged path keeps 128x128 tiles for both (a 128x256 tile
-    // would not fit two waves per SIMD there)
-    launch_prefill_tile<128, 128, 32, 4, BF16, false>(p, g, e, st);
+    // the register-staged path (256 threads) keeps 256x256 or 128x128 tiles
+    if (p.tile == 256) launch_prefill_tile<256, 256, 128, 2, 64, BF16, false>(p, g, e, st);
+    else launch_prefill_tile<128, 128, 32, 2, 64, BF16, false>(p, g, e, st);
   }
 }
 
