@@ -123,6 +123,12 @@ __device__ __forceinline__ int head_kind(const QkvEpi& e, int64_t head) {
   return head < e.hq ? 0 : (head < e.hq + e.hkv ? 1 : 2);
 }
 
+// Position p wrapped like a torch negative index; -1 when outside the table.
+__device__ __forceinline__ int32_t epi_pos_check(const QkvEpi& e, int64_t p) {
+  if (p < 0) p += e.max_pos;
+  return (p >= 0 && p < e.max_pos) ? static_cast<int32_t>(p) : -1;
+}
+
 __device__ __forceinline__ int64_t epi_position(const QkvEpi& e, int64_t row, bool& ok) {
   int64_t p = e.pos_is_i64 ? static_cast<const int64_t*>(e.positions)[row]
                            : static_cast<const int32_t*>(e.positions)[row];
@@ -229,8 +235,11 @@ __device__ __forceinline__ void issue_stage(const uint16_t* a, const uint16_t* w
 // Waits until at most `later` (< NS) stages of DPW DMAs each are still in flight.
 template <int DPW, int NS>
 __device__ __forceinline__ void wait_stages(int64_t later) {
-  static_assert(NS >= 2 && NS <= 4, "cases below cover up to 3 later stages");
-  if (NS > 3 && later >= 3) wait_vm<(NS > 3 ? 3 : 0) * DPW>();
+  static_assert(NS >= 2 && NS <= 6, "cases below cover up to 5 later stages");
+  static_assert(DPW * (NS - 1) < 64, "vmcnt range");
+  if (NS > 5 && later >= 5) wait_vm<(NS > 5 ? 5 : 0) * DPW>();
+  else if (NS > 4 && later >= 4) wait_vm<(NS > 4 ? 4 : 0) * DPW>();
+  else if (NS > 3 && later >= 3) wait_vm<(NS > 3 ? 3 : 0) * DPW>();
   else if (NS > 2 && later >= 2) wait_vm<(NS > 2 ? 2 : 0) * DPW>();
   else if (later >= 1) wait_vm<DPW>();
   else wait_vm<0>();
@@ -523,6 +532,26 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, (WM * WN <= 8192 ? 2 : 
       g2[t] = nw ? load_any(nw, e.qk_w_dtype, HD / 2 + q * 4 + t) : 1.f;
     }
     const int dt_after = nw ? e.norm_dt : e.qkv_dt;  // dtype RoPE receives
+    // Positions of every row this lane will rotate, fetched up front (one
+    // batch of independent loads) so that each row iteration has a single
+    // dependent load level (its cos/sin) instead of two; -1 marks a position
+    // outside the table.
+    int32_t posv[MB][8];
+    if (rope) {
+      if (e.pos_is_i64) {
+#pragma unroll
+        for (int i = 0; i < MB; ++i)
+#pragma unroll
+          for (int it = 0; it < 8; ++it)
+            posv[i][it] = epi_pos_check(e, static_cast<const int64_t*>(e.positions)[min(wrow0 + i * 32 + rg + 4 * it, g.m - 1)]);
+      } else {
+#pragma unroll
+        for (int i = 0; i < MB; ++i)
+#pragma unroll
+          for (int it = 0; it < 8; ++it)
+            posv[i][it] = epi_pos_check(e, static_cast<const int32_t*>(e.positions)[min(wrow0 + i * 32 + rg + 4 * it, g.m - 1)]);
+      }
+    }
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < MB; ++i) {
@@ -532,6 +561,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, (WM * WN <= 8192 ? 2 : 
         for (int v = 0; v < 16; ++v)
           et[(8 * (v / 4) + 4 * fhalf + (v % 4)) * LDR + j * 32 + frow] = acc[i][j][v];
       __syncthreads();
+#pragma unroll
       for (int it = 0; it < 8; ++it) {
         const int rl = rg + 4 * it;
         const int64_t row = wrow0 + i * 32 + rl;
@@ -557,8 +587,8 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, (WM * WN <= 8192 ? 2 : 
           }
         }
         if (rope) {
-          bool ok;
-          const int64_t p = epi_position(e, min(row, g.m - 1), ok);
+          const bool ok = posv[i][it] >= 0;
+          const int64_t p = ok ? posv[i][it] : 0;
           if (!ok && row < g.m && q == 0) flag_status(e.status, BFA_STATUS_INDEX_OOB);
           const float4 cv = *reinterpret_cast<const float4*>(e.cs + p * HD + q * 4);
           const float4 sv = *reinterpret_cast<const float4*>(e.cs + p * HD + HD / 2 + q * 4);
@@ -896,7 +926,7 @@ struct QkvPlan {
   int64_t splits;
   int64_t kchunk;
   bool fused_epi;  // prefill: in-register epilogue
-  int tile;        // prefill: 256 (256x256, 4 waves), 2 (256x256, 8 waves), 1 (128x256), 128
+  int tile;        // prefill: 2 (256x256, 8 waves), 3 (128x256, 8 waves), 1 (128x256, 4 waves), 128
   bool stream;     // decode: weight-streaming kernel (k % 64 == 0)
   int ks;          // decode stream: 64-deep K segments per split
   int64_t operand_bytes;
@@ -944,15 +974,15 @@ static QkvPlan make_plan(int64_t m, int64_t n, int64_t k, int64_t hd) {
     p.fused_epi = (hd == 32 || hd == 64 || hd == 128) && n % hd == 0;
     // Largest tile that still fills the CUs: 256x256 with 8 waves (two per
     // SIMD, full-line 64-deep DMA stages) from one tile per CU; else 128x256
-    // with 4 waves at two workgroups per CU; else 128x128.  BFA_QKV_TILE (2 for
-    // 256x256 with 8 waves, 256 for 256x256 with 4 waves, 1 for 128x256, 128)
-    // overrides the choice for measurements.
+    // with 8 waves from 192 tiles; else 128x128 with 4 waves (two workgroups
+    // per CU).  BFA_QKV_TILE (2: 256x256 8 waves, 3: 128x256 8 waves, 1:
+    // 128x256 4 waves, 128: 128x128) overrides the choice for measurements.
     if (cdiv(m, 256) * cdiv(n, 256) >= 256) p.tile = 2;
-    else if (cdiv(m, 128) * cdiv(n, 256) >= 512) p.tile = 1;
+    else if (cdiv(m, 128) * cdiv(n, 256) >= 192) p.tile = 3;
     else p.tile = 128;
     if (const char* t = getenv("BFA_QKV_TILE")) {
       const int v = atoi(t);
-      if (v == 256 || v == 2 || v == 1 || v == 128) p.tile = v;
+      if ((v >= 1 && v <= 3) || v == 128) p.tile = v;
     }
     p.splits = 1;
     p.part_bytes = p.fused_epi ? 0 : align256(m * n * 4);
@@ -1029,15 +1059,15 @@ template <bool BF16, bool DIRECT>
 static void launch_prefill_t(const QkvPlan& p, const GemmArgs& g, const QkvEpi& e, hipStream_t st) {
   if constexpr (DIRECT) {
     switch (p.tile) {
-      case 256: launch_prefill_tile<256, 256, 128, 4, 32, BF16, true>(p, g, e, st); break;
       case 2: launch_prefill_tile<256, 256, 64, 2, 64, BF16, true>(p, g, e, st); break;
+      case 3: launch_prefill_tile<128, 256, 32, 2, 64, BF16, true>(p, g, e, st); break;
       case 1: launch_prefill_tile<128, 256, 64, 3, 32, BF16, true>(p, g, e, st); break;
       default: launch_prefill_tile<128, 128, 32, 4, 32, BF16, true>(p, g, e, st); break;
     }
   } else {
-    // the register-staged path (256 threads) keeps 256x256 or 128x128 tiles
-    if (p.tile == 256) launch_prefill_tile<256, 256, 128, 2, 64, BF16, false>(p, g, e, st);
-    else launch_prefill_tile<128, 128, 32, 2, 64, BF16, false>(p, g, e, st);
+    // the register-staged path (256 threads, K not a multiple of 64 or
+    // unaligned rows) uses 128x128 tiles
+    launch_prefill_tile<128, 128, 32, 2, 64, BF16, false>(p, g, e, st);
   }
 }
 
@@ -1097,6 +1127,8 @@ extern "C" int bfa_qkv_projection(const void* operand, int64_t tokens, int64_t h
                                                          positions_dtype == BFA_DTYPE_I32)),
               "%s: RoPE needs int32/int64 positions", what);
   BFA_REQUIRE(cos_sin_cache == nullptr || hd % 2 == 0, "%s: RoPE needs an even head_dim", what);
+  BFA_REQUIRE(cos_sin_cache == nullptr || (max_position > 0 && max_position <= 0x7fffffffLL),
+              "%s: RoPE table length %lld out of range", what, (long long)max_position);
   BFA_REQUIRE(hd <= 512, "%s: head_dim %lld > 512 unsupported", what, (long long)hd);
   if (tokens == 0) return BFA_OK;
   BFA_REQUIRE(out, "%s: null output", what);

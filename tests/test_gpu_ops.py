@@ -296,6 +296,25 @@ def test_rerotate_paged_k(hkv, d):
     braidinfer_amd.check_device_status()
 
 
+def test_rerotate_paged_k_full_config():
+    """The configured workload at full size: 4096 cached tokens x 8 kv heads x 128
+    in 256 pages of 16 (HND), pages in shuffled order, 16 chunks of 16 pages,
+    one delta per chunk from U[-4096, 4096], theta 1e6, table of 40960 positions
+    (negative deltas wrap): bit-exact against the oracle."""
+    g = gen(4)
+    pages, hkv, ps, d, maxp = 256, 8, 16, 128, 40960
+    kv = randn(g, pages, 2, hkv, ps, d)
+    idx = torch.randperm(pages, generator=g).to(torch.int32)
+    indptr = (torch.arange(17, dtype=torch.int32) * 16)
+    delta = torch.randint(-4096, 4097, (16,), generator=g)
+    last = torch.full((16,), ps, dtype=torch.int32)
+    cache = R.cos_sin_cache(d, maxp, 1e6)
+    out = rerotate_paged_k(kv.to(DEV), idx.to(DEV), indptr.to(DEV), delta.to(DEV), last.to(DEV), cache.to(DEV))
+    ref = R.rerotate_paged_k(kv, idx, indptr, delta, last, cache)
+    assert torch.equal(bits(out), bits(ref))
+    braidinfer_amd.check_device_status()
+
+
 def test_rerotate_delta_out_of_table():
     cache = R.cos_sin_cache(64, 128, 1e4).to(DEV)
     kv = torch.zeros(2, 2, 1, 16, 64, device=DEV, dtype=torch.bfloat16)

@@ -19,7 +19,7 @@ from braidinfer_amd.kernels import (FusedRMSNormQKV, FusedRMSNormQKVMinimalF32,
                                     FusedRMSNormQKVMixedPrecision, FusedRMSNormQKVWithBias)
 from braidinfer_amd.layers import llama_attention_input, qwen3_attention_input
 from oracle import torch_ref as R
-from tests.helpers import assert_close, gen, randn
+from tests.helpers import assert_close, gen, randn, rope_flip_slack
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -154,16 +154,31 @@ def _qwen3_case(seed, t, h=1024, hq=16, hkv=8, d=128):
     return x, ln, w, qn, kn, pos
 
 
-@pytest.mark.parametrize("t", [1, 7, 64, 300])
+def _qwen3_rope_inputs(x, ln, w, qn, kn, hq=16, hkv=8, eps=1e-6):
+    """The oracle's normalised q and k (the RoPE inputs), for rope_flip_slack."""
+    q, k, _ = R.split_qkv(R.qkv_mixed_precision(x, ln, w, None, eps), hq, hkv)
+    return (R.rms_forward(q.float(), qn, eps).to(x.dtype),
+            R.rms_forward(k.float(), kn, eps).to(x.dtype))
+
+
+@pytest.mark.parametrize("t", [1, 7, 64, 300, 2048])
 def test_qwen3_chain(t):
-    """Qwen3-0.6B: fused QKV + per-head q/k RMSNorm (extreme k_norm weights) + RoPE."""
+    """Qwen3-0.6B: fused QKV + per-head q/k RMSNorm (extreme k_norm weights) + RoPE.
+
+    q and k carry, on top of the path tolerance, two bf16 ulps of each RoPE input
+    (rope_flip_slack) for at most 1e-4 of their elements: with k_norm weights up
+    to 100 the normalised k reaches ~100 (ulp 0.5), and a projection summed in
+    another order than the oracle's can round one element an ulp away; where the
+    rotation cancels, that reaches the output.  At 2048 tokens 15 of 2.1 M k
+    elements need it; v has no allowance."""
     x, ln, w, qn, kn, pos = _qwen3_case(206, t)
     cache = R.cos_sin_cache(128, 40960, 1e6)
     q, k, v = qwen3_attention_input(x.to(DEV), ln.to(DEV), w.to(DEV), None, 16, 8, 1e-6,
                                     pos.to(DEV), cache.to(DEV), qn.to(DEV), kn.to(DEV))
     rq, rk, rv = R.qwen3_attention_input(x, ln, w, None, 16, 8, 1e-6, pos, cache, qn, kn)
-    assert_close(q, rq, what="qwen3 q")
-    assert_close(k, rk, what="qwen3 k")
+    pq, pk = _qwen3_rope_inputs(x, ln, w, qn, kn)
+    assert_close(q, rq, what="qwen3 q", slack=rope_flip_slack(pq).reshape(rq.shape))
+    assert_close(k, rk, what="qwen3 k", slack=rope_flip_slack(pk).reshape(rk.shape))
     assert_close(v, rv, what="qwen3 v")
     # extreme k_norm weights: fp32-accumulated k stays finite and inside bf16 / fp16 range
     assert torch.isfinite(k).all() and k.abs().max().item() < 65504.0
@@ -224,5 +239,10 @@ def test_prefill_8192_sampled_rows(chain):
                                         pos.to(DEV), cache.to(DEV), qn.to(DEV), kn.to(DEV))
         ref = R.qwen3_attention_input(x[rows], ln, w, None, hq, hkv, 1e-6, pos[rows], cache, qn, kn)
     rd = rows.to(DEV)
-    for got, exp, name in zip((q, k, v), ref, "qkv"):
-        assert_close(got[rd], exp, what=f"{chain} 8192 {name}")
+    slack = [None, None, None]
+    if chain == "qwen3":  # see test_qwen3_chain
+        pq, pk = _qwen3_rope_inputs(x[rows], ln, w, qn, kn, hq, hkv)
+        slack[0], slack[1] = rope_flip_slack(pq), rope_flip_slack(pk)
+    for got, exp, name, sl in zip((q, k, v), ref, "qkv", slack):
+        assert_close(got[rd], exp, what=f"{chain} 8192 {name}",
+                     slack=None if sl is None else sl.reshape(exp.shape))
