@@ -123,6 +123,21 @@ __device__ __forceinline__ int head_kind(const QkvEpi& e, int64_t head) {
   return head < e.hq ? 0 : (head < e.hq + e.hkv ? 1 : 2);
 }
 
+// Two elements of a small float vector of runtime dtype, with one dispatch.
+__device__ __forceinline__ void load2_any(const void* p, int dt, int64_t i1, int64_t i2, float& v1,
+                                          float& v2) {
+  if (dt == BFA_DTYPE_BF16) {
+    v1 = load1<BFA_DTYPE_BF16>(p, i1);
+    v2 = load1<BFA_DTYPE_BF16>(p, i2);
+  } else if (dt == BFA_DTYPE_F16) {
+    v1 = load1<BFA_DTYPE_F16>(p, i1);
+    v2 = load1<BFA_DTYPE_F16>(p, i2);
+  } else {
+    v1 = static_cast<const float*>(p)[i1];
+    v2 = static_cast<const float*>(p)[i2];
+  }
+}
+
 // Position p wrapped like a torch negative index; -1 when outside the table.
 __device__ __forceinline__ int32_t epi_pos_check(const QkvEpi& e, int64_t p) {
   if (p < 0) p += e.max_pos;
@@ -724,7 +739,7 @@ __device__ __forceinline__ int wslot(int r, int g) { return r * 8 + (g ^ ((r >> 
 // KS: 64-deep K segments per split (every split has exactly KS; the host picks
 // KS dividing k / 64), fixed at compile time so the weight loads carry no
 // branches and each segment waits only for its own four loads.
-template <int MT, int KS, bool BF16>
+template <int MT, int KS, bool BF16, bool REG_ORDER>
 __global__ __launch_bounds__(256) void qkv_decode_kernel(DecodeArgs d) {
   static_assert(KS >= 1 && KS * 64 <= KC_MAX, "segments per split");
   constexpr int GPR = KC_MAX / 8;      // 16-byte granules per LDS operand row (row pitch 1 KiB)
@@ -812,20 +827,194 @@ __global__ __launch_bounds__(256) void qkv_decode_kernel(DecodeArgs d) {
         }
     }
   }
-  // 4. partial tile: 16x16 layout, lane holds column (lane & 15), rows 4*(lane/16) + v
-  float* dst = d.part + static_cast<int64_t>(blockIdx.y) * d.m * d.n;
+  // 4. partial tile in register order: the wave's MT x 2 blocks of 64 lanes x
+  //    float4 (16x16 MFMA layout: lane holds column lane % 16 and rows
+  //    4 (lane / 16) .. +3 of its block) are contiguous, so every store writes
+  //    1 KiB of consecutive bytes.  Rows >= m and columns >= n hold garbage that
+  //    the reduction never reads.  Layout per split: [column tile][wave][MT][2][64]
+  //    float4 (see qkv_decode_epilogue_kernel).
+  //    For a single 16-token block (REG_ORDER false) the split is written row
+  //    major [m, n] instead, for the one-wave-per-(token, head) reduction, which
+  //    has the shorter latency chain when there are this few tokens.
+  if constexpr (REG_ORDER) {
+    float4* tb = reinterpret_cast<float4*>(d.part) +
+                 ((static_cast<int64_t>(blockIdx.y) * gridDim.x + blockIdx.x) * 4 + wid) * (MT * 2 * 64);
 #pragma unroll
-  for (int i = 0; i < MT; ++i)
+    for (int i = 0; i < MT; ++i)
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const int64_t row = i * 16 + lq * 4 + v;
-      if (row >= d.m) continue;
+      for (int j = 0; j < 2; ++j)
+        tb[(i * 2 + j) * 64 + lane] = make_float4(acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]);
+  } else {
+    float* dst = d.part + static_cast<int64_t>(blockIdx.y) * d.m * d.n;
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int64_t col = n0 + j * 16 + lr;
-        if (col < d.n) dst[row * d.n + col] = acc[i][j][v];
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int64_t row = i * 16 + lq * 4 + v;
+        if (row >= d.m) continue;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const int64_t col = n0 + j * 16 + lr;
+          if (col < d.n) dst[row * d.n + col] = acc[i][j][v];
+        }
+      }
+  }
+}
+
+// Split-K reduction + epilogue for the register-order partials of
+// qkv_decode_kernel.  One wave per (group of 4 tokens, head): lane p owns the
+// RoPE pair (p, p + D/2) of the head for all 4 tokens, which in the partial
+// layout is one float4 per split and column, and 16 consecutive lanes read 256
+// consecutive bytes.  The splits are summed in order (deterministic), then each
+// token goes through bias -> rounding -> per-head RMSNorm (a wave reduction per
+// token) -> rounding -> RoPE -> store, as in the prefill epilogue.
+template <int MAXP>  // RoPE pairs per lane: head_dim <= 2 * 64 * MAXP
+__global__ __launch_bounds__(256) void qkv_decode_epilogue_kernel(const float4* part, int64_t splits,
+                                                                  int64_t ntiles, int mt, int64_t m,
+                                                                  QkvEpi e) {
+  const int lane = threadIdx.x & 63;
+  const int64_t heads = e.hq + 2 * e.hkv;
+  const int64_t item = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (item >= cdiv(m, 4) * heads) return;
+  const int64_t tg = item / heads, h = item - tg * heads;
+  const int64_t i = tg / 4, lq = tg % 4;  // 16-token block, 4-token group inside it
+  const int64_t half = e.hd / 2;
+  const int kd = head_kind(e, h);
+  const int64_t base = h * e.hd;
+  const int64_t sstride = ntiles * 4 * mt * 2 * 64;  // float4 per split
+  const bool rope = kd != 2 && e.cs != nullptr;
+  const void* nw = kd == 0 ? e.qn_w : (kd == 1 ? e.kn_w : nullptr);
+  auto index = [&](int64_t c) {
+    const int64_t cw = c % 128;
+    return (((c / 128) * 4 + cw / 32) * mt * 2 + i * 2 + (cw % 32) / 16) * 64 + lq * 16 + cw % 16;
+  };
+  // Loads go out in two dependent levels: positions, bias, norm weights and
+  // the partials first; the cos/sin rows (which need the positions) next; only
+  // then arithmetic and stores.  Every load is unconditional (indices clamped,
+  // values masked) so that none waits behind a per-token or per-dtype branch.
+  // absent inputs read a valid stand-in (the partials) and are masked after
+  const void* posp = rope ? e.positions : part;
+  const void* biasp = e.bias ? e.bias : part;
+  const void* nwp = nw ? nw : part;
+  int64_t raw[4];
+  if (rope && e.pos_is_i64) {
+#pragma unroll
+    for (int v = 0; v < 4; ++v) raw[v] = static_cast<const int64_t*>(posp)[min(tg * 4 + v, m - 1)];
+  } else {
+#pragma unroll
+    for (int v = 0; v < 4; ++v) raw[v] = static_cast<const int32_t*>(posp)[min(tg * 4 + v, m - 1)];
+  }
+  float4 a1[MAXP], a2[MAXP];
+#pragma unroll
+  for (int pp = 0; pp < MAXP; ++pp) {
+    const int64_t pc = min<int64_t>(lane + 64 * pp, half - 1);
+    const float4* p1 = part + index(base + pc);
+    const float4* p2 = part + index(base + half + pc);
+    a1[pp] = a2[pp] = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int64_t sp0 = 0; sp0 < splits; sp0 += 8) {
+      // up to 8 splits in flight, summed in split order
+      float4 l1[8], l2[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int64_t sp = min(sp0 + u, splits - 1);
+        l1[u] = p1[sp * sstride];
+        l2[u] = p2[sp * sstride];
+      }
+      asm volatile("" ::: "memory");  // all 16 loads issue before the first sum waits
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const float f = sp0 + u < splits ? 1.f : 0.f;
+        a1[pp].x += f * l1[u].x; a1[pp].y += f * l1[u].y; a1[pp].z += f * l1[u].z; a1[pp].w += f * l1[u].w;
+        a2[pp].x += f * l2[u].x; a2[pp].y += f * l2[u].y; a2[pp].z += f * l2[u].z; a2[pp].w += f * l2[u].w;
       }
     }
+  }
+  int64_t pos[4];
+  bool pok[4];
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    const int32_t c = epi_pos_check(e, raw[v]);
+    pok[v] = c >= 0;
+    pos[v] = pok[v] ? c : 0;
+  }
+  float cs1[MAXP][4], sn1[MAXP][4];
+#pragma unroll
+  for (int pp = 0; pp < MAXP; ++pp) {
+    const int64_t pc = min<int64_t>(lane + 64 * pp, half - 1);
+    const float* csp = rope ? e.cs : reinterpret_cast<const float*>(part);
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int64_t o = rope ? pos[v] * e.hd : 0;
+      cs1[pp][v] = csp[o + pc];
+      sn1[pp][v] = csp[o + half + pc];
+      if (!rope) cs1[pp][v] = 1.f, sn1[pp][v] = 0.f;
+    }
+  }
+  // bias and norm weights last: their dtype dispatch waits for the loads
+  // issued before them, which by now are all in flight
+  float b1[MAXP], b2[MAXP], g1[MAXP], g2[MAXP];
+#pragma unroll
+  for (int pp = 0; pp < MAXP; ++pp) {
+    const int64_t pc = min<int64_t>(lane + 64 * pp, half - 1);  // lanes past the head re-read its last pair
+    load2_any(biasp, e.bias ? e.bias_dtype : BFA_DTYPE_F32, base + pc, base + half + pc, b1[pp], b2[pp]);
+    load2_any(nwp, nw ? e.qk_w_dtype : BFA_DTYPE_F32, pc, half + pc, g1[pp], g2[pp]);
+    if (!e.bias) b1[pp] = b2[pp] = 0.f;
+    if (!nw) g1[pp] = g2[pp] = 1.f;
+  }
+  float x1[MAXP][4], x2[MAXP][4];
+  float ss[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int pp = 0; pp < MAXP; ++pp) {
+    const float s1[4] = {a1[pp].x, a1[pp].y, a1[pp].z, a1[pp].w};
+    const float s2[4] = {a2[pp].x, a2[pp].y, a2[pp].z, a2[pp].w};
+    const bool act = lane + 64 * pp < half;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      x1[pp][v] = round_to(s1[v] + b1[pp], e.qkv_dt);
+      x2[pp][v] = round_to(s2[v] + b2[pp], e.qkv_dt);
+      if (act) ss[v] += x1[pp][v] * x1[pp][v] + x2[pp][v] * x2[pp][v];
+    }
+  }
+  int dt = e.qkv_dt;
+  if (kd != 2 && (e.qn_w || e.kn_w)) {
+#pragma unroll
+    for (int v = 0; v < 4; ++v) ss[v] = group_sum<kWave>(ss[v]);
+    if (nw) {
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const float r = 1.0f / sqrtf(ss[v] / static_cast<float>(e.hd) + e.qk_eps);
+#pragma unroll
+        for (int pp = 0; pp < MAXP; ++pp) {
+          x1[pp][v] = round_to((x1[pp][v] * r) * g1[pp], e.norm_dt);
+          x2[pp][v] = round_to((x2[pp][v] * r) * g2[pp], e.norm_dt);
+        }
+      }
+      dt = e.norm_dt;
+    }
+  }
+  if (rope && lane == 0 && h == 0) {
+#pragma unroll
+    for (int v = 0; v < 4; ++v)
+      if (!pok[v] && tg * 4 + v < m) flag_status(e.status, BFA_STATUS_INDEX_OOB);
+  }
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    const int64_t t = tg * 4 + v;
+    if (t >= m) continue;
+#pragma unroll
+    for (int pp = 0; pp < MAXP; ++pp) {
+      const int64_t p = lane + 64 * pp;
+      if (p >= half) continue;
+      float a = x1[pp][v], b = x2[pp][v];
+      if (rope) {
+        const float u = a, w = b, c = cs1[pp][v], sn = sn1[pp][v];
+        a = pok[v] ? round_to(u * c - w * sn, dt) : 0.f;
+        b = pok[v] ? round_to(w * c + u * sn, dt) : 0.f;
+      }
+      store_any(e.out, e.out_dt, t * e.ldo + base + p, a);
+      store_any(e.out, e.out_dt, t * e.ldo + base + half + p, b);
+    }
+  }
 }
 
 // ============================================== reduction + row epilogue
@@ -968,7 +1157,10 @@ static QkvPlan make_plan(int64_t m, int64_t n, int64_t k, int64_t hd) {
       p.kchunk = cdiv(cdiv(k, splits), 64) * 64;
       p.splits = cdiv(k, p.kchunk);
     }
-    p.part_bytes = align256(p.splits * m * n * 4);
+    // stream kernel from 2 token blocks: register-order partial tiles padded to
+    // 128 columns x 16 MT rows; otherwise row-major [splits, m, n]
+    p.part_bytes = (p.stream && p.mt > 1) ? align256(p.splits * cdiv(n, 128) * 128 * p.mt * 16 * 4)
+                                          : align256(p.splits * m * n * 4);
   } else {
     p.decode = false;
     p.fused_epi = (hd == 32 || hd == 64 || hd == 128) && n % hd == 0;
@@ -1003,15 +1195,16 @@ static void launch_decode_cpw(const QkvPlan& p, const SplitArgs& s, hipStream_t 
 
 template <int MT, bool BF16>
 static void launch_stream(int ks, dim3 grid, const DecodeArgs& d, hipStream_t st) {
+  constexpr bool RO = MT > 1;  // register-order partials from two 16-token blocks up
   switch (ks) {
-    case 1: hipLaunchKernelGGL((qkv_decode_kernel<MT, 1, BF16>), grid, dim3(256), 0, st, d); break;
-    case 2: hipLaunchKernelGGL((qkv_decode_kernel<MT, 2, BF16>), grid, dim3(256), 0, st, d); break;
-    case 3: hipLaunchKernelGGL((qkv_decode_kernel<MT, 3, BF16>), grid, dim3(256), 0, st, d); break;
-    case 4: hipLaunchKernelGGL((qkv_decode_kernel<MT, 4, BF16>), grid, dim3(256), 0, st, d); break;
-    case 5: hipLaunchKernelGGL((qkv_decode_kernel<MT, 5, BF16>), grid, dim3(256), 0, st, d); break;
-    case 6: hipLaunchKernelGGL((qkv_decode_kernel<MT, 6, BF16>), grid, dim3(256), 0, st, d); break;
-    case 7: hipLaunchKernelGGL((qkv_decode_kernel<MT, 7, BF16>), grid, dim3(256), 0, st, d); break;
-    default: hipLaunchKernelGGL((qkv_decode_kernel<MT, 8, BF16>), grid, dim3(256), 0, st, d); break;
+    case 1: hipLaunchKernelGGL((qkv_decode_kernel<MT, 1, BF16, RO>), grid, dim3(256), 0, st, d); break;
+    case 2: hipLaunchKernelGGL((qkv_decode_kernel<MT, 2, BF16, RO>), grid, dim3(256), 0, st, d); break;
+    case 3: hipLaunchKernelGGL((qkv_decode_kernel<MT, 3, BF16, RO>), grid, dim3(256), 0, st, d); break;
+    case 4: hipLaunchKernelGGL((qkv_decode_kernel<MT, 4, BF16, RO>), grid, dim3(256), 0, st, d); break;
+    case 5: hipLaunchKernelGGL((qkv_decode_kernel<MT, 5, BF16, RO>), grid, dim3(256), 0, st, d); break;
+    case 6: hipLaunchKernelGGL((qkv_decode_kernel<MT, 6, BF16, RO>), grid, dim3(256), 0, st, d); break;
+    case 7: hipLaunchKernelGGL((qkv_decode_kernel<MT, 7, BF16, RO>), grid, dim3(256), 0, st, d); break;
+    default: hipLaunchKernelGGL((qkv_decode_kernel<MT, 8, BF16, RO>), grid, dim3(256), 0, st, d); break;
   }
 }
 
@@ -1139,6 +1332,8 @@ extern "C" int bfa_qkv_projection(const void* operand, int64_t tokens, int64_t h
   BFA_REQUIRE(part_workspace_bytes >= p.part_bytes && (p.part_bytes == 0 || part_workspace),
               "%s: workspace too small (%lld < %lld bytes)", what, (long long)part_workspace_bytes,
               (long long)p.part_bytes);
+  BFA_REQUIRE(p.part_bytes == 0 || aligned16(part_workspace), "%s: workspace must be 16-byte aligned",
+              what);
 
   QkvEpi e{};
   e.bias = bias; e.bias_dtype = bias_dtype;
@@ -1161,7 +1356,23 @@ extern "C" int bfa_qkv_projection(const void* operand, int64_t tokens, int64_t h
     if (bf16) launch_decode<true>(p, s, st); else launch_decode<false>(p, s, st);
     int rc = check_launch(what);
     if (rc != BFA_OK) return rc;
-    launch_epilogue(part, p.splits, tokens, e, st);
+    if (p.stream && p.mt > 1) {
+      const int64_t items = cdiv(tokens, 4) * heads;
+      const dim3 grid(static_cast<unsigned>(cdiv(items, 4)));
+      const float4* p4 = reinterpret_cast<const float4*>(part);
+      if (hd <= 128) {
+        hipLaunchKernelGGL(qkv_decode_epilogue_kernel<1>, grid, dim3(256), 0, st, p4, p.splits,
+                           cdiv(qkv_dim, 128), p.mt, tokens, e);
+      } else if (hd <= 256) {
+        hipLaunchKernelGGL(qkv_decode_epilogue_kernel<2>, grid, dim3(256), 0, st, p4, p.splits,
+                           cdiv(qkv_dim, 128), p.mt, tokens, e);
+      } else {
+        hipLaunchKernelGGL(qkv_decode_epilogue_kernel<4>, grid, dim3(256), 0, st, p4, p.splits,
+                           cdiv(qkv_dim, 128), p.mt, tokens, e);
+      }
+    } else {
+      launch_epilogue(part, p.splits, tokens, e, st);
+    }
     return check_launch(what);
   }
   GemmArgs g{};
