@@ -246,9 +246,7 @@ def config_table(dev, iters: int) -> dict:
             for name, fn, nbytes, flops in config_cases(dev)}
 
 
-def time_graph(fn, iters: int, reps: int = 20) -> float:
-    """Average milliseconds per call of `fn` captured `reps` times into one HIP
-    graph and replayed: the GPU time of the kernels without Python launch gaps."""
+def _capture(fn, reps: int) -> torch.cuda.CUDAGraph:
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(side):
@@ -259,8 +257,27 @@ def time_graph(fn, iters: int, reps: int = 20) -> float:
     with torch.cuda.graph(graph):
         for _ in range(reps):
             fn()
-    graph.replay()
-    torch.cuda.synchronize()
+    return graph
+
+
+def _settle(graph: torch.cuda.CUDAGraph, min_s: float) -> None:
+    """Replays `graph` until `min_s` seconds have passed: the GPU clock ramps up
+    over the first ~100 ms of sustained load, so a measurement that starts cold
+    reads up to 30 % slow."""
+    t0 = time.perf_counter()
+    while True:
+        graph.replay()
+        torch.cuda.synchronize()
+        if time.perf_counter() - t0 >= min_s:
+            return
+
+
+def time_graph(fn, iters: int, reps: int = 20, settle_s: float = 0.2) -> float:
+    """Average milliseconds per call of `fn` captured `reps` times into one HIP
+    graph and replayed (after `settle_s` seconds of untimed replays): the GPU
+    time of the kernels without Python launch gaps."""
+    graph = _capture(fn, reps)
+    _settle(graph, settle_s)
     s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     n = max(1, iters // reps)
     s.record()
@@ -308,8 +325,22 @@ def cold_decode_table(dev, t: int, iters: int) -> dict:
     return out
 
 
-def chain_graph_us(c: Chain, steps: int) -> float:
-    return time_graph(c.step, steps) * 1e3
+def chain_graph_us(c: Chain, steps: int, warmup: int) -> float:
+    """Microseconds per chain step: `steps` steps captured into one HIP graph;
+    `warmup` untimed steps (whole replays of the graph, at least one), then
+    exactly `steps` timed steps between HIP events."""
+    graph = _capture(c.step, steps)
+    done = 0
+    while done < max(warmup, 1):
+        graph.replay()
+        done += steps
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    graph.replay()
+    e.record()
+    torch.cuda.synchronize()
+    return s.elapsed_time(e) / steps * 1e3
 
 
 def chain_us(c: Chain, steps: int, warmup: int) -> float:
@@ -406,8 +437,8 @@ def profile_one(kernel: str, tokens: int, steps: int, dev) -> int:
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=300)
     ap.add_argument("--tokens", type=int, default=8192)
     ap.add_argument("--decode-tokens", type=int, default=64)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
@@ -437,7 +468,7 @@ def main(argv=None) -> int:
     progress(f"prefill chain, {args.tokens} tokens")
     prefill = Chain(args.tokens, dev)
     us_eager = chain_us(prefill, args.steps, args.warmup)
-    us = chain_graph_us(prefill, args.steps)
+    us = chain_graph_us(prefill, args.steps, args.warmup)
     kp = kernel_table(prefill, dev, max(10, args.steps))
     proj = kp["qkv_projection_rope"]
     del prefill
@@ -446,7 +477,7 @@ def main(argv=None) -> int:
     progress(f"decode chain, {args.decode_tokens} tokens")
     decode = Chain(args.decode_tokens, dev)
     us_dec_eager = chain_us(decode, max(args.steps, 100), args.warmup)
-    us_dec = chain_graph_us(decode, max(args.steps, 100))
+    us_dec = chain_graph_us(decode, max(args.steps, 100), max(args.warmup, 1000))
     kd = kernel_table(decode, dev, max(50, args.steps))
     del decode
     torch.cuda.empty_cache()

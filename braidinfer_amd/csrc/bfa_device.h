@@ -110,6 +110,23 @@ __device__ __forceinline__ float load_any(const void* p, int dt, int64_t i) {
   return load1<BFA_DTYPE_F32>(p, i);
 }
 
+// ------------------------------------------------------- integer division
+// n / d for 32-bit n < 2^31 and 1 <= d < 2^31 by multiply-high (the
+// round-up reciprocal method of Granlund and Montgomery, "Division by invariant
+// integers using multiplication", 1994): with s = ceil(log2 d) and
+// m = floor(2^32 (2^s - d) / d) + 1, n / d = (mulhi(n, m) + n) >> s.  Built on
+// the host, used in kernels whose flat index must be split into (row, column).
+struct FastDiv {
+  uint32_t d = 1, m = 1, s = 0;
+  FastDiv() = default;
+  __host__ explicit FastDiv(uint32_t div) : d(div) {
+    s = 0;
+    while ((uint64_t{1} << s) < div) ++s;
+    m = static_cast<uint32_t>(((uint64_t{1} << 32) * ((uint64_t{1} << s) - div)) / div + 1);
+  }
+  __device__ __forceinline__ uint32_t div(uint32_t n) const { return (__umulhi(n, m) + n) >> s; }
+};
+
 // ------------------------------------------------------------- reductions
 // Butterfly sum over aligned groups of L lanes (L a power of two <= 64).
 template <int L>

@@ -1,9 +1,9 @@
 // Row-wise RMSNorm family on gfx950.
 //
 // One kernel template serves every RMSNorm flavour on the hot path; they
-// differ only in rounding points and in whether the statistic is applied as a
-// multiplication by rsqrt (torch op chain) or a division by sqrt (the Triton
-// kernels):
+// differ only in their rounding points (the torch op chain multiplies by
+// rsqrt(var + eps), the Triton kernels divide by sqrt(mean + eps); both are
+// computed here as a multiply by one reciprocal per row):
 //   kRms          RMSNorm.rms_forward         layers/layernorm.py:35-44
 //   kAddRms       RMSNorm.add_rms_forward     layers/layernorm.py:46-57
 //   kF32          RMSNormF32.forward          kernels/rmsnorm_f32.py:47-96
@@ -50,29 +50,28 @@ __device__ __forceinline__ void load8_dyn(const void* p, int dt, int64_t i, floa
   }
 }
 
-// Applies the mode's normalisation to one value.  `stat` is rsqrt(var+eps)
-// for the torch-chain modes and sqrt(sum/H+eps) for the Triton-kernel modes.
+// Applies the mode's normalisation to one value.  `inv` = 1 / sqrt(sum/H + eps)
+// for every mode: the torch chain multiplies by rsqrt(var + eps), and the
+// Triton kernels' x / rms is computed as x * (1 / rms) -- one correctly rounded
+// reciprocal per row, then a multiply, within 1.5 fp32 ulp of the quotient
+// (a per-element IEEE division costs about ten VALU instructions, which made
+// the operand pre-pass ALU-bound).
 template <int DT_IN, int MODE>
-__device__ __forceinline__ float norm_apply(float v, float stat, float g) {
+__device__ __forceinline__ float norm_apply(float v, float inv, float g) {
   if constexpr (MODE == kRms || MODE == kAddRms) {
     // x.mul_(rsqrt(var+eps)); x.to(orig_dtype).mul_(weight)
-    return Elem<DT_IN>::round(v * stat) * g;
+    return Elem<DT_IN>::round(v * inv) * g;
   } else if constexpr (MODE == kOperandMixed) {
     // (x / rms) -> bf16, then * weight (result rounded by the store)
-    return round_bf16(v / stat) * g;
+    return round_bf16(v * inv) * g;
   } else {
     // kF32 / kOperandProd: (x / rms) * weight in fp32
-    return (v / stat) * g;
+    return (v * inv) * g;
   }
 }
 
-template <int MODE>
-__device__ __forceinline__ float norm_stat(float ss, int64_t hidden, float eps) {
-  if constexpr (MODE == kRms || MODE == kAddRms) {
-    return 1.0f / sqrtf(ss / static_cast<float>(hidden) + eps);
-  } else {
-    return sqrtf(ss / static_cast<float>(hidden) + eps);
-  }
+__device__ __forceinline__ float norm_inv(float ss, int64_t hidden, float eps) {
+  return 1.0f / sqrtf(ss / static_cast<float>(hidden) + eps);
 }
 
 template <int DT_IN, int DT_OUT, int MODE, int L, int MAXC>
@@ -85,7 +84,7 @@ __global__ __launch_bounds__(256) void norm_vec_kernel(NormArgs a) {
   const int64_t row = static_cast<int64_t>(blockIdx.x) * RPW + ((L >= 256) ? 0 : tid / L);
   if (row >= a.rows) return;  // uniform per row group (whole WG when L == 256)
 
-  const int64_t ro = row / a.rows_inner, ri = row - ro * a.rows_inner;
+  const int64_t ro = a.rows_inner == 1 ? row : row / a.rows_inner, ri = row - ro * a.rows_inner;
   const TIN* xp = static_cast<const TIN*>(a.x) + ro * a.x_so + ri * a.x_si;
   TOUT* yp = static_cast<TOUT*>(a.y) + ro * a.y_so + ri * a.y_si;
   const int nchunks = static_cast<int>(a.hidden / 8);
@@ -117,7 +116,7 @@ __global__ __launch_bounds__(256) void norm_vec_kernel(NormArgs a) {
 #pragma unroll
     for (int w = 0; w < L / kWave; ++w) ss += red[w];
   }
-  const float stat = norm_stat<MODE>(ss, a.hidden, a.eps);
+  const float inv = norm_inv(ss, a.hidden, a.eps);
 
 #pragma unroll
   for (int c = 0; c < MAXC; ++c) {
@@ -126,7 +125,7 @@ __global__ __launch_bounds__(256) void norm_vec_kernel(NormArgs a) {
       float g[8], o[8];
       load8_dyn(a.w, a.w_dtype, static_cast<int64_t>(ch) * 8, g);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) o[i] = norm_apply<DT_IN, MODE>(v[c][i], stat, g[i]);
+      for (int i = 0; i < 8; ++i) o[i] = norm_apply<DT_IN, MODE>(v[c][i], inv, g[i]);
       store8<DT_OUT>(yp + ch * 8, o);
     }
   }
@@ -155,7 +154,7 @@ __global__ __launch_bounds__(256) void norm_scalar_kernel(NormArgs a) {
   ss = 0.f;
 #pragma unroll
   for (int w = 0; w < 256 / kWave; ++w) ss += red[w];
-  const float stat = norm_stat<MODE>(ss, a.hidden, a.eps);
+  const float inv = norm_inv(ss, a.hidden, a.eps);
 
   for (int64_t i = tid; i < a.hidden; i += 256) {
     float v = load1<DT_IN>(a.x, xoff + i * a.x_sc);
@@ -164,7 +163,7 @@ __global__ __launch_bounds__(256) void norm_scalar_kernel(NormArgs a) {
       if (a.res_out) store1<DT_IN>(a.res_out, row * a.ro_s + i, v);
     }
     const float g = load_any(a.w, a.w_dtype, i);
-    store1<DT_OUT>(a.y, yoff + i * a.y_sc, norm_apply<DT_IN, MODE>(v, stat, g));
+    store1<DT_OUT>(a.y, yoff + i * a.y_sc, norm_apply<DT_IN, MODE>(v, inv, g));
   }
 }
 

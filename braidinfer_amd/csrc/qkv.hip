@@ -118,6 +118,33 @@ __device__ __forceinline__ void store4_any(void* p, int dt, int64_t i, const flo
   }
 }
 
+// Branch-free forms for the GEMM epilogue, whose code is unrolled over every
+// row a lane owns: a rounding or store that dispatches on the dtype with
+// branches there grew the kernel past the instruction cache.  dt is uniform.
+__device__ __forceinline__ float round_sel(float v, int dt) {
+  const float rb = Elem<BFA_DTYPE_BF16>::round(v);
+  const float rh = Elem<BFA_DTYPE_F16>::round(v);
+  return dt == BFA_DTYPE_BF16 ? rb : (dt == BFA_DTYPE_F16 ? rh : v);
+}
+
+__device__ __forceinline__ uint32_t pack2_sel(float lo, float hi, bool bf) {
+  const uint32_t b = f32_to_bf16_bits(lo) | (static_cast<uint32_t>(f32_to_bf16_bits(hi)) << 16);
+  const uint32_t h = f32_to_f16_bits(lo) | (static_cast<uint32_t>(f32_to_f16_bits(hi)) << 16);
+  return bf ? b : h;
+}
+
+// 4 consecutive elements (column multiple of 4, row stride multiple of 4):
+// one 16-byte store for fp32, one 8-byte store for the 16-bit types.
+__device__ __forceinline__ void store4_sel(void* p, int dt, int64_t i, const float (&v)[4]) {
+  if (dt == BFA_DTYPE_F32) {
+    *reinterpret_cast<float4*>(static_cast<float*>(p) + i) = make_float4(v[0], v[1], v[2], v[3]);
+  } else {
+    const bool bf = dt == BFA_DTYPE_BF16;
+    *reinterpret_cast<uint2*>(static_cast<uint16_t*>(p) + i) =
+        make_uint2(pack2_sel(v[0], v[1], bf), pack2_sel(v[2], v[3], bf));
+  }
+}
+
 // 0 = q head, 1 = k head, 2 = v head
 __device__ __forceinline__ int head_kind(const QkvEpi& e, int64_t head) {
   return head < e.hq ? 0 : (head < e.hq + e.hkv ? 1 : 2);
@@ -570,12 +597,30 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, (WM * WN <= 8192 ? 2 : 
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < MB; ++i) {
+      // The cos/sin rows of the block's 8 rows are all requested before the
+      // accumulators are staged: in the row loop below each load would sit
+      // behind the previous row's stores (the table and the output may alias
+      // as far as the compiler knows), paying the table's L2 latency 8 times.
+      float4 cvv[8], svv[8];
+      if (rope) {
+#pragma unroll
+        for (int it = 0; it < 8; ++it) {
+          const int64_t p = posv[i][it] >= 0 ? posv[i][it] : 0;
+          cvv[it] = *reinterpret_cast<const float4*>(e.cs + p * HD + q * 4);
+          svv[it] = *reinterpret_cast<const float4*>(e.cs + p * HD + HD / 2 + q * 4);
+        }
+      }
 #pragma unroll
       for (int j = 0; j < NB; ++j)
 #pragma unroll
         for (int v = 0; v < 16; ++v)
           et[(8 * (v / 4) + 4 * fhalf + (v % 4)) * LDR + j * 32 + frow] = acc[i][j][v];
-      __syncthreads();
+      // The slice is private to this wave and LDS executes one wave's accesses
+      // in issue order, so the row reads below see these writes (and the next
+      // block's writes follow this block's reads) without a barrier; only the
+      // compiler's order must be kept.
+      __asm__ volatile("" ::: "memory");
+      bool bad = false;
 #pragma unroll
       for (int it = 0; it < 8; ++it) {
         const int rl = rg + 4 * it;
@@ -586,8 +631,8 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, (WM * WN <= 8192 ? 2 : 
         float ss = 0.f;
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
-          x1[t] = round_to(x1[t] + b1[t], e.qkv_dt);
-          x2[t] = round_to(x2[t] + b2[t], e.qkv_dt);
+          x1[t] = round_sel(x1[t] + b1[t], e.qkv_dt);
+          x2[t] = round_sel(x2[t] + b2[t], e.qkv_dt);
           ss += x1[t] * x1[t] + x2[t] * x2[t];
         }
         if (any_norm) {
@@ -596,31 +641,30 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, (WM * WN <= 8192 ? 2 : 
             const float r = 1.0f / sqrtf(ss / static_cast<float>(HD) + e.qk_eps);
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
-              x1[t] = round_to((x1[t] * r) * g1[t], e.norm_dt);
-              x2[t] = round_to((x2[t] * r) * g2[t], e.norm_dt);
+              x1[t] = round_sel((x1[t] * r) * g1[t], e.norm_dt);
+              x2[t] = round_sel((x2[t] * r) * g2[t], e.norm_dt);
             }
           }
         }
         if (rope) {
           const bool ok = posv[i][it] >= 0;
-          const int64_t p = ok ? posv[i][it] : 0;
-          if (!ok && row < g.m && q == 0) flag_status(e.status, BFA_STATUS_INDEX_OOB);
-          const float4 cv = *reinterpret_cast<const float4*>(e.cs + p * HD + q * 4);
-          const float4 sv = *reinterpret_cast<const float4*>(e.cs + p * HD + HD / 2 + q * 4);
+          bad = bad || (!ok && row < g.m);
+          const float4 cv = cvv[it], sv = svv[it];
           const float c[4] = {cv.x, cv.y, cv.z, cv.w}, sn[4] = {sv.x, sv.y, sv.z, sv.w};
 #pragma unroll
           for (int t = 0; t < 4; ++t) {
             const float u = x1[t], w = x2[t];
-            x1[t] = ok ? round_to(u * c[t] - w * sn[t], dt_after) : 0.f;
-            x2[t] = ok ? round_to(w * c[t] + u * sn[t], dt_after) : 0.f;
+            x1[t] = ok ? round_sel(u * c[t] - w * sn[t], dt_after) : 0.f;
+            x2[t] = ok ? round_sel(w * c[t] + u * sn[t], dt_after) : 0.f;
           }
         }
         if (row < g.m && colok) {
-          store4_any(e.out, e.out_dt, row * e.ldo + gc1, x1);
-          store4_any(e.out, e.out_dt, row * e.ldo + gc2, x2);
+          store4_sel(e.out, e.out_dt, row * e.ldo + gc1, x1);
+          store4_sel(e.out, e.out_dt, row * e.ldo + gc2, x2);
         }
       }
-      __syncthreads();
+      if (bad && q == 0) flag_status(e.status, BFA_STATUS_INDEX_OOB);
+      __asm__ volatile("" ::: "memory");
     }
   }
 }

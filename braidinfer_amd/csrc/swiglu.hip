@@ -3,9 +3,16 @@
 // torch rounds twice for a reduced-float x: F.silu computes g/(1+exp(-g)) in
 // fp32 and rounds to the tensor dtype, then the product of two reduced-float
 // tensors is computed in fp32 and rounded again.  The kernel keeps both
-// rounding points.  Each lane owns 8 consecutive outputs: one 16-byte load of
-// gate, one of up, one 16-byte store (fp32: two of each), so a row of
-// [T, 2I] is streamed once and the [T, I] result written once.
+// rounding points.  Each lane owns 2 x 8 outputs of one flattened
+// (row, 8-column chunk) index space: two 16-byte loads of gate and of up are in
+// flight together, then two 16-byte stores, so a row of [T, 2I] is streamed once
+// and the [T, I] result written once.
+//
+// The arithmetic is kept small enough that the kernel stays bound by HBM: the
+// sigmoid is 1/(1 + 2^(-g log2 e)) with the hardware base-2 exponential and
+// reciprocal (v_exp_f32, v_rcp_f32; about 1 ulp each in fp32, far below the
+// bf16 rounding that follows), and the chunk index is split into (row, column)
+// with a 32-bit multiply-high division instead of a 64-bit divide.
 #include "bfa_device.h"
 #include "bfa_host.h"
 
@@ -15,27 +22,45 @@ struct SwigluArgs {
   const void* x;
   void* y;
   int64_t rows, inter, x_stride, y_stride;
-  int64_t chunks_per_row;  // inter / 8
-  int64_t total;           // rows * chunks_per_row
+  FastDiv cpr;      // division by chunks per row (inter / 8)
+  uint32_t total;   // rows * chunks per row (< 2^31)
 };
 
-__device__ __forceinline__ float silu_f32(float g) { return g / (1.0f + expf(-g)); }
+// silu(g) = g * sigmoid(g), sigmoid(g) = 1 / (1 + 2^(-g * log2(e)))
+__device__ __forceinline__ float silu_fast(float g) {
+  const float e = __builtin_amdgcn_exp2f(g * -1.4426950408889634f);
+  return g * __builtin_amdgcn_rcpf(1.0f + e);
+}
+
+constexpr int kSwigluPerLane = 2;  // 8-column chunks per lane
 
 template <int DT>
 __global__ __launch_bounds__(256) void silu_mul_vec_kernel(SwigluArgs a) {
   using T = typename Elem<DT>::T;
-  const int64_t stride = static_cast<int64_t>(gridDim.x) * 256;
-  for (int64_t item = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; item < a.total;
-       item += stride) {
-    const int64_t row = item / a.chunks_per_row;
-    const int64_t col = (item - row * a.chunks_per_row) * 8;
-    const T* xr = static_cast<const T*>(a.x) + row * a.x_stride;
-    float g[8], u[8], o[8];
-    load8<DT>(xr + col, g);
-    load8<DT>(xr + a.inter + col, u);
+  constexpr int U = kSwigluPerLane;
+  const uint32_t item0 = blockIdx.x * (256u * U) + threadIdx.x;
+  float g[U][8], u[U][8];
+  int64_t yoff[U];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) o[i] = Elem<DT>::round(silu_f32(g[i])) * u[i];
-    store8<DT>(static_cast<T*>(a.y) + row * a.y_stride + col, o);
+  for (int c = 0; c < U; ++c) {
+    const uint32_t item = item0 + c * 256u;
+    yoff[c] = -1;
+    if (item < a.total) {
+      const uint32_t row = a.cpr.div(item);
+      const uint32_t col = (item - row * a.cpr.d) * 8u;
+      const T* xr = static_cast<const T*>(a.x) + row * a.x_stride + col;
+      load8<DT>(xr, g[c]);
+      load8<DT>(xr + a.inter, u[c]);
+      yoff[c] = row * a.y_stride + col;
+    }
+  }
+#pragma unroll
+  for (int c = 0; c < U; ++c) {
+    if (yoff[c] < 0) continue;
+    float o[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o[i] = Elem<DT>::round(silu_fast(g[c][i])) * u[c][i];
+    store8<DT>(static_cast<T*>(a.y) + yoff[c], o);
   }
 }
 
@@ -49,19 +74,19 @@ __global__ __launch_bounds__(256) void silu_mul_scalar_kernel(SwigluArgs a) {
     const int64_t col = item - row * a.inter;
     const float g = load1<DT>(a.x, row * a.x_stride + col);
     const float u = load1<DT>(a.x, row * a.x_stride + a.inter + col);
-    store1<DT>(a.y, row * a.y_stride + col, Elem<DT>::round(silu_f32(g)) * u);
+    store1<DT>(a.y, row * a.y_stride + col, Elem<DT>::round(silu_fast(g)) * u);
   }
 }
 
 template <int DT>
 static void launch_silu(const SwigluArgs& a, bool vec, hipStream_t s) {
-  // Grid: enough workgroups to cover the tensor once, capped so that each lane
-  // loops a few times on large tensors (256 CUs x 16 resident workgroups).
-  const int64_t items = vec ? a.total : a.rows * a.inter;
-  const int64_t grid = std::max<int64_t>(1, std::min<int64_t>(cdiv(items, 256), 256 * 16));
   if (vec) {
+    const int64_t grid = std::max<int64_t>(1, cdiv(a.total, 256 * kSwigluPerLane));
     hipLaunchKernelGGL((silu_mul_vec_kernel<DT>), dim3(grid), dim3(256), 0, s, a);
   } else {
+    // grid-stride: enough workgroups to cover the tensor once, capped so that
+    // each lane loops a few times on large tensors (256 CUs x 16 workgroups)
+    const int64_t grid = std::max<int64_t>(1, std::min<int64_t>(cdiv(a.rows * a.inter, 256), 256 * 16));
     hipLaunchKernelGGL((silu_mul_scalar_kernel<DT>), dim3(grid), dim3(256), 0, s, a);
   }
 }
@@ -80,10 +105,13 @@ extern "C" int bfa_silu_and_mul(const void* x, void* y, int dtype, int64_t rows,
   SwigluArgs a{};
   a.x = x; a.y = y; a.rows = rows; a.inter = inter;
   a.x_stride = x_row_stride; a.y_stride = y_row_stride;
-  a.chunks_per_row = inter / 8;
-  a.total = rows * a.chunks_per_row;
+  const int64_t total = rows * (inter / 8);
   const bool vec = inter % 8 == 0 && x_row_stride % 8 == 0 && y_row_stride % 8 == 0 &&
-                   aligned16(x) && aligned16(y);
+                   aligned16(x) && aligned16(y) && total < (int64_t{1} << 31);
+  if (vec) {
+    a.cpr = FastDiv(static_cast<uint32_t>(inter / 8));
+    a.total = static_cast<uint32_t>(total);
+  }
   const hipStream_t s = as_stream(stream);
   switch (dtype) {
     case BFA_DTYPE_BF16: launch_silu<BFA_DTYPE_BF16>(a, vec, s); break;
