@@ -70,7 +70,7 @@ __global__ __launch_bounds__(256) void gather_vec_kernel(GatherArgs a) {
 #pragma unroll
   for (int c = 0; c < CPT; ++c) {
     const int64_t ch = base + c * 256;
-    if (ch < a.row_chunks) v[c] = ok ? src[ch] : make_uint4(0, 0, 0, 0);
+    if (ch < a.row_chunks) v[c] = ok ? load16_nt(src + ch) : make_uint4(0, 0, 0, 0);
   }
 #pragma unroll
   for (int c = 0; c < CPT; ++c) {

@@ -95,10 +95,10 @@ __global__ __launch_bounds__(256) void norm_vec_kernel(NormArgs a) {
   for (int c = 0; c < MAXC; ++c) {
     const int ch = lane + c * L;
     if (ch < nchunks) {
-      load8<DT_IN>(xp + ch * 8, v[c]);
+      load8_nt<DT_IN>(xp + ch * 8, v[c]);
       if constexpr (MODE == kAddRms) {
         float r[8];
-        load8<DT_IN>(static_cast<const TIN*>(a.res) + row * a.r_s + ch * 8, r);
+        load8_nt<DT_IN>(static_cast<const TIN*>(a.res) + row * a.r_s + ch * 8, r);
 #pragma unroll
         for (int i = 0; i < 8; ++i) v[c][i] = v[c][i] + r[i];
         if (a.res_out) store8<DT_IN>(static_cast<TIN*>(a.res_out) + row * a.ro_s + ch * 8, v[c]);

@@ -107,8 +107,8 @@ __global__ __launch_bounds__(256) void rope_vec_kernel(RopeArgs a, int64_t total
   if (ok) {
     const T* xp = static_cast<const T*>(tt.x) + tok * tt.s_tok + head * tt.s_head;
     float c[8], s[8];
-    load8<DT>(xp + j, x1);
-    load8<DT>(xp + half + j, x2);
+    load8_nt<DT>(xp + j, x1);
+    load8_nt<DT>(xp + half + j, x2);
     load8<BFA_DTYPE_F32>(crow + j, c);
     load8<BFA_DTYPE_F32>(srow + j, s);
     rotate8(x1, x2, c, s);
@@ -249,8 +249,8 @@ __global__ __launch_bounds__(256) void rerotate_kernel(RerotArgs a) {
     }
     T* src = kpage + tok * a.head_dim;
     float x1[8], x2[8];
-    load8<DT>(src + j, x1);
-    load8<DT>(src + half + j, x2);
+    load8_nt<DT>(src + j, x1);
+    load8_nt<DT>(src + half + j, x2);
     if (rotate) {
       rotate8(x1, x2, cs, sn);
 #pragma unroll

@@ -36,8 +36,8 @@ constexpr int kSwigluPerLane = 2;  // 8-column chunks per lane
 
 template <int DT>
 __global__ __launch_bounds__(256) void silu_mul_vec_kernel(SwigluArgs a) {
-  using T = typename Elem<DT>::T;
   constexpr int U = kSwigluPerLane;
+  using T = typename Elem<DT>::T;
   const uint32_t item0 = blockIdx.x * (256u * U) + threadIdx.x;
   float g[U][8], u[U][8];
   int64_t yoff[U];
@@ -49,8 +49,8 @@ __global__ __launch_bounds__(256) void silu_mul_vec_kernel(SwigluArgs a) {
       const uint32_t row = a.cpr.div(item);
       const uint32_t col = (item - row * a.cpr.d) * 8u;
       const T* xr = static_cast<const T*>(a.x) + row * a.x_stride + col;
-      load8<DT>(xr, g[c]);
-      load8<DT>(xr + a.inter, u[c]);
+      load8_nt<DT>(xr, g[c]);
+      load8_nt<DT>(xr + a.inter, u[c]);
       yoff[c] = row * a.y_stride + col;
     }
   }
