@@ -565,6 +565,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, (WM * WN <= 8192 ? 2 : 
     const void* nw = kd == 0 ? e.qn_w : (kd == 1 ? e.kn_w : nullptr);
     const bool any_norm = e.qn_w != nullptr || e.kn_w != nullptr;
     const bool rope = e.cs != nullptr && kd != 2;
+    const bool has_bias = e.bias != nullptr;
     float b1[4], b2[4], g1[4], g2[4];
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
@@ -628,14 +629,22 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, (WM * WN <= 8192 ? 2 : 
         const float4 a1 = *reinterpret_cast<const float4*>(et + rl * LDR + c1);
         const float4 a2 = *reinterpret_cast<const float4*>(et + rl * LDR + c2);
         float x1[4] = {a1.x, a1.y, a1.z, a1.w}, x2[4] = {a2.x, a2.y, a2.z, a2.w};
-        float ss = 0.f;
+        if (has_bias) {
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            x1[t] = x1[t] + b1[t];
+            x2[t] = x2[t] + b2[t];
+          }
+        }
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
-          x1[t] = round_sel(x1[t] + b1[t], e.qkv_dt);
-          x2[t] = round_sel(x2[t] + b2[t], e.qkv_dt);
-          ss += x1[t] * x1[t] + x2[t] * x2[t];
+          x1[t] = round_sel(x1[t], e.qkv_dt);
+          x2[t] = round_sel(x2[t], e.qkv_dt);
         }
         if (any_norm) {
+          float ss = 0.f;
+#pragma unroll
+          for (int t = 0; t < 4; ++t) ss += x1[t] * x1[t] + x2[t] * x2[t];
           ss = group_sum<LH>(ss);  // lanes of one head form an aligned group
           if (nw) {
             const float r = 1.0f / sqrtf(ss / static_cast<float>(HD) + e.qk_eps);
