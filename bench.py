@@ -178,7 +178,9 @@ def config_cases(dev) -> list:
       qwen3       fused RMSNorm+QKV(1024 -> 4096, 16/8 heads, D 128)+q/k norm+RoPE(theta 1e6), T 1/2048
       rerotate    paged K [256 pages, 2, 8, 16, 128] in shuffled page order, 16 chunks of
                   16 pages, delta U[-4096, 4096], theta 1e6, rotated copy out
-      swiglu      SiLU*mul [2048, 2 x 3072]"""
+      swiglu      SiLU*mul [2048, 2 x 3072]
+      kv_append   paged KV append, 8 kv heads x 128, page 16: 8192-token prefill,
+                  and a 64-sequence decode batch in one launch"""
     from braidinfer_amd.layers import llama_attention_input, qwen3_attention_input, rerotate_paged_k
     bf = torch.bfloat16
     cases = []
@@ -237,6 +239,31 @@ def config_cases(dev) -> list:
     gu = randn(2048, 2 * 3072)
     silu = SiluAndMul()
     cases.append(("swiglu_t2048_i3072", lambda: silu(gu), 3 * 2048 * 3072 * 2, 0.0))
+
+    # paged KV append at Llama-3-8B kv geometry (8 heads x 128, page 16, HND):
+    # an 8192-token prefill into 512 of 1024 shuffled pages, and a 64-sequence
+    # decode batch (one new token each) in one batched launch
+    from braidinfer_amd.kernels import append_paged_kv_batch, append_to_paged_kv_cache_custom
+    g, randn = gen(6)
+    hkv, d, ps, pages = 8, 128, 16, 1024
+    kvc = randn(pages, 2, hkv, ps, d)
+    table = torch.randperm(pages, generator=g)[:512].to(torch.int32).to(dev)
+    kp, vp = randn(8192, hkv, d), randn(8192, hkv, d)
+    pp = torch.arange(8192, dtype=torch.int32, device=dev)
+    cases.append(("kv_append_t8192", lambda: append_to_paged_kv_cache_custom(kp, vp, kvc, table, pp, ps),
+                  4 * 8192 * hkv * d * 2 + 8192 * 4 + 512 * 4, 0.0))
+    lens = torch.randint(0, 4000, (64,), generator=g)
+    perm = torch.randperm(pages, generator=g)
+    # sequence s: a table of lens[s] // 16 + 1 entries whose last (the one written) is a
+    # page of its own
+    per = lens // ps + 1
+    ind = torch.cat([perm[s].repeat(int(per[s])) for s in range(64)]).to(torch.int32).to(dev)
+    indptr = torch.cat([torch.zeros(1, dtype=torch.int64), per.cumsum(0)]).to(torch.int32).to(dev)
+    bat = torch.arange(64, device=dev)
+    pd = lens.to(dev)
+    kd, vd = randn(64, hkv, d), randn(64, hkv, d)
+    cases.append(("kv_append_batch_b64", lambda: append_paged_kv_batch(kd, vd, kvc, ind, indptr, bat, pd, ps),
+                  4 * 64 * hkv * d * 2 + 64 * (8 + 8 + 4) + 65 * 4, 0.0))
     return cases
 
 

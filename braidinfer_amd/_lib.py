@@ -11,6 +11,7 @@ from __future__ import annotations
 
 import ctypes
 import threading
+import warnings
 from ctypes import c_float, c_int, c_int64, c_void_p
 from pathlib import Path
 
@@ -28,6 +29,7 @@ _DTYPE_CODE = {
     torch.int64: I64,
 }
 STATUS_INDEX_OOB = 1
+STATUS_APPEND_SKIPPED = 2
 
 _P = c_void_p
 # name -> (restype, argtypes); mirrors include/braidinfer_amd.h
@@ -65,6 +67,11 @@ _SIGNATURES = {
                                    c_int, c_int64, c_int64, c_int, _P, _P, c_int, c_float,
                                    c_int, _P, c_int, _P, c_int64, _P, c_int, c_int64, _P,
                                    c_int64, _P, _P]),
+    "bfa_append_paged_kv": (c_int, [_P, _P, c_int, c_int64, c_int64, c_int64, c_int64,
+                                    c_int64, c_int64, c_int64, _P, c_int, c_int64, c_int64,
+                                    c_int64, c_int64, c_int64, c_int64, _P, c_int, c_int64,
+                                    _P, _P, c_int, c_int64,
+                                    _P, c_int, c_int64, _P, _P]),
 }
 
 _lib = None
@@ -176,6 +183,11 @@ def check_device_status(device: torch.device | int | None = None, reset: bool = 
     bits = int(t.item())
     if bits and reset:
         t.zero_()
+    if bits & STATUS_APPEND_SKIPPED:
+        # append_to_paged_kv_cache_custom prints an error for such a token and
+        # carries on (kernels/kv_cache_utils.py:58-59); so does this check
+        warnings.warn("braidinfer_amd: a KV append skipped a token whose page offset is "
+                      "past the page list", RuntimeWarning, stacklevel=2)
     if bits & STATUS_INDEX_OOB:
         raise IndexError("braidinfer_amd: index out of range in a device kernel "
-                         "(token id, rotary position or chunk delta)")
+                         "(token id, rotary position, chunk delta or cache page)")

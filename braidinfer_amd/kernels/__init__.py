@@ -3,6 +3,8 @@ from .fused_rmsnorm_qkv_minimal_f32 import FusedRMSNormQKVMinimalF32
 from .fused_rmsnorm_qkv_mixed_precision import FusedRMSNormQKVMixedPrecision
 from .fused_rmsnorm_qkv_production import FusedRMSNormQKV
 from .fused_rmsnorm_qkv_with_bias import FusedRMSNormQKVWithBias
+from .kv_cache_utils import (append_paged_kv_batch, append_to_paged_kv_cache_custom,
+                             build_paged_kv_indices)
 from .rmsnorm_f32 import RMSNormF32
 
 __all__ = [
@@ -11,4 +13,7 @@ __all__ = [
     "FusedRMSNormQKVMixedPrecision",
     "FusedRMSNormQKVWithBias",
     "RMSNormF32",
+    "append_paged_kv_batch",
+    "append_to_paged_kv_cache_custom",
+    "build_paged_kv_indices",
 ]

@@ -39,7 +39,9 @@ extern "C" {
 #define BFA_ERR_LAUNCH (-3)      /* HIP launch / runtime error                */
 
 /* bits a kernel may OR into a caller-provided device status word (int32) */
-#define BFA_STATUS_INDEX_OOB 1 /* an index (token id, position, delta) was out of range */
+#define BFA_STATUS_INDEX_OOB 1 /* an index (token id, position, delta, page) was out of range */
+#define BFA_STATUS_APPEND_SKIPPED 2 /* a KV append skipped a token whose page offset is past
+                                       the page list (the reference prints an error) */
 
 #define BFA_ABI_VERSION 1
 
@@ -218,6 +220,41 @@ int bfa_qkv_projection(const void* operand, int64_t tokens, int64_t hidden,
                        const float* cos_sin_cache, int64_t max_position, void* out,
                        int out_dtype, int64_t out_stride, void* part_workspace,
                        int64_t part_workspace_bytes, int32_t* status, void* stream);
+
+/* ------------------------------------------------------- paged KV append --
+ * append_to_paged_kv_cache_custom — braidinfer/kernels/kv_cache_utils.py:9-78
+ * (called per layer by PageManager.append_kv_to_cache / append_kv_to_cache_for_chunk,
+ * braidinfer/engine/page_manager.py:159-218,313-353).
+ * k, v: [num_tokens, num_kv_heads, head_dim] views (token / head strides, unit
+ * element stride), dtype kv_dtype.  layer_cache: one layer of the paged cache,
+ * addressed by element strides (page, K|V, head, slot; unit stride along
+ * head_dim): HND [pages, 2, heads, page, D] is (2*H*P*D, H*P*D, P*D, D), NHD
+ * [pages, 2, page, heads, D] is (2*P*H*D, P*H*D, D, H*D).  cache_page_slots is the
+ * cache's page dimension; page_size divides positions.
+ * Token t goes to page kv_indices[pos // page_size] (Python floor division;
+ * negative offsets >= -num_indices wrap; page ids in [-num_pages, 0) wrap), slot
+ * pos % page_size, K at index 0 and V at index 1, converted to cache_dtype with
+ * round-to-nearest-even (a raw copy when the dtypes match).  An offset
+ * >= num_indices skips the token and sets BFA_STATUS_APPEND_SKIPPED; any other
+ * out-of-range index skips it and sets BFA_STATUS_INDEX_OOB.  Tokens are
+ * assumed to target distinct slots.
+ * Batched form (kv_indptr != NULL; no single reference function -- it does in
+ * one launch what PageManager.append_kv_to_cache does with one call per
+ * sequence): token t belongs to sequence batch_indices[t] in [0, num_seqs),
+ * whose page table is kv_indices[kv_indptr[s] .. kv_indptr[s+1]) (int32 CSR, as
+ * build_paged_kv_indices, kernels/kv_cache_utils.py:81-118, returns it); the
+ * rule above applies within that slice.  kv_indptr == NULL: one sequence owning
+ * all num_indices entries (batch_indices and num_seqs are ignored). */
+int bfa_append_paged_kv(const void* k, const void* v, int kv_dtype, int64_t num_tokens,
+                        int64_t num_kv_heads, int64_t head_dim, int64_t k_stride_token,
+                        int64_t k_stride_head, int64_t v_stride_token, int64_t v_stride_head,
+                        void* layer_cache, int cache_dtype, int64_t num_pages,
+                        int64_t cache_page_slots, int64_t stride_page, int64_t stride_kv,
+                        int64_t stride_head, int64_t stride_slot, const void* kv_indices,
+                        int kv_indices_dtype, int64_t num_indices, const int32_t* kv_indptr,
+                        const void* batch_indices, int batch_indices_dtype, int64_t num_seqs,
+                        const void* positions, int positions_dtype, int64_t page_size,
+                        int32_t* status, void* stream);
 
 #ifdef __cplusplus
 }

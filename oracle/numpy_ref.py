@@ -141,3 +141,32 @@ def head_norm(x, w, eps, out_dtype):
     x = np.asarray(x, np.float64)
     r = 1.0 / np.sqrt(np.mean(x * x, axis=-1, keepdims=True) + eps)
     return round_to((x * r) * np.asarray(w, np.float64), out_dtype)
+
+
+def append_paged_kv(k, v, cache, kv_indices, positions, page_size, layout="HND"):
+    """Paged KV append (kernels/kv_cache_utils.py:9-78) with the index arithmetic
+    written out: offset = floor(pos / page_size), slot = pos - offset * page_size,
+    Python-style wrap of negative offsets and page ids.  cache is copied; returns
+    (cache, skipped token indices).  Values are moved, not converted."""
+    out = np.array(cache, copy=True)
+    n_idx, n_pages = len(kv_indices), out.shape[0]
+    skipped = []
+    for t in range(k.shape[0]):
+        pos = int(positions[t])
+        off = int(np.floor(pos / page_size))
+        slot = pos - off * page_size
+        if off >= n_idx:
+            skipped.append(t)
+            continue
+        if off < -n_idx:
+            raise IndexError("page offset out of range")
+        page = int(kv_indices[off + n_idx if off < 0 else off])
+        if page < -n_pages or page >= n_pages:
+            raise IndexError("page id out of range")
+        page = page + n_pages if page < 0 else page
+        for kv, src in ((0, k), (1, v)):
+            if layout == "HND":
+                out[page, kv, :, slot, :] = src[t]
+            else:
+                out[page, kv, slot, :, :] = src[t]
+    return out, skipped

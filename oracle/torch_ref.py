@@ -131,6 +131,56 @@ def rerotate_paged_k(kv_cache_layer: torch.Tensor, page_indices: torch.Tensor,
     return out
 
 
+# ---------------------------------------------------------- paged KV append
+def append_to_paged_kv_cache(k: torch.Tensor, v: torch.Tensor, layer_cache: torch.Tensor,
+                             kv_indices: torch.Tensor, positions: torch.Tensor, page_size: int,
+                             kv_layout: str = "HND") -> tuple[torch.Tensor, list[int]]:
+    """append_to_paged_kv_cache_custom, braidinfer/kernels/kv_cache_utils.py:9-78, applied
+    to a clone of layer_cache: per token, page_offset = pos // page_size (Python
+    floor), pos_in_page = pos % page_size; a token with page_offset >=
+    len(kv_indices) is skipped; otherwise K and V are assigned into page
+    kv_indices[page_offset] (torch indexing, so negative offsets and page ids
+    wrap and out-of-range ones raise IndexError).  Returns (cache, skipped tokens)."""
+    if kv_layout not in ("HND", "NHD"):
+        raise ValueError(f"Unknown kv_layout: {kv_layout}")
+    cache = layer_cache.clone()
+    skipped = []
+    for t in range(k.shape[0]):
+        seq_pos = int(positions[t])
+        page_offset = seq_pos // page_size
+        pos_in_page = seq_pos % page_size
+        if page_offset < len(kv_indices):
+            page_idx = int(kv_indices[page_offset])
+            if kv_layout == "HND":
+                cache[page_idx, 0, :, pos_in_page, :] = k[t]
+                cache[page_idx, 1, :, pos_in_page, :] = v[t]
+            else:
+                cache[page_idx, 0, pos_in_page, :, :] = k[t]
+                cache[page_idx, 1, pos_in_page, :, :] = v[t]
+        else:
+            skipped.append(t)
+    return cache, skipped
+
+
+def append_paged_kv_batch(k, v, layer_cache, kv_indices, kv_indptr, batch_indices, positions,
+                          page_size, kv_layout="HND"):
+    """The batched append as the reference's page manager composes it
+    (engine/page_manager.py:180-210): append_to_paged_kv_cache_custom once per
+    sequence s, with the tokens of s (in order) and its slice
+    kv_indices[kv_indptr[s]:kv_indptr[s+1]] of the CSR page table."""
+    cache, skipped = layer_cache.clone(), []
+    for s in range(kv_indptr.numel() - 1):
+        toks = [t for t in range(k.shape[0]) if int(batch_indices[t]) == s]
+        if not toks:
+            continue
+        sel = torch.tensor(toks)
+        table = kv_indices[int(kv_indptr[s]):int(kv_indptr[s + 1])]
+        cache, sk = append_to_paged_kv_cache(k[sel], v[sel], cache, table, positions[sel],
+                                             page_size, kv_layout)
+        skipped += [toks[i] for i in sk]
+    return cache, sorted(skipped)
+
+
 # ------------------------------------------------------- fused RMSNorm + QKV
 def _rms(x32: torch.Tensor, eps: float) -> torch.Tensor:
     # tl.sqrt(acc_var / hidden_dim + eps) with acc_var = sum(x*x) in fp32

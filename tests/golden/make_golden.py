@@ -120,6 +120,20 @@ def build() -> dict:
     f["rerot.kv"], f["rerot.pidx"], f["rerot.indptr"] = kv, pidx, indptr
     f["rerot.delta"], f["rerot.last"], f["rerot.table"], f["rerot.out"] = delta, last, rtab, out
 
+    # paged KV append (kernels/kv_cache_utils.py:9-78): HND cache, shuffled page
+    # table, one negative position (lands on the last page of the table through
+    # Python floor division and negative indexing) and one past the table (skipped)
+    pages, hkv, ps, d = 7, 2, 4, 16
+    cache0 = _bf16(rng, (pages, 2, hkv, ps, d))
+    ptab = np.array([5, 2, 6, 0], dtype=np.int32)
+    kpos = np.array([0, 1, 2, 3, 4, 9, 14, 15, -3, 16], dtype=np.int64)
+    ka = _bf16(rng, (len(kpos), hkv, d))
+    va = _bf16(rng, (len(kpos), hkv, d))
+    app, skipped = N.append_paged_kv(ka, va, cache0, ptab, kpos, ps)
+    assert skipped == [9]
+    f["kvapp.cache"], f["kvapp.ptab"], f["kvapp.pos"] = cache0, ptab, kpos
+    f["kvapp.k"], f["kvapp.v"], f["kvapp.out"] = ka, va, app
+
     # bf16-valued arrays and the float32 RoPE tables fit float32 exactly;
     # fp32 results computed in float64 keep float64
     keep64 = {"rmsf32.y", "qkv.f32", "qkv.with_bias"}

@@ -88,6 +88,11 @@ def test_torch_oracle_reproduces_golden(gold):
                              torch.from_numpy(g["rerot.indptr"]), torch.from_numpy(g["rerot.delta"]),
                              torch.from_numpy(g["rerot.last"]), f32(g["rerot.table"]))
     within_ulp(out, g["rerot.out"], "rerotate")
+    cache, skipped = R.append_to_paged_kv_cache(bf(g["kvapp.k"]), bf(g["kvapp.v"]), bf(g["kvapp.cache"]),
+                                                torch.from_numpy(g["kvapp.ptab"]),
+                                                torch.from_numpy(g["kvapp.pos"]), 4)
+    assert skipped == [9]
+    assert np.array_equal(cache.float().numpy(), g["kvapp.out"]), "KV append must be bit-exact"
 
 
 # ------------------------------------------------------------------------ GPU
@@ -145,3 +150,13 @@ def test_hip_path_reproduces_golden(gold):
                            on(torch.from_numpy(g["rerot.indptr"])), on(torch.from_numpy(g["rerot.delta"])),
                            on(torch.from_numpy(g["rerot.last"])), on(f32(g["rerot.table"])))
     close(out, "rerot.out")
+    from braidinfer_amd.kernels import append_to_paged_kv_cache_custom
+    import braidinfer_amd
+    braidinfer_amd.check_device_status()
+    cache = on(bf(g["kvapp.cache"]))
+    with pytest.warns(RuntimeWarning, match="skipped"):
+        append_to_paged_kv_cache_custom(on(bf(g["kvapp.k"])), on(bf(g["kvapp.v"])), cache,
+                                        on(torch.from_numpy(g["kvapp.ptab"])),
+                                        on(torch.from_numpy(g["kvapp.pos"])), 4)
+        braidinfer_amd.check_device_status()
+    assert np.array_equal(cache.float().cpu().numpy(), g["kvapp.out"]), "KV append must be bit-exact"

@@ -264,6 +264,77 @@ def test_rerotate_paged_k_pinned():
     assert torch.equal(outn[e], R.rms_forward(out[e], w, 1e-6))
 
 
+# ----------------------------------------------------------- paged KV append
+def pin_kv_append(fn):
+    """fn(k, v, cache, kv_indices, positions, page_size, layout) -> (cache, skipped)."""
+    g = gen(31)
+    pages, hkv, ps, d = 12, 3, 4, 8
+    # round trip: a sequence of L tokens at positions 0..L-1 through a shuffled
+    # table of distinct pages is read back, token by token, from
+    # (kv_indices[p // ps], p % ps); every other slot keeps its old value
+    L = 29
+    table = torch.randperm(pages, generator=g)[: (L + ps - 1) // ps].to(torch.int32)
+    k, v = randn(g, L, hkv, d), randn(g, L, hkv, d)
+    cache0 = randn(g, pages, 2, hkv, ps, d)
+    pos = torch.arange(L)
+    out, skipped = fn(k, v, cache0, table, pos, ps, "HND")
+    assert skipped == []
+    touched = torch.zeros(pages, ps, dtype=torch.bool)
+    for t in range(L):
+        page, slot = int(table[t // ps]), t % ps
+        assert torch.equal(out[page, 0, :, slot], k[t]) and torch.equal(out[page, 1, :, slot], v[t])
+        touched[page, slot] = True
+    keep = ~touched
+    assert torch.equal(out.permute(0, 3, 1, 2, 4)[keep], cache0.permute(0, 3, 1, 2, 4)[keep])
+    # NHD holds the same values as HND with the head and slot axes swapped
+    out_nhd, _ = fn(k, v, cache0.transpose(2, 3).contiguous(), table, pos, ps, "NHD")
+    assert torch.equal(out_nhd, out.transpose(2, 3))
+    # negative positions: Python floor division (-1 -> last entry of the table, slot ps-1),
+    # and a page offset past the table skips the token
+    pos2 = torch.tensor([-1, -ps - 1, len(table) * ps])
+    k2, v2 = randn(g, 3, hkv, d), randn(g, 3, hkv, d)
+    out2, skipped2 = fn(k2, v2, cache0, table, pos2, ps, "HND")
+    assert skipped2 == [2]
+    assert torch.equal(out2[int(table[-1]), 0, :, ps - 1], k2[0])
+    assert torch.equal(out2[int(table[-2]), 1, :, ps - 1], v2[1])
+    # independent numpy restatement, both layouts, int64 table
+    for layout, c0 in (("HND", cache0), ("NHD", cache0.transpose(2, 3).contiguous())):
+        allpos = torch.cat([pos, pos2])
+        kk, vv = torch.cat([k, k2]), torch.cat([v, v2])
+        got, sk = fn(kk, vv, c0, table.long(), allpos, ps, layout)
+        exp, sk_np = N.append_paged_kv(_np(kk), _np(vv), _np(c0), table.numpy(), allpos.numpy(), ps, layout)
+        assert sk == sk_np and np.array_equal(_np(got), exp), layout
+
+
+def test_kv_append_pinned():
+    pin_kv_append(R.append_to_paged_kv_cache)
+    # the batched composition equals one per-sequence call for each sequence
+    g = gen(32)
+    pages, hkv, ps, d = 40, 2, 4, 8
+    lens = [5, 0, 9, 3]
+    tables = [torch.randperm(pages, generator=g)[:3].to(torch.int32) for _ in lens]
+    indptr = torch.tensor([0, 3, 6, 9, 12], dtype=torch.int32)
+    flat = torch.cat(tables)
+    batch = torch.tensor([0, 2, 3, 2, 0, 3, 2], dtype=torch.int64)
+    pos = torch.tensor([5, 9, 3, 10, 6, 4, 40])
+    k, v = randn(g, 7, hkv, d), randn(g, 7, hkv, d)
+    cache0 = randn(g, pages, 2, hkv, ps, d)
+    got, skipped = R.append_paged_kv_batch(k, v, cache0, flat, indptr, batch, pos, ps)
+    exp = cache0.clone()
+    for s_ in range(4):
+        toks = [t for t in range(7) if int(batch[t]) == s_]
+        for t in toks:
+            p = int(pos[t])
+            if p // ps < 3:
+                exp[int(tables[s_][p // ps]), 0, :, p % ps] = k[t]
+                exp[int(tables[s_][p // ps]), 1, :, p % ps] = v[t]
+    assert torch.equal(got, exp) and skipped == [6]
+    with pytest.raises(ValueError):
+        R.append_to_paged_kv_cache(torch.zeros(1, 1, 8), torch.zeros(1, 1, 8),
+                                   torch.zeros(1, 2, 1, 4, 8), torch.zeros(1, dtype=torch.int32),
+                                   torch.zeros(1, dtype=torch.int64), 4, "XYZ")
+
+
 # ------------------------------------------------------- fused RMSNorm+QKV
 def _qkv_inputs(seed, t=24, h=256, hq=8, hkv=2, d=32):
     g = gen(seed)
@@ -399,6 +470,40 @@ def test_planted_mistakes_are_caught():
 
     with pytest.raises(AssertionError):
         pin_qkv(mixed_rounds_late, R.qkv_production, R.qkv_minimal_f32)
+
+
+def test_planted_kv_append_mistakes_are_caught():
+    def truncating(k, v, cache, idx, pos, ps, layout):  # C-style division for negatives
+        cache, skipped = cache.clone(), []
+        for t in range(k.shape[0]):
+            p = int(pos[t])
+            off = int(p / ps)  # rounds toward zero
+            slot = p - off * ps  # then negative: wraps as a torch index
+            if off < len(idx):
+                page = int(idx[off])
+                if layout == "HND":
+                    cache[page, 0, :, slot], cache[page, 1, :, slot] = k[t], v[t]
+                else:
+                    cache[page, 0, slot], cache[page, 1, slot] = k[t], v[t]
+            else:
+                skipped.append(t)
+        return cache, skipped
+
+    with pytest.raises(AssertionError):
+        pin_kv_append(truncating)
+
+    def kv_swapped(k, v, cache, idx, pos, ps, layout):
+        return R.append_to_paged_kv_cache(v, k, cache, idx, pos, ps, layout)
+
+    with pytest.raises(AssertionError):
+        pin_kv_append(kv_swapped)
+
+    def slot_as_page(k, v, cache, idx, pos, ps, layout):  # table indexed by slot, not by page offset
+        swapped = (pos % ps) * ps + pos // ps
+        return R.append_to_paged_kv_cache(k, v, cache, idx, swapped, ps, layout)
+
+    with pytest.raises(AssertionError):
+        pin_kv_append(slot_as_page)
 
 
 def test_rope_rounding_allowance_is_a_property_of_the_arithmetic():
