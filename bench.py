@@ -243,15 +243,24 @@ def config_cases(dev) -> list:
     # paged KV append at Llama-3-8B kv geometry (8 heads x 128, page 16, HND):
     # an 8192-token prefill into 512 of 1024 shuffled pages, and a 64-sequence
     # decode batch (one new token each) in one batched launch
+    cases += kv_append_cases(dev)
+    return cases
+
+
+def kv_append_cases(dev) -> list:
+    """Paged KV append cases (seed 6), own scope so the lambdas bind their own tensors."""
     from braidinfer_amd.kernels import append_paged_kv_batch, append_to_paged_kv_cache_custom
-    g, randn = gen(6)
+    g = torch.Generator().manual_seed(6)
+    bf = torch.bfloat16
+
+    def randn(*shape):
+        return torch.randn(*shape, generator=g).to(bf).to(dev)
+
     hkv, d, ps, pages = 8, 128, 16, 1024
-    kvc = randn(pages, 2, hkv, ps, d)
+    cache = randn(pages, 2, hkv, ps, d)
     table = torch.randperm(pages, generator=g)[:512].to(torch.int32).to(dev)
     kp, vp = randn(8192, hkv, d), randn(8192, hkv, d)
     pp = torch.arange(8192, dtype=torch.int32, device=dev)
-    cases.append(("kv_append_t8192", lambda: append_to_paged_kv_cache_custom(kp, vp, kvc, table, pp, ps),
-                  4 * 8192 * hkv * d * 2 + 8192 * 4 + 512 * 4, 0.0))
     lens = torch.randint(0, 4000, (64,), generator=g)
     perm = torch.randperm(pages, generator=g)
     # sequence s: a table of lens[s] // 16 + 1 entries whose last (the one written) is a
@@ -262,9 +271,10 @@ def config_cases(dev) -> list:
     bat = torch.arange(64, device=dev)
     pd = lens.to(dev)
     kd, vd = randn(64, hkv, d), randn(64, hkv, d)
-    cases.append(("kv_append_batch_b64", lambda: append_paged_kv_batch(kd, vd, kvc, ind, indptr, bat, pd, ps),
-                  4 * 64 * hkv * d * 2 + 64 * (8 + 8 + 4) + 65 * 4, 0.0))
-    return cases
+    return [("kv_append_t8192", lambda: append_to_paged_kv_cache_custom(kp, vp, cache, table, pp, ps),
+             4 * 8192 * hkv * d * 2 + 8192 * 4 + 512 * 4, 0.0),
+            ("kv_append_batch_b64", lambda: append_paged_kv_batch(kd, vd, cache, ind, indptr, bat, pd, ps),
+             4 * 64 * hkv * d * 2 + 64 * (8 + 8 + 4) + 65 * 4, 0.0)]
 
 
 def config_table(dev, iters: int) -> dict:

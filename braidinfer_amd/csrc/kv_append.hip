@@ -55,7 +55,7 @@ struct AppendArgs {
 };
 
 // Destination (page, slot) of token t, or false when the token is not written
-// (the reason is flagged by thread 0).
+// (the reason is flagged by the first lane of each wave that resolves t).
 __device__ __forceinline__ bool append_target(const AppendArgs& a, int64_t t, int64_t& page,
                                               int64_t& slot) {
   const int64_t pos = a.pos_is_i64 ? static_cast<const int64_t*>(a.positions)[t]
@@ -71,7 +71,7 @@ __device__ __forceinline__ bool append_target(const AppendArgs& a, int64_t t, in
     const int64_t sq = a.batch_is_i64 ? static_cast<const int64_t*>(a.batch)[t]
                                       : static_cast<const int32_t*>(a.batch)[t];
     if (sq < 0 || sq >= a.num_seqs) {
-      if (threadIdx.x == 0) flag_status(a.status, BFA_STATUS_INDEX_OOB);
+      if ((threadIdx.x & 63) == 0) flag_status(a.status, BFA_STATUS_INDEX_OOB);
       return false;
     }
     first = a.indptr[sq];
@@ -96,7 +96,7 @@ __device__ __forceinline__ bool append_target(const AppendArgs& a, int64_t t, in
       slot = s;
     }
   }
-  if (bad && threadIdx.x == 0) flag_status(a.status, bad);
+  if (bad && (threadIdx.x & 63) == 0) flag_status(a.status, bad);
   return bad == 0;
 }
 
@@ -120,10 +120,10 @@ __global__ __launch_bounds__(256) void kv_append_vec_kernel(AppendArgs a) {
   using TS = typename Elem<DTS>::T;
   using TD = typename Elem<DTD>::T;
   const int64_t t = blockIdx.x;
+  const uint32_t items = 2u * a.chunks_per_kv.d;
   int64_t page = 0, slot = 0;
   if (!append_target(a, t, page, slot)) return;  // uniform over the workgroup
   TD* base = static_cast<TD*>(a.cache) + page * a.c_sp + slot * a.c_ss;
-  const uint32_t items = 2u * a.chunks_per_kv.d;
   for (uint32_t i = threadIdx.x; i < items; i += 256) {
     const uint32_t kv = a.chunks_per_kv.div(i);
     const uint32_t r = i - kv * a.chunks_per_kv.d;
@@ -133,6 +133,41 @@ __global__ __launch_bounds__(256) void kv_append_vec_kernel(AppendArgs a) {
                             : static_cast<const TS*>(a.v) + t * a.v_st + h * a.v_sh;
     copy8<DTS, DTD>(src + c, base + kv * a.c_skv + h * a.c_sh + c);
   }
+}
+
+// Equal 16-bit dtypes with at most 4 x 64 chunks per token: four tokens per
+// workgroup, 64 lanes per token, each lane's source chunks requested before the
+// destination is resolved.
+template <int DT>
+__global__ __launch_bounds__(256) void kv_append_group_kernel(AppendArgs a, int64_t tokens) {
+  using T = typename Elem<DT>::T;
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (t >= tokens) return;
+  const uint32_t lane = threadIdx.x & 63;
+  const uint32_t items = 2u * a.chunks_per_kv.d;
+  uint4 buf[4];
+  int64_t dst_off[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const uint32_t i = lane + c * 64u;
+    dst_off[c] = -1;
+    if (i < items) {
+      const uint32_t kv = a.chunks_per_kv.div(i);
+      const uint32_t r = i - kv * a.chunks_per_kv.d;
+      const uint32_t h = a.chunks_per_head.div(r);
+      const uint32_t e = (r - h * a.chunks_per_head.d) * 8u;
+      const T* src = kv == 0 ? static_cast<const T*>(a.k) + t * a.k_st + h * a.k_sh
+                             : static_cast<const T*>(a.v) + t * a.v_st + h * a.v_sh;
+      buf[c] = load16_nt(src + e);
+      dst_off[c] = kv * a.c_skv + h * a.c_sh + e;
+    }
+  }
+  int64_t page = 0, slot = 0;
+  if (!append_target(a, t, page, slot)) return;  // uniform over the token's 64 lanes
+  T* base = static_cast<T*>(a.cache) + page * a.c_sp + slot * a.c_ss;
+#pragma unroll
+  for (int c = 0; c < 4; ++c)
+    if (dst_off[c] >= 0) *reinterpret_cast<uint4*>(base + dst_off[c]) = buf[c];
 }
 
 // Any strides and head_dim: one element per lane.
@@ -165,6 +200,13 @@ template <int DTS, int DTD>
 static void launch_append(AppendArgs a, int64_t tokens, bool vec, hipStream_t s) {
   a.chunks_per_head = FastDiv(vec ? a.head_dim / 8 : a.head_dim);
   a.chunks_per_kv = FastDiv(a.heads * a.chunks_per_head.d);
+  if constexpr (DTS == DTD && DTS != BFA_DTYPE_F32) {
+    if (vec && 2 * a.chunks_per_kv.d <= 256) {
+      hipLaunchKernelGGL((kv_append_group_kernel<DTS>), dim3(static_cast<unsigned>(cdiv(tokens, 4))),
+                         dim3(256), 0, s, a, tokens);
+      return;
+    }
+  }
   if (vec) {
     hipLaunchKernelGGL((kv_append_vec_kernel<DTS, DTD>), dim3(static_cast<unsigned>(tokens)), dim3(256), 0, s, a);
   } else {
