@@ -14,22 +14,23 @@
 // QKVParallelLinear (layers/linear.py:78-114).
 //
 // Kernels
-//  * qkv_gemm_kernel   prefill.  BMxBN = 256x256 tile per 256-thread workgroup,
-//    four waves of 128x128, v_mfma_f32_32x32x16_{bf16,f16}.  Operand tiles
-//    (64-deep K slices) go HBM -> registers -> LDS (double-buffered, 16-byte
-//    granules XOR-swizzled by row so the MFMA fragment reads spread over the
-//    banks).  The epilogue runs on the accumulators in registers: a wave's
-//    128 columns hold whole heads (head_dim 64 or 128), so the q/k RMSNorm is
-//    a 32-lane butterfly and both RoPE halves (columns j and j+D/2) sit in the
-//    same lane.
-//  * qkv_splitk_kernel decode (T <= 64).  The weight stream dominates, so the
-//    grid is (column tiles) x (K splits) to put every CU on the weight; each
-//    lane loads 32 contiguous bytes per weight row straight into MFMA
-//    registers (v_mfma_f32_16x16x32) without LDS; fp32 partial tiles go to the
-//    workspace.
-//  * qkv_epilogue_kernel sums the split-K partials (or reads the raw fp32
-//    projection for head_dim the in-register epilogue does not cover) and
-//    applies bias / q-k norm / RoPE / rounding per (token, head) row.
+//  * qkv_gemm_kernel   prefill.  BMxBN tile per workgroup of 4 or 8 waves, each
+//    wave WMx128 with v_mfma_f32_32x32x16_{bf16,f16}; 256x256 with 8 waves (two
+//    per SIMD) for large token counts.  Operand and weight K-slices move HBM ->
+//    LDS by LDS DMA (global_load_lds_dwordx4) into XOR-swizzled buffers, so the
+//    MFMA fragment reads spread over the banks; unaligned or odd K goes through a
+//    register-staged path with masking.  The epilogue stages each wave's
+//    accumulators through a wave-private LDS slice and runs bias / rounding / q-k
+//    RMSNorm / RoPE / store per (row, head) with 16 lanes per row.
+//  * qkv_decode_kernel decode (T <= 64).  The weight stream dominates, so the grid
+//    is (128-column tiles) x (K splits) to put every CU on the weight; weight rows
+//    are loaded 8 lanes per row into registers and transposed through a small
+//    wave-private LDS area into 16x16x32 MFMA fragments; fp32 partial tiles go to
+//    the workspace.  qkv_splitk_kernel (fragments loaded straight from memory,
+//    K masked) covers hidden sizes that are not a multiple of 64.
+//  * qkv_decode_epilogue_kernel / qkv_epilogue_kernel sum the split-K partials (or
+//    read the raw fp32 projection for head_dim the GEMM epilogue does not cover)
+//    and apply bias / q-k norm / RoPE / rounding per (token, head) row.
 #include <cstdlib>
 
 #include "bfa_device.h"
