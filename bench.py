@@ -180,7 +180,9 @@ def config_cases(dev) -> list:
                   16 pages, delta U[-4096, 4096], theta 1e6, rotated copy out
       swiglu      SiLU*mul [2048, 2 x 3072]
       kv_append   paged KV append, 8 kv heads x 128, page 16: 8192-token prefill,
-                  and a 64-sequence decode batch in one launch"""
+                  and a 64-sequence decode batch in one launch
+      cascade     paged cascade attention over 4096 cached Qwen3 tokens (16 moved
+                  chunks, k_norm), 1 and 256 query tokens"""
     from braidinfer_amd.layers import llama_attention_input, qwen3_attention_input, rerotate_paged_k
     bf = torch.bfloat16
     cases = []
@@ -244,6 +246,7 @@ def config_cases(dev) -> list:
     # an 8192-token prefill into 512 of 1024 shuffled pages, and a 64-sequence
     # decode batch (one new token each) in one batched launch
     cases += kv_append_cases(dev)
+    cases += cascade_cases(dev)
     return cases
 
 
@@ -275,6 +278,42 @@ def kv_append_cases(dev) -> list:
              4 * 8192 * hkv * d * 2 + 8192 * 4 + 512 * 4, 0.0),
             ("kv_append_batch_b64", lambda: append_paged_kv_batch(kd, vd, cache, ind, indptr, bat, pd, ps),
              4 * 64 * hkv * d * 2 + 64 * (8 + 8 + 4) + 65 * 4, 0.0)]
+
+
+def cascade_cases(dev) -> list:
+    """Cascade attention at Qwen3-0.6B shape (seed 7): 4096 cached tokens in 16 chunks of
+    256, shuffled 16-token HND pages, each chunk moved by a delta in [-4096, 4096]
+    (theta 1e6, rotary table 40960), k_norm with log-uniform weights; 16 query heads
+    over 8 kv heads of 128.  A one-token decode step and a 256-token query chunk."""
+    import math as _m
+    from types import SimpleNamespace
+    from braidinfer_amd.layers import CascadeAttention, RMSNorm, RotaryEmbedding
+    g = torch.Generator().manual_seed(7)
+    bf = torch.bfloat16
+    hq, hkv, d, ps, pages = 16, 8, 128, 16, 512
+    kv = torch.randn(pages, 2, hkv, ps, d, generator=g).to(bf).to(dev)
+    perm = torch.randperm(pages, generator=g).tolist()
+    deltas = torch.randint(-4096, 4097, (16,), generator=g).tolist()
+    chunks = [SimpleNamespace(page_table=perm[16 * c:16 * c + 16], kv_length=256,
+                              cached_position_start=8192 + 256 * c,
+                              global_position_start=8192 + 256 * c + deltas[c],
+                              chunk_type=SimpleNamespace(value="system_prompt" if c == 0 else "context"))
+              for c in range(16)]
+    rope = RotaryEmbedding(d, d, 40960, 1e6).to(dev)
+    att = CascadeAttention(hq, d, d ** -0.5, hkv, ps, rotary_emb=rope)
+    levels = att.create_cascade_levels(chunks)
+    k_norm = RMSNorm(d, eps=1e-6).to(dev)
+    with torch.no_grad():
+        k_norm.weight.data = torch.exp(torch.empty(d).uniform_(_m.log(0.05), _m.log(100.0), generator=g)).to(bf).to(dev)
+    kv_bytes = 4096 * hkv * d * 2 * 2
+    out = []
+    for t in (1, 256):
+        q = torch.randn(t, hq, d, generator=g).to(bf).to(dev)
+        qpos = torch.arange(4096 - t + 1, 4097, device=dev)
+        out.append((f"cascade_attention_qwen3_4096kv_t{t}",
+                    (lambda q=q, qpos=qpos: att.forward(q, qpos, kv, levels, 0, k_norm=k_norm)),
+                    kv_bytes + 2 * t * hq * d * 2, 4.0 * t * hq * 4096 * d))
+    return out
 
 
 def config_table(dev, iters: int) -> dict:

@@ -72,6 +72,18 @@ _SIGNATURES = {
                                     c_int64, c_int64, c_int64, c_int64, _P, c_int, c_int64,
                                     _P, _P, c_int, c_int64,
                                     _P, c_int, c_int64, _P, _P]),
+    "bfa_online_softmax_update": (c_int, [_P, _P, _P, c_int, c_int, _P, _P, _P, _P, c_int, _P,
+                                          c_int, c_int64, c_int64, c_int64, c_int64, c_int64,
+                                          c_int64, c_int64, c_int64, c_int64, c_int64, c_int64,
+                                          c_int64, c_int64, c_int64, c_int64, c_int64, c_float,
+                                          c_int, _P]),
+    "bfa_cascade_attention_workspace_size": (c_int64, [c_int64, c_int64, c_int64, c_int64,
+                                                       c_int64, c_int64]),
+    "bfa_cascade_attention": (c_int, [_P, c_int, c_int64, c_int64, c_int64, c_int64, _P, c_int,
+                                      _P, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64,
+                                      c_int64, c_int64, c_int64, _P, _P, _P, _P, _P, c_int64,
+                                      _P, c_int, c_float, c_float, c_int, _P, c_int64, _P,
+                                      c_int64, _P, _P]),
 }
 
 _lib = None

@@ -1,0 +1,603 @@
+// Paged cascade attention on gfx950: the per-page loop of CascadeAttention.forward
+// (braidinfer/layers/cascade_attention.py:50-231) in one launch, and the online
+// softmax state update it calls per page (kernels/online_softmax.py:14-297).
+//
+// Reference semantics (per query token t, query head h, kv head h / (Hq / Hkv)):
+//   for every level, every chunk with pages and kv_length > 0, every page of it
+//   (tokens = last_page_len on the chunk's last page, else page_size; pages with
+//   tokens <= 0 skipped):
+//     k = cache[page, 0, kv, :tokens]; v = cache[page, 1, kv, :tokens]
+//     if the chunk moved (delta = global_position_start - cached_position_start
+//     != 0) and a rotary table is given: k = RoPE(k, cos_sin_cache[delta]) (torch
+//     indexing: a negative delta wraps), rounded to the cache dtype
+//     if k_norm is given: k = RMSNorm(k) over head_dim (bf16 rounding points)
+//     key positions = (kv_length of the earlier valid chunks) + page offset + slot
+//     online softmax update in fp32 with score = (q . k) * scale, keys with
+//     position > the query's position masked when causal
+//   out = acc / max(l, 1e-12), in the query dtype.
+//
+// Kernel design.  Rows are (query token, query head of a kv group) pairs of one kv
+// head; a workgroup of 4 waves owns 64 rows and one kv head and walks a range of
+// the padded key space (entry e, slot s) -> e * page_size + s in steps of 32 key
+// slots.  Per step: 256 lanes stage the 32 keys of K into LDS (rotated and
+// normalised on the way, with the rounding of the re-rotation kernel) and V
+// transposed into LDS; each wave computes S = Q K^T for its 16 rows with
+// v_mfma_f32_16x16x32_bf16, masks, updates its running max / sum in fp32, writes
+// P (bf16) through a wave-private LDS tile into the A-operand layout and adds
+// P V with 8 more MFMAs.  For few rows (decode) the key range is split across
+// workgroups and a merge kernel combines the partial (m, l, acc) rows.
+#include <cmath>
+
+#include "bfa_device.h"
+#include "bfa_host.h"
+
+namespace bfa {
+
+typedef __attribute__((ext_vector_type(8))) __bf16 cas_bf16x8_t;
+typedef __attribute__((ext_vector_type(8))) _Float16 cas_f16x8_t;
+typedef __attribute__((ext_vector_type(4))) float cas_f32x4_t;
+
+template <bool BF16>
+__device__ __forceinline__ cas_f32x4_t mfma16x32(const uint4& a, const uint4& b, cas_f32x4_t c) {
+  if constexpr (BF16) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(cas_bf16x8_t, a),
+                                                   __builtin_bit_cast(cas_bf16x8_t, b), c, 0, 0, 0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(cas_f16x8_t, a),
+                                                  __builtin_bit_cast(cas_f16x8_t, b), c, 0, 0, 0);
+  }
+}
+
+// ================================================== online softmax update
+// One wave per (head, batch) query: lanes split head_dim (up to 4 elements each),
+// keys are taken in order, one at a time, as the reference kernel does.
+struct OsmArgs {
+  const void* q;
+  const void* k;
+  const void* v;
+  int q_dt, kv_dt;
+  float* m;
+  float* l;
+  float* acc;
+  const void* qpos;
+  const void* kpos;
+  int qpos_i64, kpos_i64;
+  int64_t heads, batch, tokens, head_dim;
+  int64_t q_sh, q_sb, k_sh, k_st, v_sh, v_st;  // element strides (unit stride along head_dim)
+  int64_t m_sh, m_sb, l_sh, l_sb, a_sh, a_sb;
+  float scale;
+  int causal;
+};
+
+__global__ __launch_bounds__(256) void online_softmax_kernel(OsmArgs a) {
+  const int64_t item = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (item >= a.heads * a.batch) return;
+  const int64_t h = item / a.batch, b = item - h * a.batch;
+  const int lane = threadIdx.x & 63;
+  const int64_t qp = a.qpos_i64 ? static_cast<const int64_t*>(a.qpos)[b]
+                                : static_cast<const int32_t*>(a.qpos)[b];
+  float qv[4], av[4];
+  float* accp = a.acc + h * a.a_sh + b * a.a_sb;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int64_t d = lane + 64 * i;
+    const bool in = d < a.head_dim;
+    qv[i] = in ? load_any(a.q, a.q_dt, h * a.q_sh + b * a.q_sb + d) : 0.f;
+    av[i] = in ? accp[d] : 0.f;
+  }
+  float m = a.m[h * a.m_sh + b * a.m_sb];
+  float l = a.l[h * a.l_sh + b * a.l_sb];
+  for (int64_t t = 0; t < a.tokens; ++t) {
+    const int64_t kp = a.kpos_i64 ? static_cast<const int64_t*>(a.kpos)[t]
+                                  : static_cast<const int32_t*>(a.kpos)[t];
+    if (a.causal && kp > qp) continue;  // uniform over the wave
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int64_t d = lane + 64 * i;
+      if (d < a.head_dim) s += qv[i] * load_any(a.k, a.kv_dt, h * a.k_sh + t * a.k_st + d);
+    }
+    s = group_sum<kWave>(s) * a.scale;
+    const float m_new = fmaxf(m, s);
+    const float alpha = expf(m - m_new);
+    const float beta = expf(s - m_new);
+    l = l * alpha + beta;
+    m = m_new;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int64_t d = lane + 64 * i;
+      if (d < a.head_dim) av[i] = alpha * av[i] + beta * load_any(a.v, a.kv_dt, h * a.v_sh + t * a.v_st + d);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int64_t d = lane + 64 * i;
+    if (d < a.head_dim) accp[d] = av[i];
+  }
+  if (lane == 0) {
+    a.m[h * a.m_sh + b * a.m_sb] = m;
+    a.l[h * a.l_sh + b * a.l_sb] = l;
+  }
+}
+
+// ===================================================== paged cascade attention
+struct CasArgs {
+  const uint16_t* q;        // [T, Hq, D] with strides q_st, q_sh
+  int64_t q_st, q_sh;
+  const void* qpos;
+  int qpos_i64;
+  const uint16_t* cache;    // one layer [pages, 2, Hkv, page_size, D]
+  int64_t c_sp, c_skv, c_sh, c_ss;
+  int64_t num_pages, page_size;
+  const int32_t* pages;     // [E] page of each entry
+  const int64_t* kstart;    // [E] key position of the entry's first slot
+  const int64_t* delta;     // [E] RoPE shift of the entry's chunk
+  const int32_t* info;      // [E] bits 0-15: tokens attended on the page, bit 16: rotate
+  int64_t num_entries;
+  const float* cs;          // [max_pos, D] or nullptr
+  int64_t max_pos;
+  const void* knorm_w;      // [D] or nullptr
+  int knorm_dt;
+  float knorm_eps;
+  int64_t tokens, hq, hkv, group;  // group = Hq / Hkv
+  float scale;
+  int causal;
+  int64_t steps, steps_per_split;
+  void* out;                // [T, Hq * D] (q dtype), row stride out_st
+  int64_t out_st;
+  float* part;              // [splits, Hkv, rows, D + 2] (m, l, acc) when split
+  int* status;
+};
+
+constexpr int CAS_D = 128;          // head_dim of the MFMA path
+constexpr int CAS_KP = CAS_D + 8;   // K row pitch in LDS (bf16): 272 bytes, conflict-free reads
+constexpr int CAS_VP = 32 + 8;      // V^T row pitch (bf16): 80 bytes
+constexpr int CAS_PP = 32 + 8;      // P row pitch (bf16): 80 bytes
+
+template <bool BF16>
+__global__ __launch_bounds__(256) void cascade_attn_kernel(CasArgs a) {
+  using E = Elem<BF16 ? BFA_DTYPE_BF16 : BFA_DTYPE_F16>;
+  __shared__ uint16_t ks[32 * CAS_KP];
+  __shared__ uint16_t vt[CAS_D * CAS_VP];
+  __shared__ uint16_t pt[4][16 * CAS_PP];
+  __shared__ int64_t kpos_s[32];
+  __shared__ int kval_s[32];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int64_t g = blockIdx.y;                                  // kv head
+  const int64_t rows = a.tokens * a.group;
+  const int64_t row0 = static_cast<int64_t>(blockIdx.x) * 64 + wid * 16;
+  const int64_t step0 = static_cast<int64_t>(blockIdx.z) * a.steps_per_split;
+  const int64_t step1 = min(step0 + a.steps_per_split, a.steps);
+
+  // Q fragments (A operand, 16 rows x 32 head-dim per MFMA): lane holds row
+  // lane % 16 and head-dim 32 j + 8 (lane / 16) .. +7 for j = 0..3.
+  uint4 qf[4];
+  {
+    const int64_t r = min(row0 + (lane & 15), rows - 1);
+    const int64_t t = r / a.group, hh = g * a.group + (r - t * a.group);
+    const uint16_t* qrow = a.q + t * a.q_st + hh * a.q_sh;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) qf[j] = *reinterpret_cast<const uint4*>(qrow + 32 * j + 8 * (lane >> 4));
+  }
+  // query positions of the 4 rows this lane holds in the 16x16 output layout
+  // (rows 4 (lane / 16) + i)
+  int64_t qp[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int64_t r = min(row0 + 4 * (lane >> 4) + i, rows - 1);
+    const int64_t t = r / a.group;
+    qp[i] = a.qpos_i64 ? static_cast<const int64_t*>(a.qpos)[t] : static_cast<const int32_t*>(a.qpos)[t];
+  }
+
+  float m[4], l[4];
+  cas_f32x4_t o[8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    m[i] = -INFINITY;
+    l[i] = 0.f;
+  }
+#pragma unroll
+  for (int j = 0; j < 8; ++j) o[j] = cas_f32x4_t{};
+
+  // Staging roles: K -- key row tid / 8, head-dim pair chunk tid % 8 (columns
+  // 8c..8c+7 and 64+8c..64+8c+7, the RoPE pairs); V -- the same row, chunks c and
+  // c + 8 of 8 elements.  The global loads of step i+1 (entry metadata, then K, V
+  // and cos/sin) are issued before step i's matrix work, so their latency hides
+  // behind it.
+  const int sk = tid >> 3, sc = tid & 7;
+  float kg1[8], kg2[8];  // k_norm weights of this lane's columns
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    kg1[i] = a.knorm_w ? load_any(a.knorm_w, a.knorm_dt, 8 * sc + i) : 1.f;
+    kg2[i] = a.knorm_w ? load_any(a.knorm_w, a.knorm_dt, CAS_D / 2 + 8 * sc + i) : 1.f;
+  }
+  struct Meta {
+    int64_t page, kp, dpos, s;
+    int ntok_rot;
+    bool in;
+  };
+  auto load_meta = [&](int64_t step) {
+    Meta mt{};
+    const int64_t slot_g = step * 32 + sk;  // padded key index
+    const int64_t e = slot_g / a.page_size;
+    mt.s = slot_g - e * a.page_size;
+    mt.in = step < step1 && e < a.num_entries;
+    if (mt.in) {
+      mt.page = a.pages[e];
+      mt.kp = a.kstart[e] + mt.s;
+      mt.dpos = a.delta[e];
+      mt.ntok_rot = a.info[e];
+    }
+    return mt;
+  };
+  struct Buf {
+    uint4 k1, k2, v0, v1;
+    float4 c0, c1, s0, s1;
+    bool valid, rot;
+    int64_t kp;
+  };
+  // resolves a slot (bounds, wrap) and issues its K / V / cos / sin loads
+  auto issue = [&](const Meta& mt) {
+    Buf b{};
+    b.valid = mt.in && mt.s < (mt.ntok_rot & 0xffff);
+    const int64_t page = mt.page < 0 ? mt.page + a.num_pages : mt.page;  // kv_cache[-1] is the last page
+    if (b.valid && (page < 0 || page >= a.num_pages)) {
+      if (sc == 0) flag_status(a.status, BFA_STATUS_INDEX_OOB);
+      b.valid = false;
+    }
+    b.rot = b.valid && a.cs != nullptr && ((mt.ntok_rot >> 16) & 1);
+    int64_t dpos = mt.dpos;
+    if (b.rot) {
+      if (dpos < 0) dpos += a.max_pos;
+      if (dpos < 0 || dpos >= a.max_pos) {
+        if (sc == 0) flag_status(a.status, BFA_STATUS_INDEX_OOB);
+        b.valid = false;
+        b.rot = false;
+      }
+    }
+    b.kp = mt.kp;
+    if (b.valid) {
+      const uint16_t* krow = a.cache + page * a.c_sp + g * a.c_sh + mt.s * a.c_ss;
+      b.k1 = load16_nt(krow + 8 * sc);
+      b.k2 = load16_nt(krow + CAS_D / 2 + 8 * sc);
+      b.v0 = load16_nt(krow + a.c_skv + 8 * sc);
+      b.v1 = load16_nt(krow + a.c_skv + 64 + 8 * sc);
+    }
+    if (b.rot) {
+      const float4* cr = reinterpret_cast<const float4*>(a.cs + dpos * CAS_D + 8 * sc);
+      const float4* sr = reinterpret_cast<const float4*>(a.cs + dpos * CAS_D + CAS_D / 2 + 8 * sc);
+      b.c0 = cr[0]; b.c1 = cr[1]; b.s0 = sr[0]; b.s1 = sr[1];
+    }
+    return b;
+  };
+  auto unpack8 = [](const uint4& u, float (&x)[8]) {
+    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      x[2 * i] = E::to_f32(static_cast<uint16_t>(w[i] & 0xffffu));
+      x[2 * i + 1] = E::to_f32(static_cast<uint16_t>(w[i] >> 16));
+    }
+  };
+
+  Buf buf = issue(load_meta(step0));
+  for (int64_t step = step0; step < step1; ++step) {
+    const Meta mnext = load_meta(step + 1);
+    // ---- K row (rotated, normalised) -> LDS
+    float x1[8], x2[8];
+    if (buf.valid) {
+      unpack8(buf.k1, x1);
+      unpack8(buf.k2, x2);
+      if (buf.rot) {
+        const float cs[8] = {buf.c0.x, buf.c0.y, buf.c0.z, buf.c0.w, buf.c1.x, buf.c1.y, buf.c1.z, buf.c1.w};
+        const float sn[8] = {buf.s0.x, buf.s0.y, buf.s0.z, buf.s0.w, buf.s1.x, buf.s1.y, buf.s1.z, buf.s1.w};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {  // apply_rotary_emb: fp32, result in the cache dtype
+          const float u = x1[i], w = x2[i];
+          x1[i] = E::round(u * cs[i] - w * sn[i]);
+          x2[i] = E::round(w * cs[i] + u * sn[i]);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) x1[i] = x2[i] = 0.f;
+    }
+    if (a.knorm_w) {  // uniform: every lane joins the 8-lane sum
+      float ss = 0.f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) ss += x1[i] * x1[i] + x2[i] * x2[i];
+      ss = group_sum<8>(ss);
+      const float r = 1.0f / sqrtf(ss / static_cast<float>(CAS_D) + a.knorm_eps);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        x1[i] = buf.valid ? E::round(E::round(x1[i] * r) * kg1[i]) : 0.f;
+        x2[i] = buf.valid ? E::round(E::round(x2[i] * r) * kg2[i]) : 0.f;
+      }
+    }
+    store8<BF16 ? BFA_DTYPE_BF16 : BFA_DTYPE_F16>(ks + sk * CAS_KP + 8 * sc, x1);
+    store8<BF16 ? BFA_DTYPE_BF16 : BFA_DTYPE_F16>(ks + sk * CAS_KP + CAS_D / 2 + 8 * sc, x2);
+    // ---- V row -> LDS transposed (zeros for masked slots: 0 x garbage would be NaN)
+    {
+      const uint4 v0 = buf.valid ? buf.v0 : make_uint4(0, 0, 0, 0);
+      const uint4 v1 = buf.valid ? buf.v1 : make_uint4(0, 0, 0, 0);
+      const uint32_t w0[4] = {v0.x, v0.y, v0.z, v0.w}, w1[4] = {v1.x, v1.y, v1.z, v1.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        vt[(8 * sc + 2 * i) * CAS_VP + sk] = static_cast<uint16_t>(w0[i] & 0xffffu);
+        vt[(8 * sc + 2 * i + 1) * CAS_VP + sk] = static_cast<uint16_t>(w0[i] >> 16);
+        vt[(64 + 8 * sc + 2 * i) * CAS_VP + sk] = static_cast<uint16_t>(w1[i] & 0xffffu);
+        vt[(64 + 8 * sc + 2 * i + 1) * CAS_VP + sk] = static_cast<uint16_t>(w1[i] >> 16);
+      }
+    }
+    if (sc == 0) {
+      kpos_s[sk] = buf.kp;
+      kval_s[sk] = buf.valid ? 1 : 0;
+    }
+    __syncthreads();
+    buf = issue(mnext);  // step + 1's loads fly while this step's matrix work runs
+
+    // ---- S = Q K^T for 2 blocks of 16 keys (B operand: lane holds key lane % 16,
+    //      head-dim 32 j + 8 (lane / 16) .. +7)
+    cas_f32x4_t sacc[2];
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      sacc[b] = cas_f32x4_t{};
+      const uint16_t* kr = ks + (16 * b + (lane & 15)) * CAS_KP + 8 * (lane >> 4);
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        sacc[b] = mfma16x32<BF16>(qf[j], *reinterpret_cast<const uint4*>(kr + 32 * j), sacc[b]);
+    }
+    // ---- mask, running max / sum (lane holds key 16 b + lane % 16 of rows 4 (lane/16) + i)
+    float p[2][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float mx = -INFINITY;
+#pragma unroll
+      for (int b = 0; b < 2; ++b) {
+        const int kk = 16 * b + (lane & 15);
+        const bool use = kval_s[kk] && (!a.causal || kpos_s[kk] <= qp[i]);
+        p[b][i] = use ? sacc[b][i] * a.scale : -INFINITY;
+        mx = fmaxf(mx, p[b][i]);
+      }
+#pragma unroll
+      for (int d = 1; d < 16; d <<= 1) mx = fmaxf(mx, __shfl_xor(mx, d, kWave));
+      const float m_new = fmaxf(m[i], mx);
+      const float alpha = m[i] == -INFINITY ? 0.f : expf(m[i] - m_new);
+      float rs = 0.f;
+#pragma unroll
+      for (int b = 0; b < 2; ++b) {
+        p[b][i] = p[b][i] == -INFINITY ? 0.f : expf(p[b][i] - m_new);
+        rs += p[b][i];
+      }
+#pragma unroll
+      for (int d = 1; d < 16; d <<= 1) rs += __shfl_xor(rs, d, kWave);
+      l[i] = l[i] * alpha + rs;
+      m[i] = m_new;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) o[j][i] *= alpha;
+    }
+    // ---- P (16 rows x 32 keys) through LDS into the A-operand layout
+    uint16_t* pw = pt[wid];
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        pw[(4 * (lane >> 4) + i) * CAS_PP + 16 * b + (lane & 15)] = E::from_f32(p[b][i]);
+    __asm__ volatile("" ::: "memory");  // wave-private tile, LDS keeps a wave's order
+    const uint4 pf = *reinterpret_cast<const uint4*>(pw + (lane & 15) * CAS_PP + 8 * (lane >> 4));
+    // ---- O += P V (B operand: lane holds head-dim column 16 j + lane % 16, keys
+    //      8 (lane / 16) .. +7, read from V^T)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const uint4 vf = *reinterpret_cast<const uint4*>(vt + (16 * j + (lane & 15)) * CAS_VP + 8 * (lane >> 4));
+      o[j] = mfma16x32<BF16>(pf, vf, o[j]);
+    }
+    __syncthreads();  // every wave is done with ks / vt before the next step refills them
+  }
+
+  // ---- rows out: lane holds head-dim column 16 j + lane % 16 of rows 4 (lane/16) + i
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int64_t r = row0 + 4 * (lane >> 4) + i;
+    if (r >= rows) continue;
+    if (gridDim.z == 1) {
+      const int64_t t = r / a.group, hh = g * a.group + (r - t * a.group);
+      const float inv = 1.0f / fmaxf(l[i], 1e-12f);
+      uint16_t* orow = static_cast<uint16_t*>(a.out) + t * a.out_st + hh * CAS_D;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) orow[16 * j + (lane & 15)] = E::from_f32(o[j][i] * inv);
+    } else {
+      float* pr = a.part + ((static_cast<int64_t>(blockIdx.z) * a.hkv + g) * rows + r) * (CAS_D + 2);
+      if ((lane & 15) == 0) {
+        pr[0] = m[i];
+        pr[1] = l[i];
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) pr[2 + 16 * j + (lane & 15)] = o[j][i];
+    }
+  }
+}
+
+// Combines the splits' (m, l, acc) rows: one wave per (kv head, row).  Lanes take
+// the splits for the maximum and the weights (64 at a time); each lane then sums
+// two head-dim columns over the splits with the weights broadcast from their
+// lanes, loads unrolled so they are in flight together.
+template <bool BF16>
+__global__ __launch_bounds__(256) void cascade_merge_kernel(CasArgs a, int64_t splits) {
+  using E = Elem<BF16 ? BFA_DTYPE_BF16 : BFA_DTYPE_F16>;
+  const int64_t rows = a.tokens * a.group;
+  const int64_t item = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (item >= a.hkv * rows) return;
+  const int64_t g = item / rows, r = item - g * rows;
+  const int lane = threadIdx.x & 63;
+  const int64_t zstride = a.hkv * rows * (CAS_D + 2);
+  const float* base = a.part + (g * rows + r) * (CAS_D + 2);
+  float mx = -INFINITY;
+  for (int64_t z0 = 0; z0 < splits; z0 += 64) {
+    const int64_t z = z0 + lane;
+    const float mz = z < splits ? base[z * zstride] : -INFINITY;
+    mx = fmaxf(mx, mz);
+  }
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) mx = fmaxf(mx, __shfl_xor(mx, d, kWave));
+  float lsum = 0.f, o0 = 0.f, o1 = 0.f;
+  for (int64_t z0 = 0; z0 < splits; z0 += 64) {
+    const int64_t z = z0 + lane;
+    float w = 0.f, lz = 0.f;
+    if (z < splits) {
+      const float mz = base[z * zstride];
+      w = mz == -INFINITY ? 0.f : expf(mz - mx);
+      lz = base[z * zstride + 1];
+    }
+    lsum += w * lz;
+    // 8 splits per round; a lane past the last split holds w = 0 and its row
+    // index is clamped to a real one
+    const int nz8 = static_cast<int>((min<int64_t>(64, splits - z0) + 7) & ~7);
+    for (int j0 = 0; j0 < nz8; j0 += 8) {
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const float wj = __shfl(w, j0 + u, kWave);
+        const float* pr = base + min<int64_t>(z0 + j0 + u, splits - 1) * zstride + 2;
+        o0 += wj * pr[lane];
+        o1 += wj * pr[64 + lane];
+      }
+    }
+  }
+  lsum = group_sum<kWave>(lsum);
+  const float inv = 1.0f / fmaxf(lsum, 1e-12f);
+  const int64_t t = r / a.group, hh = g * a.group + (r - t * a.group);
+  uint16_t* orow = static_cast<uint16_t*>(a.out) + t * a.out_st + hh * CAS_D;
+  orow[lane] = E::from_f32(o0 * inv);
+  orow[64 + lane] = E::from_f32(o1 * inv);
+}
+
+static int64_t cascade_splits(int64_t rows, int64_t hkv, int64_t steps) {
+  const int64_t blocks = cdiv(rows, 64) * hkv;
+  if (blocks >= 256 || steps <= 1) return 1;
+  return std::max<int64_t>(1, std::min<int64_t>(cdiv(512, blocks), steps));
+}
+
+}  // namespace bfa
+
+using namespace bfa;
+
+extern "C" int bfa_online_softmax_update(
+    const void* query, const void* key, const void* value, int q_dtype, int kv_dtype,
+    float* m_i, float* l_i, float* acc_i, const void* query_positions, int qpos_dtype,
+    const void* key_positions, int kpos_dtype, int64_t num_heads, int64_t batch,
+    int64_t num_tokens, int64_t head_dim, int64_t q_stride_head, int64_t q_stride_batch,
+    int64_t k_stride_head, int64_t k_stride_token, int64_t v_stride_head, int64_t v_stride_token,
+    int64_t m_stride_head, int64_t m_stride_batch, int64_t l_stride_head, int64_t l_stride_batch,
+    int64_t acc_stride_head, int64_t acc_stride_batch, float scale, int apply_causal_mask,
+    void* stream) {
+  const char* what = "bfa_online_softmax_update";
+  BFA_REQUIRE(is_float_dtype(q_dtype) && is_float_dtype(kv_dtype), "%s: bad dtype", what);
+  BFA_REQUIRE((qpos_dtype == BFA_DTYPE_I32 || qpos_dtype == BFA_DTYPE_I64) &&
+                  (kpos_dtype == BFA_DTYPE_I32 || kpos_dtype == BFA_DTYPE_I64),
+              "%s: positions must be int32/int64", what);
+  BFA_REQUIRE(num_heads >= 0 && batch >= 0 && num_tokens >= 0 && head_dim >= 0, "%s: bad geometry", what);
+  BFA_REQUIRE(head_dim <= 256, "%s: head_dim above 256", what);
+  if (num_heads == 0 || batch == 0) return BFA_OK;
+  BFA_REQUIRE(query && m_i && l_i && acc_i && query_positions, "%s: null pointer", what);
+  BFA_REQUIRE(num_tokens == 0 || (key && value && key_positions), "%s: null pointer", what);
+  OsmArgs a{};
+  a.q = query; a.k = key; a.v = value; a.q_dt = q_dtype; a.kv_dt = kv_dtype;
+  a.m = m_i; a.l = l_i; a.acc = acc_i;
+  a.qpos = query_positions; a.kpos = key_positions;
+  a.qpos_i64 = qpos_dtype == BFA_DTYPE_I64; a.kpos_i64 = kpos_dtype == BFA_DTYPE_I64;
+  a.heads = num_heads; a.batch = batch; a.tokens = num_tokens; a.head_dim = head_dim;
+  a.q_sh = q_stride_head; a.q_sb = q_stride_batch;
+  a.k_sh = k_stride_head; a.k_st = k_stride_token;
+  a.v_sh = v_stride_head; a.v_st = v_stride_token;
+  a.m_sh = m_stride_head; a.m_sb = m_stride_batch;
+  a.l_sh = l_stride_head; a.l_sb = l_stride_batch;
+  a.a_sh = acc_stride_head; a.a_sb = acc_stride_batch;
+  a.scale = scale; a.causal = apply_causal_mask;
+  const int64_t grid = cdiv(num_heads * batch, 4);
+  hipLaunchKernelGGL(online_softmax_kernel, dim3(static_cast<unsigned>(grid)), dim3(256), 0,
+                     as_stream(stream), a);
+  return check_launch(what);
+}
+
+extern "C" int64_t bfa_cascade_attention_workspace_size(int64_t tokens, int64_t num_q_heads,
+                                                        int64_t num_kv_heads, int64_t head_dim,
+                                                        int64_t num_entries, int64_t page_size) {
+  if (tokens <= 0 || num_kv_heads <= 0 || num_q_heads % num_kv_heads != 0 || page_size <= 0) return 0;
+  const int64_t rows = tokens * (num_q_heads / num_kv_heads);
+  const int64_t steps = cdiv(num_entries * page_size, 32);
+  const int64_t splits = cascade_splits(rows, num_kv_heads, steps);
+  return splits > 1 ? splits * num_kv_heads * rows * (head_dim + 2) * 4 : 0;
+}
+
+extern "C" int bfa_cascade_attention(
+    const void* query, int dtype, int64_t num_tokens, int64_t num_q_heads, int64_t q_stride_token,
+    int64_t q_stride_head, const void* query_positions, int qpos_dtype, const void* kv_cache,
+    int64_t num_pages, int64_t num_kv_heads, int64_t page_size, int64_t head_dim,
+    int64_t stride_page, int64_t stride_kv, int64_t stride_head, int64_t stride_slot,
+    int64_t num_entries, const int32_t* entry_page, const int64_t* entry_key_start,
+    const int64_t* entry_delta, const int32_t* entry_info, const float* cos_sin_cache,
+    int64_t max_position, const void* k_norm_weight, int k_norm_dtype, float k_norm_eps,
+    float scale, int causal, void* out, int64_t out_stride_token, void* workspace,
+    int64_t workspace_bytes, int32_t* status, void* stream) {
+  const char* what = "bfa_cascade_attention";
+  BFA_REQUIRE(dtype == BFA_DTYPE_BF16 || dtype == BFA_DTYPE_F16,
+              "%s: query and cache must be bf16 or fp16", what);
+  BFA_REQUIRE(head_dim == CAS_D, "%s: head_dim %lld (this kernel covers 128)", what,
+              static_cast<long long>(head_dim));
+  BFA_REQUIRE(qpos_dtype == BFA_DTYPE_I32 || qpos_dtype == BFA_DTYPE_I64, "%s: bad positions dtype", what);
+  BFA_REQUIRE(num_tokens >= 0 && num_kv_heads > 0 && num_q_heads % num_kv_heads == 0 && page_size > 0 &&
+                  page_size < 65536 && num_entries >= 0 && num_pages >= 0,
+              "%s: bad geometry", what);
+  BFA_REQUIRE(k_norm_weight == nullptr || is_float_dtype(k_norm_dtype), "%s: bad k_norm dtype", what);
+  BFA_REQUIRE(q_stride_token % 8 == 0 && q_stride_head % 8 == 0 && stride_page % 8 == 0 &&
+                  stride_kv % 8 == 0 && stride_head % 8 == 0 && stride_slot % 8 == 0 &&
+                  out_stride_token % 8 == 0 && aligned16(query) && aligned16(kv_cache) && aligned16(out) &&
+                  (cos_sin_cache == nullptr || aligned16(cos_sin_cache)),
+              "%s: tensors must be 16-byte aligned with strides in multiples of 8", what);
+  if (num_tokens == 0) return BFA_OK;
+  BFA_REQUIRE(query && query_positions && out, "%s: null pointer", what);
+  BFA_REQUIRE(num_entries == 0 || (entry_page && entry_key_start && entry_delta && entry_info),
+              "%s: null entry metadata", what);
+  BFA_REQUIRE(cos_sin_cache == nullptr || max_position > 0, "%s: empty rotary table", what);
+  CasArgs a{};
+  a.q = static_cast<const uint16_t*>(query);
+  a.q_st = q_stride_token; a.q_sh = q_stride_head;
+  a.qpos = query_positions; a.qpos_i64 = qpos_dtype == BFA_DTYPE_I64;
+  a.cache = static_cast<const uint16_t*>(kv_cache);
+  a.c_sp = stride_page; a.c_skv = stride_kv; a.c_sh = stride_head; a.c_ss = stride_slot;
+  a.num_pages = num_pages; a.page_size = page_size;
+  a.pages = entry_page; a.kstart = entry_key_start; a.delta = entry_delta; a.info = entry_info;
+  a.num_entries = num_entries;
+  a.cs = cos_sin_cache; a.max_pos = max_position;
+  a.knorm_w = k_norm_weight; a.knorm_dt = k_norm_dtype; a.knorm_eps = k_norm_eps;
+  a.tokens = num_tokens; a.hq = num_q_heads; a.hkv = num_kv_heads;
+  a.group = num_q_heads / num_kv_heads;
+  a.scale = scale; a.causal = causal;
+  a.out = out; a.out_st = out_stride_token;
+  a.status = status;
+  const int64_t rows = num_tokens * a.group;
+  a.steps = cdiv(num_entries * page_size, 32);
+  const int64_t splits = cascade_splits(rows, num_kv_heads, a.steps);
+  a.steps_per_split = std::max<int64_t>(1, cdiv(a.steps, splits));
+  const int64_t zs = a.steps > 0 ? cdiv(a.steps, a.steps_per_split) : 1;
+  if (zs > 1) {
+    BFA_REQUIRE(workspace && workspace_bytes >= zs * num_kv_heads * rows * (head_dim + 2) * 4,
+                "%s: workspace too small", what);
+    a.part = static_cast<float*>(workspace);
+  }
+  BFA_REQUIRE(cdiv(rows, 64) < (int64_t{1} << 31) && zs < 65536 && num_kv_heads < 65536,
+              "%s: grid too large", what);
+  const dim3 grid(static_cast<unsigned>(cdiv(rows, 64)), static_cast<unsigned>(num_kv_heads),
+                  static_cast<unsigned>(zs));
+  const dim3 mgrid(static_cast<unsigned>(cdiv(num_kv_heads * rows, 4)));
+  const hipStream_t s = as_stream(stream);
+  if (dtype == BFA_DTYPE_BF16) {
+    hipLaunchKernelGGL(cascade_attn_kernel<true>, grid, dim3(256), 0, s, a);
+    if (zs > 1) hipLaunchKernelGGL(cascade_merge_kernel<true>, mgrid, dim3(256), 0, s, a, zs);
+  } else {
+    hipLaunchKernelGGL(cascade_attn_kernel<false>, grid, dim3(256), 0, s, a);
+    if (zs > 1) hipLaunchKernelGGL(cascade_merge_kernel<false>, mgrid, dim3(256), 0, s, a, zs);
+  }
+  return check_launch(what);
+}

@@ -5,6 +5,7 @@ from .fused_rmsnorm_qkv_production import FusedRMSNormQKV
 from .fused_rmsnorm_qkv_with_bias import FusedRMSNormQKVWithBias
 from .kv_cache_utils import (append_paged_kv_batch, append_to_paged_kv_cache_custom,
                              build_paged_kv_indices)
+from .online_softmax import online_softmax_update
 from .rmsnorm_f32 import RMSNormF32
 
 __all__ = [
@@ -16,4 +17,5 @@ __all__ = [
     "append_paged_kv_batch",
     "append_to_paged_kv_cache_custom",
     "build_paged_kv_indices",
+    "online_softmax_update",
 ]

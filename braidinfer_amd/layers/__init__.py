@@ -1,5 +1,6 @@
 """MI355X layers under the module and class names of braidinfer/layers."""
 from .activation import SiluAndMul, silu_and_mul
+from .cascade_attention import CascadeAttention, CascadeLevel
 from .cascade_rope import rerotate_paged_k
 from .embed_head import VocabParallelEmbedding, embedding
 from .fused_attention_input import llama_attention_input, qwen3_attention_input
@@ -7,7 +8,7 @@ from .layernorm import RMSNorm, rms_norm
 from .rotary_embedding import RotaryEmbedding, apply_rotary_emb, get_rope
 
 __all__ = [
-    "RMSNorm", "RotaryEmbedding", "SiluAndMul", "VocabParallelEmbedding", "apply_rotary_emb",
+    "CascadeAttention", "CascadeLevel", "RMSNorm", "RotaryEmbedding", "SiluAndMul", "VocabParallelEmbedding", "apply_rotary_emb",
     "embedding", "get_rope", "llama_attention_input", "qwen3_attention_input",
     "rerotate_paged_k", "rms_norm", "silu_and_mul",
 ]

@@ -256,6 +256,66 @@ int bfa_append_paged_kv(const void* k, const void* v, int kv_dtype, int64_t num_
                         const void* positions, int positions_dtype, int64_t page_size,
                         int32_t* status, void* stream);
 
+/* ------------------------------------------------------ cascade attention --
+ * online_softmax_update — braidinfer/kernels/online_softmax.py:214-297 (kernel
+ * :14-211): updates the running state (m_i [H, B], l_i [H, B], acc_i [H, B, D],
+ * fp32, in place) of B queries per head with N keys taken in order:
+ *   s = (q . k) * scale; keys with position > the query's skipped when causal;
+ *   m' = max(m, s); l = l e^(m-m') + e^(s-m'); acc = acc e^(m-m') + e^(s-m') v.
+ * query [H, B, D], key/value [H, N, D]: element strides, unit stride along D
+ * (D <= 256); query_positions [B], key_positions [N] int32/int64. */
+int bfa_online_softmax_update(const void* query, const void* key, const void* value, int q_dtype,
+                              int kv_dtype, float* m_i, float* l_i, float* acc_i,
+                              const void* query_positions, int qpos_dtype,
+                              const void* key_positions, int kpos_dtype, int64_t num_heads,
+                              int64_t batch, int64_t num_tokens, int64_t head_dim,
+                              int64_t q_stride_head, int64_t q_stride_batch, int64_t k_stride_head,
+                              int64_t k_stride_token, int64_t v_stride_head,
+                              int64_t v_stride_token, int64_t m_stride_head,
+                              int64_t m_stride_batch, int64_t l_stride_head,
+                              int64_t l_stride_batch, int64_t acc_stride_head,
+                              int64_t acc_stride_batch, float scale, int apply_causal_mask,
+                              void* stream);
+
+/* CascadeAttention.forward — braidinfer/layers/cascade_attention.py:50-231 — in one
+ * launch (plus a merge launch when the key range is split).  query [T, Hq, 128]
+ * (bf16/fp16; token / head strides), query_positions [T]; kv_cache one layer of the
+ * paged cache, strides (page, K|V, head, slot), K at index 0.  The attended pages
+ * are num_entries entries in the reference's walk order (levels, chunks, pages;
+ * :112-224), each spanning page_size key positions:
+ *   entry_page[e]      page id (int32; a negative id counts from the end, as
+ *                      kv_cache[-1] does; out of range sets BFA_STATUS_INDEX_OOB),
+ *   entry_key_start[e] key position of the entry's slot 0 (the kv_length of the
+ *                      attended chunks before its chunk + page_size x its index
+ *                      in the chunk, :199-203),
+ *   entry_delta[e]     global - cached position start of its chunk (:153-170),
+ *   entry_info[e]      bits 0-15: tokens attended on the page (page_size, or
+ *                      kv_last_page_len on a chunk's last page, :131-134), bit 16:
+ *                      rotate K by cos_sin_cache[delta] (fp32 [max_position, 128];
+ *                      a negative delta wraps; out of range sets
+ *                      BFA_STATUS_INDEX_OOB).
+ * k_norm_weight [128] (optional) applies RMSNorm(eps) to K after the rotation
+ * (:175-178).  Query head h attends kv head h / (Hq / Hkv); causal masks keys
+ * whose position exceeds the query's.  out [T, Hq * 128] (query dtype, token
+ * stride out_stride_token) = acc / max(l, 1e-12) (:226-231).  workspace:
+ * bfa_cascade_attention_workspace_size bytes. */
+int64_t bfa_cascade_attention_workspace_size(int64_t tokens, int64_t num_q_heads,
+                                             int64_t num_kv_heads, int64_t head_dim,
+                                             int64_t num_entries, int64_t page_size);
+int bfa_cascade_attention(const void* query, int dtype, int64_t num_tokens, int64_t num_q_heads,
+                          int64_t q_stride_token, int64_t q_stride_head,
+                          const void* query_positions, int qpos_dtype, const void* kv_cache,
+                          int64_t num_pages, int64_t num_kv_heads, int64_t page_size,
+                          int64_t head_dim, int64_t stride_page, int64_t stride_kv,
+                          int64_t stride_head, int64_t stride_slot, int64_t num_entries,
+                          const int32_t* entry_page, const int64_t* entry_key_start,
+                          const int64_t* entry_delta, const int32_t* entry_info,
+                          const float* cos_sin_cache, int64_t max_position,
+                          const void* k_norm_weight, int k_norm_dtype, float k_norm_eps,
+                          float scale, int causal, void* out, int64_t out_stride_token,
+                          void* workspace, int64_t workspace_bytes, int32_t* status,
+                          void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -170,3 +170,25 @@ def append_paged_kv(k, v, cache, kv_indices, positions, page_size, layout="HND")
             else:
                 out[page, kv, slot, :, :] = src[t]
     return out, skipped
+
+
+def attention(q, k, v, qpos, kpos, scale, group, causal=True):
+    """Softmax attention in float64, written directly: q [T, H, D], k/v [N, Hkv, D],
+    query head h reads kv head h // group; keys whose position exceeds the query's
+    are excluded when causal; a query with no key gets 0.  Returns [T, H, D]."""
+    q = np.asarray(q, np.float64)
+    k = np.asarray(k, np.float64)
+    v = np.asarray(v, np.float64)
+    t_, h, d = q.shape
+    out = np.zeros((t_, h, d))
+    for hh in range(h):
+        kh, vh = k[:, hh // group], v[:, hh // group]
+        s = q[:, hh] @ kh.T * scale  # [T, N]
+        if causal:
+            s = np.where(np.asarray(kpos)[None, :] <= np.asarray(qpos)[:, None], s, -np.inf)
+        mx = np.max(s, axis=1, keepdims=True)
+        ok = np.isfinite(mx[:, 0])
+        w = np.where(ok[:, None], np.exp(s - np.where(ok[:, None], mx, 0.0)), 0.0)
+        den = w.sum(axis=1, keepdims=True)
+        out[:, hh] = np.where(ok[:, None], (w @ vh) / np.where(den > 0, den, 1.0), 0.0)
+    return out

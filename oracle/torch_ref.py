@@ -181,6 +181,85 @@ def append_paged_kv_batch(k, v, layer_cache, kv_indices, kv_indptr, batch_indice
     return cache, sorted(skipped)
 
 
+# ---------------------------------------------------------- cascade attention
+def online_softmax_update(query, key, value, m_i, l_i, acc_i, query_positions, key_positions,
+                          scale, apply_causal_mask=True):
+    """The recurrence of online_softmax_kernel, braidinfer/kernels/online_softmax.py:80-125,
+    in fp32, keys in order: s = (q . k) * scale; m' = max(m, s);
+    l = l e^(m-m') + e^(s-m'); acc = acc e^(m-m') + e^(s-m') v; a key whose position
+    exceeds the query's is skipped when causal.  query [H, B, D], key/value [H, N, D];
+    returns new (m [H, B], l [H, B], acc [H, B, D])."""
+    m, l, acc = m_i.clone().float(), l_i.clone().float(), acc_i.clone().float()
+    q, k, v = query.float(), key.float(), value.float()
+    for t in range(key.shape[1]):
+        use = torch.ones(query.shape[1], dtype=torch.bool)
+        if apply_causal_mask:
+            use = key_positions[t] <= query_positions
+        s = (q * k[:, t].unsqueeze(1)).sum(-1) * scale  # [H, B]
+        m_new = torch.maximum(m, s)
+        alpha = torch.exp(m - m_new)
+        beta = torch.exp(s - m_new)
+        u = use.unsqueeze(0)
+        l = torch.where(u, l * alpha + beta, l)
+        acc = torch.where(u.unsqueeze(-1), alpha.unsqueeze(-1) * acc + beta.unsqueeze(-1) * v[:, t].unsqueeze(1), acc)
+        m = torch.where(u, m_new, m)
+    return m, l, acc
+
+
+def cascade_attention(query, query_positions, kv_cache, cascade_levels, num_heads, num_kv_heads,
+                      scale, page_size, cos_sin_cache=None, k_norm_weight=None, k_norm_eps=1e-6,
+                      causal_mask=True):
+    """CascadeAttention.forward, braidinfer/layers/cascade_attention.py:50-231, page by page:
+    K of each page is rotated by cos_sin_cache[global - cached position start] when the
+    chunk moved (and a table is given), then RMS-normalised when k_norm_weight is given;
+    GQA by repeat_interleave; the online softmax recurrence above per page with key
+    positions counted over the attended chunks.  Levels and chunks are any objects with
+    the reference's attributes (kv_page_indices / kv_page_indptr / kv_last_page_len /
+    chunks; page_table / kv_length / global_position_start / cached_position_start).
+    query [T, H, D]; returns [T, H * D] in the query dtype."""
+    t_, h, d = query.shape
+    q = query.transpose(0, 1)
+    m = torch.full((h, t_), float("-inf"))
+    l = torch.zeros(h, t_)
+    acc = torch.zeros(h, t_, d)
+    cumulative = 0
+    for level in cascade_levels:
+        for ci, chunk in enumerate(level.chunks):
+            if not chunk.page_table or chunk.kv_length == 0:
+                continue
+            start, end = int(level.kv_page_indptr[ci]), int(level.kv_page_indptr[ci + 1])
+            chunk_pages = level.kv_page_indices[start:end]
+            for local, page in enumerate(chunk_pages):
+                page = int(page)
+                tokens = int(level.kv_last_page_len[ci]) if local == len(chunk_pages) - 1 else page_size
+                if tokens <= 0:
+                    continue
+                page_k = kv_cache[page, 0, :, :tokens, :].transpose(0, 1)
+                page_v = kv_cache[page, 1, :, :tokens, :].transpose(0, 1)
+                if cos_sin_cache is not None and hasattr(chunk, "global_position_start"):
+                    before = local * page_size
+                    cached = getattr(chunk, "cached_position_start", 0)
+                    glob = getattr(chunk, "global_position_start", cached)
+                    cpos = torch.arange(cached + before, cached + before + tokens)
+                    gpos = torch.arange(glob + before, glob + before + tokens)
+                    if not torch.equal(cpos, gpos):
+                        flat = page_k.reshape(tokens, num_kv_heads * d)
+                        _, rot = rotary_forward(cos_sin_cache, d, gpos - cpos, torch.zeros_like(flat), flat)
+                        page_k = rot.reshape(tokens, num_kv_heads, d)
+                if k_norm_weight is not None:
+                    page_k = rms_forward(page_k, k_norm_weight, k_norm_eps)
+                if num_kv_heads != num_heads:
+                    rep = num_heads // num_kv_heads
+                    page_k = page_k.repeat_interleave(rep, dim=1)
+                    page_v = page_v.repeat_interleave(rep, dim=1)
+                kpos = torch.arange(cumulative + local * page_size, cumulative + local * page_size + tokens)
+                m, l, acc = online_softmax_update(q, page_k.transpose(0, 1), page_v.transpose(0, 1), m, l,
+                                                  acc, query_positions, kpos, scale, causal_mask)
+            cumulative += chunk.kv_length
+    out = (acc / torch.clamp(l, min=1e-12).unsqueeze(-1)).to(query.dtype)
+    return out.transpose(0, 1).contiguous().view(-1, h * d)
+
+
 # ------------------------------------------------------- fused RMSNorm + QKV
 def _rms(x32: torch.Tensor, eps: float) -> torch.Tensor:
     # tl.sqrt(acc_var / hidden_dim + eps) with acc_var = sum(x*x) in fp32

@@ -1,0 +1,181 @@
+"""GPU parity of the paged cascade attention (CascadeAttention.forward,
+layers/cascade_attention.py:50-231) and of online_softmax_update
+(kernels/online_softmax.py:214-297) against the oracle's page-by-page restatement.
+
+online_softmax_update: fp32 state within 1e-5, the reference test's bound
+(tests/test_online_softmax_kernel.py:95-103).  Cascade attention: the output
+within |d| <= 2e-2 + 1e-2 |r| (tests/helpers.py); the kernel computes scores in
+fp32 from bf16 q and k like the reference, and rounds the softmax weights to
+bf16 for the P.V matrix product (a relative error of at most 2^-9 per weight)."""
+from __future__ import annotations
+
+import math
+import zlib
+from types import SimpleNamespace
+
+import pytest
+import torch
+
+import braidinfer_amd
+from braidinfer_amd.kernels import online_softmax_update
+from braidinfer_amd.layers import CascadeAttention, RMSNorm, RotaryEmbedding
+from oracle import torch_ref as R
+from tests.helpers import assert_close, gen, randn
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+@pytest.mark.parametrize("dtype,d,causal", [(torch.float32, 64, False), (torch.float32, 64, True),
+                                            (torch.bfloat16, 128, True), (torch.float16, 96, False)])
+def test_online_softmax_update(dtype, d, causal):
+    g = gen(60)
+    h, b, n = 8, 4, 16
+    q = randn(g, h, b, d, dtype=dtype)
+    k, v = randn(g, h, n, d, dtype=dtype), randn(g, h, n, d, dtype=dtype)
+    m0 = torch.full((h, b), float("-inf"))
+    l0, a0 = torch.zeros(h, b), torch.zeros(h, b, d)
+    qpos, kpos = torch.tensor([0, 5, 8, 30]), torch.arange(n)
+    em, el, ea = R.online_softmax_update(q, k, v, m0, l0, a0, qpos, kpos, d ** -0.5, causal)
+    m, l, acc = m0.to(DEV), l0.to(DEV), a0.to(DEV)
+    online_softmax_update(q.to(DEV), k.to(DEV), v.to(DEV), m, l, acc, qpos.to(DEV), kpos.to(DEV),
+                          d ** -0.5, causal)
+    # a second block continues from the state (the per-page use in cascade attention)
+    k2, v2 = randn(g, h, 5, d, dtype=dtype), randn(g, h, 5, d, dtype=dtype)
+    kpos2 = torch.arange(n, n + 5)
+    em, el, ea = R.online_softmax_update(q, k2, v2, em, el, ea, qpos, kpos2, d ** -0.5, causal)
+    online_softmax_update(q.to(DEV), k2.to(DEV), v2.to(DEV), m, l, acc, qpos.to(DEV), kpos2.to(DEV),
+                          d ** -0.5, causal)
+    torch.cuda.synchronize()
+    for got, exp, name in ((m, em, "m"), (l, el, "l"), (acc, ea, "acc")):
+        fin = torch.isfinite(exp)
+        assert torch.equal(torch.isfinite(got.cpu()), fin), name
+        assert (got.cpu()[fin] - exp[fin]).abs().max().item() < 1e-5 * max(1.0, exp[fin].abs().max().item()), name
+
+
+def make_levels(att, chunks_per_level, dev):
+    return [att._create_level(chunks, position_offset=0) for chunks in chunks_per_level]
+
+
+def cpu_levels(levels):
+    return [SimpleNamespace(chunks=lv.chunks, kv_page_indices=lv.kv_page_indices.cpu(),
+                            kv_page_indptr=lv.kv_page_indptr.cpu(), kv_last_page_len=lv.kv_last_page_len.cpu())
+            for lv in levels]
+
+
+def chunk(page_table, kv_length, cached=0, glob=0, kind="context"):
+    return SimpleNamespace(page_table=page_table, kv_length=kv_length, cached_position_start=cached,
+                           global_position_start=glob, chunk_type=SimpleNamespace(value=kind))
+
+
+def build_case(seed, hq, hkv, lengths, deltas, pages, ps=16, dtype=torch.bfloat16):
+    """A system chunk and context chunks of the given token counts in shuffled pages,
+    each moved by its delta; plus an empty chunk and one with pages but no tokens."""
+    g = gen(seed)
+    perm = torch.randperm(pages, generator=g).tolist()
+    chunks, used, pos = [], 0, 0
+    for i, (n, dl) in enumerate(zip(lengths, deltas)):
+        npg = max(1, (n + ps - 1) // ps)
+        chunks.append(chunk(perm[used:used + npg], n, 1000 + pos, 1000 + pos + dl,
+                            "system_prompt" if i == 0 else "context"))
+        used += npg
+        pos += n
+    chunks.insert(2, chunk([], 0))
+    chunks.insert(3, chunk(perm[used:used + 1], 0))
+    kv = randn(g, pages, 2, hkv, ps, 128, dtype=dtype)
+    return chunks, kv, sum(lengths)
+
+
+@pytest.mark.parametrize("name,tokens,hq,hkv,lengths,deltas,causal,knorm", [
+    ("llama decode", 1, 32, 8, [100, 37, 516], [0, 4000, -77], True, False),
+    ("llama decode batch", 4, 32, 8, [64, 300, 5], [0, 0, 12], True, False),
+    ("qwen3 decode k-norm", 1, 16, 8, [200, 17, 1000], [0, -4096, 3000], True, True),
+    ("qwen3 prefill chunk", 37, 16, 8, [48, 130, 64], [0, 77, -5], True, True),
+    ("llama prefill", 300, 32, 8, [128, 700, 300], [0, 2048, 0], True, False),
+    ("non-causal", 9, 16, 8, [33, 16, 1], [0, 5, 0], False, True),
+])
+def test_cascade_attention(name, tokens, hq, hkv, lengths, deltas, causal, knorm):
+    seed = zlib.crc32(name.encode()) % 1000
+    g = gen(seed)
+    d, ps, max_pos = 128, 16, 40960
+    chunks, kv, total = build_case(seed + 1, hq, hkv, lengths, deltas, pages=300)
+    rope = RotaryEmbedding(d, d, max_pos, 1e6).to(DEV)
+    att = CascadeAttention(hq, d, d ** -0.5, hkv, ps, rotary_emb=rope)
+    levels = att.create_cascade_levels(chunks)
+    q = randn(g, tokens, hq, d)
+    qpos = torch.arange(total - tokens + 1, total + 1) if causal else torch.full((tokens,), 5)
+    k_norm, kn_w = None, None
+    if knorm:
+        k_norm = RMSNorm(d, eps=1e-6).to(DEV)
+        kn_w = torch.exp(torch.empty(d).uniform_(math.log(0.05), math.log(100.0), generator=g)).to(torch.bfloat16)
+        with torch.no_grad():
+            k_norm.weight.data = kn_w.to(DEV)
+    braidinfer_amd.check_device_status()
+    out = att.forward(q.to(DEV), qpos.to(DEV), kv.to(DEV), levels, 0, causal_mask=causal, k_norm=k_norm)
+    torch.cuda.synchronize()
+    braidinfer_amd.check_device_status()
+    exp = R.cascade_attention(q, qpos, kv, cpu_levels(levels), hq, hkv, d ** -0.5, ps,
+                              rope.cos_sin_cache.cpu(), kn_w, 1e-6, causal)
+    assert out.shape == (tokens, hq * d) and out.dtype == q.dtype
+    assert_close(out, exp, what=name)
+
+
+def test_cascade_attention_fp16_query_before_keys_and_empty():
+    g = gen(70)
+    hq, hkv, d, ps = 16, 8, 128, 16
+    chunks, kv, total = build_case(71, hq, hkv, [20, 40], [0, 3], pages=20, dtype=torch.float16)
+    att = CascadeAttention(hq, d, d ** -0.5, hkv, ps)
+    levels = att.create_cascade_levels(chunks)
+    q = randn(g, 3, hq, d, dtype=torch.float16)
+    qpos = torch.tensor([-1, 10, 70])  # the first query precedes every key: zeros
+    out = att.forward(q.to(DEV), qpos.to(DEV), kv.to(DEV), levels, 0)
+    exp = R.cascade_attention(q, qpos, kv, cpu_levels(levels), hq, hkv, d ** -0.5, ps, None, None, 1e-6, True)
+    assert torch.count_nonzero(out[0]) == 0
+    assert_close(out, exp, what="fp16")
+    # no levels at all: every query attends nothing
+    out = att.forward(q.to(DEV), qpos.to(DEV), kv.to(DEV), [], 0)
+    assert torch.count_nonzero(out) == 0
+    # flat and 2-D query shapes are accepted as in the reference
+    out2 = att.forward(q.reshape(-1).to(DEV), qpos.to(DEV), kv.to(DEV), levels, 0)
+    out3 = att.forward(q.reshape(3, -1).to(DEV), qpos.to(DEV), kv.to(DEV), levels, 0)
+    assert torch.equal(out2, out3)
+
+
+def test_cascade_attention_delta_out_of_table_raises():
+    hq, hkv, d, ps = 16, 8, 128, 16
+    chunks, kv, total = build_case(72, hq, hkv, [20, 40], [0, -5000], pages=20)
+    rope = RotaryEmbedding(d, d, 4096, 1e6).to(DEV)
+    att = CascadeAttention(hq, d, d ** -0.5, hkv, ps, rotary_emb=rope)
+    levels = att.create_cascade_levels(chunks)
+    q = randn(gen(73), 2, hq, d)
+    braidinfer_amd.check_device_status()
+    att.forward(q.to(DEV), torch.tensor([60, 61], device=DEV), kv.to(DEV), levels, 0)
+    with pytest.raises(IndexError):
+        braidinfer_amd.check_device_status()
+
+
+def test_cascade_attention_graph_replays_match_eager():
+    """After one eager call the forward makes no host-to-device copy, so it can be
+    captured; every replay (with eager work in between) equals the eager result."""
+    hq, hkv, d, ps = 16, 8, 128, 16
+    chunks, kv, total = build_case(74, hq, hkv, [64, 300, 40], [0, 9, -3], pages=40)
+    rope = RotaryEmbedding(d, d, 4096, 1e6).to(DEV)
+    att = CascadeAttention(hq, d, d ** -0.5, hkv, ps, rotary_emb=rope)
+    levels = att.create_cascade_levels(chunks)
+    q = randn(gen(75), 1, hq, d).to(DEV)
+    qpos = torch.tensor([total], device=DEV)
+    kvd = kv.to(DEV)
+    eager = att.forward(q, qpos, kvd, levels, 0).clone()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        att.forward(q, qpos, kvd, levels, 0)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = att.forward(q, qpos, kvd, levels, 0)
+    for i in range(4):
+        torch.randn(1000, device=DEV).sum()  # unrelated eager work between replays
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {i}"

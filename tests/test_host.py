@@ -25,3 +25,47 @@ def test_rope_table_is_the_reference_table():
 def test_get_rope_is_cached():
     a = get_rope(64, 64, 2048, 10000.0)
     assert get_rope(64, 64, 2048, 10000.0) is a
+
+
+def _level(chunks, pages, indptr, last):
+    from braidinfer_amd.layers import CascadeLevel
+    i32 = torch.int32
+    return CascadeLevel(chunks, torch.tensor(pages, dtype=i32), torch.tensor(indptr, dtype=i32),
+                        torch.tensor(last, dtype=i32), 0)
+
+
+def test_cascade_plan_walks_pages_like_the_reference():
+    """The per-entry arrays of the cascade plan, worked out by hand from
+    cascade_attention.py:112-224 for page_size 4: a system chunk of 7 tokens on two
+    pages; a chunk with no pages and one with pages but no tokens (both skipped,
+    neither advances the key position); a moved chunk of 12 tokens (rotated by
+    -10); a chunk without global_position_start (never rotated); a chunk whose
+    last page holds 0 tokens (that page dropped); a one-page chunk on page -1
+    moved by 3."""
+    from types import SimpleNamespace as NS
+    from braidinfer_amd.layers import CascadeAttention
+
+    a = NS(page_table=[5, 6], kv_length=7, cached_position_start=0, global_position_start=0)
+    b = NS(page_table=[], kv_length=0, cached_position_start=0, global_position_start=50)
+    c = NS(page_table=[9], kv_length=0, cached_position_start=0, global_position_start=50)
+    d = NS(page_table=[1, 2, 3], kv_length=12, cached_position_start=100, global_position_start=90)
+    e = NS(page_table=[4], kv_length=3, cached_position_start=40)
+    f = NS(page_table=[7, 8], kv_length=4, cached_position_start=10, global_position_start=10)
+    h = NS(page_table=[-1], kv_length=2, cached_position_start=0, global_position_start=3)
+    levels = [_level([a], [5, 6], [0, 2], [3]),
+              _level([b, c, d, e, f, h], [9, 1, 2, 3, 4, 7, 8, -1], [0, 0, 1, 4, 5, 7, 8],
+                     [0, 0, 4, 3, 0, 2])]
+    att = CascadeAttention(4, 128, 1.0, 2, page_size=4, rotary_emb=NS())
+    meta = att._chunk_meta(levels)
+    page, kstart, delta, info = att._plan(levels, meta, torch.device("cpu"))
+    rot = 1 << 16
+    assert page.tolist() == [5, 6, 1, 2, 3, 4, 7, -1]
+    assert kstart.tolist() == [0, 4, 7, 11, 15, 19, 22, 26]
+    assert delta.tolist() == [0, 0, -10, -10, -10, 0, 0, 3]
+    assert info.tolist() == [4, 3, 4 | rot, 4 | rot, 4 | rot, 3, 4, 2 | rot]
+    # no rotary table: nothing rotates
+    plain = CascadeAttention(4, 128, 1.0, 2, page_size=4)
+    _, _, _, info2 = plain._plan(levels, plain._chunk_meta(levels), torch.device("cpu"))
+    assert info2.tolist() == [4, 3, 4, 4, 4, 3, 4, 2]
+    # the plan is cached per level set
+    assert att._plan(levels, meta, torch.device("cpu"))[0] is page

@@ -335,6 +335,149 @@ def test_kv_append_pinned():
                                    torch.zeros(1, dtype=torch.int64), 4, "XYZ")
 
 
+# --------------------------------------------------------- cascade attention
+def pin_online_softmax(fn):
+    g = gen(41)
+    h, b, n, d = 4, 3, 20, 16
+    q, k, v = (torch.randn(h, b, d, generator=g), torch.randn(h, n, d, generator=g),
+               torch.randn(h, n, d, generator=g))
+    scale = d ** -0.5
+    m0, l0, a0 = torch.full((h, b), float("-inf")), torch.zeros(h, b), torch.zeros(h, b, d)
+    qpos, kpos = torch.tensor([3, 11, 40]), torch.arange(n)
+    for causal in (False, True):
+        m, l, acc = fn(q, k, v, m0, l0, a0, qpos, kpos, scale, causal)
+        exp = N.attention(q.transpose(0, 1).numpy(), k.transpose(0, 1).numpy(), v.transpose(0, 1).numpy(),
+                          qpos.numpy(), kpos.numpy(), scale, 1, causal)
+        np.testing.assert_allclose((acc / l.unsqueeze(-1)).transpose(0, 1).numpy(), exp, rtol=1e-5, atol=1e-5)
+        # two blocks of keys in sequence give the state of one block
+        m1, l1, a1 = fn(q, k[:, :7], v[:, :7], m0, l0, a0, qpos, kpos[:7], scale, causal)
+        m2, l2, a2 = fn(q, k[:, 7:], v[:, 7:], m1, l1, a1, qpos, kpos[7:], scale, causal)
+        np.testing.assert_allclose(a2.numpy(), acc.numpy(), rtol=1e-5, atol=1e-5)
+        np.testing.assert_allclose(l2.numpy(), l.numpy(), rtol=1e-5, atol=1e-6)
+    # causal: a query at position 3 sees keys 0..3 only
+    m, l, acc = fn(q, k, v, m0, l0, a0, qpos, kpos, scale, True)
+    exp = N.attention(q[:, :1].transpose(0, 1).numpy(), k[:, :4].transpose(0, 1).numpy(),
+                      v[:, :4].transpose(0, 1).numpy(), qpos[:1].numpy(), kpos[:4].numpy(), scale, 1, False)
+    np.testing.assert_allclose((acc[:, :1] / l[:, :1].unsqueeze(-1)).transpose(0, 1).numpy(), exp, rtol=1e-5, atol=1e-5)
+
+
+class _Chunk:
+    def __init__(self, page_table, kv_length, cached=0, glob=0):
+        self.page_table, self.kv_length = page_table, kv_length
+        self.cached_position_start, self.global_position_start = cached, glob
+
+
+class _Level:
+    def __init__(self, chunks, ps):
+        idx, ptr, last = [], [0], []
+        for c in chunks:
+            if c.page_table:
+                idx += c.page_table
+                ptr.append(len(idx))
+                n = c.kv_length if len(c.page_table) == 1 else (c.kv_length % ps or (ps if c.kv_length else 0))
+                last.append(n)
+            else:
+                ptr.append(len(idx))
+                last.append(0)
+        self.chunks = chunks
+        self.kv_page_indices = torch.tensor(idx, dtype=torch.int32)
+        self.kv_page_indptr = torch.tensor(ptr, dtype=torch.int32)
+        self.kv_last_page_len = torch.tensor(last, dtype=torch.int32)
+
+
+def cascade_case(seed, hq=8, hkv=2, d=32, ps=4, t=5, pages=24, deltas=(0, 9, -3, 0)):
+    """Two levels: a 6-token system chunk, then a context chunk of 11 tokens, an empty
+    chunk, a chunk with pages but kv_length 0, and a 9-token chunk; shuffled pages."""
+    g = gen(seed)
+    perm = torch.randperm(pages, generator=g).tolist()
+    c0 = _Chunk(perm[0:2], 6, 100, 100 + deltas[0])
+    c1 = _Chunk(perm[2:5], 11, 7, 7 + deltas[1])
+    c2 = _Chunk([], 0)
+    c3 = _Chunk(perm[5:6], 0)
+    c4 = _Chunk(perm[6:9], 9, 50, 50 + deltas[2])
+    levels = [_Level([c0], ps), _Level([c1, c2, c3, c4], ps)]
+    kv = randn(g, pages, 2, hkv, ps, d)
+    q = randn(g, t, hq, d)
+    return levels, kv, q
+
+
+def flat_keys(levels, kv, ps, cache, hkv, d, k_norm_weight=None):
+    """K (rotated by the re-rotation oracle, normalised) and V of every attended token,
+    in the walk order, with their key positions."""
+    ks, vs, pos, cum = [], [], [], 0
+    for level in levels:
+        for ci, ch in enumerate(level.chunks):
+            if not ch.page_table or ch.kv_length == 0:
+                continue
+            s_, e_ = int(level.kv_page_indptr[ci]), int(level.kv_page_indptr[ci + 1])
+            pidx = level.kv_page_indices[s_:e_]
+            delta = torch.tensor([ch.global_position_start - ch.cached_position_start])
+            rot = R.rerotate_paged_k(kv, pidx, torch.tensor([0, e_ - s_], dtype=torch.int32), delta,
+                                     level.kv_last_page_len[ci:ci + 1], cache, k_norm_weight, 1e-6)
+            for j in range(e_ - s_):
+                n = int(level.kv_last_page_len[ci]) if j == e_ - s_ - 1 else ps
+                ks.append(rot[j, :n])
+                vs.append(kv[int(pidx[j]), 1, :, :n].transpose(0, 1))
+                pos += list(range(cum + j * ps, cum + j * ps + n))
+            cum += ch.kv_length
+    return torch.cat(ks), torch.cat(vs), torch.tensor(pos)
+
+
+def pin_cascade(fn):
+    hq, hkv, d, ps = 8, 2, 32, 4
+    cache = R.cos_sin_cache(d, 256, 1e4)
+    for causal, kn in ((True, None), (False, randn(gen(43), d, mean=1.0, std=0.3))):
+        levels, kv, q = cascade_case(42)
+        qpos = torch.tensor([0, 5, 12, 17, 40])
+        got = fn(q, qpos, kv, levels, hq, hkv, d ** -0.5, ps, cache, kn, 1e-6, causal)
+        k, v, kpos = flat_keys(levels, kv, ps, cache, hkv, d, kn)
+        exp = N.attention(_np(q), _np(k), _np(v), qpos.numpy(), kpos.numpy(), d ** -0.5, hq // hkv, causal)
+        check_bf16_agreement(got.view(q.shape), N.round_bf16(exp), max_frac=0.05, what="cascade")
+    # a query before every key attends nothing: zeros
+    levels, kv, q = cascade_case(44)
+    got = fn(q[:1], torch.tensor([-1]), kv, levels, hq, hkv, 1.0, ps, cache, None, 1e-6, True)
+    assert torch.count_nonzero(got) == 0
+
+
+def _cascade_oracle(q, qpos, kv, levels, hq, hkv, scale, ps, cache, kn, eps, causal):
+    return R.cascade_attention(q, qpos, kv, levels, hq, hkv, scale, ps, cache, kn, eps, causal)
+
+
+def test_cascade_attention_pinned():
+    pin_online_softmax(R.online_softmax_update)
+    pin_cascade(_cascade_oracle)
+
+
+def test_planted_cascade_mistakes_are_caught():
+    def no_scale(q, k, v, m, l, a, qp, kp, scale, causal):
+        return R.online_softmax_update(q, k, v, m, l, a, qp, kp, 1.0, causal)
+
+    with pytest.raises(AssertionError):
+        pin_online_softmax(no_scale)
+
+    def strict_causal(q, k, v, m, l, a, qp, kp, scale, causal):  # key_pos < query_pos
+        return R.online_softmax_update(q, k, v, m, l, a, qp - 1, kp, scale, causal)
+
+    with pytest.raises(AssertionError):
+        pin_online_softmax(strict_causal)
+
+    def gqa_modulo(q, qpos, kv, levels, hq, hkv, scale, ps, cache, kn, eps, causal):
+        # query head h reads kv head h % Hkv instead of h // (Hq / Hkv)
+        perm = torch.arange(hq).view(hkv, hq // hkv).t().reshape(-1)
+        out = R.cascade_attention(q[:, perm], qpos, kv, levels, hq, hkv, scale, ps, cache, kn, eps, causal)
+        inv = torch.argsort(perm)
+        return out.view(q.shape)[:, inv].reshape(q.shape[0], -1)
+
+    with pytest.raises(AssertionError):
+        pin_cascade(gqa_modulo)
+
+    def no_rotation(q, qpos, kv, levels, hq, hkv, scale, ps, cache, kn, eps, causal):
+        return R.cascade_attention(q, qpos, kv, levels, hq, hkv, scale, ps, None, kn, eps, causal)
+
+    with pytest.raises(AssertionError):
+        pin_cascade(no_rotation)
+
+
 # ------------------------------------------------------- fused RMSNorm+QKV
 def _qkv_inputs(seed, t=24, h=256, hq=8, hkv=2, d=32):
     g = gen(seed)
