@@ -173,6 +173,35 @@ __device__ __forceinline__ float group_sum(float v) {
   return v;
 }
 
+// Lane permutations inside a 16-lane DPP row (no LDS round trip, unlike
+// __shfl_xor, which goes through ds_bpermute).  Control codes of the gfx9 DPP
+// encoding: quad_perm [1,0,3,2] = 0xB1, quad_perm [2,3,0,1] = 0x4E,
+// row_half_mirror (lane i <- 7 - i within 8) = 0x141, row_mirror (lane i <-
+// 15 - i within 16) = 0x140.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+// Sum over aligned groups of 8 lanes; every lane of a group gets the same bits
+// (each step adds a pair of partial sums in commutable order).
+__device__ __forceinline__ float group8_sum_dpp(float v) {
+  v += dpp_f32<0xB1>(v);
+  v += dpp_f32<0x4E>(v);
+  v += dpp_f32<0x141>(v);
+  return v;
+}
+// Sum / maximum over aligned groups of 16 lanes, the same bits in every lane.
+__device__ __forceinline__ float group16_sum_dpp(float v) {
+  v = group8_sum_dpp(v);
+  return v + dpp_f32<0x140>(v);
+}
+__device__ __forceinline__ float group16_max_dpp(float v) {
+  v = fmaxf(v, dpp_f32<0xB1>(v));
+  v = fmaxf(v, dpp_f32<0x4E>(v));
+  v = fmaxf(v, dpp_f32<0x141>(v));
+  return fmaxf(v, dpp_f32<0x140>(v));
+}
+
 // Device status word: kernels that detect out-of-range indices OR a bit into
 // it with an ordinary store (every writer stores the same value).
 __device__ __forceinline__ void flag_status(int* status, int bit) {

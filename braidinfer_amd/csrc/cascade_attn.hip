@@ -19,13 +19,18 @@
 // Kernel design.  Rows are (query token, query head of a kv group) pairs of one kv
 // head; a workgroup of 4 waves owns 64 rows and one kv head and walks a range of
 // the padded key space (entry e, slot s) -> e * page_size + s in steps of 32 key
-// slots.  Per step: 256 lanes stage the 32 keys of K into LDS (rotated and
-// normalised on the way, with the rounding of the re-rotation kernel) and V
-// transposed into LDS; each wave computes S = Q K^T for its 16 rows with
-// v_mfma_f32_16x16x32_bf16, masks, updates its running max / sum in fp32, writes
-// P (bf16) through a wave-private LDS tile into the A-operand layout and adds
-// P V with 8 more MFMAs.  For few rows (decode) the key range is split across
-// workgroups and a merge kernel combines the partial (m, l, acc) rows.
+// slots.  The entries are the attended pages in walk order, each with its page
+// id, first key position, chunk delta and token count / rotate flag, flattened
+// on the host once per set of levels.  Per step: 256 lanes stage the 32 keys of
+// K into LDS (rotated and normalised on the way, with the rounding of the
+// re-rotation kernel) and V transposed into LDS; each wave computes S = Q K^T for
+// its 16 rows with v_mfma_f32_16x16x32_bf16, masks, updates its running max / sum
+// in fp32 (base 2, row reductions by DPP inside 16-lane rows), writes P (bf16)
+// through a wave-private LDS tile into the A-operand layout and adds P V with 8
+// more MFMAs.  The next step's K / V / cos-sin rows and the step after's entry
+// metadata are in flight during a step's matrix work.  For few rows (decode) the
+// key range is split across workgroups and a merge kernel combines the partial
+// (m, l, acc) rows.
 #include <cmath>
 
 #include "bfa_device.h"
@@ -150,6 +155,9 @@ struct CasArgs {
 };
 
 constexpr int CAS_D = 128;          // head_dim of the MFMA path
+
+// a zeroed row that masked slots load from instead of the cache and the rotary table
+__device__ __align__(16) float cas_zero_row[CAS_D];
 constexpr int CAS_KP = CAS_D + 8;   // K row pitch in LDS (bf16): 272 bytes, conflict-free reads
 constexpr int CAS_VP = 32 + 8;      // V^T row pitch (bf16): 80 bytes
 constexpr int CAS_PP = 32 + 8;      // P row pitch (bf16): 80 bytes
@@ -169,7 +177,7 @@ __global__ __launch_bounds__(256) void cascade_attn_kernel(CasArgs a) {
   const int64_t rows = a.tokens * a.group;
   const int64_t row0 = static_cast<int64_t>(blockIdx.x) * 64 + wid * 16;
   const int64_t step0 = static_cast<int64_t>(blockIdx.z) * a.steps_per_split;
-  const int64_t step1 = min(step0 + a.steps_per_split, a.steps);
+  int64_t step1 = min(step0 + a.steps_per_split, a.steps);
 
   // Q fragments (A operand, 16 rows x 32 head-dim per MFMA): lane holds row
   // lane % 16 and head-dim 32 j + 8 (lane / 16) .. +7 for j = 0..3.
@@ -183,14 +191,18 @@ __global__ __launch_bounds__(256) void cascade_attn_kernel(CasArgs a) {
   }
   // query positions of the 4 rows this lane holds in the 16x16 output layout
   // (rows 4 (lane / 16) + i)
-  int64_t qp[4];
+  int64_t qp[4], qt[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int64_t r = min(row0 + 4 * (lane >> 4) + i, rows - 1);
-    const int64_t t = r / a.group;
-    qp[i] = a.qpos_i64 ? static_cast<const int64_t*>(a.qpos)[t] : static_cast<const int32_t*>(a.qpos)[t];
+  for (int i = 0; i < 4; ++i) qt[i] = min(row0 + 4 * (lane >> 4) + i, rows - 1) / a.group;
+  if (a.qpos_i64) {  // one uniform branch, four loads in flight together
+#pragma unroll
+    for (int i = 0; i < 4; ++i) qp[i] = static_cast<const int64_t*>(a.qpos)[qt[i]];
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) qp[i] = static_cast<const int32_t*>(a.qpos)[qt[i]];
   }
 
+  const float sl2 = a.scale * 1.4426950408889634f;  // scale x log2(e)
   float m[4], l[4];
   cas_f32x4_t o[8];
 #pragma unroll
@@ -203,33 +215,46 @@ __global__ __launch_bounds__(256) void cascade_attn_kernel(CasArgs a) {
 
   // Staging roles: K -- key row tid / 8, head-dim pair chunk tid % 8 (columns
   // 8c..8c+7 and 64+8c..64+8c+7, the RoPE pairs); V -- the same row, chunks c and
-  // c + 8 of 8 elements.  The global loads of step i+1 (entry metadata, then K, V
-  // and cos/sin) are issued before step i's matrix work, so their latency hides
-  // behind it.
+  // c + 8 of 8 elements.  Loads run ahead of use: the K, V and cos/sin rows of
+  // step i+1 are issued before step i's matrix work, and the entry metadata of
+  // step i+2 right after them, raw, so that nothing waits on it before step i+1
+  // resolves its slots (the memory counter retires loads in issue order).
   const int sk = tid >> 3, sc = tid & 7;
-  float kg1[8], kg2[8];  // k_norm weights of this lane's columns
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    kg1[i] = a.knorm_w ? load_any(a.knorm_w, a.knorm_dt, 8 * sc + i) : 1.f;
-    kg2[i] = a.knorm_w ? load_any(a.knorm_w, a.knorm_dt, CAS_D / 2 + 8 * sc + i) : 1.f;
+  float kg1[8] = {1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f};  // k_norm weights of this lane's columns
+  float kg2[8] = {1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f};
+  if (a.knorm_w) {
+    const char* w = static_cast<const char*>(a.knorm_w);
+    if (a.knorm_dt == BFA_DTYPE_F32) {
+      load8<BFA_DTYPE_F32>(w + 4 * (8 * sc), kg1);
+      load8<BFA_DTYPE_F32>(w + 4 * (CAS_D / 2 + 8 * sc), kg2);
+    } else if (a.knorm_dt == BFA_DTYPE_BF16) {
+      load8<BFA_DTYPE_BF16>(w + 2 * (8 * sc), kg1);
+      load8<BFA_DTYPE_BF16>(w + 2 * (CAS_D / 2 + 8 * sc), kg2);
+    } else {
+      load8<BFA_DTYPE_F16>(w + 2 * (8 * sc), kg1);
+      load8<BFA_DTYPE_F16>(w + 2 * (CAS_D / 2 + 8 * sc), kg2);
+    }
   }
-  struct Meta {
-    int64_t page, kp, dpos, s;
-    int ntok_rot;
+  struct Meta {  // an entry's metadata as loaded; used only by issue()
+    int64_t kst, dpos, s;
+    int32_t page, info;
     bool in;
   };
+  // Every load below is unconditional (a slot past the range reads entry 0, a
+  // masked slot reads cas_zero_row) so that no load sits behind a branch: the
+  // memory-counter waits are then exact and a wait for one step's rows does not
+  // also wait for the next step's metadata.
   auto load_meta = [&](int64_t step) {
-    Meta mt{};
+    Meta mt;
     const int64_t slot_g = step * 32 + sk;  // padded key index
     const int64_t e = slot_g / a.page_size;
     mt.s = slot_g - e * a.page_size;
     mt.in = step < step1 && e < a.num_entries;
-    if (mt.in) {
-      mt.page = a.pages[e];
-      mt.kp = a.kstart[e] + mt.s;
-      mt.dpos = a.delta[e];
-      mt.ntok_rot = a.info[e];
-    }
+    const int64_t ec = mt.in ? e : 0;  // num_entries > 0 inside the loop
+    mt.page = a.pages[ec];
+    mt.kst = a.kstart[ec];
+    mt.dpos = a.delta[ec];
+    mt.info = a.info[ec];
     return mt;
   };
   struct Buf {
@@ -240,14 +265,14 @@ __global__ __launch_bounds__(256) void cascade_attn_kernel(CasArgs a) {
   };
   // resolves a slot (bounds, wrap) and issues its K / V / cos / sin loads
   auto issue = [&](const Meta& mt) {
-    Buf b{};
-    b.valid = mt.in && mt.s < (mt.ntok_rot & 0xffff);
-    const int64_t page = mt.page < 0 ? mt.page + a.num_pages : mt.page;  // kv_cache[-1] is the last page
+    Buf b;
+    b.valid = mt.in && mt.s < (mt.info & 0xffff);
+    const int64_t page = mt.page < 0 ? static_cast<int64_t>(mt.page) + a.num_pages : mt.page;  // kv_cache[-1] is the last page
     if (b.valid && (page < 0 || page >= a.num_pages)) {
       if (sc == 0) flag_status(a.status, BFA_STATUS_INDEX_OOB);
       b.valid = false;
     }
-    b.rot = b.valid && a.cs != nullptr && ((mt.ntok_rot >> 16) & 1);
+    b.rot = b.valid && a.cs != nullptr && ((mt.info >> 16) & 1);
     int64_t dpos = mt.dpos;
     if (b.rot) {
       if (dpos < 0) dpos += a.max_pos;
@@ -257,19 +282,18 @@ __global__ __launch_bounds__(256) void cascade_attn_kernel(CasArgs a) {
         b.rot = false;
       }
     }
-    b.kp = mt.kp;
-    if (b.valid) {
-      const uint16_t* krow = a.cache + page * a.c_sp + g * a.c_sh + mt.s * a.c_ss;
-      b.k1 = load16_nt(krow + 8 * sc);
-      b.k2 = load16_nt(krow + CAS_D / 2 + 8 * sc);
-      b.v0 = load16_nt(krow + a.c_skv + 8 * sc);
-      b.v1 = load16_nt(krow + a.c_skv + 64 + 8 * sc);
-    }
-    if (b.rot) {
-      const float4* cr = reinterpret_cast<const float4*>(a.cs + dpos * CAS_D + 8 * sc);
-      const float4* sr = reinterpret_cast<const float4*>(a.cs + dpos * CAS_D + CAS_D / 2 + 8 * sc);
-      b.c0 = cr[0]; b.c1 = cr[1]; b.s0 = sr[0]; b.s1 = sr[1];
-    }
+    b.kp = mt.kst + mt.s;
+    const uint16_t* zero = reinterpret_cast<const uint16_t*>(cas_zero_row);
+    const uint16_t* krow = b.valid ? a.cache + page * a.c_sp + g * a.c_sh + mt.s * a.c_ss : zero;
+    const uint16_t* vrow = b.valid ? krow + a.c_skv : zero;
+    b.k1 = load16_nt(krow + 8 * sc);
+    b.k2 = load16_nt(krow + CAS_D / 2 + 8 * sc);
+    b.v0 = load16_nt(vrow + 8 * sc);
+    b.v1 = load16_nt(vrow + 64 + 8 * sc);
+    const float* csrow = b.rot ? a.cs + dpos * CAS_D : cas_zero_row;
+    const float4* cr = reinterpret_cast<const float4*>(csrow + 8 * sc);
+    const float4* sr = reinterpret_cast<const float4*>(csrow + CAS_D / 2 + 8 * sc);
+    b.c0 = cr[0]; b.c1 = cr[1]; b.s0 = sr[0]; b.s1 = sr[1];
     return b;
   };
   auto unpack8 = [](const uint4& u, float (&x)[8]) {
@@ -281,47 +305,48 @@ __global__ __launch_bounds__(256) void cascade_attn_kernel(CasArgs a) {
     }
   };
 
-  Buf buf = issue(load_meta(step0));
+  if (step0 >= step1) step1 = step0;  // an empty range (no entries): the loop below does not run
+  Buf buf;
+  Meta mnext;
+  if (step0 < step1) {
+    buf = issue(load_meta(step0));
+    mnext = load_meta(step0 + 1);
+  }
   for (int64_t step = step0; step < step1; ++step) {
-    const Meta mnext = load_meta(step + 1);
     // ---- K row (rotated, normalised) -> LDS
+    // (a masked slot loaded zeros; its S column is masked below and its V row
+    // must be zero, since 0 x a NaN would poison the sum)
     float x1[8], x2[8];
-    if (buf.valid) {
-      unpack8(buf.k1, x1);
-      unpack8(buf.k2, x2);
-      if (buf.rot) {
-        const float cs[8] = {buf.c0.x, buf.c0.y, buf.c0.z, buf.c0.w, buf.c1.x, buf.c1.y, buf.c1.z, buf.c1.w};
-        const float sn[8] = {buf.s0.x, buf.s0.y, buf.s0.z, buf.s0.w, buf.s1.x, buf.s1.y, buf.s1.z, buf.s1.w};
+    unpack8(buf.k1, x1);
+    unpack8(buf.k2, x2);
+    if (buf.rot) {
+      const float cs[8] = {buf.c0.x, buf.c0.y, buf.c0.z, buf.c0.w, buf.c1.x, buf.c1.y, buf.c1.z, buf.c1.w};
+      const float sn[8] = {buf.s0.x, buf.s0.y, buf.s0.z, buf.s0.w, buf.s1.x, buf.s1.y, buf.s1.z, buf.s1.w};
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {  // apply_rotary_emb: fp32, result in the cache dtype
-          const float u = x1[i], w = x2[i];
-          x1[i] = E::round(u * cs[i] - w * sn[i]);
-          x2[i] = E::round(w * cs[i] + u * sn[i]);
-        }
+      for (int i = 0; i < 8; ++i) {  // apply_rotary_emb: fp32, result in the cache dtype
+        const float u = x1[i], w = x2[i];
+        x1[i] = E::round(u * cs[i] - w * sn[i]);
+        x2[i] = E::round(w * cs[i] + u * sn[i]);
       }
-    } else {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) x1[i] = x2[i] = 0.f;
     }
-    if (a.knorm_w) {  // uniform: every lane joins the 8-lane sum
+    if (a.knorm_w) {  // uniform: every lane joins the 8-lane sum (one key row per 8 lanes)
       float ss = 0.f;
 #pragma unroll
       for (int i = 0; i < 8; ++i) ss += x1[i] * x1[i] + x2[i] * x2[i];
-      ss = group_sum<8>(ss);
+      ss = group8_sum_dpp(ss);
       const float r = 1.0f / sqrtf(ss / static_cast<float>(CAS_D) + a.knorm_eps);
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        x1[i] = buf.valid ? E::round(E::round(x1[i] * r) * kg1[i]) : 0.f;
-        x2[i] = buf.valid ? E::round(E::round(x2[i] * r) * kg2[i]) : 0.f;
+        x1[i] = E::round(E::round(x1[i] * r) * kg1[i]);
+        x2[i] = E::round(E::round(x2[i] * r) * kg2[i]);
       }
     }
     store8<BF16 ? BFA_DTYPE_BF16 : BFA_DTYPE_F16>(ks + sk * CAS_KP + 8 * sc, x1);
     store8<BF16 ? BFA_DTYPE_BF16 : BFA_DTYPE_F16>(ks + sk * CAS_KP + CAS_D / 2 + 8 * sc, x2);
-    // ---- V row -> LDS transposed (zeros for masked slots: 0 x garbage would be NaN)
+    // ---- V row -> LDS transposed
     {
-      const uint4 v0 = buf.valid ? buf.v0 : make_uint4(0, 0, 0, 0);
-      const uint4 v1 = buf.valid ? buf.v1 : make_uint4(0, 0, 0, 0);
-      const uint32_t w0[4] = {v0.x, v0.y, v0.z, v0.w}, w1[4] = {v1.x, v1.y, v1.z, v1.w};
+      const uint32_t w0[4] = {buf.v0.x, buf.v0.y, buf.v0.z, buf.v0.w};
+      const uint32_t w1[4] = {buf.v1.x, buf.v1.y, buf.v1.z, buf.v1.w};
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         vt[(8 * sc + 2 * i) * CAS_VP + sk] = static_cast<uint16_t>(w0[i] & 0xffffu);
@@ -335,7 +360,8 @@ __global__ __launch_bounds__(256) void cascade_attn_kernel(CasArgs a) {
       kval_s[sk] = buf.valid ? 1 : 0;
     }
     __syncthreads();
-    buf = issue(mnext);  // step + 1's loads fly while this step's matrix work runs
+    buf = issue(mnext);  // step + 1's rows and step + 2's metadata fly during this step's matrix work
+    mnext = load_meta(step + 2);
 
     // ---- S = Q K^T for 2 blocks of 16 keys (B operand: lane holds key lane % 16,
     //      head-dim 32 j + 8 (lane / 16) .. +7)
@@ -348,7 +374,10 @@ __global__ __launch_bounds__(256) void cascade_attn_kernel(CasArgs a) {
       for (int j = 0; j < 4; ++j)
         sacc[b] = mfma16x32<BF16>(qf[j], *reinterpret_cast<const uint4*>(kr + 32 * j), sacc[b]);
     }
-    // ---- mask, running max / sum (lane holds key 16 b + lane % 16 of rows 4 (lane/16) + i)
+    // ---- mask, running max / sum (lane holds key 16 b + lane % 16 of rows
+    //      4 (lane/16) + i).  The running state is kept in base 2: scores are
+    //      scaled by scale x log2(e) and exponentiated with v_exp_f32, so
+    //      m holds max(s) x log2(e); l and acc are unchanged in meaning.
     float p[2][4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -357,21 +386,20 @@ __global__ __launch_bounds__(256) void cascade_attn_kernel(CasArgs a) {
       for (int b = 0; b < 2; ++b) {
         const int kk = 16 * b + (lane & 15);
         const bool use = kval_s[kk] && (!a.causal || kpos_s[kk] <= qp[i]);
-        p[b][i] = use ? sacc[b][i] * a.scale : -INFINITY;
+        p[b][i] = use ? sacc[b][i] * sl2 : -INFINITY;
         mx = fmaxf(mx, p[b][i]);
       }
-#pragma unroll
-      for (int d = 1; d < 16; d <<= 1) mx = fmaxf(mx, __shfl_xor(mx, d, kWave));
+      mx = group16_max_dpp(mx);
       const float m_new = fmaxf(m[i], mx);
-      const float alpha = m[i] == -INFINITY ? 0.f : expf(m[i] - m_new);
+      const float mref = m_new == -INFINITY ? 0.f : m_new;  // a fully masked row so far stays at 0
+      const float alpha = __builtin_amdgcn_exp2f(m[i] - mref);
       float rs = 0.f;
 #pragma unroll
       for (int b = 0; b < 2; ++b) {
-        p[b][i] = p[b][i] == -INFINITY ? 0.f : expf(p[b][i] - m_new);
+        p[b][i] = __builtin_amdgcn_exp2f(p[b][i] - mref);
         rs += p[b][i];
       }
-#pragma unroll
-      for (int d = 1; d < 16; d <<= 1) rs += __shfl_xor(rs, d, kWave);
+      rs = group16_sum_dpp(rs);
       l[i] = l[i] * alpha + rs;
       m[i] = m_new;
 #pragma unroll
@@ -419,52 +447,58 @@ __global__ __launch_bounds__(256) void cascade_attn_kernel(CasArgs a) {
   }
 }
 
-// Combines the splits' (m, l, acc) rows: one wave per (kv head, row).  Lanes take
-// the splits for the maximum and the weights (64 at a time); each lane then sums
-// two head-dim columns over the splits with the weights broadcast from their
-// lanes, loads unrolled so they are in flight together.
+// Combines the splits' (m, l, acc) rows: one workgroup per (kv head, row).
+// Every wave finds the maximum over all splits (lanes over splits); wave w then
+// sums splits w, w + 4, ... -- each lane two head-dim columns, the weights
+// broadcast from the lanes that computed them, loads unrolled so they are in
+// flight together -- and the four partial sums meet in LDS.
 template <bool BF16>
 __global__ __launch_bounds__(256) void cascade_merge_kernel(CasArgs a, int64_t splits) {
   using E = Elem<BF16 ? BFA_DTYPE_BF16 : BFA_DTYPE_F16>;
+  __shared__ float red[4][2 * 64 + 1];
   const int64_t rows = a.tokens * a.group;
-  const int64_t item = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
-  if (item >= a.hkv * rows) return;
+  const int64_t item = blockIdx.x;
   const int64_t g = item / rows, r = item - g * rows;
-  const int lane = threadIdx.x & 63;
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   const int64_t zstride = a.hkv * rows * (CAS_D + 2);
   const float* base = a.part + (g * rows + r) * (CAS_D + 2);
   float mx = -INFINITY;
-  for (int64_t z0 = 0; z0 < splits; z0 += 64) {
-    const int64_t z = z0 + lane;
-    const float mz = z < splits ? base[z * zstride] : -INFINITY;
-    mx = fmaxf(mx, mz);
-  }
+  for (int64_t z = lane; z < splits; z += 64) mx = fmaxf(mx, base[z * zstride]);
 #pragma unroll
   for (int d = 32; d >= 1; d >>= 1) mx = fmaxf(mx, __shfl_xor(mx, d, kWave));
   float lsum = 0.f, o0 = 0.f, o1 = 0.f;
-  for (int64_t z0 = 0; z0 < splits; z0 += 64) {
-    const int64_t z = z0 + lane;
-    float w = 0.f, lz = 0.f;
+  // this wave's splits: z = wid + 4 k; lane k holds the weight of the k-th
+  for (int64_t k0 = 0; 4 * k0 + wid < splits; k0 += 64) {
+    const int64_t z = 4 * (k0 + lane) + wid;
+    float w = 0.f;
     if (z < splits) {
       const float mz = base[z * zstride];
-      w = mz == -INFINITY ? 0.f : expf(mz - mx);
-      lz = base[z * zstride + 1];
+      w = mz == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mz - mx);  // m is kept in base 2
+      lsum += w * base[z * zstride + 1];
     }
-    lsum += w * lz;
-    // 8 splits per round; a lane past the last split holds w = 0 and its row
-    // index is clamped to a real one
-    const int nz8 = static_cast<int>((min<int64_t>(64, splits - z0) + 7) & ~7);
-    for (int j0 = 0; j0 < nz8; j0 += 8) {
+    // a lane past the wave's last split holds w = 0; its row index is clamped
+    const int64_t nk = min<int64_t>(64, (splits - wid + 3) / 4 - k0);
+    const int nk8 = static_cast<int>((nk + 7) & ~7);
+    for (int j0 = 0; j0 < nk8; j0 += 8) {
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
         const float wj = __shfl(w, j0 + u, kWave);
-        const float* pr = base + min<int64_t>(z0 + j0 + u, splits - 1) * zstride + 2;
+        const int64_t zj = min<int64_t>(4 * (k0 + j0 + u) + wid, splits - 1);
+        const float* pr = base + zj * zstride + 2;
         o0 += wj * pr[lane];
         o1 += wj * pr[64 + lane];
       }
     }
   }
   lsum = group_sum<kWave>(lsum);
+  red[wid][lane] = o0;
+  red[wid][64 + lane] = o1;
+  if (lane == 0) red[wid][128] = lsum;
+  __syncthreads();
+  if (wid != 0) return;
+  o0 = red[0][lane] + red[1][lane] + red[2][lane] + red[3][lane];
+  o1 = red[0][64 + lane] + red[1][64 + lane] + red[2][64 + lane] + red[3][64 + lane];
+  lsum = red[0][128] + red[1][128] + red[2][128] + red[3][128];
   const float inv = 1.0f / fmaxf(lsum, 1e-12f);
   const int64_t t = r / a.group, hh = g * a.group + (r - t * a.group);
   uint16_t* orow = static_cast<uint16_t*>(a.out) + t * a.out_st + hh * CAS_D;
@@ -553,7 +587,8 @@ extern "C" int bfa_cascade_attention(
   BFA_REQUIRE(q_stride_token % 8 == 0 && q_stride_head % 8 == 0 && stride_page % 8 == 0 &&
                   stride_kv % 8 == 0 && stride_head % 8 == 0 && stride_slot % 8 == 0 &&
                   out_stride_token % 8 == 0 && aligned16(query) && aligned16(kv_cache) && aligned16(out) &&
-                  (cos_sin_cache == nullptr || aligned16(cos_sin_cache)),
+                  (cos_sin_cache == nullptr || aligned16(cos_sin_cache)) &&
+                  (k_norm_weight == nullptr || aligned16(k_norm_weight)),
               "%s: tensors must be 16-byte aligned with strides in multiples of 8", what);
   if (num_tokens == 0) return BFA_OK;
   BFA_REQUIRE(query && query_positions && out, "%s: null pointer", what);
@@ -590,7 +625,8 @@ extern "C" int bfa_cascade_attention(
               "%s: grid too large", what);
   const dim3 grid(static_cast<unsigned>(cdiv(rows, 64)), static_cast<unsigned>(num_kv_heads),
                   static_cast<unsigned>(zs));
-  const dim3 mgrid(static_cast<unsigned>(cdiv(num_kv_heads * rows, 4)));
+  BFA_REQUIRE(zs == 1 || num_kv_heads * rows < (int64_t{1} << 31), "%s: grid too large", what);
+  const dim3 mgrid(static_cast<unsigned>(num_kv_heads * rows));
   const hipStream_t s = as_stream(stream);
   if (dtype == BFA_DTYPE_BF16) {
     hipLaunchKernelGGL(cascade_attn_kernel<true>, grid, dim3(256), 0, s, a);
