@@ -30,6 +30,7 @@ _DTYPE_CODE = {
 }
 STATUS_INDEX_OOB = 1
 STATUS_APPEND_SKIPPED = 2
+LINEAR_PLAIN, LINEAR_SILU_AND_MUL = 0, 1
 
 _P = c_void_p
 # name -> (restype, argtypes); mirrors include/braidinfer_amd.h
@@ -84,6 +85,10 @@ _SIGNATURES = {
                                       c_int64, c_int64, c_int64, _P, _P, _P, _P, _P, c_int64,
                                       _P, c_int, c_float, c_float, c_int, _P, c_int64, _P,
                                       c_int64, _P, _P]),
+    "bfa_linear_workspace_size": (c_int64, [c_int64, c_int64, c_int64, c_int]),
+    "bfa_linear": (c_int, [_P, c_int, c_int64, c_int64, c_int64, _P, c_int64, c_int64, _P, c_int,
+                           c_int, c_int, _P, c_int, c_int64, c_int, _P, c_int, c_int64, _P, c_int64,
+                           _P]),
 }
 
 _lib = None

@@ -164,6 +164,14 @@ struct FastDiv {
   __device__ __forceinline__ uint32_t div(uint32_t n) const { return (__umulhi(n, m) + n) >> s; }
 };
 
+// silu(g) = g * sigmoid(g), sigmoid(g) = 1 / (1 + 2^(-g * log2(e))), with the
+// hardware exp2 and reciprocal (about 1 ulp each; the result is rounded to a
+// 16-bit type by every caller)
+__device__ __forceinline__ float silu_fast(float g) {
+  const float e = __builtin_amdgcn_exp2f(g * -1.4426950408889634f);
+  return g * __builtin_amdgcn_rcpf(1.0f + e);
+}
+
 // ------------------------------------------------------------- reductions
 // Butterfly sum over aligned groups of L lanes (L a power of two <= 64).
 template <int L>

@@ -87,6 +87,14 @@ struct QkvEpi {
   void* out;
   int64_t ldo;
   int* status;
+  // EPI_LINEAR / EPI_SWIGLU: y = out_dt(mid_dt(qkv_dt(acc) + residual)) or
+  // out_dt(qkv_dt(silu(qkv_dt(gate))) * qkv_dt(up)); vec = 16-byte row access is
+  // allowed for out and residual (aligned bases, strides multiple of 8)
+  const void* res;
+  int res_dt;
+  int64_t ldr;
+  int mid_dt;
+  int vec;
 };
 
 __device__ __forceinline__ float round_to(float v, int dt) {
@@ -183,12 +191,35 @@ __device__ __forceinline__ int64_t epi_position(const QkvEpi& e, int64_t row, bo
 // ============================================================ prefill GEMM
 struct GemmArgs {
   const uint16_t* a;  // operand [m, k]
-  const uint16_t* w;  // weight  [n, k]
-  int64_t m, n, k, lda, ldw;
+  const uint16_t* w;  // weight  [n, k] ([2 n, k] gate rows then up rows for EPI_SWIGLU)
+  int64_t m, n, k, lda, ldw;  // n: output columns
   float* raw;         // EPI_RAW: fp32 [m, n] destination
 };
 
-enum { EPI_RAW = 0, EPI_FUSED = 1 };
+// EPI_RAW: fp32 tile out.  EPI_FUSED: the QKV row epilogue (bias, q/k norm,
+// RoPE).  EPI_LINEAR: rounding, + residual, rounding.  EPI_SWIGLU: each
+// 128-column wave tile holds 64 gate columns and the 64 matching up columns,
+// and the epilogue writes SiLU(gate) * up.
+enum { EPI_RAW = 0, EPI_FUSED = 1, EPI_LINEAR = 2, EPI_SWIGLU = 3 };
+
+// Output columns one BN-wide weight tile yields.
+template <int EPI, int BN>
+constexpr int out_cols() { return EPI == EPI_SWIGLU ? BN / 2 : BN; }
+
+// Weight row that feeds column c (0 <= c < BN) of the tile starting at output
+// column n0, clamped to the matrix.  EPI_SWIGLU: wave tile w = c / 128 takes
+// gate rows n0 + 64 w .. +63 in its first 64 columns and the up rows n + the
+// same in its last 64, so a lane holds both factors of an output element.
+template <int EPI>
+__device__ __forceinline__ int64_t weight_row(const GemmArgs& g, int64_t n0, int c) {
+  if constexpr (EPI == EPI_SWIGLU) {
+    const int cc = c & 127;
+    const int64_t o = min(n0 + (c >> 7) * 64 + (cc & 63), g.n - 1);
+    return cc < 64 ? o : g.n + o;
+  } else {
+    return min(n0 + c, g.n - 1);
+  }
+}
 
 // LDS tile rows are 64 elements = 8 granules of 16 bytes; granule g of row r is
 // stored at slot g ^ ((r / 2) & 7).  A 16-lane phase of a ds_read_b128 fragment
@@ -367,7 +398,8 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, (WM * WN <= 8192 ? 2 : 
   // so that each XCD walks a contiguous range of tiles, and walk tiles
   // column-major inside groups of 8 row-tiles so that concurrently resident
   // workgroups on one XCD share operand rows and weight columns in its L2.
-  const int64_t tiles_m = cdiv(g.m, BM), tiles_n = cdiv(g.n, BN);
+  constexpr int BNO = out_cols<EPI, BN>();
+  const int64_t tiles_m = cdiv(g.m, BM), tiles_n = cdiv(g.n, BNO);
   const int64_t ntiles = tiles_m * tiles_n;
   int64_t bid = blockIdx.x;
   if (ntiles % 8 == 0) bid = (bid % 8) * (ntiles / 8) + bid / 8;
@@ -377,7 +409,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, (WM * WN <= 8192 ? 2 : 
   const int64_t gsize = min(tiles_m - first_m, GROUP_M);
   const int64_t tm = first_m + (bid % (GROUP_M * tiles_n)) % gsize;
   const int64_t tn = (bid % (GROUP_M * tiles_n)) / gsize;
-  const int64_t m0 = tm * BM, n0 = tn * BN;
+  const int64_t m0 = tm * BM, n0 = tn * BNO;
   const int64_t KT = cdiv(g.k, 64);
   const int frow = lane & 31, fhalf = lane >> 5;
 
@@ -410,7 +442,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, (WM * WN <= 8192 ? 2 : 
       aoff[i] = static_cast<uint32_t>((min(m0 + (i * NW + wid) * 16 + lrow, g.m - 1) * g.lda + lgran * 8) * 2);
 #pragma unroll
     for (int i = 0; i < BDPW; ++i)
-      boff[i] = static_cast<uint32_t>((min(n0 + (i * NW + wid) * 16 + lrow, g.n - 1) * g.ldw + lgran * 8) * 2);
+      boff[i] = static_cast<uint32_t>((weight_row<EPI>(g, n0, (i * NW + wid) * 16 + lrow) * g.ldw + lgran * 8) * 2);
     const uint32_t lbase = lds_addr(lds) + wid * 1024;
     constexpr uint32_t SB = STAGE_U4 * 16;  // stage bytes
     const int64_t nst = g.k / 32;  // 32-deep stages
@@ -454,7 +486,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, (WM * WN <= 8192 ? 2 : 
       aoff[i] = static_cast<uint32_t>((min(m0 + (i * NW + wid) * 8 + lrow, g.m - 1) * g.lda + lgran * 8) * 2);
 #pragma unroll
     for (int i = 0; i < BDPW; ++i)
-      boff[i] = static_cast<uint32_t>((min(n0 + (i * NW + wid) * 8 + lrow, g.n - 1) * g.ldw + lgran * 8) * 2);
+      boff[i] = static_cast<uint32_t>((weight_row<EPI>(g, n0, (i * NW + wid) * 8 + lrow) * g.ldw + lgran * 8) * 2);
     const uint32_t l0 = lds_addr(lds0) + wid * 1024, l1 = lds_addr(lds1) + wid * 1024;
     uint4 fa0[MB], fb0[NB], fa1[MB], fb1[NB];
     issue_stage<ADPW, BDPW, BM, 64, NW>(g.a, g.w, 0, aoff, boff, l0);
@@ -489,7 +521,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, (WM * WN <= 8192 ? 2 : 
       aoff[i] = static_cast<uint32_t>(min(m0 + gr + 32 * i, g.m - 1) * g.lda + gg * 8);
   #pragma unroll
     for (int i = 0; i < BG; ++i)
-      boff[i] = static_cast<uint32_t>(min(n0 + gr + 32 * i, g.n - 1) * g.ldw + gg * 8);
+      boff[i] = static_cast<uint32_t>(weight_row<EPI>(g, n0, gr + 32 * i) * g.ldw + gg * 8);
     uint4 ra[AG], rb[BG];
     // Two register sets keep the loads of tiles kt+1 and kt+2 in flight while
     // tile kt is multiplied (the K loop is unrolled by two so the sets are
@@ -545,6 +577,93 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, (WM * WN <= 8192 ? 2 : 
         }
       }
     return;
+  } else if constexpr (EPI == EPI_LINEAR || EPI == EPI_SWIGLU) {
+    static_assert(WN == 128, "the row epilogue maps 8 lanes x 16 columns onto 128 columns");
+    // Each 32-row accumulator block is staged through this wave's LDS slice;
+    // then 8 lanes per row each take 8 consecutive output columns (twice for
+    // EPI_LINEAR's 128), so residual reads and output writes are 16-byte rows.
+    float* et = reinterpret_cast<float*>(lds) + wid * (32 * LDR);
+    static_assert(EPI_U4 <= LDS_U4, "epilogue staging fits");
+    constexpr int CH = EPI == EPI_SWIGLU ? 1 : 2;  // 8-column chunks per lane
+    const int c8 = lane & 7, r8 = lane >> 3;
+    const int64_t ocol0 = EPI == EPI_SWIGLU ? n0 + wn * 64 : wcol0;  // first output column of the wave
+    const bool bf_out = e.out_dt == BFA_DTYPE_BF16;
+    __syncthreads();  // the K loop's last LDS reads are done before the slices are reused
+#pragma unroll
+    for (int i = 0; i < MB; ++i) {
+#pragma unroll
+      for (int j = 0; j < NB; ++j)
+#pragma unroll
+        for (int v = 0; v < 16; ++v)
+          et[(8 * (v / 4) + 4 * fhalf + (v % 4)) * LDR + j * 32 + frow] = acc[i][j][v];
+      __asm__ volatile("" ::: "memory");  // wave-private slice, LDS keeps a wave's order
+      // Kept rolled: unrolled over the 4 row groups the residual / store paths
+      // grew the kernel past the instruction cache, and the K loop of the other
+      // workgroup on the CU missed in it (o_proj 8192x4096x4096: 1320 vs 232 us).
+#pragma unroll 1
+      for (int it = 0; it < 4; ++it) {
+        const int rl = r8 + 8 * it;
+        const int64_t row = wrow0 + i * 32 + rl;
+#pragma unroll
+        for (int ch = 0; ch < CH; ++ch) {
+          const int lc = 64 * ch + 8 * c8;  // column inside the wave tile
+          const int64_t col = ocol0 + lc;
+          float y[8];
+          const float4 a0 = *reinterpret_cast<const float4*>(et + rl * LDR + lc);
+          const float4 a1 = *reinterpret_cast<const float4*>(et + rl * LDR + lc + 4);
+          const float av[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+          if constexpr (EPI == EPI_SWIGLU) {
+            const float4 u0 = *reinterpret_cast<const float4*>(et + rl * LDR + 64 + lc);
+            const float4 u1 = *reinterpret_cast<const float4*>(et + rl * LDR + 64 + lc + 4);
+            const float uv[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+              const float gt = round_sel(av[t], e.qkv_dt), ut = round_sel(uv[t], e.qkv_dt);
+              y[t] = round_sel(round_sel(silu_fast(gt), e.qkv_dt) * ut, e.out_dt);
+            }
+          } else {
+            float bv[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+            if (e.bias) {
+#pragma unroll
+              for (int t = 0; t < 8; ++t) bv[t] = load_any(e.bias, e.bias_dtype, min(col + t, g.n - 1));
+            }
+            float rv[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+            if (e.res && row < g.m) {
+              if (e.vec && col + 8 <= g.n) {
+                if (e.res_dt == BFA_DTYPE_BF16) load8<BFA_DTYPE_BF16>(static_cast<const uint16_t*>(e.res) + row * e.ldr + col, rv);
+                else if (e.res_dt == BFA_DTYPE_F16) load8<BFA_DTYPE_F16>(static_cast<const uint16_t*>(e.res) + row * e.ldr + col, rv);
+                else load8<BFA_DTYPE_F32>(static_cast<const float*>(e.res) + row * e.ldr + col, rv);
+              } else {
+#pragma unroll
+                for (int t = 0; t < 8; ++t)
+                  if (col + t < g.n) rv[t] = load_any(e.res, e.res_dt, row * e.ldr + col + t);
+              }
+            }
+#pragma unroll
+            for (int t = 0; t < 8; ++t)
+              y[t] = round_sel(round_sel(round_sel(av[t] + bv[t], e.qkv_dt) + rv[t], e.mid_dt), e.out_dt);
+          }
+          if (row < g.m) {
+            if (e.vec && col + 8 <= g.n) {
+              if (e.out_dt == BFA_DTYPE_F32) {
+                float4* q = reinterpret_cast<float4*>(static_cast<float*>(e.out) + row * e.ldo + col);
+                q[0] = make_float4(y[0], y[1], y[2], y[3]);
+                q[1] = make_float4(y[4], y[5], y[6], y[7]);
+              } else {
+                *reinterpret_cast<uint4*>(static_cast<uint16_t*>(e.out) + row * e.ldo + col) =
+                    make_uint4(pack2_sel(y[0], y[1], bf_out), pack2_sel(y[2], y[3], bf_out),
+                               pack2_sel(y[4], y[5], bf_out), pack2_sel(y[6], y[7], bf_out));
+              }
+            } else {
+#pragma unroll
+              for (int t = 0; t < 8; ++t)
+                if (col + t < g.n) store_any(e.out, e.out_dt, row * e.ldo + col + t, y[t]);
+            }
+          }
+        }
+      }
+      __asm__ volatile("" ::: "memory");
+    }
   } else {
     static_assert(HD == 32 || HD == 64 || HD == 128, "fused epilogue covers head_dim 32/64/128");
     static_assert(WN == 128, "the row epilogue maps 16 lanes x 8 columns onto 128 columns");
@@ -768,9 +887,9 @@ __global__ __launch_bounds__(256) void qkv_splitk_kernel(SplitArgs s) {
 // loads stream faster back to back but slow the kernel by a third once the
 // reduction kernel has read the partial tiles in between, so they are not used.)
 struct DecodeArgs {
-  const uint16_t* a;  // operand [m, k] (row stride k)
+  const uint16_t* a;  // operand [m, k] (row stride lda)
   const uint16_t* w;  // weight [n, k]
-  int64_t m, n, k, ldw;
+  int64_t m, n, k, lda, ldw;
   float* part;        // [splits, m, n]
 };
 
@@ -818,7 +937,7 @@ __global__ __launch_bounds__(256) void qkv_decode_kernel(DecodeArgs d) {
     for (int row = wid; row < d.m; row += 4) {
       const int g = (lane & ~15) | ((lane & 15) ^ (row & 15));
       if (g < gpr) {
-        dma16(abase, static_cast<uint32_t>((static_cast<int64_t>(row) * d.k + g * 8) * 2),
+        dma16(abase, static_cast<uint32_t>((static_cast<int64_t>(row) * d.lda + g * 8) * 2),
               lbase + row * 1024);
       }
     }
@@ -1071,6 +1190,78 @@ __global__ __launch_bounds__(256) void qkv_decode_epilogue_kernel(const float4* 
   }
 }
 
+// ================================== decode epilogue of the linear fusions
+// One thread per (4-token group, output column): sums the split-K partials of
+// the column (and of its up column, n + c, for EPI_SWIGLU) in split order and
+// applies the EPI_LINEAR / EPI_SWIGLU element chain.  Partials are row-major
+// [splits, m, nw] floats, or, from the weight-streaming kernel with more than
+// one 16-token block (reg_order), float4 = 4 tokens of one column in the
+// kernel's register order.
+__global__ __launch_bounds__(256) void linear_decode_epilogue_kernel(const float* part, int64_t splits,
+                                                                    int reg_order, int mt, int64_t m,
+                                                                    int64_t nw, int swiglu, GemmArgs g,
+                                                                    QkvEpi e) {
+  const int64_t id = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (id >= cdiv(m, 4) * g.n) return;
+  const int64_t tg = id / g.n, c = id - tg * g.n;
+  float acc[2][4];
+#pragma unroll
+  for (int f = 0; f < 2; ++f)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) acc[f][v] = 0.f;
+  const int nf = swiglu ? 2 : 1;
+  for (int f = 0; f < nf; ++f) {
+    const int64_t col = c + f * g.n;
+    if (reg_order) {
+      const int64_t i = tg / 4, lq = tg % 4, cw = col % 128;
+      const int64_t ntiles = cdiv(nw, 128);
+      const int64_t idx = (((col / 128) * 4 + cw / 32) * mt * 2 + i * 2 + (cw % 32) / 16) * 64 + lq * 16 + cw % 16;
+      const int64_t sstride = ntiles * 4 * mt * 2 * 64;
+      const float4* p4 = reinterpret_cast<const float4*>(part) + idx;
+      for (int64_t sp0 = 0; sp0 < splits; sp0 += 8) {
+        float4 l[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) l[u] = p4[min(sp0 + u, splits - 1) * sstride];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          if (sp0 + u >= splits) break;
+          acc[f][0] += l[u].x; acc[f][1] += l[u].y; acc[f][2] += l[u].z; acc[f][3] += l[u].w;
+        }
+      }
+    } else {
+      for (int64_t sp0 = 0; sp0 < splits; sp0 += 8) {
+        float l[8][4];
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+#pragma unroll
+          for (int v = 0; v < 4; ++v)
+            l[u][v] = part[(min(sp0 + u, splits - 1) * m + min(tg * 4 + v, m - 1)) * nw + col];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          if (sp0 + u >= splits) break;
+#pragma unroll
+          for (int v = 0; v < 4; ++v) acc[f][v] += l[u][v];
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    const int64_t t = tg * 4 + v;
+    if (t >= m) break;
+    float y;
+    if (swiglu) {
+      const float gt = round_to(acc[0][v], e.qkv_dt), ut = round_to(acc[1][v], e.qkv_dt);
+      y = round_to(silu_fast(gt), e.qkv_dt) * ut;
+    } else {
+      const float r = e.res ? load_any(e.res, e.res_dt, t * e.ldr + c) : 0.f;
+      const float b = e.bias ? load_any(e.bias, e.bias_dtype, c) : 0.f;
+      y = round_to(round_to(acc[0][v] + b, e.qkv_dt) + r, e.mid_dt);
+    }
+    store_any(e.out, e.out_dt, t * e.ldo + c, y);
+  }
+}
+
 // ============================================== reduction + row epilogue
 // One wave per (token, head).  v = sum over splits of part[s, t, col] (+bias),
 // then the same rounding / norm / RoPE chain as the in-register epilogue.
@@ -1266,7 +1457,7 @@ template <bool BF16>
 static void launch_decode(const QkvPlan& p, const SplitArgs& s, hipStream_t st) {
   if (p.stream) {
     DecodeArgs d{};
-    d.a = s.a; d.w = s.w; d.m = s.m; d.n = s.n; d.k = s.k; d.ldw = s.ldw;
+    d.a = s.a; d.w = s.w; d.m = s.m; d.n = s.n; d.k = s.k; d.lda = s.lda; d.ldw = s.ldw;
     d.part = s.part;
     const dim3 grid(static_cast<unsigned>(cdiv(s.n, 128)), static_cast<unsigned>(p.splits));
     switch (p.mt) {
@@ -1299,6 +1490,39 @@ static void launch_prefill_tile(const QkvPlan& p, const GemmArgs& g, const QkvEp
   } else {
     hipLaunchKernelGGL((qkv_gemm_kernel<BM, BN, WM, 128, BF16, EPI_FUSED, 32, DIRECT, NS, BK>),
                        dim3(grid), block, 0, st, g, e);
+  }
+}
+
+// The linear fusions: same tiles, EPI_LINEAR or EPI_SWIGLU epilogue.
+template <int BM, int BN, int WM, int NS, int BK, bool BF16, bool DIRECT>
+static void launch_linear_tile(const GemmArgs& g, const QkvEpi& e, bool swiglu, hipStream_t st) {
+  const int64_t bno = swiglu ? BN / 2 : BN;
+  const unsigned grid = static_cast<unsigned>(cdiv(g.m, BM) * cdiv(g.n, bno));
+  const dim3 block((BM / WM) * (BN / 128) * 64);
+  if (swiglu) {
+    hipLaunchKernelGGL((qkv_gemm_kernel<BM, BN, WM, 128, BF16, EPI_SWIGLU, 128, DIRECT, NS, BK>),
+                       dim3(grid), block, 0, st, g, e);
+  } else {
+    hipLaunchKernelGGL((qkv_gemm_kernel<BM, BN, WM, 128, BF16, EPI_LINEAR, 128, DIRECT, NS, BK>),
+                       dim3(grid), block, 0, st, g, e);
+  }
+}
+
+template <bool BF16>
+static void launch_linear(const QkvPlan& p, const GemmArgs& g, const QkvEpi& e, bool swiglu,
+                          int64_t wrows, hipStream_t st) {
+  const bool dma = g.k % 64 == 0 && g.lda % 8 == 0 && g.ldw % 8 == 0 && aligned16(g.a) &&
+                   aligned16(g.w) && g.m * g.lda * 2 < (int64_t(1) << 32) &&
+                   wrows * g.ldw * 2 < (int64_t(1) << 32);
+  if (!dma) {
+    launch_linear_tile<128, 128, 32, 2, 64, BF16, false>(g, e, swiglu, st);
+    return;
+  }
+  switch (p.tile) {
+    case 2: launch_linear_tile<256, 256, 64, 2, 64, BF16, true>(g, e, swiglu, st); break;
+    case 3: launch_linear_tile<128, 256, 32, 2, 64, BF16, true>(g, e, swiglu, st); break;
+    case 1: launch_linear_tile<128, 256, 64, 3, 32, BF16, true>(g, e, swiglu, st); break;
+    default: launch_linear_tile<128, 128, 32, 4, 32, BF16, true>(g, e, swiglu, st); break;
   }
 }
 
@@ -1472,4 +1696,75 @@ extern "C" int bfa_fused_rmsnorm_qkv(const void* x, int x_dtype, int64_t tokens,
                             positions_dtype, cos_sin_cache, max_position, out, out_dtype,
                             out_stride, ws + p.operand_bytes, workspace_bytes - p.operand_bytes,
                             status, stream);
+}
+
+// ------------------------------------------------------- linear fusions
+extern "C" int64_t bfa_linear_workspace_size(int64_t tokens, int64_t k, int64_t n, int mode) {
+  if (tokens <= 0 || n <= 0) return 0;
+  const int64_t nw = mode == BFA_LINEAR_SILU_AND_MUL ? 2 * n : n;
+  const QkvPlan p = make_plan(tokens, nw, k, 0);
+  return p.decode ? p.part_bytes : 0;  // prefill tiles finish in their epilogue
+}
+
+extern "C" int bfa_linear(const void* x, int dtype, int64_t tokens, int64_t k, int64_t x_stride,
+                          const void* weight, int64_t n, int64_t w_stride, const void* bias,
+                          int bias_dtype, int mode, int proj_dtype, const void* residual, int residual_dtype, int64_t residual_stride,
+                          int sum_dtype, void* out, int out_dtype, int64_t out_stride,
+                          void* workspace, int64_t workspace_bytes, void* stream) {
+  const char* what = "bfa_linear";
+  BFA_REQUIRE(dtype == BFA_DTYPE_BF16 || dtype == BFA_DTYPE_F16, "%s: x and weight must be bf16 or fp16",
+              what);
+  BFA_REQUIRE(mode == BFA_LINEAR_PLAIN || mode == BFA_LINEAR_SILU_AND_MUL, "%s: bad mode %d", what, mode);
+  BFA_REQUIRE(is_float_dtype(proj_dtype) && is_float_dtype(sum_dtype) && is_float_dtype(out_dtype),
+              "%s: bad dtype", what);
+  BFA_REQUIRE(residual == nullptr || is_float_dtype(residual_dtype), "%s: bad residual dtype", what);
+  BFA_REQUIRE(mode == BFA_LINEAR_PLAIN || (residual == nullptr && bias == nullptr),
+              "%s: no bias or residual with silu_and_mul", what);
+  BFA_REQUIRE(bias == nullptr || is_float_dtype(bias_dtype), "%s: bad bias dtype", what);
+  BFA_REQUIRE(tokens >= 0 && k > 0 && n > 0, "%s: bad geometry", what);
+  BFA_REQUIRE(k % 16 == 0, "%s: k must be a multiple of 16 (got %lld)", what, (long long)k);
+  BFA_REQUIRE(x_stride >= k && w_stride >= k && x_stride % 8 == 0 && w_stride % 8 == 0 &&
+                  aligned16(x) && aligned16(weight),
+              "%s: x / weight rows must be 16-byte aligned", what);
+  BFA_REQUIRE(out_stride >= n && (residual == nullptr || residual_stride >= n), "%s: bad strides", what);
+  if (tokens == 0) return BFA_OK;
+  BFA_REQUIRE(x && weight && out, "%s: null pointer", what);
+  const bool swiglu = mode == BFA_LINEAR_SILU_AND_MUL;
+  const int64_t nw = swiglu ? 2 * n : n;
+  const QkvPlan p = make_plan(tokens, nw, k, 0);
+  const int64_t need = p.decode ? p.part_bytes : 0;
+  BFA_REQUIRE(workspace_bytes >= need && (need == 0 || workspace),
+              "%s: workspace too small (%lld < %lld bytes)", what, (long long)workspace_bytes,
+              (long long)need);
+  BFA_REQUIRE(need == 0 || aligned16(workspace), "%s: workspace must be 16-byte aligned", what);
+
+  QkvEpi e{};
+  e.qkv_dt = proj_dtype; e.mid_dt = sum_dtype; e.out_dt = out_dtype;
+  e.res = residual; e.res_dt = residual_dtype; e.ldr = residual_stride;
+  e.bias = bias; e.bias_dtype = bias_dtype;
+  e.out = out; e.ldo = out_stride; e.n = n;
+  e.vec = aligned16(out) && out_stride % 8 == 0 &&
+          (residual == nullptr || (aligned16(residual) && residual_stride % 8 == 0));
+  GemmArgs g{};
+  g.a = static_cast<const uint16_t*>(x);
+  g.w = static_cast<const uint16_t*>(weight);
+  g.m = tokens; g.n = n; g.k = k; g.lda = x_stride; g.ldw = w_stride;
+  const hipStream_t st = as_stream(stream);
+  const bool bf16 = dtype == BFA_DTYPE_BF16;
+  if (p.decode) {
+    SplitArgs sa{};
+    sa.a = g.a; sa.w = g.w;
+    sa.m = tokens; sa.n = nw; sa.k = k; sa.lda = x_stride; sa.ldw = w_stride;
+    sa.kchunk = p.kchunk; sa.part = static_cast<float*>(workspace);
+    if (bf16) launch_decode<true>(p, sa, st); else launch_decode<false>(p, sa, st);
+    const int rc = check_launch(what);
+    if (rc != BFA_OK) return rc;
+    const int64_t threads = cdiv(tokens, 4) * n;
+    hipLaunchKernelGGL(linear_decode_epilogue_kernel, dim3(static_cast<unsigned>(cdiv(threads, 256))),
+                       dim3(256), 0, st, static_cast<const float*>(workspace), p.splits,
+                       (p.stream && p.mt > 1) ? 1 : 0, p.mt, tokens, nw, swiglu ? 1 : 0, g, e);
+    return check_launch(what);
+  }
+  if (bf16) launch_linear<true>(p, g, e, swiglu, nw, st); else launch_linear<false>(p, g, e, swiglu, nw, st);
+  return check_launch(what);
 }

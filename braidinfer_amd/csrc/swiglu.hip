@@ -26,12 +26,6 @@ struct SwigluArgs {
   uint32_t total;   // rows * chunks per row (< 2^31)
 };
 
-// silu(g) = g * sigmoid(g), sigmoid(g) = 1 / (1 + 2^(-g * log2(e)))
-__device__ __forceinline__ float silu_fast(float g) {
-  const float e = __builtin_amdgcn_exp2f(g * -1.4426950408889634f);
-  return g * __builtin_amdgcn_rcpf(1.0f + e);
-}
-
 constexpr int kSwigluPerLane = 2;  // 8-column chunks per lane
 
 template <int DT>

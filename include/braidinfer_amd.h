@@ -316,6 +316,36 @@ int bfa_cascade_attention(const void* query, int dtype, int64_t num_tokens, int6
                           void* workspace, int64_t workspace_bytes, int32_t* status,
                           void* stream);
 
+/* ------------------------------------------------ linear layer fusions --
+ * y = x W^T on the projection GEMM, with the element epilogue fused:
+ *   BFA_LINEAR_PLAIN:  y = out_dtype(sum_dtype(proj_dtype(x W^T + bias) + residual))
+ *       (bias [n] and residual optional; F.linear of ReplicatedLinear /
+ *       ColumnParallelLinear / RowParallelLinear, layers/linear.py:20-61,
+ *       136-160, is proj_dtype = out_dtype = x's dtype without residual).  proj_dtype = x's dtype, sum_dtype = F32 gives
+ *       residual + F.linear(x, W) in torch's rounding (the o_proj / down_proj
+ *       + residual fusion of models/qwen3.py:336-366); proj_dtype = F32,
+ *       sum_dtype = F16, out_dtype = x's dtype gives
+ *       FusedAttentionOutput.forward (kernels/fused_attention_output.py:
+ *       76-134, 173-225), and without residual FusedAttentionOutput.gemv
+ *       (:17-72, 137-171).
+ *   BFA_LINEAR_SILU_AND_MUL:  weight [2 n, k] = [gate rows; up rows] (the
+ *       MergedColumnParallelLinear gate_up_proj, layers/linear.py:63-75);
+ *       g, u = proj_dtype(x Wg^T), proj_dtype(x Wu^T);
+ *       y = out_dtype(proj_dtype(silu(g)) * u) -- SiluAndMul(F.linear(x, W))
+ *       (layers/activation.py:11-13, models/qwen3.py:388-392) without the
+ *       [tokens, 2 n] intermediate.
+ * x [tokens, k] and weight (row strides x_stride / w_stride, multiples of 8,
+ * 16-byte aligned) share a dtype, bf16 or fp16; k a multiple of 16.  out
+ * [tokens, n] (row stride out_stride).  workspace: bfa_linear_workspace_size
+ * bytes (split-K partials for up to 64 tokens; 0 above). */
+enum { BFA_LINEAR_PLAIN = 0, BFA_LINEAR_SILU_AND_MUL = 1 };
+int64_t bfa_linear_workspace_size(int64_t tokens, int64_t k, int64_t n, int mode);
+int bfa_linear(const void* x, int dtype, int64_t tokens, int64_t k, int64_t x_stride,
+               const void* weight, int64_t n, int64_t w_stride, const void* bias, int bias_dtype,
+               int mode, int proj_dtype, const void* residual, int residual_dtype, int64_t residual_stride, int sum_dtype,
+               void* out, int out_dtype, int64_t out_stride, void* workspace,
+               int64_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -192,3 +192,21 @@ def attention(q, k, v, qpos, kpos, scale, group, causal=True):
         den = w.sum(axis=1, keepdims=True)
         out[:, hh] = np.where(ok[:, None], (w @ vh) / np.where(den > 0, den, 1.0), 0.0)
     return out
+
+
+def linear(x, w, bias=None, residual=None, proj="bf16", mid="f32", out="bf16"):
+    """out(mid(proj(x W^T + bias) + residual)) in float64 arithmetic: F.linear
+    (layers/linear.py:37-38) and its residual / FusedAttentionOutput
+    (kernels/fused_attention_output.py:17-134) roundings."""
+    acc = np.asarray(x, np.float64) @ np.asarray(w, np.float64).T
+    if bias is not None:
+        acc = acc + np.asarray(bias, np.float64)
+    acc = round_to(acc, proj)
+    if residual is not None:
+        acc = acc + np.asarray(residual, np.float64)
+    return round_to(round_to(acc, mid), out)
+
+
+def gate_up_silu_and_mul(x, w, dtype="bf16"):
+    """SiluAndMul(F.linear(x, [Wg; Wu])) (models/qwen3.py:388-392)."""
+    return silu_and_mul(linear(x, w, proj=dtype, out=dtype), dtype)

@@ -347,3 +347,38 @@ def llama_attention_input(x, ln_w, qkv_w, hq, hkv, eps, positions, cache):
     t = x.shape[0]
     qf, kf = rotary_forward(cache, q.shape[-1], positions, q.reshape(t, -1), k.reshape(t, -1))
     return qf.to(dtype), kf.to(dtype), v.reshape(t, -1).to(dtype)
+
+
+# ------------------------------------------------------ linear layer fusions
+def linear(x, weight, bias=None):
+    """F.linear(x, weight, bias) of ReplicatedLinear / ColumnParallelLinear /
+    RowParallelLinear.forward (braidinfer/layers/linear.py:37-38, 159-160): fp32
+    products and sums, the bias added in fp32, one rounding to x's dtype."""
+    acc = x.to(torch.float32) @ weight.to(torch.float32).t()
+    if bias is not None:
+        acc = acc + bias.to(torch.float32)
+    return acc.to(x.dtype)
+
+
+def linear_add_residual(x, weight, residual, bias=None):
+    """residual + F.linear(x, weight, bias) in torch's rounding: the projection
+    rounded to x's dtype, the sum formed in fp32 and rounded again (the o_proj /
+    down_proj output joining the residual stream, braidinfer/models/qwen3.py:
+    336-366, 388-392)."""
+    return (linear(x, weight, bias).to(torch.float32) + residual.to(torch.float32)).to(x.dtype)
+
+
+def gate_up_silu_and_mul(x, gate_up_weight):
+    """SiluAndMul()(gate_up_proj(x)), braidinfer/models/qwen3.py:388-392 with
+    layers/linear.py:64-75 and layers/activation.py:11-13."""
+    return silu_and_mul(linear(x, gate_up_weight))
+
+
+def fused_attention_output(x, weight, residual=None):
+    """fused_o_proj_add_residual_kernel / tiled_gemv_kernel, braidinfer/kernels/
+    fused_attention_output.py:17-72, 76-134: acc = x W^T in fp32 (+ residual in
+    fp32), stored as acc.to(float16) into an output of x's dtype."""
+    acc = x.to(torch.float32) @ weight.to(torch.float32).t()
+    if residual is not None:
+        acc = acc + residual.to(torch.float32)
+    return acc.to(torch.float16).to(x.dtype)

@@ -690,3 +690,82 @@ def test_rope_rounding_allowance_is_a_property_of_the_arithmetic():
     beyond = diff > strict
     assert 0 < int(beyond.sum()) <= 1e-4 * diff.numel()
     assert torch.all(diff <= strict + rope_flip_slack(pre32.reshape(t, -1)))
+
+
+# ------------------------------------------------------- linear fusions
+def pin_linear_family(lin, lin_res, gate_up, attn_out):
+    """Pins of the four linear-layer restatements.
+    * small-integer operands make every product and sum exact in fp32 and the
+      result exact in bf16: x W^T + b must equal the integer matmul (a
+      transposed or column-flipped W, or a dropped bias, fails);
+    * a residual of 2^-8 on a projection of 1 + 2^-8: rounding the projection
+      first gives 1.0 twice (ties to even), adding before rounding gives
+      1 + 2^-7 -- the order of the two roundings is fixed;
+    * SiluAndMul of the projection: gate rows first (a swapped [up; gate] fails);
+    * the fp16 store of FusedAttentionOutput: 75000 is beyond fp16 and must
+      come out inf even for a bf16 output (skipping the fp16 rounding fails);
+    * random operands against the float64 numpy restatements."""
+    rng = np.random.default_rng(5)
+    bf = torch.bfloat16
+    x = rng.integers(-2, 3, (5, 16))
+    w = rng.integers(-2, 3, (24, 16))
+    b = rng.integers(-8, 9, 24)
+    t = lambda a: torch.tensor(a, dtype=torch.float32).to(bf)  # noqa: E731
+    got = lin(t(x), t(w), t(b)).float().numpy()
+    assert np.array_equal(got, (x @ w.T + b).astype(np.float64)), "linear != integer matmul"
+    xs = torch.zeros(1, 16, dtype=bf)
+    xs[0, 0], xs[0, 1] = 1.0, 2.0 ** -8
+    ws = torch.zeros(3, 16, dtype=bf)
+    ws[:, 0], ws[:, 1] = 1.0, 1.0
+    r = torch.full((1, 3), 2.0 ** -8, dtype=bf)
+    assert torch.equal(lin_res(xs, ws, r).float(), torch.ones(1, 3)), "residual rounding order"
+    wg, wu = rng.integers(-2, 3, (8, 16)), rng.integers(-2, 3, (8, 16))
+    gu = gate_up(t(x), t(np.concatenate([wg, wu]))).float().numpy()
+    g_, u_ = (x @ wg.T).astype(np.float64), (x @ wu.T).astype(np.float64)
+    expect = N.round_bf16(N.round_bf16(g_ / (1.0 + np.exp(-g_))) * u_)
+    assert np.array_equal(gu, expect), "gate/up order or SiLU rounding"
+    xb = torch.zeros(1, 16, dtype=bf)
+    xb[0, 0] = 300.0
+    wb = torch.zeros(2, 16, dtype=bf)
+    wb[:, 0] = 250.0
+    assert torch.isinf(attn_out(xb, wb, None).float()).all(), "fp16 store of the output"
+    xr, wr, br, rr = randn(gen(31), 37, 256), randn(gen(32), 96, 256), randn(gen(33), 96), randn(gen(34), 37, 96)
+    check_bf16_agreement(lin(xr, wr, br), N.linear(_np(xr), _np(wr), _np(br)), what="linear")
+    check_bf16_agreement(lin_res(xr, wr, rr), N.linear(_np(xr), _np(wr), residual=_np(rr)), what="linear+res")
+    check_bf16_agreement(gate_up(xr, wr), N.gate_up_silu_and_mul(_np(xr), _np(wr)), what="gate_up")
+    a = attn_out(xr, wr, rr).float().numpy()
+    e = N.linear(_np(xr), _np(wr), residual=_np(rr), proj="f32", mid="f16", out="bf16")
+    assert np.all(np.abs(a - e) <= 2 * BF16_REL_ULP * np.abs(e) + 1e-30), "attention output"
+
+
+def test_linear_family_pinned():
+    pin_linear_family(R.linear, R.linear_add_residual, R.gate_up_silu_and_mul,
+                      R.fused_attention_output)
+
+
+def test_planted_linear_mistakes_are_caught():
+    def lin_flipped(x, w, b=None):
+        return R.linear(x, w.flip(1), b)
+
+    def lin_no_bias(x, w, b=None):
+        return R.linear(x, w)
+
+    def res_adds_first(x, w, res, b=None):
+        acc = x.float() @ w.float().t() + res.float()
+        return acc.to(x.dtype)
+
+    def gate_up_swapped(x, w):
+        g, u = w.chunk(2, 0)
+        return R.gate_up_silu_and_mul(x, torch.cat([u, g]))
+
+    def attn_no_f16(x, w, res=None):
+        acc = x.float() @ w.float().t()
+        return (acc if res is None else acc + res.float()).to(x.dtype)
+
+    ok = (R.linear, R.linear_add_residual, R.gate_up_silu_and_mul, R.fused_attention_output)
+    for i, bad in ((0, lin_flipped), (0, lin_no_bias), (1, res_adds_first), (2, gate_up_swapped),
+                   (3, attn_no_f16)):
+        fns = list(ok)
+        fns[i] = bad
+        with pytest.raises(AssertionError):
+            pin_linear_family(*fns)
