@@ -182,7 +182,9 @@ def config_cases(dev) -> list:
       kv_append   paged KV append, 8 kv heads x 128, page 16: 8192-token prefill,
                   and a 64-sequence decode batch in one launch
       cascade     paged cascade attention over 4096 cached Qwen3 tokens (16 moved
-                  chunks, k_norm), 1 and 256 query tokens"""
+                  chunks, k_norm), 1 and 256 query tokens
+      linear      gate_up+SiluAndMul, down_proj+residual, o_proj+residual at
+                  Llama-3-8B shapes, T 8192 and 64"""
     from braidinfer_amd.layers import llama_attention_input, qwen3_attention_input, rerotate_paged_k
     bf = torch.bfloat16
     cases = []
@@ -247,7 +249,36 @@ def config_cases(dev) -> list:
     # decode batch (one new token each) in one batched launch
     cases += kv_append_cases(dev)
     cases += cascade_cases(dev)
+    cases += linear_cases(dev)
     return cases
+
+
+def linear_cases(dev) -> list:
+    """GEMM-epilogue fusions at Llama-3-8B layer shapes (seed 8): gate_up_proj with
+    SiluAndMul (4096 -> 2 x 14336 -> 14336), down_proj + residual (14336 -> 4096)
+    and o_proj + residual (4096 -> 4096), for an 8192-token prefill and a 64-token
+    decode batch.  Algorithmic bytes: operand, weight, residual and output once."""
+    from braidinfer_amd.layers import gate_up_silu_and_mul, linear_add_residual
+    g = torch.Generator().manual_seed(8)
+    bf = torch.bfloat16
+    h, inter = 4096, 14336
+
+    def randn(*shape, std=1.0):
+        return (torch.randn(*shape, generator=g) * std).to(bf).to(dev)
+
+    w_gu, w_down, w_o = randn(2 * inter, h, std=0.02), randn(h, inter, std=0.01), randn(h, h, std=0.02)
+    out = []
+    for t in (8192, 64):
+        x, xi, res = randn(t, h), randn(t, inter), randn(t, h)
+        out += [
+            (f"gate_up_silu_llama3_8b_t{t}", (lambda x=x: gate_up_silu_and_mul(x, w_gu)),
+             (t * h + 2 * inter * h + t * inter) * 2, 2.0 * t * h * 2 * inter),
+            (f"down_proj_residual_llama3_8b_t{t}", (lambda xi=xi, res=res: linear_add_residual(xi, w_down, res)),
+             (t * inter + inter * h + 2 * t * h) * 2, 2.0 * t * inter * h),
+            (f"o_proj_residual_llama3_8b_t{t}", (lambda x=x, res=res: linear_add_residual(x, w_o, res)),
+             (2 * t * h + h * h + t * h) * 2, 2.0 * t * h * h),
+        ]
+    return out
 
 
 def kv_append_cases(dev) -> list:
