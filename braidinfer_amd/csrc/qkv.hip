@@ -1197,10 +1197,10 @@ __global__ __launch_bounds__(256) void qkv_decode_epilogue_kernel(const float4* 
 // [splits, m, nw] floats, or, from the weight-streaming kernel with more than
 // one 16-token block (reg_order), float4 = 4 tokens of one column in the
 // kernel's register order.
+template <bool SWIGLU>
 __global__ __launch_bounds__(256) void linear_decode_epilogue_kernel(const float* part, int64_t splits,
                                                                     int reg_order, int mt, int64_t m,
-                                                                    int64_t nw, int swiglu, GemmArgs g,
-                                                                    QkvEpi e) {
+                                                                    int64_t nw, GemmArgs g, QkvEpi e) {
   const int64_t id = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   if (id >= cdiv(m, 4) * g.n) return;
   const int64_t tg = id / g.n, c = id - tg * g.n;
@@ -1209,7 +1209,8 @@ __global__ __launch_bounds__(256) void linear_decode_epilogue_kernel(const float
   for (int f = 0; f < 2; ++f)
 #pragma unroll
     for (int v = 0; v < 4; ++v) acc[f][v] = 0.f;
-  const int nf = swiglu ? 2 : 1;
+  constexpr int nf = SWIGLU ? 2 : 1;
+#pragma unroll
   for (int f = 0; f < nf; ++f) {
     const int64_t col = c + f * g.n;
     if (reg_order) {
@@ -1222,10 +1223,14 @@ __global__ __launch_bounds__(256) void linear_decode_epilogue_kernel(const float
         float4 l[8];
 #pragma unroll
         for (int u = 0; u < 8; ++u) l[u] = p4[min(sp0 + u, splits - 1) * sstride];
+        // all 8 loads issue before the first sum waits: a conditional exit in the
+        // sum loop lets the compiler sink each load to its use, one round trip each
+        asm volatile("" ::: "memory");
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
-          if (sp0 + u >= splits) break;
-          acc[f][0] += l[u].x; acc[f][1] += l[u].y; acc[f][2] += l[u].z; acc[f][3] += l[u].w;
+          const bool in = sp0 + u < splits;
+          acc[f][0] += in ? l[u].x : 0.f; acc[f][1] += in ? l[u].y : 0.f;
+          acc[f][2] += in ? l[u].z : 0.f; acc[f][3] += in ? l[u].w : 0.f;
         }
       }
     } else {
@@ -1236,11 +1241,12 @@ __global__ __launch_bounds__(256) void linear_decode_epilogue_kernel(const float
 #pragma unroll
           for (int v = 0; v < 4; ++v)
             l[u][v] = part[(min(sp0 + u, splits - 1) * m + min(tg * 4 + v, m - 1)) * nw + col];
+        asm volatile("" ::: "memory");
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
-          if (sp0 + u >= splits) break;
+          const bool in = sp0 + u < splits;
 #pragma unroll
-          for (int v = 0; v < 4; ++v) acc[f][v] += l[u][v];
+          for (int v = 0; v < 4; ++v) acc[f][v] += in ? l[u][v] : 0.f;
         }
       }
     }
@@ -1250,7 +1256,7 @@ __global__ __launch_bounds__(256) void linear_decode_epilogue_kernel(const float
     const int64_t t = tg * 4 + v;
     if (t >= m) break;
     float y;
-    if (swiglu) {
+    if constexpr (SWIGLU) {
       const float gt = round_to(acc[0][v], e.qkv_dt), ut = round_to(acc[1][v], e.qkv_dt);
       y = round_to(silu_fast(gt), e.qkv_dt) * ut;
     } else {
@@ -1385,6 +1391,11 @@ static QkvPlan make_plan(int64_t m, int64_t n, int64_t k, int64_t hd) {
       int ks = 1;
       for (int c = 8; c >= 1; --c)
         if (segs % c == 0 && ntile * (segs / c) >= 256) { ks = c; break; }
+      // BFA_DECODE_KS (1..8, dividing k / 64) overrides the depth for measurements
+      if (const char* v = getenv("BFA_DECODE_KS")) {
+        const int c = atoi(v);
+        if (c >= 1 && c <= 8 && segs % c == 0) ks = c;
+      }
       p.ks = ks;
       p.kchunk = 64 * ks;
       p.splits = segs / ks;
@@ -1760,9 +1771,16 @@ extern "C" int bfa_linear(const void* x, int dtype, int64_t tokens, int64_t k, i
     const int rc = check_launch(what);
     if (rc != BFA_OK) return rc;
     const int64_t threads = cdiv(tokens, 4) * n;
-    hipLaunchKernelGGL(linear_decode_epilogue_kernel, dim3(static_cast<unsigned>(cdiv(threads, 256))),
-                       dim3(256), 0, st, static_cast<const float*>(workspace), p.splits,
-                       (p.stream && p.mt > 1) ? 1 : 0, p.mt, tokens, nw, swiglu ? 1 : 0, g, e);
+    const dim3 egrid(static_cast<unsigned>(cdiv(threads, 256)));
+    const float* part = static_cast<const float*>(workspace);
+    const int reg_order = (p.stream && p.mt > 1) ? 1 : 0;
+    if (swiglu) {
+      hipLaunchKernelGGL(linear_decode_epilogue_kernel<true>, egrid, dim3(256), 0, st, part, p.splits,
+                         reg_order, p.mt, tokens, nw, g, e);
+    } else {
+      hipLaunchKernelGGL(linear_decode_epilogue_kernel<false>, egrid, dim3(256), 0, st, part, p.splits,
+                         reg_order, p.mt, tokens, nw, g, e);
+    }
     return check_launch(what);
   }
   if (bf16) launch_linear<true>(p, g, e, swiglu, nw, st); else launch_linear<false>(p, g, e, swiglu, nw, st);
