@@ -261,8 +261,16 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 // inline assembly so the compiler does not serialise consecutive copies; the
 // caller waits (wait_vmem) and barriers before the LDS is read.
 __device__ __forceinline__ void dma16(const void* base, uint32_t voff, uint32_t m0) {
+  // the base is wave-uniform; readfirstlane lets the compiler see that when the
+  // pointer came through a path it cannot prove uniform (an SGPR operand).  The
+  // builtin returns a signed int: each half is taken back to uint32_t before it
+  // is widened, or a low half with bit 31 set would fill the high word with ones.
+  const uint64_t b = reinterpret_cast<uint64_t>(base);
+  const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(b)));
+  const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(b >> 32)));
+  const uint64_t bu = (static_cast<uint64_t>(hi) << 32) | lo;
   asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(__builtin_amdgcn_readfirstlane(m0)),
-               "v"(voff), "s"(base)
+               "v"(voff), "s"(reinterpret_cast<const void*>(bu))
                : "memory");
 }
 
@@ -1042,14 +1050,10 @@ __global__ __launch_bounds__(256) void qkv_decode_kernel(DecodeArgs d) {
 // token goes through bias -> rounding -> per-head RMSNorm (a wave reduction per
 // token) -> rounding -> RoPE -> store, as in the prefill epilogue.
 template <int MAXP>  // RoPE pairs per lane: head_dim <= 2 * 64 * MAXP
-__global__ __launch_bounds__(256) void qkv_decode_epilogue_kernel(const float4* part, int64_t splits,
-                                                                  int64_t ntiles, int mt, int64_t m,
-                                                                  QkvEpi e) {
-  const int lane = threadIdx.x & 63;
-  const int64_t heads = e.hq + 2 * e.hkv;
-  const int64_t item = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
-  if (item >= cdiv(m, 4) * heads) return;
-  const int64_t tg = item / heads, h = item - tg * heads;
+__device__ __forceinline__ void decode_epilogue_item(const float4* part, int64_t splits,
+                                                              int64_t ntiles, int mt, int64_t m,
+                                                              const QkvEpi& e, int64_t tg, int64_t h,
+                                                              int lane) {
   const int64_t i = tg / 4, lq = tg % 4;  // 16-token block, 4-token group inside it
   const int64_t half = e.hd / 2;
   const int kd = head_kind(e, h);
@@ -1268,17 +1272,24 @@ __global__ __launch_bounds__(256) void linear_decode_epilogue_kernel(const float
   }
 }
 
+template <int MAXP>
+__global__ __launch_bounds__(256) void qkv_decode_epilogue_kernel(const float4* part, int64_t splits,
+                                                                  int64_t ntiles, int mt, int64_t m,
+                                                                  QkvEpi e) {
+  const int64_t heads = e.hq + 2 * e.hkv;
+  const int64_t item = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (item >= cdiv(m, 4) * heads) return;
+  const int64_t tg = item / heads;
+  decode_epilogue_item<MAXP>(part, splits, ntiles, mt, m, e, tg, item - tg * heads, threadIdx.x & 63);
+}
+
 // ============================================== reduction + row epilogue
 // One wave per (token, head).  v = sum over splits of part[s, t, col] (+bias),
 // then the same rounding / norm / RoPE chain as the in-register epilogue.
-__global__ __launch_bounds__(256) void qkv_epilogue_kernel(const float* part, int64_t splits,
-                                                           int64_t m, QkvEpi e) {
+__device__ __forceinline__ void row_epilogue_item(const float* part, int64_t splits, int64_t m,
+                                                           const QkvEpi& e, int64_t t, int64_t h,
+                                                           int lane) {
   constexpr int MAXP = 4;  // pairs per lane: head_dim <= 2*64*MAXP
-  const int lane = threadIdx.x & 63;
-  const int64_t heads = e.hq + 2 * e.hkv;
-  const int64_t item = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
-  if (item >= m * heads) return;
-  const int64_t t = item / heads, h = item - t * heads;
   const int64_t half = e.hd / 2;
   const int kd = head_kind(e, h);
   const int64_t base = h * e.hd;
@@ -1356,6 +1367,15 @@ __global__ __launch_bounds__(256) void qkv_epilogue_kernel(const float* part, in
       store_any(e.out, e.out_dt, t * e.ldo + base + half + j, x2[p]);
     }
   }
+}
+
+__global__ __launch_bounds__(256) void qkv_epilogue_kernel(const float* part, int64_t splits,
+                                                           int64_t m, QkvEpi e) {
+  const int64_t heads = e.hq + 2 * e.hkv;
+  const int64_t item = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (item >= m * heads) return;
+  const int64_t t = item / heads;
+  row_epilogue_item(part, splits, m, e, t, item - t * heads, threadIdx.x & 63);
 }
 
 // ================================================================== host

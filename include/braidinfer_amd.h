@@ -180,7 +180,8 @@ int bfa_rerotate_paged_k(void* kv_cache, int dtype, int64_t num_cache_pages,
  * Output: out[tokens, qkv_dim] (q | k | v columns, row stride out_stride) in
  * out_dtype.  W is [qkv_dim, hidden] (bf16 or fp16), rows [q; k; v]
  * (layers/linear.py:78-114).  The normalised operand is rounded to W's dtype
- * for the matrix cores (the fp32 variants round it once; see DESIGN).
+ * for the matrix cores (the fp32 variants round it once, where the reference's
+ * fp32 dot product runs at TF32 on its GPUs).
  * workspace: device scratch of bfa_fused_rmsnorm_qkv_workspace_size() bytes,
  * 16-byte aligned; calls sharing a workspace must be stream-ordered. */
 int64_t bfa_fused_rmsnorm_qkv_workspace_size(int64_t tokens, int64_t hidden, int64_t qkv_dim,
