@@ -23,11 +23,11 @@
 // id, first key position, chunk delta and token count / rotate flag, flattened
 // on the host once per set of levels.  Per step: 256 lanes stage the 32 keys of
 // K into LDS (rotated and normalised on the way, with the rounding of the
-// re-rotation kernel) and V transposed into LDS; each wave computes S = Q K^T for
-// its 16 rows with v_mfma_f32_16x16x32_bf16, masks, updates its running max / sum
-// in fp32 (base 2, row reductions by DPP inside 16-lane rows), writes P (bf16)
-// through a wave-private LDS tile into the A-operand layout and adds P V with 8
-// more MFMAs.  The next step's K / V / cos-sin rows and the step after's entry
+// re-rotation kernel) and V transposed into LDS; each wave computes S^T = K Q^T
+// for its 16 rows with v_mfma_f32_16x16x32_bf16 (a lane then holds 8 scores of
+// one query), masks, updates its running max / sum in fp32 (base 2; in-lane plus
+// two gfx950 lane swaps) and adds O^T += V^T P^T with 8 more MFMAs, P^T going
+// from its registers straight into the B operand.  The next step's K / V / cos-sin rows and the step after's entry
 // metadata are in flight during a step's matrix work.  For few rows (decode) the
 // key range is split across workgroups and a merge kernel combines the partial
 // (m, l, acc) rows.
@@ -160,14 +160,50 @@ constexpr int CAS_D = 128;          // head_dim of the MFMA path
 __device__ __align__(16) float cas_zero_row[CAS_D];
 constexpr int CAS_KP = CAS_D + 8;   // K row pitch in LDS (bf16): 272 bytes, conflict-free reads
 constexpr int CAS_VP = 32 + 8;      // V^T row pitch (bf16): 80 bytes
-constexpr int CAS_PP = 32 + 8;      // P row pitch (bf16): 80 bytes
+
+// two floats rounded to the 16-bit type, packed low | high << 16
+template <bool BF16>
+__device__ __forceinline__ uint32_t pack_pair(float lo, float hi) {
+  using E = Elem<BF16 ? BFA_DTYPE_BF16 : BFA_DTYPE_F16>;
+  return static_cast<uint32_t>(E::from_f32(lo)) | (static_cast<uint32_t>(E::from_f32(hi)) << 16);
+}
+
+// Reductions over lanes l, l ^ 16, l ^ 32, l ^ 48 with the gfx950 lane swaps.
+// v_permlane16_swap x, y exchanges the odd 16-lane rows of x with the even rows
+// of y; with x = y = v on entry, each lane ends up holding its own value in one
+// of x, y and its xor-16 partner's in the other (v_permlane32_swap: halves, xor
+// 32), so a commutative op on the pair gives every lane of the group the same
+// bits.  Written as inline assembly: given one value for both operands, the
+// compiler's model of the builtins takes the two results to be equal and drops
+// one of them.  The s_nop covers the VALU-write -> permlane-read wait states.
+__device__ __forceinline__ void swap16(uint32_t& x, uint32_t& y) {
+  asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1\n\ts_nop 1" : "+v"(x), "+v"(y));
+}
+__device__ __forceinline__ void swap32(uint32_t& x, uint32_t& y) {
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(x), "+v"(y));
+}
+__device__ __forceinline__ float lanes4_max(float v) {
+  uint32_t x = __builtin_bit_cast(uint32_t, v), y = x;
+  swap16(x, y);
+  v = fmaxf(__builtin_bit_cast(float, x), __builtin_bit_cast(float, y));
+  x = y = __builtin_bit_cast(uint32_t, v);
+  swap32(x, y);
+  return fmaxf(__builtin_bit_cast(float, x), __builtin_bit_cast(float, y));
+}
+__device__ __forceinline__ float lanes4_sum(float v) {
+  uint32_t x = __builtin_bit_cast(uint32_t, v), y = x;
+  swap16(x, y);
+  v = __builtin_bit_cast(float, x) + __builtin_bit_cast(float, y);
+  x = y = __builtin_bit_cast(uint32_t, v);
+  swap32(x, y);
+  return __builtin_bit_cast(float, x) + __builtin_bit_cast(float, y);
+}
 
 template <bool BF16>
 __global__ __launch_bounds__(256) void cascade_attn_kernel(CasArgs a) {
   using E = Elem<BF16 ? BFA_DTYPE_BF16 : BFA_DTYPE_F16>;
   __shared__ uint16_t ks[32 * CAS_KP];
   __shared__ uint16_t vt[CAS_D * CAS_VP];
-  __shared__ uint16_t pt[4][16 * CAS_PP];
   __shared__ int64_t kpos_s[32];
   __shared__ int kval_s[32];
 
@@ -189,27 +225,17 @@ __global__ __launch_bounds__(256) void cascade_attn_kernel(CasArgs a) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) qf[j] = *reinterpret_cast<const uint4*>(qrow + 32 * j + 8 * (lane >> 4));
   }
-  // query positions of the 4 rows this lane holds in the 16x16 output layout
-  // (rows 4 (lane / 16) + i)
-  int64_t qp[4], qt[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) qt[i] = min(row0 + 4 * (lane >> 4) + i, rows - 1) / a.group;
-  if (a.qpos_i64) {  // one uniform branch, four loads in flight together
-#pragma unroll
-    for (int i = 0; i < 4; ++i) qp[i] = static_cast<const int64_t*>(a.qpos)[qt[i]];
-  } else {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) qp[i] = static_cast<const int32_t*>(a.qpos)[qt[i]];
-  }
+  // The matrix work is done transposed: S^T = K Q^T and O^T = V^T P^T, so a lane
+  // owns one query row (lane % 16) throughout -- its scores, its running max and
+  // sum, and its output columns -- and P^T is already the B operand of the PV
+  // product in the registers that hold it.
+  const int64_t qt = min(row0 + (lane & 15), rows - 1) / a.group;
+  const int64_t qp = a.qpos_i64 ? static_cast<const int64_t*>(a.qpos)[qt]
+                                : static_cast<const int32_t*>(a.qpos)[qt];
 
   const float sl2 = a.scale * 1.4426950408889634f;  // scale x log2(e)
-  float m[4], l[4];
-  cas_f32x4_t o[8];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    m[i] = -INFINITY;
-    l[i] = 0.f;
-  }
+  float m = -INFINITY, l = 0.f;
+  cas_f32x4_t o[8];  // o[j][i] = O^T[head-dim 16 j + 4 (lane / 16) + i][query lane % 16]
 #pragma unroll
   for (int j = 0; j < 8; ++j) o[j] = cas_f32x4_t{};
 
@@ -343,16 +369,19 @@ __global__ __launch_bounds__(256) void cascade_attn_kernel(CasArgs a) {
     }
     store8<BF16 ? BFA_DTYPE_BF16 : BFA_DTYPE_F16>(ks + sk * CAS_KP + 8 * sc, x1);
     store8<BF16 ? BFA_DTYPE_BF16 : BFA_DTYPE_F16>(ks + sk * CAS_KP + CAS_D / 2 + 8 * sc, x2);
-    // ---- V row -> LDS transposed
+    // ---- V row -> LDS transposed, in the PV product's key order: the score of
+    //      key slot 16 b + 4 g + i sits in lane group g at position 4 b + i of its
+    //      8-key B fragment, so that slot is V^T column 8 g + 4 b + i
     {
+      const int kc = 8 * ((sk >> 2) & 3) + 4 * (sk >> 4) + (sk & 3);
       const uint32_t w0[4] = {buf.v0.x, buf.v0.y, buf.v0.z, buf.v0.w};
       const uint32_t w1[4] = {buf.v1.x, buf.v1.y, buf.v1.z, buf.v1.w};
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        vt[(8 * sc + 2 * i) * CAS_VP + sk] = static_cast<uint16_t>(w0[i] & 0xffffu);
-        vt[(8 * sc + 2 * i + 1) * CAS_VP + sk] = static_cast<uint16_t>(w0[i] >> 16);
-        vt[(64 + 8 * sc + 2 * i) * CAS_VP + sk] = static_cast<uint16_t>(w1[i] & 0xffffu);
-        vt[(64 + 8 * sc + 2 * i + 1) * CAS_VP + sk] = static_cast<uint16_t>(w1[i] >> 16);
+        vt[(8 * sc + 2 * i) * CAS_VP + kc] = static_cast<uint16_t>(w0[i] & 0xffffu);
+        vt[(8 * sc + 2 * i + 1) * CAS_VP + kc] = static_cast<uint16_t>(w0[i] >> 16);
+        vt[(64 + 8 * sc + 2 * i) * CAS_VP + kc] = static_cast<uint16_t>(w1[i] & 0xffffu);
+        vt[(64 + 8 * sc + 2 * i + 1) * CAS_VP + kc] = static_cast<uint16_t>(w1[i] >> 16);
       }
     }
     if (sc == 0) {
@@ -363,8 +392,10 @@ __global__ __launch_bounds__(256) void cascade_attn_kernel(CasArgs a) {
     buf = issue(mnext);  // step + 1's rows and step + 2's metadata fly during this step's matrix work
     mnext = load_meta(step + 2);
 
-    // ---- S = Q K^T for 2 blocks of 16 keys (B operand: lane holds key lane % 16,
-    //      head-dim 32 j + 8 (lane / 16) .. +7)
+    // ---- S^T = K Q^T for 2 blocks of 16 keys (A operand: lane holds key row
+    //      16 b + lane % 16, head-dim 32 j + 8 (lane / 16) .. +7; B: the query
+    //      fragment).  sacc[b][i] = score of key slot 16 b + 4 (lane / 16) + i
+    //      for query lane % 16.
     cas_f32x4_t sacc[2];
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
@@ -372,77 +403,77 @@ __global__ __launch_bounds__(256) void cascade_attn_kernel(CasArgs a) {
       const uint16_t* kr = ks + (16 * b + (lane & 15)) * CAS_KP + 8 * (lane >> 4);
 #pragma unroll
       for (int j = 0; j < 4; ++j)
-        sacc[b] = mfma16x32<BF16>(qf[j], *reinterpret_cast<const uint4*>(kr + 32 * j), sacc[b]);
+        sacc[b] = mfma16x32<BF16>(*reinterpret_cast<const uint4*>(kr + 32 * j), qf[j], sacc[b]);
     }
-    // ---- mask, running max / sum (lane holds key 16 b + lane % 16 of rows
-    //      4 (lane/16) + i).  The running state is kept in base 2: scores are
-    //      scaled by scale x log2(e) and exponentiated with v_exp_f32, so
-    //      m holds max(s) x log2(e); l and acc are unchanged in meaning.
+    // ---- mask, running max / sum.  The running state is kept in base 2: scores
+    //      are scaled by scale x log2(e) and exponentiated with v_exp_f32, so m
+    //      holds max(s) x log2(e); l and acc are unchanged in meaning.  A query's
+    //      32 scores sit in 8 registers of each of 4 lanes (lane % 16 fixed), so
+    //      its reductions are in-lane plus two lane swaps.
     float p[2][4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      float mx = -INFINITY;
-#pragma unroll
-      for (int b = 0; b < 2; ++b) {
-        const int kk = 16 * b + (lane & 15);
-        const bool use = kval_s[kk] && (!a.causal || kpos_s[kk] <= qp[i]);
-        p[b][i] = use ? sacc[b][i] * sl2 : -INFINITY;
-        mx = fmaxf(mx, p[b][i]);
-      }
-      mx = group16_max_dpp(mx);
-      const float m_new = fmaxf(m[i], mx);
-      const float mref = m_new == -INFINITY ? 0.f : m_new;  // a fully masked row so far stays at 0
-      const float alpha = __builtin_amdgcn_exp2f(m[i] - mref);
-      float rs = 0.f;
-#pragma unroll
-      for (int b = 0; b < 2; ++b) {
-        p[b][i] = __builtin_amdgcn_exp2f(p[b][i] - mref);
-        rs += p[b][i];
-      }
-      rs = group16_sum_dpp(rs);
-      l[i] = l[i] * alpha + rs;
-      m[i] = m_new;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) o[j][i] *= alpha;
-    }
-    // ---- P (16 rows x 32 keys) through LDS into the A-operand layout
-    uint16_t* pw = pt[wid];
+    float mx = -INFINITY;
 #pragma unroll
     for (int b = 0; b < 2; ++b)
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        pw[(4 * (lane >> 4) + i) * CAS_PP + 16 * b + (lane & 15)] = E::from_f32(p[b][i]);
-    __asm__ volatile("" ::: "memory");  // wave-private tile, LDS keeps a wave's order
-    const uint4 pf = *reinterpret_cast<const uint4*>(pw + (lane & 15) * CAS_PP + 8 * (lane >> 4));
-    // ---- O += P V (B operand: lane holds head-dim column 16 j + lane % 16, keys
-    //      8 (lane / 16) .. +7, read from V^T)
+      for (int i = 0; i < 4; ++i) {
+        const int kk = 16 * b + 4 * (lane >> 4) + i;
+        const bool use = kval_s[kk] && (!a.causal || kpos_s[kk] <= qp);
+        p[b][i] = use ? sacc[b][i] * sl2 : -INFINITY;
+        mx = fmaxf(mx, p[b][i]);
+      }
+    mx = lanes4_max(mx);
+    const float m_new = fmaxf(m, mx);
+    const float mref = m_new == -INFINITY ? 0.f : m_new;  // a fully masked row so far stays at 0
+    const float alpha = __builtin_amdgcn_exp2f(m - mref);
+    float rs = 0.f;
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        p[b][i] = __builtin_amdgcn_exp2f(p[b][i] - mref);
+        rs += p[b][i];
+      }
+    rs = lanes4_sum(rs);
+    l = l * alpha + rs;
+    m = m_new;
+    if (__any(alpha != 1.0f)) {  // the running max moved for some query of the wave
+#pragma unroll
+      for (int j = 0; j < 8; ++j) o[j] *= alpha;
+    }
+    // ---- O^T += V^T P^T (A: V^T rows 16 j + lane % 16, keys 8 (lane / 16) .. +7
+    //      in the order V^T was written; B: this lane's 8 probabilities)
+    const uint4 pf = make_uint4(pack_pair<BF16>(p[0][0], p[0][1]), pack_pair<BF16>(p[0][2], p[0][3]),
+                                pack_pair<BF16>(p[1][0], p[1][1]), pack_pair<BF16>(p[1][2], p[1][3]));
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const uint4 vf = *reinterpret_cast<const uint4*>(vt + (16 * j + (lane & 15)) * CAS_VP + 8 * (lane >> 4));
-      o[j] = mfma16x32<BF16>(pf, vf, o[j]);
+      o[j] = mfma16x32<BF16>(vf, pf, o[j]);
     }
     __syncthreads();  // every wave is done with ks / vt before the next step refills them
   }
 
-  // ---- rows out: lane holds head-dim column 16 j + lane % 16 of rows 4 (lane/16) + i
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int64_t r = row0 + 4 * (lane >> 4) + i;
-    if (r >= rows) continue;
+  // ---- row out: lane holds head-dim 16 j + 4 (lane / 16) .. +3 of query lane % 16
+  const int64_t r = row0 + (lane & 15);
+  if (r < rows) {
+    const int d0 = 4 * (lane >> 4);
     if (gridDim.z == 1) {
       const int64_t t = r / a.group, hh = g * a.group + (r - t * a.group);
-      const float inv = 1.0f / fmaxf(l[i], 1e-12f);
+      const float inv = 1.0f / fmaxf(l, 1e-12f);
       uint16_t* orow = static_cast<uint16_t*>(a.out) + t * a.out_st + hh * CAS_D;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) orow[16 * j + (lane & 15)] = E::from_f32(o[j][i] * inv);
+      for (int j = 0; j < 8; ++j)
+        *reinterpret_cast<uint2*>(orow + 16 * j + d0) =
+            make_uint2(pack_pair<BF16>(o[j][0] * inv, o[j][1] * inv), pack_pair<BF16>(o[j][2] * inv, o[j][3] * inv));
     } else {
       float* pr = a.part + ((static_cast<int64_t>(blockIdx.z) * a.hkv + g) * rows + r) * (CAS_D + 2);
-      if ((lane & 15) == 0) {
-        pr[0] = m[i];
-        pr[1] = l[i];
+      if (lane < 16) {
+        pr[0] = m;
+        pr[1] = l;
       }
 #pragma unroll
-      for (int j = 0; j < 8; ++j) pr[2 + 16 * j + (lane & 15)] = o[j][i];
+      for (int j = 0; j < 8; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) pr[2 + 16 * j + d0 + i] = o[j][i];
     }
   }
 }
