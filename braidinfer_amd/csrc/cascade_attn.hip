@@ -32,6 +32,8 @@
 // key range is split across workgroups and a merge kernel combines the partial
 // (m, l, acc) rows.
 #include <cmath>
+#include <cstdlib>
+#include <type_traits>
 
 #include "bfa_device.h"
 #include "bfa_host.h"
@@ -537,6 +539,259 @@ __global__ __launch_bounds__(256) void cascade_merge_kernel(CasArgs a, int64_t s
   orow[64 + lane] = E::from_f32(o1 * inv);
 }
 
+// Decode form (at most 4 query rows per kv head): scores on the VALU.  A
+// workgroup's 16 groups of 16 lanes walk its range of (entry, 16-slot block)
+// items; group kg takes slot 16 sb + kg of each item, lane j holds head-dim
+// 4j..4j+3 and 64+4j..64+4j+3 (the RoPE pairs), and each group keeps its own
+// online-softmax state for every row, so the walk needs no barrier.  The next
+// item's metadata and K / V / cos-sin rows load while the current one is
+// processed.  At the end the 16 group states meet in LDS and are combined into
+// the split's (m, l, acc) rows -- the layout the merge kernel reads -- or, with
+// one split, into the output.
+template <bool BF16, int R>
+__global__ __launch_bounds__(256) void cascade_decode_kernel(CasArgs a, int64_t items_per_split, int64_t nsb) {
+  using E = Elem<BF16 ? BFA_DTYPE_BF16 : BFA_DTYPE_F16>;
+  constexpr int NG = 16;
+  __shared__ float red_m[NG][R], red_l[NG][R];
+  __shared__ float red_a[NG][R][CAS_D];
+  const int tid = threadIdx.x, j = tid & 15, kg = tid >> 4;
+  const int64_t g = blockIdx.x;  // kv head
+  const int64_t rows = a.tokens * a.group;
+  const int64_t items = a.num_entries * nsb;
+  const int64_t i0 = static_cast<int64_t>(blockIdx.y) * items_per_split;
+  const int64_t i1 = min(i0 + items_per_split, items);
+
+  // queries (fp32 copies of the bf16 / fp16 values) and their positions
+  float q1[R][4], q2[R][4];
+  int64_t qp[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int64_t rr = min<int64_t>(r, rows - 1);
+    const int64_t t = rr / a.group, hh = g * a.group + (rr - t * a.group);
+    const uint16_t* qrow = a.q + t * a.q_st + hh * a.q_sh;
+    const uint2 u1 = *reinterpret_cast<const uint2*>(qrow + 4 * j);
+    const uint2 u2 = *reinterpret_cast<const uint2*>(qrow + CAS_D / 2 + 4 * j);
+    q1[r][0] = E::to_f32(u1.x & 0xffffu); q1[r][1] = E::to_f32(u1.x >> 16);
+    q1[r][2] = E::to_f32(u1.y & 0xffffu); q1[r][3] = E::to_f32(u1.y >> 16);
+    q2[r][0] = E::to_f32(u2.x & 0xffffu); q2[r][1] = E::to_f32(u2.x >> 16);
+    q2[r][2] = E::to_f32(u2.y & 0xffffu); q2[r][3] = E::to_f32(u2.y >> 16);
+    qp[r] = a.qpos_i64 ? static_cast<const int64_t*>(a.qpos)[t] : static_cast<const int32_t*>(a.qpos)[t];
+  }
+  float kw1[4] = {1.f, 1.f, 1.f, 1.f}, kw2[4] = {1.f, 1.f, 1.f, 1.f};
+  if (a.knorm_w) {  // one uniform dtype branch, vector loads
+    if (a.knorm_dt == BFA_DTYPE_F32) {
+      const float4 w1 = *reinterpret_cast<const float4*>(static_cast<const float*>(a.knorm_w) + 4 * j);
+      const float4 w2 = *reinterpret_cast<const float4*>(static_cast<const float*>(a.knorm_w) + CAS_D / 2 + 4 * j);
+      kw1[0] = w1.x; kw1[1] = w1.y; kw1[2] = w1.z; kw1[3] = w1.w;
+      kw2[0] = w2.x; kw2[1] = w2.y; kw2[2] = w2.z; kw2[3] = w2.w;
+    } else {
+      const uint2 w1 = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(a.knorm_w) + 4 * j);
+      const uint2 w2 = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(a.knorm_w) + CAS_D / 2 + 4 * j);
+      const uint32_t u[4] = {w1.x, w1.y, w2.x, w2.y};
+      float f[8];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint16_t lo = static_cast<uint16_t>(u[i] & 0xffffu), hi = static_cast<uint16_t>(u[i] >> 16);
+        f[2 * i] = a.knorm_dt == BFA_DTYPE_BF16 ? Elem<BFA_DTYPE_BF16>::to_f32(lo) : Elem<BFA_DTYPE_F16>::to_f32(lo);
+        f[2 * i + 1] = a.knorm_dt == BFA_DTYPE_BF16 ? Elem<BFA_DTYPE_BF16>::to_f32(hi) : Elem<BFA_DTYPE_F16>::to_f32(hi);
+      }
+      kw1[0] = f[0]; kw1[1] = f[1]; kw1[2] = f[2]; kw1[3] = f[3];
+      kw2[0] = f[4]; kw2[1] = f[5]; kw2[2] = f[6]; kw2[3] = f[7];
+    }
+  }
+  const float sl2 = a.scale * 1.4426950408889634f;
+  float m[R], l[R], acc1[R][4], acc2[R][4];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    m[r] = -INFINITY;
+    l[r] = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc1[r][i] = acc2[r][i] = 0.f;
+  }
+
+  // An item's metadata as loaded (used only by issue(), an item later), and the
+  // group's slot of an item resolved with its loads issued.  Masked slots read
+  // the zeroed row, so no load waits behind a branch.
+  struct Meta {
+    int64_t kst, dpos, sl;
+    int32_t pg, info;
+    bool in;
+  };
+  struct Slot {
+    uint2 k1, k2, v1, v2;
+    float4 c, sn;
+    int64_t kp;
+    bool valid, rot;
+  };
+  auto load_meta = [&](int64_t it) {
+    Meta mt;
+    const int64_t e = it / nsb, sb = it - e * nsb;
+    mt.in = it < i1;
+    const int64_t ec = mt.in ? e : 0;
+    mt.pg = a.pages[ec];
+    mt.kst = a.kstart[ec];
+    mt.dpos = a.delta[ec];
+    mt.info = a.info[ec];
+    mt.sl = 16 * sb + kg;
+    return mt;
+  };
+  auto issue = [&](const Meta& mt) {
+    Slot b;
+    const bool in = mt.in;
+    const int32_t pg = mt.pg, info = mt.info;
+    const int64_t kst = mt.kst, sl = mt.sl;
+    int64_t dpos = mt.dpos;
+    b.valid = in && sl < (info & 0xffff);
+    const int64_t page = pg < 0 ? static_cast<int64_t>(pg) + a.num_pages : pg;  // kv_cache[-1] is the last page
+    if (b.valid && (page < 0 || page >= a.num_pages)) {
+      if (j == 0) flag_status(a.status, BFA_STATUS_INDEX_OOB);
+      b.valid = false;
+    }
+    b.rot = b.valid && a.cs != nullptr && ((info >> 16) & 1);
+    if (b.rot) {
+      if (dpos < 0) dpos += a.max_pos;
+      if (dpos < 0 || dpos >= a.max_pos) {
+        if (j == 0) flag_status(a.status, BFA_STATUS_INDEX_OOB);
+        b.valid = false;
+        b.rot = false;
+      }
+    }
+    b.kp = kst + sl;
+    const uint16_t* zero = reinterpret_cast<const uint16_t*>(cas_zero_row);
+    const uint16_t* krow = b.valid ? a.cache + page * a.c_sp + g * a.c_sh + sl * a.c_ss : zero;
+    const uint16_t* vrow = b.valid ? krow + a.c_skv : zero;
+    b.k1 = *reinterpret_cast<const uint2*>(krow + 4 * j);
+    b.k2 = *reinterpret_cast<const uint2*>(krow + CAS_D / 2 + 4 * j);
+    b.v1 = *reinterpret_cast<const uint2*>(vrow + 4 * j);
+    b.v2 = *reinterpret_cast<const uint2*>(vrow + CAS_D / 2 + 4 * j);
+    const float* csrow = b.rot ? a.cs + dpos * CAS_D : cas_zero_row;
+    b.c = *reinterpret_cast<const float4*>(csrow + 4 * j);
+    b.sn = *reinterpret_cast<const float4*>(csrow + CAS_D / 2 + 4 * j);
+    return b;
+  };
+
+  if (i0 < i1) {
+    Slot cur = issue(load_meta(i0));
+    Meta mn = load_meta(i0 + 1);
+    for (int64_t it = i0; it < i1; ++it) {
+      const Slot nxt = issue(mn);  // item it + 1's rows fly while this item is processed,
+      mn = load_meta(it + 2);      // and item it + 2's metadata
+      float x1[4] = {E::to_f32(cur.k1.x & 0xffffu), E::to_f32(cur.k1.x >> 16), E::to_f32(cur.k1.y & 0xffffu),
+                     E::to_f32(cur.k1.y >> 16)};
+      float x2[4] = {E::to_f32(cur.k2.x & 0xffffu), E::to_f32(cur.k2.x >> 16), E::to_f32(cur.k2.y & 0xffffu),
+                     E::to_f32(cur.k2.y >> 16)};
+      if (cur.rot) {
+        const float cs[4] = {cur.c.x, cur.c.y, cur.c.z, cur.c.w}, sn[4] = {cur.sn.x, cur.sn.y, cur.sn.z, cur.sn.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {  // apply_rotary_emb: fp32, result in the cache dtype
+          const float u = x1[i], w = x2[i];
+          x1[i] = E::round(u * cs[i] - w * sn[i]);
+          x2[i] = E::round(w * cs[i] + u * sn[i]);
+        }
+      }
+      if (a.knorm_w) {  // uniform: every lane joins its group's 16-lane sum
+        float ss = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) ss += x1[i] * x1[i] + x2[i] * x2[i];
+        ss = group16_sum_dpp(ss);
+        const float rn = 1.0f / sqrtf(ss / static_cast<float>(CAS_D) + a.knorm_eps);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          x1[i] = E::round(E::round(x1[i] * rn) * kw1[i]);
+          x2[i] = E::round(E::round(x2[i] * rn) * kw2[i]);
+        }
+      }
+      const float v1[4] = {E::to_f32(cur.v1.x & 0xffffu), E::to_f32(cur.v1.x >> 16), E::to_f32(cur.v1.y & 0xffffu),
+                           E::to_f32(cur.v1.y >> 16)};
+      const float v2[4] = {E::to_f32(cur.v2.x & 0xffffu), E::to_f32(cur.v2.x >> 16), E::to_f32(cur.v2.y & 0xffffu),
+                           E::to_f32(cur.v2.y >> 16)};
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        float d = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) d += q1[r][i] * x1[i] + q2[r][i] * x2[i];
+        d = group16_sum_dpp(d);
+        const bool use = cur.valid && (!a.causal || cur.kp <= qp[r]);
+        const float sc = use ? d * sl2 : -INFINITY;
+        const float m_new = fmaxf(m[r], sc);
+        const float mref = m_new == -INFINITY ? 0.f : m_new;  // nothing seen yet: stay at zero
+        const float alpha = __builtin_amdgcn_exp2f(m[r] - mref);
+        const float pr = __builtin_amdgcn_exp2f(sc - mref);
+        l[r] = l[r] * alpha + pr;
+        m[r] = m_new;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          acc1[r][i] = acc1[r][i] * alpha + pr * v1[i];
+          acc2[r][i] = acc2[r][i] * alpha + pr * v2[i];
+        }
+      }
+      cur = nxt;
+    }
+  }
+  // ---- the 16 group states -> one state per row
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    if (j == 0) {
+      red_m[kg][r] = m[r];
+      red_l[kg][r] = l[r];
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      red_a[kg][r][4 * j + i] = acc1[r][i];
+      red_a[kg][r][CAS_D / 2 + 4 * j + i] = acc2[r][i];
+    }
+  }
+  __syncthreads();
+  for (int idx = tid; idx < R * CAS_D; idx += 256) {
+    const int r = idx / CAS_D, dcol = idx - r * CAS_D;
+    if (r >= rows) break;
+    float mx = -INFINITY;
+#pragma unroll
+    for (int q = 0; q < NG; ++q) mx = fmaxf(mx, red_m[q][r]);
+    const float mref = mx == -INFINITY ? 0.f : mx;
+    float lsum = 0.f, asum = 0.f;
+#pragma unroll
+    for (int q = 0; q < NG; ++q) {
+      const float w = __builtin_amdgcn_exp2f(red_m[q][r] - mref);  // -inf -> 0
+      lsum += red_l[q][r] * w;
+      asum += red_a[q][r][dcol] * w;
+    }
+    if (gridDim.y == 1) {
+      const int64_t t = r / a.group, hh = g * a.group + (r - t * a.group);
+      static_cast<uint16_t*>(a.out)[t * a.out_st + hh * CAS_D + dcol] = E::from_f32(asum / fmaxf(lsum, 1e-12f));
+    } else {
+      float* pr = a.part + ((static_cast<int64_t>(blockIdx.y) * a.hkv + g) * rows + r) * (CAS_D + 2);
+      if (dcol == 0) {
+        pr[0] = mx;
+        pr[1] = lsum;
+      }
+      pr[2 + dcol] = asum;
+    }
+  }
+}
+
+// Split plan of the decode form: items of (entry, 16-slot block), about 512
+// workgroups over the kv heads (Qwen3 decode over 4096 keys: 25 / 15.9 / 13.6 /
+// 15.1 / 20.5 us at 128 / 256 / 512 / 1024 / 2048 -- fewer leave SIMDs idle,
+// more pay each workgroup's two dependent memory levels and the merge of more
+// splits for less work).
+struct DecodeSplit {
+  int64_t nsb, items, per_split, splits;
+};
+static DecodeSplit decode_split(int64_t hkv, int64_t num_entries, int64_t page_size) {
+  DecodeSplit d{};
+  d.nsb = cdiv(page_size, 16);
+  d.items = num_entries * d.nsb;
+  int64_t target = 512;
+  if (const char* v = getenv("BFA_CASCADE_DECODE_WG")) target = std::max(1, atoi(v));  // measurement override
+  const int64_t want = std::max<int64_t>(1, std::min<int64_t>(d.items, cdiv(target, hkv)));
+  d.per_split = std::max<int64_t>(1, cdiv(d.items, want));
+  d.splits = d.items > 0 ? cdiv(d.items, d.per_split) : 1;
+  return d;
+}
+
+static bool decode_form(int64_t rows) { return rows <= 4; }
+
 static int64_t cascade_splits(int64_t rows, int64_t hkv, int64_t steps) {
   const int64_t blocks = cdiv(rows, 64) * hkv;
   if (blocks >= 256 || steps <= 1) return 1;
@@ -590,8 +845,8 @@ extern "C" int64_t bfa_cascade_attention_workspace_size(int64_t tokens, int64_t 
                                                         int64_t num_entries, int64_t page_size) {
   if (tokens <= 0 || num_kv_heads <= 0 || num_q_heads % num_kv_heads != 0 || page_size <= 0) return 0;
   const int64_t rows = tokens * (num_q_heads / num_kv_heads);
-  const int64_t steps = cdiv(num_entries * page_size, 32);
-  const int64_t splits = cascade_splits(rows, num_kv_heads, steps);
+  const int64_t splits = decode_form(rows) ? decode_split(num_kv_heads, num_entries, page_size).splits
+                                           : cascade_splits(rows, num_kv_heads, cdiv(num_entries * page_size, 32));
   return splits > 1 ? splits * num_kv_heads * rows * (head_dim + 2) * 4 : 0;
 }
 
@@ -643,6 +898,27 @@ extern "C" int bfa_cascade_attention(
   a.out = out; a.out_st = out_stride_token;
   a.status = status;
   const int64_t rows = num_tokens * a.group;
+  if (decode_form(rows)) {
+    const DecodeSplit ds = decode_split(num_kv_heads, num_entries, page_size);
+    if (ds.splits > 1) {
+      BFA_REQUIRE(workspace && workspace_bytes >= ds.splits * num_kv_heads * rows * (head_dim + 2) * 4,
+                  "%s: workspace too small", what);
+      a.part = static_cast<float*>(workspace);
+    }
+    BFA_REQUIRE(ds.splits < 65536 && num_kv_heads < (int64_t{1} << 31), "%s: grid too large", what);
+    const dim3 grid(static_cast<unsigned>(num_kv_heads), static_cast<unsigned>(ds.splits));
+    const dim3 mgrid(static_cast<unsigned>(num_kv_heads * rows));
+    const hipStream_t s = as_stream(stream);
+    auto launch = [&](auto bf) {
+      constexpr bool B = decltype(bf)::value;
+      if (rows <= 1) hipLaunchKernelGGL((cascade_decode_kernel<B, 1>), grid, dim3(256), 0, s, a, ds.per_split, ds.nsb);
+      else if (rows <= 2) hipLaunchKernelGGL((cascade_decode_kernel<B, 2>), grid, dim3(256), 0, s, a, ds.per_split, ds.nsb);
+      else hipLaunchKernelGGL((cascade_decode_kernel<B, 4>), grid, dim3(256), 0, s, a, ds.per_split, ds.nsb);
+      if (ds.splits > 1) hipLaunchKernelGGL(cascade_merge_kernel<B>, mgrid, dim3(256), 0, s, a, ds.splits);
+    };
+    if (dtype == BFA_DTYPE_BF16) launch(std::true_type{}); else launch(std::false_type{});
+    return check_launch(what);
+  }
   a.steps = cdiv(num_entries * page_size, 32);
   const int64_t splits = cascade_splits(rows, num_kv_heads, a.steps);
   a.steps_per_split = std::max<int64_t>(1, cdiv(a.steps, splits));

@@ -120,6 +120,33 @@ def test_cascade_attention(name, tokens, hq, hkv, lengths, deltas, causal, knorm
     assert_close(out, exp, what=name)
 
 
+@pytest.mark.parametrize("ps,tokens,dtype", [(8, 1, torch.bfloat16), (32, 2, torch.bfloat16), (16, 2, torch.float16),
+                                             (32, 1, torch.float16)])
+def test_cascade_decode_form_page_sizes(ps, tokens, dtype):
+    """Up to 4 query rows per kv head run in the decode kernel, which walks
+    (entry, 16-slot block) items: page size 8 leaves half the lane groups idle,
+    32 takes two blocks per page.  Qwen3 geometry (16 / 8 heads), k_norm, moved
+    chunks, a partial last page."""
+    g = gen(90 + ps + tokens)
+    hq, hkv, d, max_pos = 16, 8, 128, 40960
+    chunks, kv, total = build_case(91 + ps, hq, hkv, [45, 130, 77], [0, 300, -41], pages=64, ps=ps, dtype=dtype)
+    rope = RotaryEmbedding(d, d, max_pos, 1e6).to(DEV)
+    att = CascadeAttention(hq, d, d ** -0.5, hkv, ps, rotary_emb=rope)
+    levels = att.create_cascade_levels(chunks)
+    q = randn(g, tokens, hq, d, dtype=dtype)
+    qpos = torch.arange(total - tokens + 1, total + 1)
+    kn_w = torch.exp(torch.empty(d).uniform_(math.log(0.05), math.log(100.0), generator=g)).to(dtype)
+    k_norm = RMSNorm(d, eps=1e-6).to(DEV)
+    with torch.no_grad():
+        k_norm.weight.data = kn_w.to(DEV)
+    out = att.forward(q.to(DEV), qpos.to(DEV), kv.to(DEV), levels, 0, k_norm=k_norm)
+    torch.cuda.synchronize()
+    braidinfer_amd.check_device_status()
+    exp = R.cascade_attention(q, qpos, kv, cpu_levels(levels), hq, hkv, d ** -0.5, ps,
+                              rope.cos_sin_cache.cpu(), kn_w, 1e-6, True)
+    assert_close(out, exp, what=f"decode form ps={ps} t={tokens} {dtype}")
+
+
 def test_cascade_attention_fp16_query_before_keys_and_empty():
     g = gen(70)
     hq, hkv, d, ps = 16, 8, 128, 16
