@@ -539,6 +539,48 @@ __global__ __launch_bounds__(256) void cascade_merge_kernel(CasArgs a, int64_t s
   orow[64 + lane] = E::from_f32(o1 * inv);
 }
 
+// The same combination for at most 16 splits: one wave per (kv head, row), 4
+// rows per workgroup; every split's (m, l) and this lane's two columns are
+// requested together (indices clamped, weights of absent splits zero).
+template <bool BF16>
+__global__ __launch_bounds__(256) void cascade_merge_small_kernel(CasArgs a, int64_t splits) {
+  using E = Elem<BF16 ? BFA_DTYPE_BF16 : BFA_DTYPE_F16>;
+  constexpr int ZMAX = 16;
+  const int64_t rows = a.tokens * a.group;
+  const int64_t item = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (item >= a.hkv * rows) return;
+  const int64_t g = item / rows, r = item - g * rows;
+  const int lane = threadIdx.x & 63;
+  const int64_t zstride = a.hkv * rows * (CAS_D + 2);
+  const float* base = a.part + (g * rows + r) * (CAS_D + 2);
+  float mz[ZMAX], lz[ZMAX], a0[ZMAX], a1[ZMAX];
+#pragma unroll
+  for (int z = 0; z < ZMAX; ++z) {
+    const float* pz = base + min<int64_t>(z, splits - 1) * zstride;
+    mz[z] = pz[0];
+    lz[z] = pz[1];
+    a0[z] = pz[2 + lane];
+    a1[z] = pz[2 + 64 + lane];
+  }
+  float mx = -INFINITY;
+#pragma unroll
+  for (int z = 0; z < ZMAX; ++z) mx = fmaxf(mx, z < splits ? mz[z] : -INFINITY);
+  const float mref = mx == -INFINITY ? 0.f : mx;
+  float lsum = 0.f, o0 = 0.f, o1 = 0.f;
+#pragma unroll
+  for (int z = 0; z < ZMAX; ++z) {
+    const float w = z < splits ? __builtin_amdgcn_exp2f(mz[z] - mref) : 0.f;  // m in base 2; -inf -> 0
+    lsum += w * lz[z];
+    o0 += w * a0[z];
+    o1 += w * a1[z];
+  }
+  const float inv = 1.0f / fmaxf(lsum, 1e-12f);
+  const int64_t t = r / a.group, hh = g * a.group + (r - t * a.group);
+  uint16_t* orow = static_cast<uint16_t*>(a.out) + t * a.out_st + hh * CAS_D;
+  orow[lane] = E::from_f32(o0 * inv);
+  orow[64 + lane] = E::from_f32(o1 * inv);
+}
+
 // Decode form (at most 4 query rows per kv head): scores on the VALU.  A
 // workgroup's 16 groups of 16 lanes walk its range of (entry, 16-slot block)
 // items; group kg takes slot 16 sb + kg of each item, lane j holds head-dim
@@ -792,6 +834,18 @@ static DecodeSplit decode_split(int64_t hkv, int64_t num_entries, int64_t page_s
 
 static bool decode_form(int64_t rows) { return rows <= 4; }
 
+// Split combination: a wave per row up to 16 splits, a workgroup per row above.
+template <bool BF16>
+static void launch_merge(const CasArgs& a, int64_t rows, int64_t splits, hipStream_t s) {
+  const int64_t items = a.hkv * rows;
+  if (splits <= 16) {
+    hipLaunchKernelGGL(cascade_merge_small_kernel<BF16>, dim3(static_cast<unsigned>(cdiv(items, 4))), dim3(256), 0,
+                       s, a, splits);
+  } else {
+    hipLaunchKernelGGL(cascade_merge_kernel<BF16>, dim3(static_cast<unsigned>(items)), dim3(256), 0, s, a, splits);
+  }
+}
+
 static int64_t cascade_splits(int64_t rows, int64_t hkv, int64_t steps) {
   const int64_t blocks = cdiv(rows, 64) * hkv;
   if (blocks >= 256 || steps <= 1) return 1;
@@ -907,14 +961,13 @@ extern "C" int bfa_cascade_attention(
     }
     BFA_REQUIRE(ds.splits < 65536 && num_kv_heads < (int64_t{1} << 31), "%s: grid too large", what);
     const dim3 grid(static_cast<unsigned>(num_kv_heads), static_cast<unsigned>(ds.splits));
-    const dim3 mgrid(static_cast<unsigned>(num_kv_heads * rows));
     const hipStream_t s = as_stream(stream);
     auto launch = [&](auto bf) {
       constexpr bool B = decltype(bf)::value;
       if (rows <= 1) hipLaunchKernelGGL((cascade_decode_kernel<B, 1>), grid, dim3(256), 0, s, a, ds.per_split, ds.nsb);
       else if (rows <= 2) hipLaunchKernelGGL((cascade_decode_kernel<B, 2>), grid, dim3(256), 0, s, a, ds.per_split, ds.nsb);
       else hipLaunchKernelGGL((cascade_decode_kernel<B, 4>), grid, dim3(256), 0, s, a, ds.per_split, ds.nsb);
-      if (ds.splits > 1) hipLaunchKernelGGL(cascade_merge_kernel<B>, mgrid, dim3(256), 0, s, a, ds.splits);
+      if (ds.splits > 1) launch_merge<B>(a, rows, ds.splits, s);
     };
     if (dtype == BFA_DTYPE_BF16) launch(std::true_type{}); else launch(std::false_type{});
     return check_launch(what);
@@ -933,14 +986,13 @@ extern "C" int bfa_cascade_attention(
   const dim3 grid(static_cast<unsigned>(cdiv(rows, 64)), static_cast<unsigned>(num_kv_heads),
                   static_cast<unsigned>(zs));
   BFA_REQUIRE(zs == 1 || num_kv_heads * rows < (int64_t{1} << 31), "%s: grid too large", what);
-  const dim3 mgrid(static_cast<unsigned>(num_kv_heads * rows));
   const hipStream_t s = as_stream(stream);
   if (dtype == BFA_DTYPE_BF16) {
     hipLaunchKernelGGL(cascade_attn_kernel<true>, grid, dim3(256), 0, s, a);
-    if (zs > 1) hipLaunchKernelGGL(cascade_merge_kernel<true>, mgrid, dim3(256), 0, s, a, zs);
+    if (zs > 1) launch_merge<true>(a, rows, zs, s);
   } else {
     hipLaunchKernelGGL(cascade_attn_kernel<false>, grid, dim3(256), 0, s, a);
-    if (zs > 1) hipLaunchKernelGGL(cascade_merge_kernel<false>, mgrid, dim3(256), 0, s, a, zs);
+    if (zs > 1) launch_merge<false>(a, rows, zs, s);
   }
   return check_launch(what);
 }
