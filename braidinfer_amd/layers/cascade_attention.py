@@ -151,8 +151,12 @@ class CascadeAttention:
         no tokens are dropped.  Built once per (levels, chunk metadata) and reused:
         every layer of a forward pass attends the same levels, and a reused plan
         makes no host-device copy, so the call can be captured in a HIP graph after
-        one eager call."""
-        key = (tuple(id(lv) for lv in cascade_levels), tuple(meta))
+        one eager call.  A level tensor written in place (its version counter moves)
+        or a different chunk metadata gives a new plan."""
+        # the level tensors' version counters change on every in-place write, so
+        # a page table edited in place is planned again (no device read needed)
+        key = (tuple((id(lv), lv.kv_page_indices._version, lv.kv_page_indptr._version,
+                      lv.kv_last_page_len._version) for lv in cascade_levels), tuple(meta))
         hit = self._plans.get(key)
         if hit is not None and all(r() is lv for r, lv in zip(hit[0], cascade_levels)):
             return hit[1]

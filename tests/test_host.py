@@ -69,3 +69,19 @@ def test_cascade_plan_walks_pages_like_the_reference():
     assert info2.tolist() == [4, 3, 4, 4, 4, 3, 4, 2]
     # the plan is cached per level set
     assert att._plan(levels, meta, torch.device("cpu"))[0] is page
+
+
+def test_cascade_plan_follows_in_place_page_table_edits():
+    """A level whose page table is edited in place must not reuse the cached plan."""
+    from types import SimpleNamespace as NS
+    from braidinfer_amd.layers import CascadeAttention
+
+    a = NS(page_table=[5, 6], kv_length=7, cached_position_start=0, global_position_start=0)
+    levels = [_level([a], [5, 6], [0, 2], [3])]
+    att = CascadeAttention(4, 128, 1.0, 2, page_size=4)
+    dev = torch.device("cpu")
+    page, _, _, _ = att._plan(levels, att._chunk_meta(levels), dev)
+    assert page.tolist() == [5, 6]
+    levels[0].kv_page_indices[1] = 9  # in place, as a page manager might
+    page2, _, _, _ = att._plan(levels, att._chunk_meta(levels), dev)
+    assert page2.tolist() == [5, 9]
