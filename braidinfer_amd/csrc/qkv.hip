@@ -1042,6 +1042,149 @@ __global__ __launch_bounds__(256) void qkv_decode_kernel(DecodeArgs d) {
   }
 }
 
+// Deep-K form of qkv_decode_kernel for 2..4 token blocks.  With 64 tokens each
+// split's fp32 partial tile (m x n x 4 bytes, written and read back) costs half
+// as much as the split's 512-deep weight slice, so here a split walks `nch`
+// consecutive 256-deep chunks and writes one partial tile for all of them.  The
+// operand chunk is double-buffered in LDS (rows of 512 bytes, same granule
+// swizzle; one DMA fills two rows, and rows past m re-read row m-1) and the
+// next chunk's DMAs go out as the current chunk starts.  The weight registers
+// roll: as soon as segment s of chunk c has been staged, segment s of chunk c+1
+// is requested into the same registers, so one chunk of weights is always in
+// flight.  Requests, in issue order: op(c+1) [D], W(c+1) s0..s3 [4 each]
+// interleaved with chunk c's segments; hence before segment s of chunk c the
+// wave waits for vmcnt(4 (KS - 1) + D) while a next chunk exists, and for
+// vmcnt(4 (KS - 1 - s)) in the last chunk.
+constexpr int LOOP_KS = 4;  // 64-deep segments per chunk (256 of K)
+
+// wait_vm for the last chunk's segments; n is a constant once the segment loop
+// is unrolled, so the switch folds to the one wait.
+__device__ __forceinline__ void wait_vm_last(int n) {
+  static_assert(LOOP_KS == 4, "cases below");
+  switch (n) {
+    case 12: wait_vm<12>(); break;
+    case 8: wait_vm<8>(); break;
+    case 4: wait_vm<4>(); break;
+    default: wait_vm<0>(); break;
+  }
+}
+
+template <int MT, bool BF16>
+__global__ __launch_bounds__(256) void qkv_decode_loop_kernel(DecodeArgs d, int nch) {
+  constexpr int KS = LOOP_KS;
+  constexpr int GPR = KS * 8;  // granules per operand row (512 bytes)
+  constexpr int ROWS = MT * 16;
+  constexpr int D = ROWS / 8;  // operand DMAs per wave per chunk (two rows each, four waves)
+  static_assert(MT >= 2 && MT <= 4, "two to four token blocks");
+  __shared__ uint4 abuf[2 * ROWS * GPR];  // two chunks: 2 x 64 rows x 512 B = 64 KiB at MT = 4
+  __shared__ uint4 wst[4][32 * 8];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * 128 + wid * 32;
+  const int64_t kbase = static_cast<int64_t>(blockIdx.y) * nch * (KS * 64);
+  const int lr = lane & 15, lq = lane >> 4;
+
+  // DMA i of this wave covers row pair 4 i + wid: lane l fills physical slot
+  // l % 32 of row 2 (4 i + wid) + l / 32, which holds logical granule
+  // (s & ~15) | ((s & 15) ^ (row & 15)).
+  uint32_t aoff[D];
+#pragma unroll
+  for (int i = 0; i < D; ++i) {
+    const int row = 2 * (4 * i + wid) + (lane >> 5), s = lane & 31;
+    const int gl = (s & ~15) | ((s & 15) ^ (row & 15));
+    aoff[i] = static_cast<uint32_t>((min<int64_t>(row, d.m - 1) * d.lda + gl * 8) * 2);
+  }
+  const uint32_t lbase = lds_addr(abuf);
+  auto issue_op = [&](int c) {
+    const uint16_t* ab = d.a + kbase + c * (KS * 64);
+    const uint32_t lb = lbase + (c & 1) * (ROWS * GPR * 16);
+#pragma unroll
+    for (int i = 0; i < D; ++i) dma16(ab, aoff[i], lb + (4 * i + wid) * 1024);
+  };
+
+  uint4 wr[KS][4];
+  const int wrow_l = lane >> 3, wg_l = lane & 7;
+  const uint16_t* wrow[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) wrow[i] = d.w + min(n0 + i * 8 + wrow_l, d.n - 1) * d.ldw + kbase + wg_l * 8;
+
+  issue_op(0);
+#pragma unroll
+  for (int s = 0; s < KS; ++s)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) wr[s][i] = load16(wrow[i] + s * 64);
+
+  f32x4_t acc[MT][2];
+#pragma unroll
+  for (int i = 0; i < MT; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = f32x4_t{};
+  uint4* ws = wst[wid];
+
+  // One chunk: stage, fragment reads and MFMAs per segment; NEXT requests the
+  // following chunk's segment into the registers just staged.
+  auto chunk = [&](int c, auto next_tag) {
+    constexpr bool NEXT = decltype(next_tag)::value;
+    const uint4* ab = abuf + (c & 1) * (ROWS * GPR);
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      if constexpr (NEXT) wait_vm<4 * (KS - 1) + D>();
+      else wait_vm_last(4 * (KS - 1 - s));
+#pragma unroll
+      for (int i = 0; i < 4; ++i) ws[wslot(i * 8 + wrow_l, wg_l)] = wr[s][i];
+      asm volatile("" ::: "memory");
+      if constexpr (NEXT) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) wr[s][i] = load16(wrow[i] + (c + 1) * (KS * 64) + s * 64);
+      }
+      uint4 wf[2][2], af[MT][2];
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) wf[j][h] = ws[wslot(j * 16 + lr, h * 4 + lq)];
+#pragma unroll
+      for (int i = 0; i < MT; ++i) {
+        const int row = i * 16 + lr;
+        const int g0 = s * 8 + lq, g1 = g0 + 4;
+        af[i][0] = ab[row * GPR + ((g0 & ~15) | ((g0 & 15) ^ (row & 15)))];
+        af[i][1] = ab[row * GPR + ((g1 & ~15) | ((g1 & 15) ^ (row & 15)))];
+      }
+      asm volatile("" ::: "memory");
+#pragma unroll
+      for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          acc[i][j] = mfma16<BF16>(af[i][0], wf[j][0], acc[i][j]);
+          acc[i][j] = mfma16<BF16>(af[i][1], wf[j][1], acc[i][j]);
+        }
+    }
+  };
+
+  int c = 0;
+  for (; c + 1 < nch; ++c) {
+    // op(c) was issued before W(c)'s 4 KS loads: vmcnt(4 KS) means it landed;
+    // the barrier publishes every wave's copies and shows that chunk c-1, the
+    // last reader of buffer (c+1) & 1, is finished everywhere.
+    wait_vm<4 * KS>();
+    __syncthreads();
+    issue_op(c + 1);
+    chunk(c, std::true_type{});
+  }
+  wait_vm<4 * KS>();
+  __syncthreads();
+  chunk(c, std::false_type{});
+
+  // partial tile in register order, as qkv_decode_kernel with REG_ORDER
+  float4* tb = reinterpret_cast<float4*>(d.part) +
+               ((static_cast<int64_t>(blockIdx.y) * gridDim.x + blockIdx.x) * 4 + wid) * (MT * 2 * 64);
+#pragma unroll
+  for (int i = 0; i < MT; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      tb[(i * 2 + j) * 64 + lane] = make_float4(acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]);
+}
+
 // Split-K reduction + epilogue for the register-order partials of
 // qkv_decode_kernel.  One wave per (group of 4 tokens, head): lane p owns the
 // RoPE pair (p, p + D/2) of the head for all 4 tokens, which in the partial
@@ -1389,6 +1532,7 @@ struct QkvPlan {
   int tile;        // prefill: 2 (256x256, 8 waves), 3 (128x256, 8 waves), 1 (128x256, 4 waves), 128
   bool stream;     // decode: weight-streaming kernel (k % 64 == 0)
   int ks;          // decode stream: 64-deep K segments per split
+  int nch;         // decode stream: 256-deep chunks per split of the deep-K form (0: not used)
   int64_t operand_bytes;
   int64_t part_bytes;
 };
@@ -1420,6 +1564,29 @@ static QkvPlan make_plan(int64_t m, int64_t n, int64_t k, int64_t hd) {
       p.kchunk = 64 * ks;
       p.splits = segs / ks;
       p.cpw = 2;
+      // From two token blocks up the partial tiles cost more than the extra
+      // workgroups gain: the deep-K form takes the fewest splits of 256-deep
+      // chunks that still give BFA_DECODE_WG (default 192) workgroups, with at
+      // least two chunks per split.  BFA_DECODE_SPLITS (dividing the chunk
+      // count) overrides the split count for measurements.
+      const int64_t chunks = segs / LOOP_KS;
+      if (p.mt > 1 && segs % LOOP_KS == 0 && chunks >= 2) {
+        int64_t target = 192;
+        if (const char* v = getenv("BFA_DECODE_WG")) target = std::max(1, atoi(v));
+        int64_t sp = chunks;
+        for (int64_t c = 1; c <= chunks; ++c)
+          if (chunks % c == 0 && ntile * c >= target) { sp = c; break; }
+        if (const char* v = getenv("BFA_DECODE_SPLITS")) {
+          const int64_t c = atoi(v);
+          if (c >= 1 && chunks % c == 0) sp = c;
+        }
+        if (chunks / sp >= 2) {
+          p.nch = static_cast<int>(chunks / sp);
+          p.splits = sp;
+          p.ks = LOOP_KS;
+          p.kchunk = 64 * LOOP_KS * p.nch;
+        }
+      }
     } else {
       // Column tile per workgroup: 4 waves x cpw x 16 columns.
       p.cpw = m > 16 ? 1 : 2;
@@ -1491,6 +1658,14 @@ static void launch_decode(const QkvPlan& p, const SplitArgs& s, hipStream_t st) 
     d.a = s.a; d.w = s.w; d.m = s.m; d.n = s.n; d.k = s.k; d.lda = s.lda; d.ldw = s.ldw;
     d.part = s.part;
     const dim3 grid(static_cast<unsigned>(cdiv(s.n, 128)), static_cast<unsigned>(p.splits));
+    if (p.nch > 0) {
+      switch (p.mt) {
+        case 2: hipLaunchKernelGGL((qkv_decode_loop_kernel<2, BF16>), grid, dim3(256), 0, st, d, p.nch); break;
+        case 3: hipLaunchKernelGGL((qkv_decode_loop_kernel<3, BF16>), grid, dim3(256), 0, st, d, p.nch); break;
+        default: hipLaunchKernelGGL((qkv_decode_loop_kernel<4, BF16>), grid, dim3(256), 0, st, d, p.nch); break;
+      }
+      return;
+    }
     switch (p.mt) {
       case 1: launch_stream<1, BF16>(p.ks, grid, d, st); break;
       case 2: launch_stream<2, BF16>(p.ks, grid, d, st); break;

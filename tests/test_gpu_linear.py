@@ -2,7 +2,8 @@
 F.linear with and without bias, residual + F.linear, SiluAndMul of the packed
 gate_up projection, and FusedAttentionOutput's fp16-stored projection.
 
-Shapes cover the split-K decode path (1..64 tokens, both partial layouts), the
+Shapes cover the split-K decode path (1..64 tokens, both partial layouts, and
+the deep-K form with 2, 8 and 16 chunks of 256 per split), the
 DMA prefill tiles (256x256, 128x256, 128x128) and the register-staged path (K
 not a multiple of 64, strided rows), with output widths that are not multiples
 of the tile or of 8 (masked stores).  Tolerance: |d| <= 2e-2 + 1e-2 |r|
@@ -28,7 +29,9 @@ SHAPES = [
     (1, 1024, 1024),      # Qwen3-0.6B o_proj decode
     (7, 4096, 1000),      # odd token count, n not a multiple of 8
     (33, 2048, 5632),     # three 16-token blocks (register-order partials)
-    (64, 4096, 4096),     # largest decode batch
+    (64, 4096, 4096),     # largest decode batch (deep-K form: 2 chunks of 256 per split)
+    (20, 4096, 12288),    # two 16-token blocks, 8 chunks per split
+    (40, 2048, 8192),     # three 16-token blocks, 2 chunks per split
     (65, 1024, 3072),     # smallest prefill
     (300, 4096, 1000),    # ragged prefill tile, masked columns
     (1024, 2048, 2048),   # 128x256 tiles
@@ -72,7 +75,7 @@ def test_linear_add_residual(shape):
     assert torch.equal(layer.forward_add_residual(x.to(DEV), r.to(DEV)), got)
 
 
-@pytest.mark.parametrize("shape", [(1, 1024, 3072), (16, 2048, 5632), (64, 4096, 1000),
+@pytest.mark.parametrize("shape", [(1, 1024, 3072), (16, 2048, 5632), (64, 4096, 1000), (64, 4096, 14336),
                                    (65, 1024, 3072), (500, 2048, 1000), (2048, 4096, 3584),
                                    (96, 1040, 512)], ids=_ids)
 def test_gate_up_silu_and_mul(shape):

@@ -93,7 +93,9 @@ def test_minimal_f32(t, h, hq, hkv, d):
 def test_decode_split_depths(t, heads, h):
     """Decode (T <= 64) weight-streaming path: the K slice per split is chosen from
     k / 64 and the column-tile count; these shapes give every slice depth 1..8 and
-    every 16-token block count 1..4."""
+    every 16-token block count 1..4.  From 17 tokens up, (20, 16, 6144),
+    (37, 16, 7168) and (64, 16, 8192) take the deep-K form (two chunks of 256 per
+    split, two to four token blocks)."""
     hq, hkv, d = heads - 2, 1, 128
     _, x, ln, w, _ = make(209, t, h, hq, hkv, d)
     q, k, v = FusedRMSNormQKV.forward(x.to(DEV), ln.to(DEV), w.to(DEV), hq, hkv, eps=1e-6)
