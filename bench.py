@@ -533,6 +533,13 @@ def profile_one(kernel: str, tokens: int, steps: int, dev) -> int:
         print(json.dumps({"kernel": "copy", "bytes_read": src.numel() * 2, "bytes_written": dst.numel() * 2,
                           "calls": steps, "us": round(ms * 1e3, 3)}))
         return 0
+    if kernel == "library_gemm":
+        # the projection's product alone through torch.mm (hipBLASLt, bf16 out, no
+        # epilogue): a reference point for qkv_projection's hardware counters
+        wt, out = c.w_qkv.t(), torch.empty(tokens, N, dtype=torch.bfloat16, device=dev)
+        ms = time_fn(lambda: torch.mm(c.hidden, wt, out=out), steps)
+        print(json.dumps({"kernel": kernel, "tokens": tokens, "calls": steps, "us": round(ms * 1e3, 3)}))
+        return 0
     fn = {"qkv_projection": st.projection, "qkv_operand": st.operand,
           "add_rms_norm": lambda: c.norm(c.x, c.residual), "silu_and_mul": lambda: c.silu(c.gate_up),
           "embedding": lambda: embedding(c.ids, table)}[kernel]
@@ -552,7 +559,8 @@ def main(argv=None) -> int:
     ap.add_argument("--no-cold", action="store_true", help="skip the cold-cache decode table")
     ap.add_argument("--kernel", help="only run this kernel --steps times at --tokens (for "
                     "profilers): qkv_projection, qkv_operand, add_rms_norm, silu_and_mul, "
-                    "embedding, copy, or case:<name> for a case of the configuration table")
+                    "embedding, copy, library_gemm (the projection's product through torch.mm), or "
+                    "case:<name> for a case of the configuration table")
     args = ap.parse_args(argv)
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus > 1 or world > 1:
