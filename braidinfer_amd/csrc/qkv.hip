@@ -895,11 +895,34 @@ __global__ __launch_bounds__(256) void qkv_splitk_kernel(SplitArgs s) {
 // loads stream faster back to back but slow the kernel by a third once the
 // reduction kernel has read the partial tiles in between, so they are not used.)
 struct DecodeArgs {
-  const uint16_t* a;  // operand [m, k] (row stride lda)
+  const uint16_t* a;  // operand [m, k] (row stride lda); with the fold, the raw rows x
   const uint16_t* w;  // weight [n, k]
   int64_t m, n, k, lda, ldw;
   float* part;        // [splits, m, n]
+  // operand fold (NORM): x / rms(x) * gamma rounded to the weight dtype, as the
+  // operand pre-pass computes it (mixed: x / rms rounded to bf16 before gamma)
+  const void* gamma;
+  int gamma_dt, mixed;
+  float eps;
 };
+
+// Host-side description of the fold: the raw rows and the RMSNorm parameters.
+struct OperandFold {
+  const void* gamma;
+  int gamma_dt;
+  bool mixed;
+  float eps;
+};
+
+template <int DT>
+__device__ __forceinline__ void unpack8(uint4 u, float (&v)[8]) {
+  const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    v[2 * i] = Elem<DT>::to_f32(static_cast<uint16_t>(w[i] & 0xffffu));
+    v[2 * i + 1] = Elem<DT>::to_f32(static_cast<uint16_t>(w[i] >> 16));
+  }
+}
 
 constexpr int KC_MAX = 512;  // deepest K slice per split (8 segments of 64)
 
@@ -920,9 +943,16 @@ __device__ __forceinline__ int wslot(int r, int g) { return r * 8 + (g ^ ((r >> 
 // KS: 64-deep K segments per split (every split has exactly KS; the host picks
 // KS dividing k / 64), fixed at compile time so the weight loads carry no
 // branches and each segment waits only for its own four loads.
-template <int MT, int KS, bool BF16, bool REG_ORDER>
+//
+// NORM (one to four tokens, x in the weight dtype, hidden <= 4096): the
+// operand pre-pass is folded in.  Wave w reads the whole of row w (eight
+// 16-byte chunks per lane at most) for its sum of squares and the row's K
+// slice with the matching gamma, all before the weight loads are issued, then
+// writes the normalised slice where the DMA would have put it.
+template <int MT, int KS, bool BF16, bool REG_ORDER, bool NORM = false>
 __global__ __launch_bounds__(256) void qkv_decode_kernel(DecodeArgs d) {
   static_assert(KS >= 1 && KS * 64 <= KC_MAX, "segments per split");
+  static_assert(!NORM || (MT == 1 && !REG_ORDER), "the fold covers one to four tokens");
   constexpr int GPR = KC_MAX / 8;      // 16-byte granules per LDS operand row (row pitch 1 KiB)
   __shared__ uint4 abuf[64 * GPR];     // 64 rows x KC_MAX bf16 = 64 KiB
   __shared__ uint4 wst[4][32 * 8];     // per wave: 32 weight rows x 64 bf16 = 4 KiB
@@ -934,11 +964,25 @@ __global__ __launch_bounds__(256) void qkv_decode_kernel(DecodeArgs d) {
   const int lr = lane & 15, lq = lane >> 4;
   constexpr int gpr = KS * 8;  // granules per operand row actually used
 
-  // 1. operand slice -> LDS, one 1 KiB DMA per row (KC_MAX = 512 bf16): lane i
-  //    fills physical granule slot i of row r, which holds logical granule
-  //    G = (i & ~15) | ((i & 15) ^ (r & 15)); lanes with G past the slice are
-  //    masked off.
-  {
+  constexpr int DT = BF16 ? BFA_DTYPE_BF16 : BFA_DTYPE_F16;
+  uint4 sx[NORM ? 8 : 1], xs{};
+  float gv[8];
+  if constexpr (NORM) {
+    const int64_t row = min<int64_t>(wid, d.m - 1);
+    const uint16_t* xr = d.a + row * d.lda;
+    const int nch = static_cast<int>(d.k / 8);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) sx[j] = load16(xr + min(lane + 64 * j, nch - 1) * 8);
+    const int64_t kk = k0 + min(lane, gpr - 1) * 8;
+    xs = load16(xr + kk);
+    if (d.gamma_dt == BFA_DTYPE_BF16) load8<BFA_DTYPE_BF16>(static_cast<const uint16_t*>(d.gamma) + kk, gv);
+    else if (d.gamma_dt == BFA_DTYPE_F16) load8<BFA_DTYPE_F16>(static_cast<const uint16_t*>(d.gamma) + kk, gv);
+    else load8<BFA_DTYPE_F32>(static_cast<const float*>(d.gamma) + kk, gv);
+  } else {
+    // 1. operand slice -> LDS, one 1 KiB DMA per row (KC_MAX = 512 bf16): lane i
+    //    fills physical granule slot i of row r, which holds logical granule
+    //    G = (i & ~15) | ((i & 15) ^ (r & 15)); lanes with G past the slice are
+    //    masked off.
     static_assert(GPR == 64, "one wave-wide DMA per operand row");
     const uint32_t lbase = lds_addr(abuf);
     const uint16_t* abase = d.a + k0;
@@ -964,11 +1008,39 @@ __global__ __launch_bounds__(256) void qkv_decode_kernel(DecodeArgs d) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) wr[ks][i] = load16(wrow[i] + ks * 64);
   }
-  // the operand DMAs were issued before the 4 * KS weight loads and loads
-  // complete in order: vmcnt(4 KS) means the DMAs have landed
-  // (gfx9 s_waitcnt encoding: vmcnt[3:0], expcnt[6:4], lgkmcnt[11:8], vmcnt[5:4] in [15:14])
-  constexpr int kVm = 4 * KS;
-  __builtin_amdgcn_s_waitcnt((kVm & 15) | (7 << 4) | (15 << 8) | ((kVm >> 4) << 14));
+  if constexpr (NORM) {
+    // the fold's loads went out before the weights: using them waits for them only
+    float ss = 0.f;
+    const int nch = static_cast<int>(d.k / 8);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      float v[8];
+      unpack8<DT>(sx[j], v);
+      if (lane + 64 * j < nch) {
+#pragma unroll
+        for (int t = 0; t < 8; ++t) ss += v[t] * v[t];
+      }
+    }
+    ss = group_sum<64>(ss);
+    const float inv = 1.0f / sqrtf(ss / static_cast<float>(d.k) + d.eps);
+    float v[8], o[8];
+    unpack8<DT>(xs, v);
+#pragma unroll
+    for (int t = 0; t < 8; ++t) o[t] = d.mixed ? round_bf16(v[t] * inv) * gv[t] : (v[t] * inv) * gv[t];
+    uint32_t pw[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      pw[i] = static_cast<uint32_t>(Elem<DT>::from_f32(o[2 * i])) |
+              (static_cast<uint32_t>(Elem<DT>::from_f32(o[2 * i + 1])) << 16);
+    if (wid < d.m && lane < gpr)
+      abuf[wid * GPR + ((lane & ~15) | ((lane & 15) ^ (wid & 15)))] = make_uint4(pw[0], pw[1], pw[2], pw[3]);
+  } else {
+    // the operand DMAs were issued before the 4 * KS weight loads and loads
+    // complete in order: vmcnt(4 KS) means the DMAs have landed
+    // (gfx9 s_waitcnt encoding: vmcnt[3:0], expcnt[6:4], lgkmcnt[11:8], vmcnt[5:4] in [15:14])
+    constexpr int kVm = 4 * KS;
+    __builtin_amdgcn_s_waitcnt((kVm & 15) | (7 << 4) | (15 << 8) | ((kVm >> 4) << 14));
+  }
   __syncthreads();
 
   // 3. per segment: registers -> staging -> B fragments, then MFMAs.  The
@@ -1639,6 +1711,21 @@ static void launch_decode_cpw(const QkvPlan& p, const SplitArgs& s, hipStream_t 
 template <int MT, bool BF16>
 static void launch_stream(int ks, dim3 grid, const DecodeArgs& d, hipStream_t st) {
   constexpr bool RO = MT > 1;  // register-order partials from two 16-token blocks up
+  if constexpr (MT == 1) {
+    if (d.gamma) {
+      switch (ks) {
+        case 1: hipLaunchKernelGGL((qkv_decode_kernel<1, 1, BF16, false, true>), grid, dim3(256), 0, st, d); break;
+        case 2: hipLaunchKernelGGL((qkv_decode_kernel<1, 2, BF16, false, true>), grid, dim3(256), 0, st, d); break;
+        case 3: hipLaunchKernelGGL((qkv_decode_kernel<1, 3, BF16, false, true>), grid, dim3(256), 0, st, d); break;
+        case 4: hipLaunchKernelGGL((qkv_decode_kernel<1, 4, BF16, false, true>), grid, dim3(256), 0, st, d); break;
+        case 5: hipLaunchKernelGGL((qkv_decode_kernel<1, 5, BF16, false, true>), grid, dim3(256), 0, st, d); break;
+        case 6: hipLaunchKernelGGL((qkv_decode_kernel<1, 6, BF16, false, true>), grid, dim3(256), 0, st, d); break;
+        case 7: hipLaunchKernelGGL((qkv_decode_kernel<1, 7, BF16, false, true>), grid, dim3(256), 0, st, d); break;
+        default: hipLaunchKernelGGL((qkv_decode_kernel<1, 8, BF16, false, true>), grid, dim3(256), 0, st, d); break;
+      }
+      return;
+    }
+  }
   switch (ks) {
     case 1: hipLaunchKernelGGL((qkv_decode_kernel<MT, 1, BF16, RO>), grid, dim3(256), 0, st, d); break;
     case 2: hipLaunchKernelGGL((qkv_decode_kernel<MT, 2, BF16, RO>), grid, dim3(256), 0, st, d); break;
@@ -1652,11 +1739,15 @@ static void launch_stream(int ks, dim3 grid, const DecodeArgs& d, hipStream_t st
 }
 
 template <bool BF16>
-static void launch_decode(const QkvPlan& p, const SplitArgs& s, hipStream_t st) {
+static void launch_decode(const QkvPlan& p, const SplitArgs& s, hipStream_t st,
+                          const OperandFold* fold = nullptr) {
   if (p.stream) {
     DecodeArgs d{};
     d.a = s.a; d.w = s.w; d.m = s.m; d.n = s.n; d.k = s.k; d.lda = s.lda; d.ldw = s.ldw;
     d.part = s.part;
+    if (fold) {
+      d.gamma = fold->gamma; d.gamma_dt = fold->gamma_dt; d.mixed = fold->mixed ? 1 : 0; d.eps = fold->eps;
+    }
     const dim3 grid(static_cast<unsigned>(cdiv(s.n, 128)), static_cast<unsigned>(p.splits));
     if (p.nch > 0) {
       switch (p.mt) {
@@ -1775,8 +1866,12 @@ extern "C" int64_t bfa_fused_rmsnorm_qkv_workspace_size(int64_t tokens, int64_t 
   return p.operand_bytes + p.part_bytes;
 }
 
-extern "C" int bfa_qkv_projection(const void* operand, int64_t tokens, int64_t hidden,
-                                  const void* qkv_weight, int w_dtype, int64_t qkv_dim,
+// The projection with its epilogue; `operand` rows are `lda` apart.  With a
+// fold (decode, one to four tokens) `operand` is the raw input x and the decode
+// kernel normalises it itself.
+static int qkv_projection_impl(const void* operand, int64_t lda, const OperandFold* fold,
+                               int64_t tokens, int64_t hidden,
+                               const void* qkv_weight, int w_dtype, int64_t qkv_dim,
                                   int64_t w_stride, const void* bias, int bias_dtype,
                                   int64_t num_q_heads, int64_t num_kv_heads, int qkv_dtype,
                                   const void* q_norm_weight, const void* k_norm_weight,
@@ -1785,7 +1880,7 @@ extern "C" int bfa_qkv_projection(const void* operand, int64_t tokens, int64_t h
                                   const float* cos_sin_cache, int64_t max_position, void* out,
                                   int out_dtype, int64_t out_stride, void* part_workspace,
                                   int64_t part_workspace_bytes, int32_t* status, void* stream) {
-  const char* what = "bfa_qkv_projection";
+  const char* what = fold ? "bfa_fused_rmsnorm_qkv" : "bfa_qkv_projection";
   BFA_REQUIRE(w_dtype == BFA_DTYPE_BF16 || w_dtype == BFA_DTYPE_F16, "%s: weight must be bf16/fp16", what);
   BFA_REQUIRE(is_float_dtype(qkv_dtype) && is_float_dtype(out_dtype) && is_float_dtype(qk_norm_out_dtype),
               "%s: bad dtype", what);
@@ -1835,9 +1930,9 @@ extern "C" int bfa_qkv_projection(const void* operand, int64_t tokens, int64_t h
     SplitArgs s{};
     s.a = static_cast<const uint16_t*>(operand);
     s.w = static_cast<const uint16_t*>(qkv_weight);
-    s.m = tokens; s.n = qkv_dim; s.k = hidden; s.lda = hidden; s.ldw = w_stride;
+    s.m = tokens; s.n = qkv_dim; s.k = hidden; s.lda = lda; s.ldw = w_stride;
     s.kchunk = p.kchunk; s.part = part;
-    if (bf16) launch_decode<true>(p, s, st); else launch_decode<false>(p, s, st);
+    if (bf16) launch_decode<true>(p, s, st, fold); else launch_decode<false>(p, s, st, fold);
     int rc = check_launch(what);
     if (rc != BFA_OK) return rc;
     if (p.stream && p.mt > 1) {
@@ -1871,6 +1966,23 @@ extern "C" int bfa_qkv_projection(const void* operand, int64_t tokens, int64_t h
   return check_launch(what);
 }
 
+extern "C" int bfa_qkv_projection(const void* operand, int64_t tokens, int64_t hidden,
+                                  const void* qkv_weight, int w_dtype, int64_t qkv_dim,
+                                  int64_t w_stride, const void* bias, int bias_dtype,
+                                  int64_t num_q_heads, int64_t num_kv_heads, int qkv_dtype,
+                                  const void* q_norm_weight, const void* k_norm_weight,
+                                  int qk_norm_dtype, float qk_eps, int qk_norm_out_dtype,
+                                  const void* positions, int positions_dtype,
+                                  const float* cos_sin_cache, int64_t max_position, void* out,
+                                  int out_dtype, int64_t out_stride, void* part_workspace,
+                                  int64_t part_workspace_bytes, int32_t* status, void* stream) {
+  return qkv_projection_impl(operand, hidden, nullptr, tokens, hidden, qkv_weight, w_dtype, qkv_dim,
+                             w_stride, bias, bias_dtype, num_q_heads, num_kv_heads, qkv_dtype,
+                             q_norm_weight, k_norm_weight, qk_norm_dtype, qk_eps, qk_norm_out_dtype,
+                             positions, positions_dtype, cos_sin_cache, max_position, out, out_dtype,
+                             out_stride, part_workspace, part_workspace_bytes, status, stream);
+}
+
 extern "C" int bfa_fused_rmsnorm_qkv(const void* x, int x_dtype, int64_t tokens, int64_t hidden,
                                      int64_t x_stride, const void* norm_weight, int nw_dtype,
                                      float eps, int mixed_rounding, const void* qkv_weight,
@@ -1893,6 +2005,23 @@ extern "C" int bfa_fused_rmsnorm_qkv(const void* x, int x_dtype, int64_t tokens,
               "%s: workspace too small (%lld < %lld bytes)", what, (long long)workspace_bytes,
               (long long)(p.operand_bytes + p.part_bytes));
   char* ws = static_cast<char*>(workspace);
+  // One to four decode tokens whose x is already in the weight dtype: the
+  // weight-streaming kernel normalises its own K slice, one launch fewer.
+  // BFA_NO_OPERAND_FOLD=1 keeps the pre-pass (for measurements).
+  const char* nf = getenv("BFA_NO_OPERAND_FOLD");
+  const bool no_fold = nf && atoi(nf) != 0;
+  const bool fold = !no_fold && p.decode && p.stream && tokens <= 4 && x_dtype == w_dtype &&
+                    (w_dtype == BFA_DTYPE_BF16 || w_dtype == BFA_DTYPE_F16) && hidden % 8 == 0 &&
+                    hidden <= 4096 && x_stride % 8 == 0 && aligned16(x) && aligned16(norm_weight) &&
+                    is_float_dtype(nw_dtype);
+  if (fold) {
+    const OperandFold f{norm_weight, nw_dtype, mixed_rounding != 0, eps};
+    return qkv_projection_impl(x, x_stride, &f, tokens, hidden, qkv_weight, w_dtype, qkv_dim, w_stride,
+                               bias, bias_dtype, num_q_heads, num_kv_heads, qkv_dtype, q_norm_weight,
+                               k_norm_weight, qk_norm_dtype, qk_eps, qk_norm_out_dtype, positions,
+                               positions_dtype, cos_sin_cache, max_position, out, out_dtype, out_stride,
+                               ws + p.operand_bytes, workspace_bytes - p.operand_bytes, status, stream);
+  }
   int rc = launch_qkv_operand(x, x_dtype, tokens, hidden, x_stride, norm_weight, nw_dtype,
                               mixed_rounding != 0, ws, w_dtype, eps, as_stream(stream));
   if (rc != BFA_OK) return rc;

@@ -104,6 +104,36 @@ def test_decode_split_depths(t, heads, h):
         assert_close(got, exp, what=f"decode {name} t={t} h={h}")
 
 
+@pytest.mark.parametrize("t,h,dtype,strided", [
+    (1, 4096, torch.bfloat16, False),   # Llama-3-8B batch-1 decode: eight 16-byte chunks per lane
+    (3, 4096, torch.bfloat16, True),    # rows 4160 elements apart
+    (4, 1024, torch.float16, False),    # largest folded batch, fp16
+    (2, 64, torch.bfloat16, False),     # one 64-deep segment, a partial chunk row
+])
+def test_decode_operand_fold(t, h, dtype, strided):
+    """One to four decode tokens with x in the weight dtype: the weight-streaming
+    kernel computes the row statistics and normalises its own K slice (no
+    pre-pass launch).  Mixed and production rounding, with the RMSNorm weight in
+    the input dtype and in fp32."""
+    hq, hkv, d = 6, 1, 64
+    g, x, ln, w, _ = make(211, t, h, hq, hkv, d, dtype=dtype)
+    xd = x.to(DEV)
+    if strided:
+        wide = torch.zeros(t, h + 64, dtype=dtype, device=DEV)
+        wide[:, :h] = xd
+        xd = wide[:, :h]
+        assert xd.stride(0) == h + 64
+    for lnw in (ln, ln.float()):
+        q, k, v = FusedRMSNormQKVMixedPrecision.forward(xd, lnw.to(DEV), w.to(DEV), None, hq, hkv, eps=1e-6)
+        ref = R.split_qkv(R.qkv_mixed_precision(x, lnw, w, None, 1e-6), hq, hkv)
+        for got, exp, name in zip((q, k, v), ref, "qkv"):
+            assert_close(got, exp, what=f"fold mixed {name} t={t} h={h} ln {lnw.dtype}")
+        q, k, v = FusedRMSNormQKV.forward(xd, lnw.to(DEV), w.to(DEV), hq, hkv, eps=1e-6)
+        ref = R.split_qkv(R.qkv_production(x, lnw, w, 1e-6), hq, hkv)
+        for got, exp, name in zip((q, k, v), ref, "qkv"):
+            assert_close(got, exp, what=f"fold production {name} t={t} h={h} ln {lnw.dtype}")
+
+
 def test_with_bias_reference_cases():
     """tests/test_qwen3_bias_handling.py and test_numerical_stability.py:237-294 on the HIP path."""
     g = gen(204)
