@@ -201,18 +201,24 @@ __global__ __launch_bounds__(256) void rerotate_kernel(RerotArgs a) {
   using T = typename Elem<DT>::T;
   const int64_t g = blockIdx.x;  // page-list entry
   const int64_t h = blockIdx.y;  // kv head
-  // chunk owning entry g: last c with indptr[c] <= g (indptr is non-decreasing)
-  int64_t lo = 0, hi = a.num_chunks - 1;
-  while (lo < hi) {
-    const int64_t mid = (lo + hi + 1) / 2;
-    if (a.chunk_indptr[mid] <= g) lo = mid; else hi = mid - 1;
+  const int64_t page = a.page_indices[g];  // requested before the chunk search, which it does not need
+  // chunk owning entry g: last c with indptr[c] <= g.  indptr is non-decreasing,
+  // so the chunks with indptr[c] <= g are a prefix: each wave tests 64 chunks
+  // per load and counts the prefix (one memory round trip per 64 chunks where
+  // a binary search takes log2(chunks) dependent ones).
+  const int wl = threadIdx.x & (kWave - 1);
+  int64_t c = 0;
+  for (int64_t base = 0; base < a.num_chunks; base += kWave) {
+    const int64_t idx = base + wl;
+    const bool le = idx < a.num_chunks && a.chunk_indptr[idx] <= g;
+    const uint64_t m = __ballot(le);
+    if (m) c = base + __popcll(m) - 1;
+    if (!(m >> (kWave - 1))) break;  // the prefix ended inside this block
   }
-  const int64_t c = lo;
   const bool last = (g == a.chunk_indptr[c + 1] - 1);
   const int64_t ntok =
       last ? max(static_cast<int64_t>(0), min(static_cast<int64_t>(a.last_page_len[c]), a.page_size))
            : a.page_size;
-  const int64_t page = a.page_indices[g];
   const int64_t delta = a.delta_is_i64 ? static_cast<const int64_t*>(a.delta)[c]
                                        : static_cast<const int32_t*>(a.delta)[c];
   if (page < 0 || page >= a.num_cache_pages) {
