@@ -480,6 +480,307 @@ __global__ __launch_bounds__(256) void cascade_attn_kernel(CasArgs a) {
   }
 }
 
+// ======================================================== flat form
+// For many query rows every workgroup of cascade_attn_kernel would rotate and
+// normalise the same keys again.  The flat form does that once: a pre-pass
+// writes the attended keys of each kv head in walk order (padded key slot
+// e * page_size + s, tiles of 64) as K rotated and k-normalised, row-major, and
+// V transposed (head-dim rows of 64 keys, the keys of each group of 32 in the
+// PV product's order), plus each slot's key position (INT32_MAX where the slot
+// is past the page's tokens or masked).  The attention kernel then copies K and
+// V^T tiles into LDS by DMA (no register staging, no transform) and runs the
+// same S^T / O^T scheme on 64 keys per step.
+struct FlatArgs {
+  uint16_t* kf;     // [Hkv, npad, D]
+  uint16_t* vt;     // [Hkv, D, npad]
+  int32_t* kpos;    // [npad]
+  int64_t npad;     // padded key slots, a multiple of 64
+  int64_t tiles_per_split;
+};
+
+constexpr int CAS_FT = 64;             // keys per tile of the flat form
+constexpr int CAS_FVP = CAS_FT + 8;    // V^T staging row pitch (bf16): 144 bytes
+
+// the PV product's order of key slot k inside its group of 32 (see the V^T
+// staging of cascade_attn_kernel)
+__device__ __forceinline__ int pv_order(int k) {
+  const int sk = k & 31;
+  return (k & ~31) + 8 * ((sk >> 2) & 3) + 4 * (sk >> 4) + (sk & 3);
+}
+
+template <bool BF16>
+__global__ __launch_bounds__(256) void cascade_flatten_kernel(CasArgs a, FlatArgs f) {
+  using E = Elem<BF16 ? BFA_DTYPE_BF16 : BFA_DTYPE_F16>;
+  constexpr int DT = BF16 ? BFA_DTYPE_BF16 : BFA_DTYPE_F16;
+  __shared__ uint16_t vs[CAS_D * CAS_FVP];
+  const int tid = threadIdx.x;
+  const int64_t g = blockIdx.y;  // kv head
+  const int64_t t0 = static_cast<int64_t>(blockIdx.x) * CAS_FT;
+  const int sk = tid >> 3, sc = tid & 7;  // key row (and row + 32), column chunk
+  float kg1[8] = {1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f};
+  float kg2[8] = {1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f};
+  if (a.knorm_w) {
+    const char* w = static_cast<const char*>(a.knorm_w);
+    if (a.knorm_dt == BFA_DTYPE_F32) {
+      load8<BFA_DTYPE_F32>(w + 4 * (8 * sc), kg1);
+      load8<BFA_DTYPE_F32>(w + 4 * (CAS_D / 2 + 8 * sc), kg2);
+    } else if (a.knorm_dt == BFA_DTYPE_BF16) {
+      load8<BFA_DTYPE_BF16>(w + 2 * (8 * sc), kg1);
+      load8<BFA_DTYPE_BF16>(w + 2 * (CAS_D / 2 + 8 * sc), kg2);
+    } else {
+      load8<BFA_DTYPE_F16>(w + 2 * (8 * sc), kg1);
+      load8<BFA_DTYPE_F16>(w + 2 * (CAS_D / 2 + 8 * sc), kg2);
+    }
+  }
+#pragma unroll
+  for (int pass = 0; pass < 2; ++pass) {
+    const int kk = sk + 32 * pass;
+    const int64_t slot = t0 + kk;
+    const int64_t e = slot / a.page_size, s = slot - e * a.page_size;
+    const bool in = e < a.num_entries;
+    const int64_t ec = in ? e : 0;
+    int64_t page = a.pages[ec];
+    const int64_t kst = a.kstart[ec];
+    int64_t dpos = a.delta[ec];
+    const int32_t info = a.info[ec];
+    bool valid = in && s < (info & 0xffff);
+    if (page < 0) page += a.num_pages;  // kv_cache[-1] is the last page
+    if (valid && (page < 0 || page >= a.num_pages)) {
+      if (sc == 0) flag_status(a.status, BFA_STATUS_INDEX_OOB);
+      valid = false;
+    }
+    bool rot = valid && a.cs != nullptr && ((info >> 16) & 1);
+    if (rot) {
+      if (dpos < 0) dpos += a.max_pos;
+      if (dpos < 0 || dpos >= a.max_pos) {
+        if (sc == 0) flag_status(a.status, BFA_STATUS_INDEX_OOB);
+        valid = false;
+        rot = false;
+      }
+    }
+    const int64_t kp = kst + s;
+    if (valid && kp >= INT32_MAX) {  // positions are kept in 32 bits here
+      if (sc == 0) flag_status(a.status, BFA_STATUS_INDEX_OOB);
+      valid = false;
+      rot = false;
+    }
+    const uint16_t* zero = reinterpret_cast<const uint16_t*>(cas_zero_row);
+    const uint16_t* krow = valid ? a.cache + page * a.c_sp + g * a.c_sh + s * a.c_ss : zero;
+    const uint16_t* vrow = valid ? krow + a.c_skv : zero;
+    float x1[8], x2[8], v1[8], v2[8];
+    load8<DT>(krow + 8 * sc, x1);
+    load8<DT>(krow + CAS_D / 2 + 8 * sc, x2);
+    load8<DT>(vrow + 8 * sc, v1);
+    load8<DT>(vrow + CAS_D / 2 + 8 * sc, v2);
+    if (rot) {
+      float cs[8], sn[8];
+      load8<BFA_DTYPE_F32>(a.cs + dpos * CAS_D + 8 * sc, cs);
+      load8<BFA_DTYPE_F32>(a.cs + dpos * CAS_D + CAS_D / 2 + 8 * sc, sn);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {  // apply_rotary_emb: fp32, result in the cache dtype
+        const float u = x1[i], w = x2[i];
+        x1[i] = E::round(u * cs[i] - w * sn[i]);
+        x2[i] = E::round(w * cs[i] + u * sn[i]);
+      }
+    }
+    if (a.knorm_w) {  // uniform; a zero row stays zero
+      float ss = 0.f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) ss += x1[i] * x1[i] + x2[i] * x2[i];
+      ss = group8_sum_dpp(ss);
+      const float r = 1.0f / sqrtf(ss / static_cast<float>(CAS_D) + a.knorm_eps);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        x1[i] = E::round(E::round(x1[i] * r) * kg1[i]);
+        x2[i] = E::round(E::round(x2[i] * r) * kg2[i]);
+      }
+    }
+    uint16_t* kd = f.kf + (g * f.npad + slot) * CAS_D;
+    store8<DT>(kd + 8 * sc, x1);
+    store8<DT>(kd + CAS_D / 2 + 8 * sc, x2);
+    const int kc = pv_order(kk);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      vs[(8 * sc + i) * CAS_FVP + kc] = E::from_f32(v1[i]);
+      vs[(CAS_D / 2 + 8 * sc + i) * CAS_FVP + kc] = E::from_f32(v2[i]);
+    }
+    if (g == 0 && sc == 0) f.kpos[slot] = valid ? static_cast<int32_t>(kp) : INT32_MAX;
+  }
+  __syncthreads();
+  // V^T tile out: 128 head-dim rows of 64 keys, 16-byte granules
+#pragma unroll
+  for (int i = tid; i < CAS_D * 8; i += 256) {
+    const int d = i >> 3, gr = i & 7;
+    *reinterpret_cast<uint4*>(f.vt + (g * CAS_D + d) * f.npad + t0 + 8 * gr) =
+        *reinterpret_cast<const uint4*>(vs + d * CAS_FVP + 8 * gr);
+  }
+}
+
+template <bool BF16>
+__global__ __launch_bounds__(256) void cascade_flat_kernel(CasArgs a, FlatArgs f) {
+  // K tile: 64 rows of 256 bytes, granule G of row r at slot G ^ (r & 15); V^T
+  // tile: 128 rows of 128 bytes, granule G of row r at slot G ^ ((r / 2) & 7).
+  // Both make a 16-lane fragment read touch 16 distinct bank groups.
+  __shared__ uint4 kbuf[2][CAS_FT * 16];
+  __shared__ uint4 vbuf[2][CAS_D * 8];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int64_t g = blockIdx.y;
+  const int64_t rows = a.tokens * a.group;
+  const int64_t row0 = static_cast<int64_t>(blockIdx.x) * 64 + wid * 16;
+  const int64_t tiles = f.npad / CAS_FT;
+  const int64_t tl0 = static_cast<int64_t>(blockIdx.z) * f.tiles_per_split;
+  const int64_t tl1 = min(tl0 + f.tiles_per_split, tiles);
+
+  uint4 qf[4];
+  {
+    const int64_t r = min(row0 + (lane & 15), rows - 1);
+    const int64_t t = r / a.group, hh = g * a.group + (r - t * a.group);
+    const uint16_t* qrow = a.q + t * a.q_st + hh * a.q_sh;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) qf[j] = *reinterpret_cast<const uint4*>(qrow + 32 * j + 8 * (lane >> 4));
+  }
+  const int64_t qt = min(row0 + (lane & 15), rows - 1) / a.group;
+  const int64_t qp = a.qpos_i64 ? static_cast<const int64_t*>(a.qpos)[qt]
+                                : static_cast<const int32_t*>(a.qpos)[qt];
+  const float sl2 = a.scale * 1.4426950408889634f;
+  float m = -INFINITY, l = 0.f;
+  cas_f32x4_t o[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) o[j] = cas_f32x4_t{};
+
+  // DMA roles, four 1 KiB copies of each tile per wave: K copy i moves rows
+  // 4 (4 i + wid) .. +3 (lane: row + lane / 16, slot lane % 16); V^T copy i moves
+  // rows 8 (4 i + wid) .. +7 (lane: row + lane / 8, slot lane % 8).  Offsets are
+  // in bytes from the tile's first element.
+  uint32_t koff[4], voff[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int kr = 4 * (4 * i + wid) + (lane >> 4);
+    koff[i] = static_cast<uint32_t>((kr * CAS_D + 8 * ((lane & 15) ^ (kr & 15))) * 2);
+    const int vr = 8 * (4 * i + wid) + (lane >> 3);
+    voff[i] = static_cast<uint32_t>((vr * f.npad + 8 * ((lane & 7) ^ ((vr >> 1) & 7))) * 2);
+  }
+  const uint16_t* kbase = f.kf + g * f.npad * CAS_D;
+  const uint16_t* vbase = f.vt + g * CAS_D * f.npad;
+  const uint32_t kl = lds_addr(kbuf), vl = lds_addr(vbuf);
+  auto issue = [&](int64_t t, int b) {
+    const uint16_t* kt = kbase + t * CAS_FT * CAS_D;
+    const uint16_t* vt = vbase + t * CAS_FT;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) dma16(kt, koff[i], kl + b * (CAS_FT * 256) + (4 * i + wid) * 1024);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) dma16(vt, voff[i], vl + b * (CAS_D * 128) + (4 * i + wid) * 1024);
+  };
+  // key positions of this lane's scores: slots 16 b + 4 (lane / 16) .. +3
+  auto load_kp = [&](int64_t t, int4 (&kp)[4]) {
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+      kp[b] = *reinterpret_cast<const int4*>(f.kpos + t * CAS_FT + 16 * b + 4 * (lane >> 4));
+  };
+
+  if (tl0 < tl1) {
+    int4 kp[4];
+    issue(tl0, 0);
+    load_kp(tl0, kp);
+    wait_vmem();
+    __syncthreads();
+    for (int64_t t = tl0; t < tl1; ++t) {
+      const int b = static_cast<int>((t - tl0) & 1);
+      int4 kpn[4] = {kp[0], kp[1], kp[2], kp[3]};
+      if (t + 1 < tl1) {  // the next tile flies during this one's matrix work
+        issue(t + 1, b ^ 1);
+        load_kp(t + 1, kpn);
+      }
+      // S^T = K Q^T, 4 blocks of 16 keys: sacc[c][i] is the score of key slot
+      // 16 c + 4 (lane / 16) + i for query lane % 16
+      const uint4* kb = kbuf[b];
+      cas_f32x4_t sacc[4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        sacc[c] = cas_f32x4_t{};
+        const int kr = 16 * c + (lane & 15);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          sacc[c] = mfma16x32<BF16>(kb[kr * 16 + ((4 * j + (lane >> 4)) ^ (kr & 15))], qf[j], sacc[c]);
+      }
+      float p[4][4];
+      float mx = -INFINITY;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int kq[4] = {kp[c].x, kp[c].y, kp[c].z, kp[c].w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const bool use = kq[i] != INT32_MAX && (!a.causal || kq[i] <= qp);
+          p[c][i] = use ? sacc[c][i] * sl2 : -INFINITY;
+          mx = fmaxf(mx, p[c][i]);
+        }
+      }
+      mx = lanes4_max(mx);
+      const float m_new = fmaxf(m, mx);
+      const float mref = m_new == -INFINITY ? 0.f : m_new;
+      const float alpha = __builtin_amdgcn_exp2f(m - mref);
+      float rs = 0.f;
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          p[c][i] = __builtin_amdgcn_exp2f(p[c][i] - mref);
+          rs += p[c][i];
+        }
+      rs = lanes4_sum(rs);
+      l = l * alpha + rs;
+      m = m_new;
+      if (__any(alpha != 1.0f)) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) o[j] *= alpha;
+      }
+      // O^T += V^T P^T over the two groups of 32 keys
+      const uint4* vb = vbuf[b];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const uint4 pf = make_uint4(pack_pair<BF16>(p[2 * h][0], p[2 * h][1]), pack_pair<BF16>(p[2 * h][2], p[2 * h][3]),
+                                    pack_pair<BF16>(p[2 * h + 1][0], p[2 * h + 1][1]),
+                                    pack_pair<BF16>(p[2 * h + 1][2], p[2 * h + 1][3]));
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const int vr = 16 * j + (lane & 15);
+          o[j] = mfma16x32<BF16>(vb[vr * 8 + ((4 * h + (lane >> 4)) ^ ((vr >> 1) & 7))], pf, o[j]);
+        }
+      }
+      wait_vmem();
+      __syncthreads();  // tile t+1 is in LDS everywhere; every wave is done with tile t
+#pragma unroll
+      for (int c = 0; c < 4; ++c) kp[c] = kpn[c];
+    }
+  }
+
+  const int64_t r = row0 + (lane & 15);
+  if (r < rows) {
+    const int d0 = 4 * (lane >> 4);
+    if (gridDim.z == 1) {
+      const int64_t t = r / a.group, hh = g * a.group + (r - t * a.group);
+      const float inv = 1.0f / fmaxf(l, 1e-12f);
+      uint16_t* orow = static_cast<uint16_t*>(a.out) + t * a.out_st + hh * CAS_D;
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        *reinterpret_cast<uint2*>(orow + 16 * j + d0) =
+            make_uint2(pack_pair<BF16>(o[j][0] * inv, o[j][1] * inv), pack_pair<BF16>(o[j][2] * inv, o[j][3] * inv));
+    } else {
+      float* pr = a.part + ((static_cast<int64_t>(blockIdx.z) * a.hkv + g) * rows + r) * (CAS_D + 2);
+      if (lane < 16) {
+        pr[0] = m;
+        pr[1] = l;
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) pr[2 + 16 * j + d0 + i] = o[j][i];
+    }
+  }
+}
+
 // Combines the splits' (m, l, acc) rows: one workgroup per (kv head, row).
 // Every wave finds the maximum over all splits (lanes over splits); wave w then
 // sums splits w, w + 4, ... -- each lane two head-dim columns, the weights
@@ -846,6 +1147,44 @@ static void launch_merge(const CasArgs& a, int64_t rows, int64_t splits, hipStre
   }
 }
 
+// The flat form, from more than CAS_FLAT_ROWS query rows per kv head (or as
+// BFA_CASCADE_FLAT = 0 / 1 forces, for measurements).  At Qwen3 shape over 4096
+// keys it is slower than the fused kernel up to 64 rows (26.3 against 25.3 us)
+// and faster from 128 (28.5 against 32.7; 42.3 against 79.4 at 512 rows).
+// Workspace after the split partials: K and V^T copies of the attended keys and
+// their positions.
+constexpr int64_t CAS_FLAT_ROWS = 96;
+
+static bool flat_form(int64_t rows, int64_t num_entries) {
+  if (num_entries <= 0) return false;
+  if (const char* v = getenv("BFA_CASCADE_FLAT")) return atoi(v) != 0 && rows > 4;
+  return rows > CAS_FLAT_ROWS;
+}
+
+struct FlatPlan {
+  int64_t npad, tiles, splits, tiles_per_split;
+  int64_t part_bytes, kf_bytes, vt_bytes, kp_bytes;
+  int64_t total() const { return part_bytes + kf_bytes + vt_bytes + kp_bytes; }
+};
+
+static int64_t align256c(int64_t v) { return (v + 255) / 256 * 256; }
+
+static FlatPlan flat_plan(int64_t rows, int64_t hkv, int64_t num_entries, int64_t page_size) {
+  FlatPlan fp{};
+  fp.npad = cdiv(num_entries * page_size, CAS_FT) * CAS_FT;
+  fp.tiles = fp.npad / CAS_FT;
+  const int64_t blocks = cdiv(rows, 64) * hkv;
+  int64_t zs = blocks >= 256 ? 1 : std::min<int64_t>(cdiv(512, blocks), fp.tiles);
+  zs = std::max<int64_t>(1, zs);
+  fp.tiles_per_split = std::max<int64_t>(1, cdiv(fp.tiles, zs));
+  fp.splits = std::max<int64_t>(1, cdiv(fp.tiles, fp.tiles_per_split));
+  fp.part_bytes = fp.splits > 1 ? align256c(fp.splits * hkv * rows * (CAS_D + 2) * 4) : 0;
+  fp.kf_bytes = align256c(hkv * fp.npad * CAS_D * 2);
+  fp.vt_bytes = fp.kf_bytes;
+  fp.kp_bytes = align256c(fp.npad * 4);
+  return fp;
+}
+
 static int64_t cascade_splits(int64_t rows, int64_t hkv, int64_t steps) {
   const int64_t blocks = cdiv(rows, 64) * hkv;
   if (blocks >= 256 || steps <= 1) return 1;
@@ -899,6 +1238,8 @@ extern "C" int64_t bfa_cascade_attention_workspace_size(int64_t tokens, int64_t 
                                                         int64_t num_entries, int64_t page_size) {
   if (tokens <= 0 || num_kv_heads <= 0 || num_q_heads % num_kv_heads != 0 || page_size <= 0) return 0;
   const int64_t rows = tokens * (num_q_heads / num_kv_heads);
+  if (!decode_form(rows) && flat_form(rows, num_entries))
+    return flat_plan(rows, num_kv_heads, num_entries, page_size).total();
   const int64_t splits = decode_form(rows) ? decode_split(num_kv_heads, num_entries, page_size).splits
                                            : cascade_splits(rows, num_kv_heads, cdiv(num_entries * page_size, 32));
   return splits > 1 ? splits * num_kv_heads * rows * (head_dim + 2) * 4 : 0;
@@ -968,6 +1309,33 @@ extern "C" int bfa_cascade_attention(
       else if (rows <= 2) hipLaunchKernelGGL((cascade_decode_kernel<B, 2>), grid, dim3(256), 0, s, a, ds.per_split, ds.nsb);
       else hipLaunchKernelGGL((cascade_decode_kernel<B, 4>), grid, dim3(256), 0, s, a, ds.per_split, ds.nsb);
       if (ds.splits > 1) launch_merge<B>(a, rows, ds.splits, s);
+    };
+    if (dtype == BFA_DTYPE_BF16) launch(std::true_type{}); else launch(std::false_type{});
+    return check_launch(what);
+  }
+  if (flat_form(rows, num_entries)) {
+    const FlatPlan fp = flat_plan(rows, num_kv_heads, num_entries, page_size);
+    BFA_REQUIRE(workspace && workspace_bytes >= fp.total() && aligned16(workspace), "%s: workspace too small", what);
+    BFA_REQUIRE(fp.npad * CAS_D * 2 < (int64_t{1} << 31) && fp.tiles < (int64_t{1} << 31) &&
+                    cdiv(rows, 64) < (int64_t{1} << 31) && fp.splits < 65536 && num_kv_heads < 65536,
+                "%s: too many keys for the flat form", what);
+    char* ws = static_cast<char*>(workspace);
+    if (fp.splits > 1) a.part = reinterpret_cast<float*>(ws);
+    FlatArgs f{};
+    f.kf = reinterpret_cast<uint16_t*>(ws + fp.part_bytes);
+    f.vt = reinterpret_cast<uint16_t*>(ws + fp.part_bytes + fp.kf_bytes);
+    f.kpos = reinterpret_cast<int32_t*>(ws + fp.part_bytes + fp.kf_bytes + fp.vt_bytes);
+    f.npad = fp.npad;
+    f.tiles_per_split = fp.tiles_per_split;
+    const hipStream_t s = as_stream(stream);
+    const dim3 pgrid(static_cast<unsigned>(fp.tiles), static_cast<unsigned>(num_kv_heads));
+    const dim3 grid(static_cast<unsigned>(cdiv(rows, 64)), static_cast<unsigned>(num_kv_heads),
+                    static_cast<unsigned>(fp.splits));
+    auto launch = [&](auto bf) {
+      constexpr bool B = decltype(bf)::value;
+      hipLaunchKernelGGL(cascade_flatten_kernel<B>, pgrid, dim3(256), 0, s, a, f);
+      hipLaunchKernelGGL(cascade_flat_kernel<B>, grid, dim3(256), 0, s, a, f);
+      if (fp.splits > 1) launch_merge<B>(a, rows, fp.splits, s);
     };
     if (dtype == BFA_DTYPE_BF16) launch(std::true_type{}); else launch(std::false_type{});
     return check_launch(what);

@@ -248,33 +248,6 @@ __device__ __forceinline__ void mfma_block(f32x16_t (&acc)[MB][NB], const uint4 
     for (int j = 0; j < NB; ++j) acc[i][j] = mfma32<BF16>(af[i], bf[j], acc[i][j]);
 }
 
-typedef __attribute__((address_space(3))) void lds_void_t;
-
-// LDS byte address of a __shared__ pointer, as a wave-uniform SGPR value.
-__device__ __forceinline__ uint32_t lds_addr(const void* p) {
-  return __builtin_amdgcn_readfirstlane(
-      static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const lds_void_t*)p)));
-}
-
-// Asynchronous 16-byte-per-lane copy global -> LDS (global_load_lds_dwordx4):
-// lane i's 16 bytes at base + voff land at LDS byte m0 + 16*i.  Issued as
-// inline assembly so the compiler does not serialise consecutive copies; the
-// caller waits (wait_vmem) and barriers before the LDS is read.
-__device__ __forceinline__ void dma16(const void* base, uint32_t voff, uint32_t m0) {
-  // the base is wave-uniform; readfirstlane lets the compiler see that when the
-  // pointer came through a path it cannot prove uniform (an SGPR operand).  The
-  // builtin returns a signed int: each half is taken back to uint32_t before it
-  // is widened, or a low half with bit 31 set would fill the high word with ones.
-  const uint64_t b = reinterpret_cast<uint64_t>(base);
-  const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(b)));
-  const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(b >> 32)));
-  const uint64_t bu = (static_cast<uint64_t>(hi) << 32) | lo;
-  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(__builtin_amdgcn_readfirstlane(m0)),
-               "v"(voff), "s"(reinterpret_cast<const void*>(bu))
-               : "memory");
-}
-
-__device__ __forceinline__ void wait_vmem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 // s_waitcnt vmcnt(N) for a compile-time N, other counters untouched
 // (gfx9 encoding: vmcnt[3:0], expcnt[6:4], lgkmcnt[11:8], vmcnt[5:4] in [15:14]).

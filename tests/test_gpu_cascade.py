@@ -86,15 +86,32 @@ def build_case(seed, hq, hkv, lengths, deltas, pages, ps=16, dtype=torch.bfloat1
     return chunks, kv, sum(lengths)
 
 
-@pytest.mark.parametrize("name,tokens,hq,hkv,lengths,deltas,causal,knorm", [
+CASES = [
     ("llama decode", 1, 32, 8, [100, 37, 516], [0, 4000, -77], True, False),
     ("llama decode batch", 4, 32, 8, [64, 300, 5], [0, 0, 12], True, False),
     ("qwen3 decode k-norm", 1, 16, 8, [200, 17, 1000], [0, -4096, 3000], True, True),
     ("qwen3 prefill chunk", 37, 16, 8, [48, 130, 64], [0, 77, -5], True, True),
     ("llama prefill", 300, 32, 8, [128, 700, 300], [0, 2048, 0], True, False),
     ("non-causal", 9, 16, 8, [33, 16, 1], [0, 5, 0], False, True),
-])
+]
+
+
+@pytest.mark.parametrize("name,tokens,hq,hkv,lengths,deltas,causal,knorm", CASES)
 def test_cascade_attention(name, tokens, hq, hkv, lengths, deltas, causal, knorm):
+    _check_case(name, tokens, hq, hkv, lengths, deltas, causal, knorm)
+
+
+@pytest.mark.parametrize("name,tokens,hq,hkv,lengths,deltas,causal,knorm",
+                         [c for c in CASES if c[1] * c[2] // c[3] > 4])
+def test_cascade_attention_flat_form(monkeypatch, name, tokens, hq, hkv, lengths, deltas, causal, knorm):
+    """The same oracle cases through the flat form (K rotated / normalised once
+    by a pre-pass, DMA'd tiles), which runs by itself only from 97 rows per kv
+    head: forced here for every case above 4 rows."""
+    monkeypatch.setenv("BFA_CASCADE_FLAT", "1")
+    _check_case(name, tokens, hq, hkv, lengths, deltas, causal, knorm)
+
+
+def _check_case(name, tokens, hq, hkv, lengths, deltas, causal, knorm):
     seed = zlib.crc32(name.encode()) % 1000
     g = gen(seed)
     d, ps, max_pos = 128, 16, 40960
@@ -147,7 +164,34 @@ def test_cascade_decode_form_page_sizes(ps, tokens, dtype):
     assert_close(out, exp, what=f"decode form ps={ps} t={tokens} {dtype}")
 
 
-def test_cascade_attention_fp16_query_before_keys_and_empty():
+@pytest.mark.parametrize("ps,dtype", [(8, torch.bfloat16), (32, torch.float16)])
+def test_cascade_flat_form_page_sizes(monkeypatch, ps, dtype):
+    """Flat form with pages of 8 (8 pages per 64-key tile) and 32 slots, a
+    partial last page and moved chunks, Qwen3 geometry with k_norm."""
+    monkeypatch.setenv("BFA_CASCADE_FLAT", "1")
+    g = gen(95 + ps)
+    hq, hkv, d, max_pos, tokens = 16, 8, 128, 40960, 8
+    chunks, kv, total = build_case(96 + ps, hq, hkv, [45, 130, 77], [0, 300, -41], pages=64, ps=ps, dtype=dtype)
+    rope = RotaryEmbedding(d, d, max_pos, 1e6).to(DEV)
+    att = CascadeAttention(hq, d, d ** -0.5, hkv, ps, rotary_emb=rope)
+    levels = att.create_cascade_levels(chunks)
+    q = randn(g, tokens, hq, d, dtype=dtype)
+    qpos = torch.arange(total - tokens + 1, total + 1)
+    kn_w = torch.exp(torch.empty(d).uniform_(math.log(0.05), math.log(100.0), generator=g)).to(dtype)
+    k_norm = RMSNorm(d, eps=1e-6).to(DEV)
+    with torch.no_grad():
+        k_norm.weight.data = kn_w.to(DEV)
+    out = att.forward(q.to(DEV), qpos.to(DEV), kv.to(DEV), levels, 0, k_norm=k_norm)
+    torch.cuda.synchronize()
+    braidinfer_amd.check_device_status()
+    exp = R.cascade_attention(q, qpos, kv, cpu_levels(levels), hq, hkv, d ** -0.5, ps,
+                              rope.cos_sin_cache.cpu(), kn_w, 1e-6, True)
+    assert_close(out, exp, what=f"flat form ps={ps} {dtype}")
+
+
+@pytest.mark.parametrize("flat", ["0", "1"])
+def test_cascade_attention_fp16_query_before_keys_and_empty(monkeypatch, flat):
+    monkeypatch.setenv("BFA_CASCADE_FLAT", flat)
     g = gen(70)
     hq, hkv, d, ps = 16, 8, 128, 16
     chunks, kv, total = build_case(71, hq, hkv, [20, 40], [0, 3], pages=20, dtype=torch.float16)
@@ -179,6 +223,45 @@ def test_cascade_attention_delta_out_of_table_raises():
     att.forward(q.to(DEV), torch.tensor([60, 61], device=DEV), kv.to(DEV), levels, 0)
     with pytest.raises(IndexError):
         braidinfer_amd.check_device_status()
+
+
+def test_cascade_flat_form_delta_out_of_table_raises(monkeypatch):
+    """The flat form's pre-pass reports a delta outside the rotary table the
+    same way."""
+    monkeypatch.setenv("BFA_CASCADE_FLAT", "1")
+    hq, hkv, d, ps = 16, 8, 128, 16
+    chunks, kv, total = build_case(76, hq, hkv, [20, 40], [0, -5000], pages=20)
+    rope = RotaryEmbedding(d, d, 4096, 1e6).to(DEV)
+    att = CascadeAttention(hq, d, d ** -0.5, hkv, ps, rotary_emb=rope)
+    levels = att.create_cascade_levels(chunks)
+    q = randn(gen(77), 8, hq, d)
+    braidinfer_amd.check_device_status()
+    att.forward(q.to(DEV), torch.arange(60, 68, device=DEV), kv.to(DEV), levels, 0)
+    with pytest.raises(IndexError):
+        braidinfer_amd.check_device_status()
+
+
+def test_cascade_flat_form_matches_fused_kernel(monkeypatch):
+    """The flat form (pre-pass + DMA'd tiles) and the fused kernel agree on a
+    256-query Qwen3 call with k_norm and moved chunks (the oracle check of both
+    is in test_cascade_attention)."""
+    g = gen(78)
+    hq, hkv, d, ps, max_pos = 16, 8, 128, 16, 40960
+    chunks, kv, total = build_case(79, hq, hkv, [300, 1000, 700], [0, 513, -2000], pages=200)
+    rope = RotaryEmbedding(d, d, max_pos, 1e6).to(DEV)
+    att = CascadeAttention(hq, d, d ** -0.5, hkv, ps, rotary_emb=rope)
+    levels = att.create_cascade_levels(chunks)
+    q = randn(g, 256, hq, d).to(DEV)
+    qpos = torch.arange(total - 255, total + 1, device=DEV)
+    k_norm = RMSNorm(d, eps=1e-6).to(DEV)
+    kv = kv.to(DEV)
+    monkeypatch.setenv("BFA_CASCADE_FLAT", "1")
+    flat = att.forward(q, qpos, kv, levels, 0, k_norm=k_norm).clone()
+    monkeypatch.setenv("BFA_CASCADE_FLAT", "0")
+    fused = att.forward(q, qpos, kv, levels, 0, k_norm=k_norm)
+    torch.cuda.synchronize()
+    braidinfer_amd.check_device_status()
+    assert_close(flat, fused, what="flat form vs fused kernel")
 
 
 def test_cascade_attention_graph_replays_match_eager():
