@@ -15,7 +15,8 @@ Two independent restatements:
                     pin oracle.torch_ref (a dropped term, wrong sign, wrong
                     index or transposed operand in either shows up as a
                     disagreement).
-Every function is pinned by tests/test_oracle.py (closed forms, invariants,
-the reference tests' own checks, brute force on tiny inputs, and the
-numpy-vs-torch cross check); see the table in DESIGN.md.
+Every function is pinned by tests/test_oracle.py and tests/test_golden.py
+(closed forms, invariants, the reference tests' own checks and fixtures, brute
+force on tiny inputs, and the numpy-vs-torch cross check).  No function is
+parity unpinned.
 """
