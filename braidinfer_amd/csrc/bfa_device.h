@@ -240,6 +240,41 @@ __device__ __forceinline__ float group16_max_dpp(float v) {
   return fmaxf(v, dpp_f32<0x140>(v));
 }
 
+// Reductions over lanes l, l ^ 16, l ^ 32, l ^ 48 with the gfx950 lane swaps.
+// v_permlane16_swap x, y exchanges the odd 16-lane rows of x with the even rows
+// of y; with x = y = v on entry, each lane ends up holding its own value in one
+// of x, y and its xor-16 partner's in the other (v_permlane32_swap: halves, xor
+// 32), so a commutative op on the pair gives every lane of the group the same
+// bits.  Written as inline assembly: given one value for both operands, the
+// compiler's model of the builtins takes the two results to be equal and drops
+// one of them.  The s_nop covers the VALU-write -> permlane-read wait states.
+__device__ __forceinline__ void swap16(uint32_t& x, uint32_t& y) {
+  asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1\n\ts_nop 1" : "+v"(x), "+v"(y));
+}
+__device__ __forceinline__ void swap32(uint32_t& x, uint32_t& y) {
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(x), "+v"(y));
+}
+__device__ __forceinline__ float lanes4_max(float v) {
+  uint32_t x = __builtin_bit_cast(uint32_t, v), y = x;
+  swap16(x, y);
+  v = fmaxf(__builtin_bit_cast(float, x), __builtin_bit_cast(float, y));
+  x = y = __builtin_bit_cast(uint32_t, v);
+  swap32(x, y);
+  return fmaxf(__builtin_bit_cast(float, x), __builtin_bit_cast(float, y));
+}
+__device__ __forceinline__ float lanes4_sum(float v) {
+  uint32_t x = __builtin_bit_cast(uint32_t, v), y = x;
+  swap16(x, y);
+  v = __builtin_bit_cast(float, x) + __builtin_bit_cast(float, y);
+  x = y = __builtin_bit_cast(uint32_t, v);
+  swap32(x, y);
+  return __builtin_bit_cast(float, x) + __builtin_bit_cast(float, y);
+}
+
+// Sum over all 64 lanes without LDS: DPP inside each 16-lane row, then the two
+// lane swaps; every lane gets the same bits.
+__device__ __forceinline__ float wave_sum_dpp(float v) { return lanes4_sum(group16_sum_dpp(v)); }
+
 // Device status word: kernels that detect out-of-range indices OR a bit into
 // it with an ordinary store (every writer stores the same value).
 __device__ __forceinline__ void flag_status(int* status, int bit) {

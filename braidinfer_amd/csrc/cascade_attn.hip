@@ -170,37 +170,6 @@ __device__ __forceinline__ uint32_t pack_pair(float lo, float hi) {
   return static_cast<uint32_t>(E::from_f32(lo)) | (static_cast<uint32_t>(E::from_f32(hi)) << 16);
 }
 
-// Reductions over lanes l, l ^ 16, l ^ 32, l ^ 48 with the gfx950 lane swaps.
-// v_permlane16_swap x, y exchanges the odd 16-lane rows of x with the even rows
-// of y; with x = y = v on entry, each lane ends up holding its own value in one
-// of x, y and its xor-16 partner's in the other (v_permlane32_swap: halves, xor
-// 32), so a commutative op on the pair gives every lane of the group the same
-// bits.  Written as inline assembly: given one value for both operands, the
-// compiler's model of the builtins takes the two results to be equal and drops
-// one of them.  The s_nop covers the VALU-write -> permlane-read wait states.
-__device__ __forceinline__ void swap16(uint32_t& x, uint32_t& y) {
-  asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1\n\ts_nop 1" : "+v"(x), "+v"(y));
-}
-__device__ __forceinline__ void swap32(uint32_t& x, uint32_t& y) {
-  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(x), "+v"(y));
-}
-__device__ __forceinline__ float lanes4_max(float v) {
-  uint32_t x = __builtin_bit_cast(uint32_t, v), y = x;
-  swap16(x, y);
-  v = fmaxf(__builtin_bit_cast(float, x), __builtin_bit_cast(float, y));
-  x = y = __builtin_bit_cast(uint32_t, v);
-  swap32(x, y);
-  return fmaxf(__builtin_bit_cast(float, x), __builtin_bit_cast(float, y));
-}
-__device__ __forceinline__ float lanes4_sum(float v) {
-  uint32_t x = __builtin_bit_cast(uint32_t, v), y = x;
-  swap16(x, y);
-  v = __builtin_bit_cast(float, x) + __builtin_bit_cast(float, y);
-  x = y = __builtin_bit_cast(uint32_t, v);
-  swap32(x, y);
-  return __builtin_bit_cast(float, x) + __builtin_bit_cast(float, y);
-}
-
 template <bool BF16>
 __global__ __launch_bounds__(256) void cascade_attn_kernel(CasArgs a) {
   using E = Elem<BF16 ? BFA_DTYPE_BF16 : BFA_DTYPE_F16>;

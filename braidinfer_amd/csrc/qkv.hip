@@ -877,6 +877,7 @@ struct DecodeArgs {
   const void* gamma;
   int gamma_dt, mixed;
   float eps;
+  int fold_rows;  // rows per wave of the fold: 0 (no fold), 1, 2 or 4
 };
 
 // Host-side description of the fold: the raw rows and the RMSNorm parameters.
@@ -885,6 +886,7 @@ struct OperandFold {
   int gamma_dt;
   bool mixed;
   float eps;
+  int rows_per_wave;
 };
 
 template <int DT>
@@ -917,15 +919,20 @@ __device__ __forceinline__ int wslot(int r, int g) { return r * 8 + (g ^ ((r >> 
 // KS dividing k / 64), fixed at compile time so the weight loads carry no
 // branches and each segment waits only for its own four loads.
 //
-// NORM (one to four tokens, x in the weight dtype, hidden <= 4096): the
-// operand pre-pass is folded in.  Wave w reads the whole of row w (eight
-// 16-byte chunks per lane at most) for its sum of squares and the row's K
-// slice with the matching gamma, all before the weight loads are issued, then
-// writes the normalised slice where the DMA would have put it.
-template <int MT, int KS, bool BF16, bool REG_ORDER, bool NORM = false>
+// NR > 0 (x in the weight dtype): the operand pre-pass is folded in.  Wave w
+// reads the whole of rows w, w + 4, .. (NR of them: 16-byte chunks, eight per
+// lane for one row up to hidden 4096, four per lane for two or four rows up to
+// 2048) for their sums of squares and the rows' K slices with the matching
+// gamma, all before the weight loads are issued, then writes the normalised
+// slices where the DMA would have put them.  The row sums run on DPP and the
+// lane swaps (no LDS round trips).
+template <int MT, int KS, bool BF16, bool REG_ORDER, int NR = 0>
 __global__ __launch_bounds__(256) void qkv_decode_kernel(DecodeArgs d) {
   static_assert(KS >= 1 && KS * 64 <= KC_MAX, "segments per split");
-  static_assert(!NORM || (MT == 1 && !REG_ORDER), "the fold covers one to four tokens");
+  constexpr bool NORM = NR > 0;
+  constexpr int CPL = NR == 1 ? 8 : 4;  // 16-byte chunks per lane per row of the fold
+  static_assert(NR == 0 || NR == 1 || NR == 2 || NR == 4, "fold rows per wave");
+  static_assert(!NORM || (MT == 1 && !REG_ORDER), "the fold covers up to 16 tokens");
   constexpr int GPR = KC_MAX / 8;      // 16-byte granules per LDS operand row (row pitch 1 KiB)
   __shared__ uint4 abuf[64 * GPR];     // 64 rows x KC_MAX bf16 = 64 KiB
   __shared__ uint4 wst[4][32 * 8];     // per wave: 32 weight rows x 64 bf16 = 4 KiB
@@ -938,16 +945,18 @@ __global__ __launch_bounds__(256) void qkv_decode_kernel(DecodeArgs d) {
   constexpr int gpr = KS * 8;  // granules per operand row actually used
 
   constexpr int DT = BF16 ? BFA_DTYPE_BF16 : BFA_DTYPE_F16;
-  uint4 sx[NORM ? 8 : 1], xs{};
+  uint4 sx[NORM ? NR : 1][CPL], xs[NORM ? NR : 1];
   float gv[8];
   if constexpr (NORM) {
-    const int64_t row = min<int64_t>(wid, d.m - 1);
-    const uint16_t* xr = d.a + row * d.lda;
     const int nch = static_cast<int>(d.k / 8);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) sx[j] = load16(xr + min(lane + 64 * j, nch - 1) * 8);
     const int64_t kk = k0 + min(lane, gpr - 1) * 8;
-    xs = load16(xr + kk);
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+      const uint16_t* xr = d.a + min<int64_t>(wid + 4 * r, d.m - 1) * d.lda;
+#pragma unroll
+      for (int j = 0; j < CPL; ++j) sx[r][j] = load16(xr + min(lane + 64 * j, nch - 1) * 8);
+      xs[r] = load16(xr + kk);
+    }
     if (d.gamma_dt == BFA_DTYPE_BF16) load8<BFA_DTYPE_BF16>(static_cast<const uint16_t*>(d.gamma) + kk, gv);
     else if (d.gamma_dt == BFA_DTYPE_F16) load8<BFA_DTYPE_F16>(static_cast<const uint16_t*>(d.gamma) + kk, gv);
     else load8<BFA_DTYPE_F32>(static_cast<const float*>(d.gamma) + kk, gv);
@@ -983,30 +992,39 @@ __global__ __launch_bounds__(256) void qkv_decode_kernel(DecodeArgs d) {
   }
   if constexpr (NORM) {
     // the fold's loads went out before the weights: using them waits for them only
-    float ss = 0.f;
     const int nch = static_cast<int>(d.k / 8);
+    float ss[NR];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      float v[8];
-      unpack8<DT>(sx[j], v);
-      if (lane + 64 * j < nch) {
+    for (int r = 0; r < NR; ++r) {
+      ss[r] = 0.f;
 #pragma unroll
-        for (int t = 0; t < 8; ++t) ss += v[t] * v[t];
+      for (int j = 0; j < CPL; ++j) {
+        float v[8];
+        unpack8<DT>(sx[r][j], v);
+        if (lane + 64 * j < nch) {
+#pragma unroll
+          for (int t = 0; t < 8; ++t) ss[r] += v[t] * v[t];
+        }
       }
     }
-    ss = group_sum<64>(ss);
-    const float inv = 1.0f / sqrtf(ss / static_cast<float>(d.k) + d.eps);
-    float v[8], o[8];
-    unpack8<DT>(xs, v);
 #pragma unroll
-    for (int t = 0; t < 8; ++t) o[t] = d.mixed ? round_bf16(v[t] * inv) * gv[t] : (v[t] * inv) * gv[t];
-    uint32_t pw[4];
+    for (int r = 0; r < NR; ++r) ss[r] = wave_sum_dpp(ss[r]);
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      pw[i] = static_cast<uint32_t>(Elem<DT>::from_f32(o[2 * i])) |
-              (static_cast<uint32_t>(Elem<DT>::from_f32(o[2 * i + 1])) << 16);
-    if (wid < d.m && lane < gpr)
-      abuf[wid * GPR + ((lane & ~15) | ((lane & 15) ^ (wid & 15)))] = make_uint4(pw[0], pw[1], pw[2], pw[3]);
+    for (int r = 0; r < NR; ++r) {
+      const float inv = 1.0f / sqrtf(ss[r] / static_cast<float>(d.k) + d.eps);
+      float v[8], o[8];
+      unpack8<DT>(xs[r], v);
+#pragma unroll
+      for (int t = 0; t < 8; ++t) o[t] = d.mixed ? round_bf16(v[t] * inv) * gv[t] : (v[t] * inv) * gv[t];
+      uint32_t pw[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        pw[i] = static_cast<uint32_t>(Elem<DT>::from_f32(o[2 * i])) |
+                (static_cast<uint32_t>(Elem<DT>::from_f32(o[2 * i + 1])) << 16);
+      const int row = wid + 4 * r;
+      if (row < d.m && lane < gpr)
+        abuf[row * GPR + ((lane & ~15) | ((lane & 15) ^ (row & 15)))] = make_uint4(pw[0], pw[1], pw[2], pw[3]);
+    }
   } else {
     // the operand DMAs were issued before the 4 * KS weight loads and loads
     // complete in order: vmcnt(4 KS) means the DMAs have landed
@@ -1681,23 +1699,27 @@ static void launch_decode_cpw(const QkvPlan& p, const SplitArgs& s, hipStream_t 
   }
 }
 
+template <int NR, bool BF16>
+static void launch_stream_fold(int ks, dim3 grid, const DecodeArgs& d, hipStream_t st) {
+  switch (ks) {
+    case 1: hipLaunchKernelGGL((qkv_decode_kernel<1, 1, BF16, false, NR>), grid, dim3(256), 0, st, d); break;
+    case 2: hipLaunchKernelGGL((qkv_decode_kernel<1, 2, BF16, false, NR>), grid, dim3(256), 0, st, d); break;
+    case 3: hipLaunchKernelGGL((qkv_decode_kernel<1, 3, BF16, false, NR>), grid, dim3(256), 0, st, d); break;
+    case 4: hipLaunchKernelGGL((qkv_decode_kernel<1, 4, BF16, false, NR>), grid, dim3(256), 0, st, d); break;
+    case 5: hipLaunchKernelGGL((qkv_decode_kernel<1, 5, BF16, false, NR>), grid, dim3(256), 0, st, d); break;
+    case 6: hipLaunchKernelGGL((qkv_decode_kernel<1, 6, BF16, false, NR>), grid, dim3(256), 0, st, d); break;
+    case 7: hipLaunchKernelGGL((qkv_decode_kernel<1, 7, BF16, false, NR>), grid, dim3(256), 0, st, d); break;
+    default: hipLaunchKernelGGL((qkv_decode_kernel<1, 8, BF16, false, NR>), grid, dim3(256), 0, st, d); break;
+  }
+}
+
 template <int MT, bool BF16>
 static void launch_stream(int ks, dim3 grid, const DecodeArgs& d, hipStream_t st) {
   constexpr bool RO = MT > 1;  // register-order partials from two 16-token blocks up
   if constexpr (MT == 1) {
-    if (d.gamma) {
-      switch (ks) {
-        case 1: hipLaunchKernelGGL((qkv_decode_kernel<1, 1, BF16, false, true>), grid, dim3(256), 0, st, d); break;
-        case 2: hipLaunchKernelGGL((qkv_decode_kernel<1, 2, BF16, false, true>), grid, dim3(256), 0, st, d); break;
-        case 3: hipLaunchKernelGGL((qkv_decode_kernel<1, 3, BF16, false, true>), grid, dim3(256), 0, st, d); break;
-        case 4: hipLaunchKernelGGL((qkv_decode_kernel<1, 4, BF16, false, true>), grid, dim3(256), 0, st, d); break;
-        case 5: hipLaunchKernelGGL((qkv_decode_kernel<1, 5, BF16, false, true>), grid, dim3(256), 0, st, d); break;
-        case 6: hipLaunchKernelGGL((qkv_decode_kernel<1, 6, BF16, false, true>), grid, dim3(256), 0, st, d); break;
-        case 7: hipLaunchKernelGGL((qkv_decode_kernel<1, 7, BF16, false, true>), grid, dim3(256), 0, st, d); break;
-        default: hipLaunchKernelGGL((qkv_decode_kernel<1, 8, BF16, false, true>), grid, dim3(256), 0, st, d); break;
-      }
-      return;
-    }
+    if (d.fold_rows == 1) { launch_stream_fold<1, BF16>(ks, grid, d, st); return; }
+    if (d.fold_rows == 2) { launch_stream_fold<2, BF16>(ks, grid, d, st); return; }
+    if (d.fold_rows == 4) { launch_stream_fold<4, BF16>(ks, grid, d, st); return; }
   }
   switch (ks) {
     case 1: hipLaunchKernelGGL((qkv_decode_kernel<MT, 1, BF16, RO>), grid, dim3(256), 0, st, d); break;
@@ -1720,6 +1742,7 @@ static void launch_decode(const QkvPlan& p, const SplitArgs& s, hipStream_t st,
     d.part = s.part;
     if (fold) {
       d.gamma = fold->gamma; d.gamma_dt = fold->gamma_dt; d.mixed = fold->mixed ? 1 : 0; d.eps = fold->eps;
+      d.fold_rows = fold->rows_per_wave;
     }
     const dim3 grid(static_cast<unsigned>(cdiv(s.n, 128)), static_cast<unsigned>(p.splits));
     if (p.nch > 0) {
@@ -1978,17 +2001,22 @@ extern "C" int bfa_fused_rmsnorm_qkv(const void* x, int x_dtype, int64_t tokens,
               "%s: workspace too small (%lld < %lld bytes)", what, (long long)workspace_bytes,
               (long long)(p.operand_bytes + p.part_bytes));
   char* ws = static_cast<char*>(workspace);
-  // One to four decode tokens whose x is already in the weight dtype: the
-  // weight-streaming kernel normalises its own K slice, one launch fewer.
-  // BFA_NO_OPERAND_FOLD=1 keeps the pre-pass (for measurements).
+  // Up to 16 decode tokens whose x is already in the weight dtype: the
+  // weight-streaming kernel normalises its own K slice, one launch fewer.  One
+  // row per wave up to 4 tokens (hidden <= 4096), two up to 8 (hidden <= 2048),
+  // four up to 16 (hidden <= 1024); beyond that the reads of the rows cost more
+  // than the launch (TinyLlama, 16 tokens: 11.2 against 10.1 us with the
+  // pre-pass).  BFA_NO_OPERAND_FOLD=1 keeps the pre-pass (for measurements).
   const char* nf = getenv("BFA_NO_OPERAND_FOLD");
   const bool no_fold = nf && atoi(nf) != 0;
-  const bool fold = !no_fold && p.decode && p.stream && tokens <= 4 && x_dtype == w_dtype &&
+  const int fold_rows = (tokens <= 4 && hidden <= 4096) ? 1
+                        : (tokens <= 8 && hidden <= 2048) ? 2
+                        : (tokens <= 16 && hidden <= 1024) ? 4 : 0;
+  const bool fold = !no_fold && fold_rows > 0 && p.decode && p.stream && p.mt == 1 && x_dtype == w_dtype &&
                     (w_dtype == BFA_DTYPE_BF16 || w_dtype == BFA_DTYPE_F16) && hidden % 8 == 0 &&
-                    hidden <= 4096 && x_stride % 8 == 0 && aligned16(x) && aligned16(norm_weight) &&
-                    is_float_dtype(nw_dtype);
+                    x_stride % 8 == 0 && aligned16(x) && aligned16(norm_weight) && is_float_dtype(nw_dtype);
   if (fold) {
-    const OperandFold f{norm_weight, nw_dtype, mixed_rounding != 0, eps};
+    const OperandFold f{norm_weight, nw_dtype, mixed_rounding != 0, eps, fold_rows};
     return qkv_projection_impl(x, x_stride, &f, tokens, hidden, qkv_weight, w_dtype, qkv_dim, w_stride,
                                bias, bias_dtype, num_q_heads, num_kv_heads, qkv_dtype, q_norm_weight,
                                k_norm_weight, qk_norm_dtype, qk_eps, qk_norm_out_dtype, positions,

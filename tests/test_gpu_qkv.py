@@ -109,12 +109,17 @@ def test_decode_split_depths(t, heads, h):
     (3, 4096, torch.bfloat16, True),    # rows 4160 elements apart
     (4, 1024, torch.float16, False),    # largest folded batch, fp16
     (2, 64, torch.bfloat16, False),     # one 64-deep segment, a partial chunk row
+    (8, 2048, torch.bfloat16, False),   # two rows per wave: TinyLlama batch 8
+    (6, 1024, torch.float16, True),     # two rows per wave, the second row of waves 2-3 absent
+    (16, 1024, torch.bfloat16, False),  # four rows per wave: Qwen3 batch 16
+    (13, 1024, torch.float16, True),    # four rows per wave, ragged last row group
 ])
 def test_decode_operand_fold(t, h, dtype, strided):
-    """One to four decode tokens with x in the weight dtype: the weight-streaming
+    """Up to 16 decode tokens with x in the weight dtype: the weight-streaming
     kernel computes the row statistics and normalises its own K slice (no
-    pre-pass launch).  Mixed and production rounding, with the RMSNorm weight in
-    the input dtype and in fp32."""
+    pre-pass launch; one row per wave up to 4 tokens, two up to 8, four up to
+    16).  Mixed and production rounding, with the RMSNorm weight in the input
+    dtype and in fp32."""
     hq, hkv, d = 6, 1, 64
     g, x, ln, w, _ = make(211, t, h, hq, hkv, d, dtype=dtype)
     xd = x.to(DEV)
