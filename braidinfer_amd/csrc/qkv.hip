@@ -1361,7 +1361,7 @@ __device__ __forceinline__ void decode_epilogue_item(const float4* part, int64_t
   int dt = e.qkv_dt;
   if (kd != 2 && (e.qn_w || e.kn_w)) {
 #pragma unroll
-    for (int v = 0; v < 4; ++v) ss[v] = group_sum<kWave>(ss[v]);
+    for (int v = 0; v < 4; ++v) ss[v] = wave_sum_dpp(ss[v]);
     if (nw) {
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
@@ -1536,7 +1536,7 @@ __device__ __forceinline__ void row_epilogue_item(const float* part, int64_t spl
   }
   const void* nw = kd == 0 ? e.qn_w : (kd == 1 ? e.kn_w : nullptr);
   if (kd != 2 && (e.qn_w || e.kn_w)) {
-    ss = group_sum<kWave>(ss);
+    ss = wave_sum_dpp(ss);
     if (nw) {
       const float r = 1.0f / sqrtf(ss / static_cast<float>(e.hd) + e.qk_eps);
 #pragma unroll
