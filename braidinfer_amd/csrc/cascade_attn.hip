@@ -767,8 +767,7 @@ __global__ __launch_bounds__(256) void cascade_merge_kernel(CasArgs a, int64_t s
   const float* base = a.part + (g * rows + r) * (CAS_D + 2);
   float mx = -INFINITY;
   for (int64_t z = lane; z < splits; z += 64) mx = fmaxf(mx, base[z * zstride]);
-#pragma unroll
-  for (int d = 32; d >= 1; d >>= 1) mx = fmaxf(mx, __shfl_xor(mx, d, kWave));
+  mx = lanes4_max(group16_max_dpp(mx));  // DPP and lane swaps, no LDS round trips
   float lsum = 0.f, o0 = 0.f, o1 = 0.f;
   // this wave's splits: z = wid + 4 k; lane k holds the weight of the k-th
   for (int64_t k0 = 0; 4 * k0 + wid < splits; k0 += 64) {
@@ -785,7 +784,8 @@ __global__ __launch_bounds__(256) void cascade_merge_kernel(CasArgs a, int64_t s
     for (int j0 = 0; j0 < nk8; j0 += 8) {
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
-        const float wj = __shfl(w, j0 + u, kWave);
+        // lane j0 + u's weight, read out as a scalar (the index is wave-uniform)
+        const float wj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), j0 + u));
         const int64_t zj = min<int64_t>(4 * (k0 + j0 + u) + wid, splits - 1);
         const float* pr = base + zj * zstride + 2;
         o0 += wj * pr[lane];
