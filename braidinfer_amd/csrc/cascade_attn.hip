@@ -485,10 +485,11 @@ __global__ __launch_bounds__(256) void cascade_flatten_kernel(CasArgs a, FlatArg
   const int tid = threadIdx.x;
   const int64_t g = blockIdx.y;  // kv head
   const int64_t t0 = static_cast<int64_t>(blockIdx.x) * CAS_FT;
+  const bool vrole = blockIdx.z == 1;  // z = 0: K (and the positions), z = 1: V^T
   const int sk = tid >> 3, sc = tid & 7;  // key row (and row + 32), column chunk
   float kg1[8] = {1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f};
   float kg2[8] = {1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f};
-  if (a.knorm_w) {
+  if (a.knorm_w && !vrole) {
     const char* w = static_cast<const char*>(a.knorm_w);
     if (a.knorm_dt == BFA_DTYPE_F32) {
       load8<BFA_DTYPE_F32>(w + 4 * (8 * sc), kg1);
@@ -535,12 +536,22 @@ __global__ __launch_bounds__(256) void cascade_flatten_kernel(CasArgs a, FlatArg
     }
     const uint16_t* zero = reinterpret_cast<const uint16_t*>(cas_zero_row);
     const uint16_t* krow = valid ? a.cache + page * a.c_sp + g * a.c_sh + s * a.c_ss : zero;
-    const uint16_t* vrow = valid ? krow + a.c_skv : zero;
-    float x1[8], x2[8], v1[8], v2[8];
+    if (vrole) {  // V row -> LDS, transposed in the PV order
+      const uint16_t* vrow = valid ? krow + a.c_skv : zero;
+      float v1[8], v2[8];
+      load8<DT>(vrow + 8 * sc, v1);
+      load8<DT>(vrow + CAS_D / 2 + 8 * sc, v2);
+      const int kc = pv_order(kk);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        vs[(8 * sc + i) * CAS_FVP + kc] = E::from_f32(v1[i]);
+        vs[(CAS_D / 2 + 8 * sc + i) * CAS_FVP + kc] = E::from_f32(v2[i]);
+      }
+      continue;
+    }
+    float x1[8], x2[8];
     load8<DT>(krow + 8 * sc, x1);
     load8<DT>(krow + CAS_D / 2 + 8 * sc, x2);
-    load8<DT>(vrow + 8 * sc, v1);
-    load8<DT>(vrow + CAS_D / 2 + 8 * sc, v2);
     if (rot) {
       float cs[8], sn[8];
       load8<BFA_DTYPE_F32>(a.cs + dpos * CAS_D + 8 * sc, cs);
@@ -567,14 +578,9 @@ __global__ __launch_bounds__(256) void cascade_flatten_kernel(CasArgs a, FlatArg
     uint16_t* kd = f.kf + (g * f.npad + slot) * CAS_D;
     store8<DT>(kd + 8 * sc, x1);
     store8<DT>(kd + CAS_D / 2 + 8 * sc, x2);
-    const int kc = pv_order(kk);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      vs[(8 * sc + i) * CAS_FVP + kc] = E::from_f32(v1[i]);
-      vs[(CAS_D / 2 + 8 * sc + i) * CAS_FVP + kc] = E::from_f32(v2[i]);
-    }
     if (g == 0 && sc == 0) f.kpos[slot] = valid ? static_cast<int32_t>(kp) : INT32_MAX;
   }
+  if (!vrole) return;  // uniform over the workgroup
   __syncthreads();
   // V^T tile out: 128 head-dim rows of 64 keys, 16-byte granules
 #pragma unroll
@@ -1304,7 +1310,7 @@ extern "C" int bfa_cascade_attention(
     f.npad = fp.npad;
     f.tiles_per_split = fp.tiles_per_split;
     const hipStream_t s = as_stream(stream);
-    const dim3 pgrid(static_cast<unsigned>(fp.tiles), static_cast<unsigned>(num_kv_heads));
+    const dim3 pgrid(static_cast<unsigned>(fp.tiles), static_cast<unsigned>(num_kv_heads), 2);
     const dim3 grid(static_cast<unsigned>(cdiv(rows, 64)), static_cast<unsigned>(num_kv_heads),
                     static_cast<unsigned>(fp.splits));
     auto launch = [&](auto bf) {
