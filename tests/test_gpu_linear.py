@@ -75,6 +75,18 @@ def test_linear_add_residual(shape):
     assert torch.equal(layer.forward_add_residual(x.to(DEV), r.to(DEV)), got)
 
 
+@pytest.mark.parametrize("splits,t", [("4", 64), ("1", 48), ("2", 20), ("3", 33)])
+def test_deep_k_chunk_counts(monkeypatch, splits, t):
+    """The deep-K decode form with the split count forced (K = 3072: 12 chunks of
+    256): 3, 12, 6 and 4 chunks per split, two to four 16-token blocks, against
+    the oracle."""
+    monkeypatch.setenv("BFA_DECODE_SPLITS", splits)
+    g = gen(900 + t)
+    k, n = 3072, 2048
+    x, w, b = randn(g, t, k), randn(g, n, k, std=0.03), randn(g, n, std=0.5)
+    assert_close(linear(x.to(DEV), w.to(DEV), b.to(DEV)), R.linear(x, w, b), what=f"deep-K splits={splits} t={t}")
+
+
 @pytest.mark.parametrize("shape", [(1, 1024, 3072), (16, 2048, 5632), (64, 4096, 1000), (64, 4096, 14336),
                                    (65, 1024, 3072), (500, 2048, 1000), (2048, 4096, 3584),
                                    (96, 1040, 512)], ids=_ids)
