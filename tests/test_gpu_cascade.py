@@ -6,7 +6,11 @@ online_softmax_update: fp32 state within 1e-5, the reference test's bound
 (tests/test_online_softmax_kernel.py:95-103).  Cascade attention: the output
 within |d| <= 2e-2 + 1e-2 |r| (tests/helpers.py); the kernel computes scores in
 fp32 from bf16 q and k like the reference, and rounds the softmax weights to
-bf16 for the P.V matrix product (a relative error of at most 2^-9 per weight)."""
+bf16 for the P.V matrix product (a relative error of at most 2^-9 per weight).
+Three kernel forms serve a call: the decode form (up to 4 query rows per kv
+head), the fused kernel, and from 97 rows the flat form (K rotated and
+normalised once by a pre-pass, DMA'd tiles); the oracle cases run through the
+fused kernel and, forced by BFA_CASCADE_FLAT=1, through the flat form."""
 from __future__ import annotations
 
 import math
