@@ -13,7 +13,8 @@ and ``_create_level`` restate the reference's host-side level construction
 from __future__ import annotations
 
 import weakref
-from dataclasses import dataclass
+from collections import OrderedDict
+from dataclasses import dataclass, field
 from typing import List
 
 import numpy as np
@@ -30,6 +31,34 @@ class CascadeLevel:
     kv_page_indptr: torch.Tensor   # [num_chunks + 1] int32
     kv_last_page_len: torch.Tensor  # [num_chunks] int32
     position_offset: int
+    # host copies of the three tensors, with a stamp of the tensors they were
+    # taken from (written by _create_level, or by the first forward that reads
+    # the tensors); a stale stamp makes the next forward read the tensors again
+    host_arrays: object = field(default=None, repr=False, compare=False)
+
+
+def _stamp(level: CascadeLevel):
+    """Identity of a level's three tensors: the objects, their storage and their
+    version counters (an in-place write moves the counter, an assignment of
+    another tensor changes the object)."""
+    ts = (level.kv_page_indices, level.kv_page_indptr, level.kv_last_page_len)
+    return tuple((weakref.ref(t), t.data_ptr(), t._version) for t in ts), ts
+
+
+def _stamp_matches(stamp, ts) -> bool:
+    return all(r() is t and p == t.data_ptr() and v == t._version for (r, p, v), t in zip(stamp, ts))
+
+
+def _level_arrays(level: CascadeLevel):
+    """(page indices, indptr, last page lengths) of a level as int64 numpy
+    arrays, read from the device only when the host copy is missing or stale."""
+    ts = (level.kv_page_indices, level.kv_page_indptr, level.kv_last_page_len)
+    host = level.host_arrays
+    if host is not None and _stamp_matches(host[3], ts):
+        return host[:3]
+    arrs = tuple(t.reshape(-1).cpu().numpy().astype(np.int64) for t in ts)
+    level.host_arrays = arrs + (_stamp(level)[0],)
+    return arrs
 
 
 class CascadeAttention:
@@ -44,7 +73,22 @@ class CascadeAttention:
         self.page_size = page_size
         self.heads_per_kv = num_heads // num_kv_heads
         self.rotary_emb = rotary_emb
-        self._plans: dict = {}
+
+    # Device plans shared by every CascadeAttention of the process, keyed by
+    # content (device, page size, the levels' page arrays, the chunk metadata):
+    # each layer of a forward pass builds its own levels from the same chunks,
+    # and all of them find the first layer's plan.  Plans used while a HIP
+    # graph is being captured are pinned (never evicted), since the graph reads
+    # them on every replay; release_pinned_plans() drops them.
+    _plans: "OrderedDict" = OrderedDict()
+    _pinned: dict = {}
+    _MAX_PLANS = 64
+
+    @classmethod
+    def release_pinned_plans(cls) -> None:
+        """Forgets the plans pinned by graph captures (call once the graphs that
+        captured cascade attention are destroyed)."""
+        cls._pinned.clear()
 
     def forward(self, query: torch.Tensor, query_positions: torch.Tensor, kv_cache: torch.Tensor,
                 cascade_levels: List[CascadeLevel], layer_idx: int, causal_mask: bool = True,
@@ -60,9 +104,14 @@ class CascadeAttention:
                 raise ValueError(f"Query size {query.shape[0]} not divisible by num_heads*head_dim={hd}")
             query = query.view(query.shape[0] // hd, self.num_heads, self.head_dim)
         elif query.dim() == 2:
+            if query.shape[1] != hd:
+                raise ValueError(f"query rows have {query.shape[1]} elements, num_heads*head_dim={hd}")
             query = query.view(query.shape[0], self.num_heads, self.head_dim)
         elif query.dim() != 3:
             raise ValueError(f"Unexpected query shape: {query.shape}")
+        elif tuple(query.shape[1:]) != (self.num_heads, self.head_dim):
+            raise ValueError(f"query of shape {tuple(query.shape)} does not match "
+                             f"[tokens, {self.num_heads}, {self.head_dim}]")
         tokens = query.shape[0]
         if query.stride(-1) != 1 or query.stride(1) % 8 or query.stride(0) % 8 or query.data_ptr() % 16:
             query = query.contiguous()
@@ -148,28 +197,42 @@ class CascadeAttention:
         and tokens | rotate << 16 (int32).  Each chunk's pages are
         kv_page_indices[indptr[c]:indptr[c+1]], its last page holds
         kv_last_page_len[c] tokens and the others page_size (:124-137); pages with
-        no tokens are dropped.  Built once per (levels, chunk metadata) and reused:
-        every layer of a forward pass attends the same levels, and a reused plan
-        makes no host-device copy, so the call can be captured in a HIP graph after
-        one eager call.  A level tensor written in place (its version counter moves)
-        or a different chunk metadata gives a new plan."""
-        # the level tensors' version counters change on every in-place write, so
-        # a page table edited in place is planned again (no device read needed)
-        key = (tuple((id(lv), lv.kv_page_indices._version, lv.kv_page_indptr._version,
-                      lv.kv_last_page_len._version) for lv in cascade_levels), tuple(meta))
-        hit = self._plans.get(key)
-        if hit is not None and all(r() is lv for r, lv in zip(hit[0], cascade_levels)):
-            return hit[1]
+        no tokens are dropped.  The level arrays come from their host copies
+        (no device read when _create_level built the level or an earlier call
+        read it), and the device arrays are shared by content across layers and
+        instances, so only the first layer of a forward pass copies to the
+        device, and a call with a cached plan can be captured in a HIP graph."""
+        ps = self.page_size
+        arrays = [_level_arrays(lv) if lv.chunks else None for lv in cascade_levels]
+        key = (str(dev), ps, tuple(meta),
+               tuple(None if a is None else (a[0].tobytes(), a[1].tobytes(), a[2].tobytes()) for a in arrays))
+        cls = type(self)
+        plan = cls._pinned.get(key)
+        if plan is None:
+            plan = cls._plans.get(key)
+            if plan is not None:
+                cls._plans.move_to_end(key)
+        if plan is None:
+            plan = self._build_plan(cascade_levels, arrays, meta, dev)
+            cls._plans[key] = plan
+            while len(cls._plans) > cls._MAX_PLANS:
+                cls._plans.popitem(last=False)
+        if dev.type == "cuda" and torch.cuda.is_current_stream_capturing():
+            cls._pinned[key] = plan
+        return plan
+
+    def _build_plan(self, cascade_levels, arrays, meta, dev):
         ps = self.page_size
         pages, kstart, delta, info = [], [], [], []
         ci = 0
-        for level in cascade_levels:
+        for level, arrs in zip(cascade_levels, arrays):
             n = len(level.chunks)
             if n == 0:
                 continue
-            idx = level.kv_page_indices.reshape(-1).cpu().numpy().astype(np.int64)
-            ptr = level.kv_page_indptr.reshape(-1).cpu().numpy().astype(np.int64)
-            last = level.kv_last_page_len.reshape(-1).cpu().numpy().astype(np.int64)
+            idx, ptr, last = arrs
+            if ptr.shape[0] < n + 1 or last.shape[0] < n:
+                raise ValueError(f"level with {n} chunks has {ptr.shape[0]} indptr entries and "
+                                 f"{last.shape[0]} last-page lengths")
             for c in range(n):
                 dlt, cum, flags = meta[ci + c]
                 if not flags & 1:
@@ -188,20 +251,13 @@ class CascadeAttention:
                 delta.append(np.full(int(keep.sum()), dlt, dtype=np.int64))
                 info.append(tok[keep] | ((flags >> 1) & 1) << 16)
             ci += n
-        if pages:
+        if pages and sum(p.shape[0] for p in pages):
             cat = np.concatenate
-            plan = (torch.from_numpy(cat(pages).astype(np.int32)).to(dev),
+            return (torch.from_numpy(cat(pages).astype(np.int32)).to(dev),
                     torch.from_numpy(cat(kstart)).to(dev),
                     torch.from_numpy(cat(delta)).to(dev),
                     torch.from_numpy(cat(info).astype(np.int32)).to(dev))
-            if plan[0].numel() == 0:
-                plan = (None,) * 4
-        else:
-            plan = (None,) * 4
-        if len(self._plans) >= 16:
-            self._plans.pop(next(iter(self._plans)))
-        self._plans[key] = ([weakref.ref(lv) for lv in cascade_levels], plan)
-        return plan
+        return (None,) * 4
 
     def create_cascade_levels(self, chunks, page_manager=None) -> List[CascadeLevel]:
         """Two levels: system-prompt chunks, then every other chunk
@@ -237,10 +293,14 @@ class CascadeAttention:
                 page_indptr.append(len(all_page_indices))
                 last_page_lens.append(0)
         dev = torch.device("cuda", torch.cuda.current_device())
-        return CascadeLevel(
+        level = CascadeLevel(
             chunks=chunks,
             kv_page_indices=torch.tensor(all_page_indices, dtype=torch.int32, device=dev),
             kv_page_indptr=torch.tensor(page_indptr, dtype=torch.int32, device=dev),
             kv_last_page_len=torch.tensor(last_page_lens, dtype=torch.int32, device=dev),
             position_offset=position_offset,
         )
+        # the host lists are at hand: keep them so forward reads nothing back
+        level.host_arrays = (np.asarray(all_page_indices, dtype=np.int64), np.asarray(page_indptr, dtype=np.int64),
+                             np.asarray(last_page_lens, dtype=np.int64), _stamp(level)[0])
+        return level

@@ -1,6 +1,7 @@
 """Host-side logic of the Python mirror that runs without a GPU."""
 from __future__ import annotations
 
+import pytest
 import torch
 
 from braidinfer_amd.kernels.fused_rmsnorm_qkv_with_bias import sanitize_bias
@@ -85,3 +86,61 @@ def test_cascade_plan_follows_in_place_page_table_edits():
     levels[0].kv_page_indices[1] = 9  # in place, as a page manager might
     page2, _, _, _ = att._plan(levels, att._chunk_meta(levels), dev)
     assert page2.tolist() == [5, 9]
+
+
+def test_cascade_plan_follows_reassigned_tensors_and_page_size():
+    """A level tensor replaced by another object (whose version counter starts
+    at 0 again) and a page_size changed on the instance both give a new plan."""
+    from types import SimpleNamespace as NS
+    from braidinfer_amd.layers import CascadeAttention
+
+    a = NS(page_table=[5, 6], kv_length=7, cached_position_start=0, global_position_start=0)
+    levels = [_level([a], [5, 6], [0, 2], [3])]
+    att = CascadeAttention(4, 128, 1.0, 2, page_size=4)
+    dev = torch.device("cpu")
+    assert att._plan(levels, att._chunk_meta(levels), dev)[0].tolist() == [5, 6]
+    levels[0].kv_page_indices = torch.tensor([7, 8], dtype=torch.int32)
+    assert att._plan(levels, att._chunk_meta(levels), dev)[0].tolist() == [7, 8]
+    # page_size 8: the first page now holds 8 tokens, the second starts at key 8
+    att.page_size = 8
+    _, kstart, _, info = att._plan(levels, att._chunk_meta(levels), dev)
+    assert kstart.tolist() == [0, 8] and info.tolist() == [8, 3]
+
+
+def test_cascade_plan_is_shared_across_layers_without_device_reads():
+    """Every layer builds its own levels from the same chunks (the reference's
+    Attention.forward calls create_cascade_levels per layer): the second layer
+    gets the first layer's device arrays, and levels built by _create_level
+    carry host copies, so planning reads nothing back from the device."""
+    from types import SimpleNamespace as NS
+    from braidinfer_amd.layers import CascadeAttention
+    from braidinfer_amd.layers.cascade_attention import _level_arrays
+
+    a = NS(page_table=[3, 4], kv_length=20, cached_position_start=0, global_position_start=0)
+    l1 = [_level([a], [3, 4], [0, 2], [4])]
+    l2 = [_level([a], [3, 4], [0, 2], [4])]
+    att1 = CascadeAttention(4, 128, 1.0, 2, page_size=16)
+    att2 = CascadeAttention(4, 128, 1.0, 2, page_size=16)
+    dev = torch.device("cpu")
+    p1 = att1._plan(l1, att1._chunk_meta(l1), dev)
+    p2 = att2._plan(l2, att2._chunk_meta(l2), dev)
+    assert p1[0] is p2[0]
+    # a level with fresh host copies is not read from its tensors
+    lv = _level([a], [3, 4], [0, 2], [4])
+    _level_arrays(lv)
+    poisoned = lv.host_arrays
+    lv.host_arrays = (poisoned[0] + 100,) + poisoned[1:]
+    assert _level_arrays(lv)[0].tolist() == [103, 104]
+    lv.kv_page_indices[0] = 5  # stale copy: read again
+    assert _level_arrays(lv)[0].tolist() == [5, 4]
+
+
+def test_cascade_query_shape_is_checked_before_launch():
+    from braidinfer_amd.layers import CascadeAttention
+
+    att = CascadeAttention(4, 128, 1.0, 2, page_size=16)
+    cache = torch.zeros(2, 2, 2, 16, 128, dtype=torch.bfloat16)
+    pos = torch.zeros(3, dtype=torch.int64)
+    for bad in (torch.zeros(3, 2, 128), torch.zeros(3, 4, 64), torch.zeros(3, 4 * 128 - 8)):
+        with pytest.raises(ValueError):
+            att.forward(bad.bfloat16(), pos, cache, [], 0)
