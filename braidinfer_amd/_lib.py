@@ -31,6 +31,7 @@ _DTYPE_CODE = {
 STATUS_INDEX_OOB = 1
 STATUS_APPEND_SKIPPED = 2
 LINEAR_PLAIN, LINEAR_SILU_AND_MUL = 0, 1
+NOALLOC_SCRATCH_BYTES = 16 << 20  # BFA_NOALLOC_SCRATCH_BYTES
 
 _P = c_void_p
 # name -> (restype, argtypes); mirrors include/braidinfer_amd.h
@@ -62,6 +63,10 @@ _SIGNATURES = {
                                       c_int64, c_int64, c_int, _P, _P, c_int, c_float, c_int,
                                       _P, c_int, _P, c_int64, _P, c_int, c_int64, _P,
                                       c_int64, _P, _P]),
+    "bfa_fused_rmsnorm_qkv_noalloc": (c_int, [_P, c_int, c_int64, c_int64, c_int64, _P, c_int,
+                                              c_float, c_int, _P, c_int, c_int64, c_int64, _P, c_int,
+                                              c_int64, c_int64, c_int, _P, _P, c_int, c_float, c_int,
+                                              _P, c_int, _P, c_int64, _P, c_int, c_int64, _P, _P]),
     "bfa_rmsnorm_qkv_operand": (c_int, [_P, c_int, c_int64, c_int64, c_int64, _P, c_int,
                                         c_int, _P, c_int, c_float, _P]),
     "bfa_qkv_projection": (c_int, [_P, c_int64, c_int64, _P, c_int, c_int64, c_int64, _P,

@@ -32,6 +32,7 @@
 //    read the raw fp32 projection for head_dim the GEMM epilogue does not cover)
 //    and apply bias / q-k norm / RoPE / rounding per (token, head) row.
 #include <cstdlib>
+#include <mutex>
 
 #include "bfa_device.h"
 #include "bfa_host.h"
@@ -2032,6 +2033,88 @@ extern "C" int bfa_fused_rmsnorm_qkv(const void* x, int x_dtype, int64_t tokens,
                             positions_dtype, cos_sin_cache, max_position, out, out_dtype,
                             out_stride, ws + p.operand_bytes, workspace_bytes - p.operand_bytes,
                             status, stream);
+}
+
+// ------------------------------------------------ allocation-free variant
+// bfa_fused_rmsnorm_qkv_noalloc runs bfa_fused_rmsnorm_qkv with its workspace
+// in `scratch`, a file-scope device array of BFA_NOALLOC_SCRATCH_BYTES: each GPU
+// the library runs on holds its own copy until the process ends.  On the host
+// the array's name denotes a shadow variable, not device memory, so host code
+// never passes it to a kernel or a copy: it uses the device address that
+// hipGetSymbolAddress returns for the device, looked up once per device (with
+// that device current) and kept in noalloc_scratch_addr.  Nothing in the QKV
+// kernels needs the workspace zeroed (the operand pre-pass writes every
+// operand row and every split writes its whole partial tile before a later
+// kernel reads it), so the array is never cleared; it keeps the last call's
+// contents.  Calls that overlap on one GPU (several streams, or several host
+// threads) share the array and race.
+static __device__ __align__(256) unsigned char scratch[BFA_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_addr[kMaxScratchDevices] = {};
+}  // namespace
+
+// Device address of `scratch` on the device that runs `stream` (the current
+// device for the null stream).
+static int noalloc_scratch_addr(void* stream, void** addr) {
+  int dev = -1;
+  hipError_t e = stream ? hipStreamGetDevice(as_stream(stream), &dev) : hipGetDevice(&dev);
+  if (e != hipSuccess) return set_error(BFA_ERR_LAUNCH, "bfa_fused_rmsnorm_qkv_noalloc: no device: %s",
+                                        hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxScratchDevices)
+    return set_error(BFA_ERR_UNSUPPORTED, "bfa_fused_rmsnorm_qkv_noalloc: device %d beyond %d", dev,
+                     kMaxScratchDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_addr[dev]) {
+    int cur = -1;
+    e = hipGetDevice(&cur);
+    if (e == hipSuccess && cur != dev) e = hipSetDevice(dev);
+    void* p = nullptr;
+    if (e == hipSuccess) e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (cur >= 0 && cur != dev) {
+      const hipError_t back = hipSetDevice(cur);
+      if (e == hipSuccess) e = back;
+    }
+    if (e != hipSuccess || p == nullptr)
+      return set_error(BFA_ERR_LAUNCH, "bfa_fused_rmsnorm_qkv_noalloc: scratch address on device %d: %s",
+                       dev, hipGetErrorString(e));
+    g_scratch_addr[dev] = p;
+  }
+  *addr = g_scratch_addr[dev];
+  return BFA_OK;
+}
+
+extern "C" int bfa_fused_rmsnorm_qkv_noalloc(
+    const void* x, int x_dtype, int64_t tokens, int64_t hidden, int64_t x_stride,
+    const void* norm_weight, int nw_dtype, float eps, int mixed_rounding, const void* qkv_weight,
+    int w_dtype, int64_t qkv_dim, int64_t w_stride, const void* bias, int bias_dtype,
+    int64_t num_q_heads, int64_t num_kv_heads, int qkv_dtype, const void* q_norm_weight,
+    const void* k_norm_weight, int qk_norm_dtype, float qk_eps, int qk_norm_out_dtype,
+    const void* positions, int positions_dtype, const float* cos_sin_cache, int64_t max_position,
+    void* out, int out_dtype, int64_t out_stride, int32_t* status, void* stream) {
+  const char* what = "bfa_fused_rmsnorm_qkv_noalloc";
+  BFA_REQUIRE(x && norm_weight && qkv_weight, "%s: null pointer", what);
+  if (tokens == 0) return BFA_OK;
+  BFA_REQUIRE(tokens > 0 && hidden > 0 && qkv_dim > 0, "%s: bad geometry", what);
+  const int64_t heads = num_q_heads + 2 * num_kv_heads;
+  BFA_REQUIRE(num_q_heads > 0 && num_kv_heads > 0 && qkv_dim % heads == 0, "%s: bad head geometry", what);
+  const int64_t need = bfa_fused_rmsnorm_qkv_workspace_size(tokens, hidden, qkv_dim, qkv_dim / heads);
+  BFA_REQUIRE(need <= BFA_NOALLOC_SCRATCH_BYTES,
+              "%s: %lld tokens x hidden %lld x qkv_dim %lld need %lld bytes of scratch, more than the "
+              "%lld this entry point holds; call bfa_fused_rmsnorm_qkv with a workspace",
+              what, (long long)tokens, (long long)hidden, (long long)qkv_dim, (long long)need,
+              (long long)BFA_NOALLOC_SCRATCH_BYTES);
+  void* ws = nullptr;
+  const int rc = noalloc_scratch_addr(stream, &ws);
+  if (rc != BFA_OK) return rc;
+  return bfa_fused_rmsnorm_qkv(x, x_dtype, tokens, hidden, x_stride, norm_weight, nw_dtype, eps,
+                               mixed_rounding, qkv_weight, w_dtype, qkv_dim, w_stride, bias, bias_dtype,
+                               num_q_heads, num_kv_heads, qkv_dtype, q_norm_weight, k_norm_weight,
+                               qk_norm_dtype, qk_eps, qk_norm_out_dtype, positions, positions_dtype,
+                               cos_sin_cache, max_position, out, out_dtype, out_stride, ws,
+                               BFA_NOALLOC_SCRATCH_BYTES, status, stream);
 }
 
 // ------------------------------------------------------- linear fusions

@@ -199,6 +199,31 @@ int bfa_fused_rmsnorm_qkv(const void* x, int x_dtype, int64_t tokens, int64_t hi
                           int out_dtype, int64_t out_stride, void* workspace,
                           int64_t workspace_bytes, int32_t* status, void* stream);
 
+/* Allocation-free form of bfa_fused_rmsnorm_qkv.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under
+ * HIP-graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Same arguments and results as bfa_fused_rmsnorm_qkv without the workspace:
+ * the workspace is a device array inside the library, BFA_NOALLOC_SCRATCH_BYTES
+ * per GPU, held until the process ends.  Shapes whose
+ * bfa_fused_rmsnorm_qkv_workspace_size exceeds it return BFA_ERR_INVALID (at
+ * Llama-3-8B shape, hidden 4096 -> 6144: every decode batch up to 64 tokens and
+ * prefills up to 2048 tokens fit).  The call allocates nothing (no hipMalloc,
+ * no library allocation); its first call on a device looks up the array's
+ * address there.  Every call on one GPU uses the same array: calls that
+ * overlap on a GPU (other streams, other host threads) race; stream-ordered
+ * calls do not. */
+#define BFA_NOALLOC_SCRATCH_BYTES (16LL << 20)
+int bfa_fused_rmsnorm_qkv_noalloc(const void* x, int x_dtype, int64_t tokens, int64_t hidden,
+                                  int64_t x_stride, const void* norm_weight, int nw_dtype, float eps,
+                                  int mixed_rounding, const void* qkv_weight, int w_dtype,
+                                  int64_t qkv_dim, int64_t w_stride, const void* bias, int bias_dtype,
+                                  int64_t num_q_heads, int64_t num_kv_heads, int qkv_dtype,
+                                  const void* q_norm_weight, const void* k_norm_weight,
+                                  int qk_norm_dtype, float qk_eps, int qk_norm_out_dtype,
+                                  const void* positions, int positions_dtype,
+                                  const float* cos_sin_cache, int64_t max_position, void* out,
+                                  int out_dtype, int64_t out_stride, int32_t* status, void* stream);
+
 /* The two stages of bfa_fused_rmsnorm_qkv, exposed separately.
  * Stage 1 (the RMSNorm prologue of every variant): operand[rows, hidden] =
  *   mixed_rounding ? to(op)( to(bf16)(x / rms) * w ) : to(op)( (x / rms) * w ),
