@@ -96,6 +96,13 @@ struct QkvEpi {
   int64_t ldr;
   int mid_dt;
   int vec;
+  // scale-after decode (the fp32 variants): stats[s * stat_rows + t] holds split
+  // s's sum of x^2 over its K slice for token t; the projection of x * gamma is
+  // multiplied by r = 1 / sqrt(sum / hidden + stat_eps) before the bias
+  const float* stats;
+  int64_t stat_rows;
+  int64_t hidden;
+  float stat_eps;
 };
 
 __device__ __forceinline__ float round_to(float v, int dt) {
@@ -879,6 +886,7 @@ struct DecodeArgs {
   int gamma_dt, mixed;
   float eps;
   int fold_rows;  // rows per wave of the fold: 0 (no fold), 1, 2 or 4
+  float* stats;   // scale-after form: [splits, 16 mt] partial sums of x^2
 };
 
 // Host-side description of the fold: the raw rows and the RMSNorm parameters.
@@ -888,6 +896,7 @@ struct OperandFold {
   bool mixed;
   float eps;
   int rows_per_wave;
+  float* stats;  // non-null: scale-after form of the deep-K kernel
 };
 
 template <int DT>
@@ -1133,12 +1142,25 @@ __device__ __forceinline__ void wait_vm_last(int n) {
   }
 }
 
-template <int MT, bool BF16>
+//
+// SA (scale-after, bf16 weights): the operand is x * gamma rounded to bf16
+// instead of the normalised row, and the split also returns its rows' sums of
+// x^2 over its K slice; the reduction kernel multiplies the summed projection
+// by r = 1 / sqrt(sum / hidden + eps).  For the fp32 variants (whose operand
+// is (x / rms) * gamma in fp32) this is the same product with the row scale
+// taken out of the sum, and it needs no pass over whole rows before the
+// projection.  Each wave converts, in place, the operand granules its own
+// DMAs wrote (after waiting for them and before the barrier that publishes
+// the chunk), with gamma loaded right after the DMAs: requests, in issue
+// order, op(c+1) [D], gamma(c+1) [D], W(c+1) s0..s3.
+template <int MT, bool BF16, bool SA = false>
 __global__ __launch_bounds__(256) void qkv_decode_loop_kernel(DecodeArgs d, int nch) {
   constexpr int KS = LOOP_KS;
   constexpr int GPR = KS * 8;  // granules per operand row (512 bytes)
   constexpr int ROWS = MT * 16;
   constexpr int D = ROWS / 8;  // operand DMAs per wave per chunk (two rows each, four waves)
+  constexpr int DG = SA ? D : 0;  // gamma loads per wave per chunk
+  static_assert(!SA || BF16, "scale-after takes bf16 operands");
   static_assert(MT >= 2 && MT <= 4, "two to four token blocks");
   __shared__ uint4 abuf[2 * ROWS * GPR];  // two chunks: 2 x 64 rows x 512 B = 64 KiB at MT = 4
   __shared__ uint4 wst[4][32 * 8];
@@ -1160,11 +1182,51 @@ __global__ __launch_bounds__(256) void qkv_decode_loop_kernel(DecodeArgs d, int 
     aoff[i] = static_cast<uint32_t>((min<int64_t>(row, d.m - 1) * d.lda + gl * 8) * 2);
   }
   const uint32_t lbase = lds_addr(abuf);
+  // scale-after: lane's slot of DMA i is logical granule gsl[i] of row srow[i]
+  int gsl[D];
+#pragma unroll
+  for (int i = 0; i < D; ++i) {
+    const int row = 2 * (4 * i + wid) + (lane >> 5), sl = lane & 31;
+    gsl[i] = (sl & ~15) | ((sl & 15) ^ (row & 15));
+  }
+  uint4 gam[SA ? D : 1];
+  float ssq[SA ? D : 1];
+#pragma unroll
+  for (int i = 0; i < (SA ? D : 1); ++i) ssq[i] = 0.f;
   auto issue_op = [&](int c) {
     const uint16_t* ab = d.a + kbase + c * (KS * 64);
     const uint32_t lb = lbase + (c & 1) * (ROWS * GPR * 16);
 #pragma unroll
     for (int i = 0; i < D; ++i) dma16(ab, aoff[i], lb + (4 * i + wid) * 1024);
+    if constexpr (SA) {
+      const uint16_t* gb = static_cast<const uint16_t*>(d.gamma) + kbase + c * (KS * 64);
+#pragma unroll
+      for (int i = 0; i < D; ++i) gam[i] = load16(gb + gsl[i] * 8);
+    }
+  };
+  // scale-after: x -> bf16(x * gamma) in this wave's own slots of chunk c, and
+  // the sums of squares of x (called after the chunk's DMAs and gamma landed)
+  auto convert = [&](int c) {
+    if constexpr (SA) {
+      uint4* ab = abuf + (c & 1) * (ROWS * GPR);
+      uint4 xv[D];
+#pragma unroll
+      for (int i = 0; i < D; ++i) xv[i] = ab[(2 * (4 * i + wid) + (lane >> 5)) * GPR + (lane & 31)];
+#pragma unroll
+      for (int i = 0; i < D; ++i) {
+        float xf[8], gf[8];
+        unpack8<BFA_DTYPE_BF16>(xv[i], xf);
+        unpack8<BFA_DTYPE_BF16>(gam[i], gf);
+        uint32_t o[4];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) ssq[i] += xf[j] * xf[j];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          o[j] = static_cast<uint32_t>(f32_to_bf16_bits(xf[2 * j] * gf[2 * j])) |
+                 (static_cast<uint32_t>(f32_to_bf16_bits(xf[2 * j + 1] * gf[2 * j + 1])) << 16);
+        ab[(2 * (4 * i + wid) + (lane >> 5)) * GPR + (lane & 31)] = make_uint4(o[0], o[1], o[2], o[3]);
+      }
+    }
   };
 
   uint4 wr[KS][4];
@@ -1193,7 +1255,7 @@ __global__ __launch_bounds__(256) void qkv_decode_loop_kernel(DecodeArgs d, int 
     const uint4* ab = abuf + (c & 1) * (ROWS * GPR);
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
-      if constexpr (NEXT) wait_vm<4 * (KS - 1) + D>();
+      if constexpr (NEXT) wait_vm<4 * (KS - 1) + D + DG>();
       else wait_vm_last(4 * (KS - 1 - s));
 #pragma unroll
       for (int i = 0; i < 4; ++i) ws[wslot(i * 8 + wrow_l, wg_l)] = wr[s][i];
@@ -1231,13 +1293,28 @@ __global__ __launch_bounds__(256) void qkv_decode_loop_kernel(DecodeArgs d, int 
     // the barrier publishes every wave's copies and shows that chunk c-1, the
     // last reader of buffer (c+1) & 1, is finished everywhere.
     wait_vm<4 * KS>();
+    convert(c);
     __syncthreads();
     issue_op(c + 1);
     chunk(c, std::true_type{});
   }
   wait_vm<4 * KS>();
+  convert(c);
   __syncthreads();
   chunk(c, std::false_type{});
+  if constexpr (SA) {
+    // rows 2 (4 i + wid) (lanes 0-31) and + 1 (lanes 32-63); every column tile
+    // computes the same sums, the first one stores them
+#pragma unroll
+    for (int i = 0; i < D; ++i) {
+      uint32_t x = __builtin_bit_cast(uint32_t, group16_sum_dpp(ssq[i])), y = x;
+      swap16(x, y);
+      const float tot = __builtin_bit_cast(float, x) + __builtin_bit_cast(float, y);
+      const int row = 2 * (4 * i + wid) + (lane >> 5);
+      if (blockIdx.x == 0 && (lane & 31) == 0 && row < d.m)
+        d.stats[static_cast<int64_t>(blockIdx.y) * ROWS + row] = tot;
+    }
+  }
 
   // partial tile in register order, as qkv_decode_kernel with REG_ORDER
   float4* tb = reinterpret_cast<float4*>(d.part) +
@@ -1311,6 +1388,21 @@ __device__ __forceinline__ void decode_epilogue_item(const float4* part, int64_t
         a1[pp].x += f * l1[u].x; a1[pp].y += f * l1[u].y; a1[pp].z += f * l1[u].z; a1[pp].w += f * l1[u].w;
         a2[pp].x += f * l2[u].x; a2[pp].y += f * l2[u].y; a2[pp].z += f * l2[u].z; a2[pp].w += f * l2[u].w;
       }
+    }
+  }
+  if (e.stats) {
+    // scale-after: r per token from the splits' sums of squares (split order)
+    float sq[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int64_t sp = 0; sp < splits; ++sp)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) sq[v] += e.stats[sp * e.stat_rows + min(tg * 4 + v, m - 1)];
+    float r[4];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) r[v] = 1.0f / sqrtf(sq[v] / static_cast<float>(e.hidden) + e.stat_eps);
+#pragma unroll
+    for (int pp = 0; pp < MAXP; ++pp) {
+      a1[pp].x *= r[0]; a1[pp].y *= r[1]; a1[pp].z *= r[2]; a1[pp].w *= r[3];
+      a2[pp].x *= r[0]; a2[pp].y *= r[1]; a2[pp].z *= r[2]; a2[pp].w *= r[3];
     }
   }
   int64_t pos[4];
@@ -1744,8 +1836,19 @@ static void launch_decode(const QkvPlan& p, const SplitArgs& s, hipStream_t st,
     if (fold) {
       d.gamma = fold->gamma; d.gamma_dt = fold->gamma_dt; d.mixed = fold->mixed ? 1 : 0; d.eps = fold->eps;
       d.fold_rows = fold->rows_per_wave;
+      d.stats = fold->stats;
     }
     const dim3 grid(static_cast<unsigned>(cdiv(s.n, 128)), static_cast<unsigned>(p.splits));
+    if (p.nch > 0 && d.stats) {
+      if constexpr (BF16) {
+        switch (p.mt) {
+          case 2: hipLaunchKernelGGL((qkv_decode_loop_kernel<2, true, true>), grid, dim3(256), 0, st, d, p.nch); break;
+          case 3: hipLaunchKernelGGL((qkv_decode_loop_kernel<3, true, true>), grid, dim3(256), 0, st, d, p.nch); break;
+          default: hipLaunchKernelGGL((qkv_decode_loop_kernel<4, true, true>), grid, dim3(256), 0, st, d, p.nch); break;
+        }
+      }
+      return;
+    }
     if (p.nch > 0) {
       switch (p.mt) {
         case 2: hipLaunchKernelGGL((qkv_decode_loop_kernel<2, BF16>), grid, dim3(256), 0, st, d, p.nch); break;
@@ -1919,6 +2022,9 @@ static int qkv_projection_impl(const void* operand, int64_t lda, const OperandFo
   e.positions = positions; e.pos_is_i64 = positions_dtype == BFA_DTYPE_I64;
   e.cs = cos_sin_cache; e.max_pos = max_position;
   e.out = out; e.ldo = out_stride; e.status = status;
+  if (fold && fold->stats) {
+    e.stats = fold->stats; e.stat_rows = 16 * p.mt; e.hidden = hidden; e.stat_eps = fold->eps;
+  }
 
   const hipStream_t st = as_stream(stream);
   const bool bf16 = w_dtype == BFA_DTYPE_BF16;
@@ -2016,8 +2122,25 @@ extern "C" int bfa_fused_rmsnorm_qkv(const void* x, int x_dtype, int64_t tokens,
   const bool fold = !no_fold && fold_rows > 0 && p.decode && p.stream && p.mt == 1 && x_dtype == w_dtype &&
                     (w_dtype == BFA_DTYPE_BF16 || w_dtype == BFA_DTYPE_F16) && hidden % 8 == 0 &&
                     x_stride % 8 == 0 && aligned16(x) && aligned16(norm_weight) && is_float_dtype(nw_dtype);
+  // 17 to 64 decode tokens of the fp32 variants (operand (x / rms) * gamma):
+  // the deep-K kernel projects bf16(x * gamma) and returns each split's sums of
+  // x^2, and the reduction kernel applies 1 / rms -- no operand pre-pass.  bf16
+  // only: x * gamma without the row scale could leave the fp16 range.
+  const bool scale_after = !no_fold && p.decode && p.stream && p.nch > 0 && mixed_rounding == 0 &&
+                           qkv_dtype == BFA_DTYPE_F32 && x_dtype == BFA_DTYPE_BF16 &&
+                           w_dtype == BFA_DTYPE_BF16 && nw_dtype == BFA_DTYPE_BF16 && hidden % 8 == 0 &&
+                           x_stride % 8 == 0 && aligned16(x) && aligned16(norm_weight) &&
+                           p.splits * 16 * p.mt * 4 <= p.operand_bytes;
+  if (scale_after) {
+    const OperandFold f{norm_weight, nw_dtype, false, eps, 0, reinterpret_cast<float*>(ws)};
+    return qkv_projection_impl(x, x_stride, &f, tokens, hidden, qkv_weight, w_dtype, qkv_dim, w_stride,
+                               bias, bias_dtype, num_q_heads, num_kv_heads, qkv_dtype, q_norm_weight,
+                               k_norm_weight, qk_norm_dtype, qk_eps, qk_norm_out_dtype, positions,
+                               positions_dtype, cos_sin_cache, max_position, out, out_dtype, out_stride,
+                               ws + p.operand_bytes, workspace_bytes - p.operand_bytes, status, stream);
+  }
   if (fold) {
-    const OperandFold f{norm_weight, nw_dtype, mixed_rounding != 0, eps, fold_rows};
+    const OperandFold f{norm_weight, nw_dtype, mixed_rounding != 0, eps, fold_rows, nullptr};
     return qkv_projection_impl(x, x_stride, &f, tokens, hidden, qkv_weight, w_dtype, qkv_dim, w_stride,
                                bias, bias_dtype, num_q_heads, num_kv_heads, qkv_dtype, q_norm_weight,
                                k_norm_weight, qk_norm_dtype, qk_eps, qk_norm_out_dtype, positions,

@@ -104,6 +104,34 @@ def test_decode_split_depths(t, heads, h):
         assert_close(got, exp, what=f"decode {name} t={t} h={h}")
 
 
+@pytest.mark.parametrize("t,heads,h,gdtype", [
+    (17, 48, 4096, torch.bfloat16),   # Llama-3-8B shape, two 16-token blocks
+    (33, 48, 4096, torch.bfloat16),   # three blocks
+    (64, 48, 4096, torch.bfloat16),   # four blocks, four splits of four chunks
+    (64, 16, 8192, torch.bfloat16),   # eight chunks per split
+    (64, 48, 4096, torch.float32),    # fp32 gamma: the operand pre-pass path instead
+])
+def test_decode_scale_after(t, heads, h, gdtype):
+    """The fp32 variants from 17 to 64 tokens (bf16 x, W and gamma) project
+    bf16(x * gamma) and multiply the split sum by 1 / rms in the reduction; the
+    result stays within the tolerance of the oracle's (x / rms) * gamma operand,
+    for FusedRMSNormQKVMinimalF32 and for FusedRMSNormQKVWithBias."""
+    hq, hkv, d = heads - 16, 8, 128
+    if heads == 16:
+        hq, hkv = 8, 4
+    _, x, ln, w, b = make(215, t, h, hq, hkv, d)
+    ln = ln.to(gdtype)
+    q, k, v = FusedRMSNormQKVMinimalF32.forward(x.to(DEV), ln.to(DEV), w.to(DEV), hq, hkv, eps=1e-5)
+    ref = R.split_qkv(R.qkv_minimal_f32(x, ln, w, 1e-5), hq, hkv)
+    for got, exp, name in zip((q, k, v), ref, "qkv"):
+        assert got.dtype == torch.float32
+        assert_close(got, exp, what=f"scale-after minimal_f32 {name} t={t}")
+    q, k, v = FusedRMSNormQKVWithBias.forward(x.to(DEV), ln.to(DEV), w.to(DEV), b.to(DEV), hq, hkv, eps=1e-5)
+    ref = R.split_qkv(R.qkv_with_bias(x, ln, w, b, 1e-5), hq, hkv)
+    for got, exp, name in zip((q, k, v), ref, "qkv"):
+        assert_close(got, exp, what=f"scale-after with_bias {name} t={t}")
+
+
 @pytest.mark.parametrize("t,h,dtype,strided", [
     (1, 4096, torch.bfloat16, False),   # Llama-3-8B batch-1 decode: eight 16-byte chunks per lane
     (3, 4096, torch.bfloat16, True),    # rows 4160 elements apart
