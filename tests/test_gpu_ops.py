@@ -322,3 +322,55 @@ def test_rerotate_delta_out_of_table():
     rerotate_paged_k(kv, one([0]), one([0, 1]), torch.tensor([-129], device=DEV), one([16]), cache)
     with pytest.raises(IndexError):
         braidinfer_amd.check_device_status()
+
+
+# ------------------------------------------- Llama-3-8B 8192-token prefill sizes
+# The memory-bound ops at the 8192-token configuration.  Rows are independent,
+# so the oracle runs on a seeded sample of rows (and the integer parts -- the
+# gather and the residual sum -- on every row).
+def _sample_rows(g, n, k=384):
+    return torch.randperm(n, generator=g)[:k].sort().values
+
+
+def test_add_rms_forward_8192_tokens():
+    g = gen(120)
+    t, h = 8192, 4096
+    x, r = randn(g, t, h), randn(g, t, h)
+    w = randn(g, h, mean=1.0, std=0.1)
+    norm = RMSNorm(h, eps=1e-5).to(DEV)
+    with torch.no_grad():
+        norm.weight.data = w.to(DEV)
+    y, res = norm(x.to(DEV), r.to(DEV))
+    y, res = y.cpu(), res.cpu()
+    assert torch.equal(bits(res), bits((x.float() + r.float()).bfloat16())), "residual_out exact on every row"
+    rows = _sample_rows(g, t)
+    ry, _ = R.add_rms_forward(x[rows], r[rows], w, 1e-5)
+    assert_close(y[rows], ry, what="add_rms y, 8192 tokens (sampled rows)")
+
+
+def test_silu_and_mul_8192_tokens():
+    g = gen(121)
+    t, i = 8192, 14336
+    xd = torch.randn(t, 2 * i, device=DEV, dtype=torch.float32,
+                     generator=torch.Generator(device=DEV).manual_seed(121)).bfloat16()
+    y = SiluAndMul()(xd)
+    rows = _sample_rows(g, t)
+    xs = xd[rows.to(DEV)].cpu()
+    assert_close(y[rows.to(DEV)], R.silu_and_mul(xs), what="silu_and_mul, 8192 x 2*14336 (sampled rows)")
+
+
+def test_embedding_full_llama3_table_8192_ids():
+    """The gather over the whole [128256, 4096] table with 8192 ids (about a
+    quarter of them repeated), bit for bit against indexing a host copy."""
+    v, h, t = 128256, 4096, 8192
+    gd = torch.Generator(device=DEV).manual_seed(122)
+    table = (torch.randn(v, h, device=DEV, generator=gd) * 0.02).bfloat16()
+    ids = torch.randint(0, v, (t,), device=DEV, generator=gd)
+    ids[::4] = ids[1::4]
+    emb = VocabParallelEmbedding(v, h).to(DEV)
+    with torch.no_grad():
+        emb.weight.data = table
+    out = emb(ids)
+    ref = R.embedding(ids.cpu(), table.cpu())
+    assert torch.equal(bits(out), bits(ref))
+    braidinfer_amd.check_device_status()

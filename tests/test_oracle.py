@@ -770,3 +770,120 @@ def test_planted_linear_mistakes_are_caught():
         fns[i] = bad
         with pytest.raises(AssertionError):
             pin_linear_family(*fns)
+
+
+# ------------------------------------------------------------ fp32 mode pins
+def test_fp32_mode_closed_forms():
+    """oracle/fp32_ref.py: the reference op chains in fp32 with one rounding,
+    pinned by closed forms that a dropped term, a wrong sign or a transposed
+    operand breaks."""
+    from oracle import fp32_ref as F
+    g = gen(40)
+    w = randn(g, 64, mean=1.0, std=0.1)
+    # constant rows c: x * rsqrt(c^2) = sign(c) exactly (powers of two), so y = sign * w
+    x = torch.tensor([[2.0] * 64, [-4.0] * 64], dtype=torch.bfloat16)
+    y = F.rms_forward(x, w, 0.0)
+    assert torch.equal(y[0], w) and torch.equal(y[1], -w)
+    # add_rms with a zero residual is rms_forward; residual_out is the rounded sum
+    xs, rs = randn(g, 8, 64), randn(g, 8, 64)
+    assert torch.equal(F.add_rms_forward(xs, torch.zeros_like(xs), w, 1e-5)[0], F.rms_forward(xs, w, 1e-5))
+    assert torch.equal(F.add_rms_forward(xs, rs, w, 1e-5)[1], (xs.float() + rs.float()).bfloat16())
+    # silu(0) * u = 0; silu(g) * u -> g * u for large g, -> 0 for large -g
+    u = randn(g, 4, 16)
+    assert F.silu_and_mul(torch.cat([torch.zeros_like(u), u], -1)).eq(0).all()
+    big = torch.full_like(u, 60.0)
+    assert torch.equal(F.silu_and_mul(torch.cat([big, u], -1)), (big.float() * u.float()).bfloat16())
+    assert F.silu_and_mul(torch.cat([-big, u], -1)).abs().max() < 1e-20
+    # qkv with an identity weight is the fp32 RMSNorm, plus the bias
+    h = 32
+    xq = randn(g, 5, h)
+    gq = randn(g, h, mean=1.0, std=0.1)
+    eye = torch.eye(h, dtype=torch.bfloat16)
+    bias = randn(g, h)
+    ref = xq.float() * torch.rsqrt(xq.float().pow(2).mean(-1, keepdim=True) + 1e-6) * gq.float()
+    torch.testing.assert_close(F.qkv(xq, gq, eye, None, 1e-6, torch.float32), ref, rtol=1e-6, atol=1e-6)
+    torch.testing.assert_close(F.qkv(xq, gq, eye, bias, 1e-6, torch.float32), ref + bias.float(),
+                               rtol=1e-6, atol=1e-6)
+    # permuted weight rows permute the output columns (W is [N, H], not [H, N])
+    perm = torch.randperm(h, generator=g)
+    torch.testing.assert_close(F.qkv(xq, gq, eye[perm], None, 1e-6, torch.float32), ref[:, perm],
+                               rtol=1e-6, atol=1e-6)
+
+
+def test_fp32_mode_chains_match_the_pinned_fp32_pieces():
+    """The attention-input chains of fp32_ref equal their pieces composed from
+    the ref-rounding oracle's fp32 forms: rotary_forward on fp32 q/k (it rounds
+    to the input dtype, fp32 here) and rms_forward on fp32 heads (fp32 in, so
+    no intermediate rounding) -- pinned above and in the RoPE tests."""
+    from oracle import fp32_ref as F
+    g = gen(41)
+    t, h, hq, hkv, d = 6, 64, 4, 2, 16
+    x = randn(g, t, h)
+    ln = randn(g, h, mean=1.0, std=0.1)
+    w = randn(g, (hq + 2 * hkv) * d, h, std=0.1)
+    qn, kn = randn(g, d, mean=1.0, std=0.1), randn(g, d, mean=2.0, std=0.5)
+    pos = torch.randint(0, 64, (t,), generator=g)
+    cache = R.cos_sin_cache(d, 64, 1e4)
+    acc = F.qkv(x, ln, w, None, 1e-6, torch.float32)
+    q, k, v = acc.split([hq * d, hkv * d, hkv * d], dim=-1)
+    qh = R.rms_forward(q.reshape(t, hq, d), qn.float(), 1e-6).reshape(t, -1)
+    kh = R.rms_forward(k.reshape(t, hkv, d), kn.float(), 1e-6).reshape(t, -1)
+    rq, rk = R.rotary_forward(cache, d, pos, qh, kh)
+    got = F.qwen3_attention_input(x, ln, w, None, hq, hkv, 1e-6, pos, cache, qn, kn)
+    for a, b in zip(got, (rq, rk, v)):
+        torch.testing.assert_close(a.float(), b.bfloat16().float(), rtol=0, atol=0)
+    rq, rk = R.rotary_forward(cache, d, pos, q, k)
+    got = F.llama_attention_input(x, ln, w, hq, hkv, 1e-6, pos, cache)
+    for a, b in zip(got, (rq, rk, v)):
+        torch.testing.assert_close(a.float(), b.bfloat16().float(), rtol=0, atol=0)
+
+
+def test_fp32_mode_is_within_the_reference_rounding_of_ref_mode():
+    """Both modes compute the same function: on generic data they agree to the
+    reference's own bf16 rounding (normwise relative difference of a few 1e-3)."""
+    from oracle import fp32_ref as F
+    g = gen(42)
+    x = randn(g, 64, 512)
+    w = randn(g, 512, mean=1.0, std=0.1)
+    wq = randn(g, 384, 512, std=0.05)
+
+    def nw(a, b):
+        a, b = a.float(), b.float()
+        return ((a - b).norm() / b.norm()).item()
+    assert nw(R.rms_forward(x, w, 1e-5), F.rms_forward(x, w, 1e-5)) < 5e-3
+    assert nw(R.silu_and_mul(x), F.silu_and_mul(x)) < 5e-3
+    assert nw(R.qkv_mixed_precision(x, w, wq, None, 1e-5), F.qkv(x, w, wq, None, 1e-5, torch.bfloat16)) < 8e-3
+    # minimal_f32 is fp32 in the reference too: the modes agree to fp32 rounding
+    assert nw(R.qkv_minimal_f32(x, w, wq, 1e-5), F.qkv(x, w, wq, None, 1e-5, torch.float32)) < 1e-6
+
+
+def test_planted_fp32_mode_mistakes_are_caught():
+    """Copies of fp32_ref with a planted mistake fail the pins above."""
+    from oracle import fp32_ref as F
+    g = gen(43)
+    h = 32
+    xq, gq = randn(g, 5, h), randn(g, h, mean=1.0, std=0.1)
+    eye = torch.eye(h, dtype=torch.bfloat16)
+    ref = F.qkv(xq, gq, eye, None, 1e-6, torch.float32)
+
+    def no_gamma(x, norm_weight, qkv_weight, qkv_bias, eps, out_dtype):
+        x32 = x.float()
+        return (x32 * torch.rsqrt(x32.pow(2).mean(-1, keepdim=True) + eps) @ qkv_weight.float().t()).to(out_dtype)
+
+    def transposed(x, norm_weight, qkv_weight, qkv_bias, eps, out_dtype):
+        x32 = x.float()
+        n = x32 * torch.rsqrt(x32.pow(2).mean(-1, keepdim=True) + eps) * norm_weight.float()
+        return (n @ qkv_weight.float()).to(out_dtype)
+    perm = torch.randperm(h, generator=g)
+    assert not torch.allclose(no_gamma(xq, gq, eye, None, 1e-6, torch.float32), ref, rtol=1e-4, atol=1e-4)
+    assert not torch.allclose(transposed(xq, gq, eye[perm], None, 1e-6, torch.float32), ref[:, perm],
+                              rtol=1e-4, atol=1e-4)
+    # a RoPE with the sign of the sine flipped differs from the pinned rotary_forward
+    d, t = 16, 4
+    cache = R.cos_sin_cache(d, 32, 1e4)
+    pos = torch.arange(1, t + 1)
+    q = randn(g, t, d).float()
+    cos, sin = cache[pos].chunk(2, -1)
+    x1, x2 = q.chunk(2, -1)
+    wrong = torch.cat((x1 * cos + x2 * sin, x2 * cos - x1 * sin), -1)
+    assert not torch.allclose(wrong, R.rotary_forward(cache, d, pos, q, q)[0], atol=1e-3)
