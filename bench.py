@@ -13,14 +13,22 @@ embedding gather are reported in the same JSON line.
     python bench.py [--steps K] [--warmup W] [--tokens T] [--no-cpu]
 
 Prints one JSON line.  `value` is microseconds per layer (lower is better):
-K chain steps captured into one HIP graph and replayed between HIP events,
-i.e. the GPU time of the three kernels back to back without Python launch
-gaps; `eager_us_per_layer` is the same chain launched eagerly.  Per-kernel
-rows are graph-replayed too.  `roofline` is for the dominant kernel (the QKV projection at
-8192 tokens): its algorithmic FLOPs / its own average event-timed duration
-against the 2.5 PFLOP/s dense-bf16 peak.  `cpu_baseline` times the oracle's
-torch-CPU restatement of the same chain on a bounded token sample and scales
-it linearly to T tokens.
+K chain steps captured into one HIP graph and replayed between HIP events
+after the clock has settled, i.e. the GPU time of the three kernels back to
+back without Python launch gaps; `eager_us_per_layer` is the same chain
+launched eagerly.  Every (kernel, workload) row -- kernels_prefill,
+decode.kernels, configs -- carries:
+    us, gbs / tflops, hbm_frac / mfma_frac   warm, graph-replayed
+    us_cold, hbm_frac_cold                   Infinity Cache flushed before each call
+    cpu_us, cpu_reps                         the oracle's torch-CPU restatement of the
+                                             reference at the row's full size, median
+    vs_oracle                                bit-exact, or max_abs / max_rel_normwise /
+                                             allclose / beyond_tol_elements
+`roofline` is for the dominant kernel (the QKV projection at 8192 tokens):
+its algorithmic FLOPs / its own average event-timed duration against the
+2.5 PFLOP/s dense-bf16 peak.  `cpu_baseline` is the sum of the three chain
+ops' CPU times at the full token count; `cpu` records the host's CPU model,
+threads and torch's parallel_info.
 """
 from __future__ import annotations
 
@@ -63,22 +71,27 @@ class Chain:
     def __init__(self, t: int, dev: torch.device, seed: int = 5):
         g = torch.Generator().manual_seed(seed)
         bf = torch.bfloat16
+        self.cpu = {}
 
-        def randn(*shape, std=1.0, mean=0.0):
-            return (torch.randn(*shape, generator=g) * std + mean).to(bf).to(dev)
+        def randn(name, *shape, std=1.0, mean=0.0):
+            v = (torch.randn(*shape, generator=g) * std + mean).to(bf)
+            self.cpu[name] = v
+            return v.to(dev)
 
         self.t = t
-        self.x = randn(t, H)
-        self.residual = randn(t, H)
+        self.x = randn("x", t, H)
+        self.residual = randn("residual", t, H)
         self.norm = RMSNorm(H, eps=EPS).to(dev)
         with torch.no_grad():
-            self.norm.weight.data = randn(H, std=0.1, mean=1.0)
-        self.hidden = randn(t, H)
-        self.ln_w = randn(H, std=0.1, mean=1.0)
-        self.w_qkv = randn(N, H, std=0.02)
-        self.positions = torch.randint(0, MAXPOS, (t,), generator=g).to(dev)
-        self.cache = rope_table(D, MAXPOS, THETA).to(dev)
-        self.gate_up = randn(t, 2 * INTER)
+            self.norm.weight.data = randn("norm_w", H, std=0.1, mean=1.0)
+        self.hidden = randn("hidden", t, H)
+        self.ln_w = randn("ln_w", H, std=0.1, mean=1.0)
+        self.w_qkv = randn("w_qkv", N, H, std=0.02)
+        self.cpu["positions"] = torch.randint(0, MAXPOS, (t,), generator=g)
+        self.positions = self.cpu["positions"].to(dev)
+        self.cpu["cache"] = rope_table(D, MAXPOS, THETA)
+        self.cache = self.cpu["cache"].to(dev)
+        self.gate_up = randn("gate_up", t, 2 * INTER)
         self.silu = SiluAndMul()
         self.out_qkv = torch.empty(t, N, dtype=bf, device=dev)
         self.ids = torch.randint(0, VOCAB, (t,), generator=g).to(dev)
@@ -138,25 +151,47 @@ def time_fn(fn, iters: int, warmup: int = 3) -> float:
     return s.elapsed_time(e) / iters
 
 
-def kernel_table(c: Chain, dev, iters: int) -> dict:
-    """Per-kernel event timing with algorithmic bytes / FLOPs and roofline fractions."""
+class Row:
+    """One (kernel, workload) measurement.  `fn` runs the op on device inputs and
+    returns what it produced; `ref` (optional) computes the oracle's result for
+    the same inputs on the CPU, and `got` maps fn's output to the tensor(s)
+    compared with it.  exact: integer/byte ops compared bit for bit."""
+
+    def __init__(self, name, fn, nbytes, flops=0.0, ref=None, got=None, exact=False, note=None):
+        self.name, self.fn, self.nbytes, self.flops = name, fn, nbytes, flops
+        self.ref, self.got, self.exact, self.note = ref, got, exact, note
+
+
+def chain_rows(c: Chain, dev, stages: bool) -> list:
+    """The chain's kernels at c.t tokens; `stages` adds the two stages of the
+    fused QKV op (operand pre-pass, projection) as rows of their own."""
     t = c.t
-    st = QkvStages(c, dev)
-    rows = {}
+    rows = [Row("add_rms_norm", lambda: c.norm(c.x, c.residual)[0], 4 * t * H * 2 + H * 2,
+                ref=lambda: _oracle().add_rms_forward(c.cpu["x"], c.cpu["residual"], c.cpu["norm_w"], EPS)[0])]
+    if stages:
+        st = QkvStages(c, dev)
+        rows += [Row("qkv_operand_prepass", st.operand, 2 * t * H * 2 + H * 2, note="stage of the fused op"),
+                 Row("qkv_projection_rope", st.projection,
+                     t * H * 2 + N * H * 2 + t * N * 2 + t * 8 + t * D * 4, 2.0 * t * H * N,
+                     note="stage of the fused op (operand from the pre-pass)")]
 
-    def add(name, fn, nbytes, flops=0.0):
-        rows[name] = _roof_row(time_graph(fn, iters), nbytes, flops)
-
-    add("add_rms_norm", lambda: c.norm(c.x, c.residual), 4 * t * H * 2 + H * 2)
-    add("qkv_operand_prepass", st.operand, 2 * t * H * 2 + H * 2)
-    add("qkv_projection_rope", st.projection,
-        t * H * 2 + N * H * 2 + t * N * 2 + t * 8 + t * D * 4, 2.0 * t * H * N)
-    add("fused_rmsnorm_qkv_rope", c.qkv,
-        t * H * 2 + H * 2 + N * H * 2 + t * N * 2 + t * 8 + t * D * 4, 2.0 * t * H * N)
-    add("silu_and_mul", lambda: c.silu(c.gate_up), 3 * t * INTER * 2)
+    def llama_ref():
+        q, k, v = _oracle().llama_attention_input(c.cpu["hidden"], c.cpu["ln_w"], c.cpu["w_qkv"], HQ, HKV, EPS,
+                                                  c.cpu["positions"], c.cpu["cache"])
+        return torch.cat([q, k, v], 1)
+    rows += [Row("fused_rmsnorm_qkv_rope", c.qkv, t * H * 2 + H * 2 + N * H * 2 + t * N * 2 + t * 8 + t * D * 4,
+                 2.0 * t * H * N, ref=llama_ref),
+             Row("silu_and_mul", lambda: c.silu(c.gate_up), 3 * t * INTER * 2,
+                 ref=lambda: _oracle().silu_and_mul(c.cpu["gate_up"]))]
     table = torch.empty(VOCAB, H, dtype=torch.bfloat16, device=dev).normal_(0, 0.02)
-    add("embedding_gather", lambda: embedding(c.ids, table), 2 * t * H * 2 + 8 * t)
-    del table
+    host = {}
+
+    def gather_ref():
+        if not host:  # one host copy of the table and ids, in the untimed first run
+            host["table"], host["ids"] = table.cpu(), c.ids.cpu()
+        return _oracle().embedding(host["ids"], host["table"])
+    rows.append(Row("embedding_gather", lambda: embedding(c.ids, table), 2 * t * H * 2 + 8 * t,
+                    ref=gather_ref, exact=True))
     return rows
 
 
@@ -170,9 +205,28 @@ def _roof_row(ms: float, nbytes: float, flops: float = 0.0) -> dict:
     return row
 
 
+def _oracle():
+    """The CPU restatement of the reference (oracle/): imported only by the CPU
+    leg, which times it and checks the GPU results against it."""
+    from oracle import torch_ref
+    return torch_ref
+
+
+class _Gen:
+    """Seeded CPU generator: draws fp32, rounds to bf16, keeps the CPU copy."""
+
+    def __init__(self, seed, dev):
+        self.g = torch.Generator().manual_seed(seed)
+        self.dev = dev
+
+    def randn(self, *shape, std=1.0, mean=0.0):
+        v = (torch.randn(*shape, generator=self.g) * std + mean).to(torch.bfloat16)
+        return v, v.to(self.dev)
+
+
 def config_cases(dev) -> list:
-    """The path's other workloads as (name, fn, algorithmic bytes, FLOPs), inputs
-    drawn per configuration (seeds 1-4, CPU generator, fp32 then bf16):
+    """The path's other workloads, inputs drawn per configuration (seeds 1-4,
+    CPU generator, fp32 then bf16):
       rmsnorm     TinyLlama RMSNorm, x [128, 2048], eps 1e-5
       tinyllama   fused RMSNorm+QKV(2048 -> 2560, 32/4 heads, D 64)+RoPE(theta 1e4), T 1/8/512
       qwen3       fused RMSNorm+QKV(1024 -> 4096, 16/8 heads, D 128)+q/k norm+RoPE(theta 1e6), T 1/2048
@@ -187,70 +241,74 @@ def config_cases(dev) -> list:
                   Llama-3-8B shapes, T 8192 and 64"""
     from braidinfer_amd.layers import llama_attention_input, qwen3_attention_input, rerotate_paged_k
     bf = torch.bfloat16
-    cases = []
+    rows = []
 
-    def gen(seed):
-        g = torch.Generator().manual_seed(seed)
-
-        def randn(*shape, std=1.0, mean=0.0):
-            return (torch.randn(*shape, generator=g) * std + mean).to(bf).to(dev)
-        return g, randn
-
-    g, randn = gen(1)
-    x = randn(128, 2048)
+    r = _Gen(1, dev)
+    xc, x = r.randn(128, 2048)
+    wc, w = r.randn(2048, std=0.1, mean=1.0)
     norm = RMSNorm(2048, eps=1e-5).to(dev)
     with torch.no_grad():
-        norm.weight.data = randn(2048, std=0.1, mean=1.0)
-    cases.append(("rmsnorm_t128_h2048", lambda: norm(x), 2 * 128 * 2048 * 2 + 2048 * 2, 0.0))
+        norm.weight.data = w
+    rows.append(Row("rmsnorm_t128_h2048", lambda: norm(x), 2 * 128 * 2048 * 2 + 2048 * 2,
+                    ref=lambda: _oracle().rms_forward(xc, wc, 1e-5)))
 
-    def tiny(t, h=2048, hq=32, hkv=4, d=64):
+    def cat3(qkv):
+        return torch.cat([t.reshape(t.shape[0], -1) for t in qkv], 1)
+
+    def tiny(r, t, h=2048, hq=32, hkv=4, d=64):
         n = (hq + 2 * hkv) * d
-        xt, ln, w = randn(t, h), randn(h, std=0.1, mean=1.0), randn(n, h, std=0.02)
-        pos = torch.randint(0, 2048, (t,), generator=g).to(dev)
-        cache = rope_table(d, 2048, 1e4).to(dev)
-        return (f"tinyllama_qkv_rope_t{t}", lambda: llama_attention_input(xt, ln, w, hq, hkv, 1e-5, pos, cache),
-                t * h * 2 + h * 2 + n * h * 2 + t * n * 2 + t * 8 + t * d * 4, 2.0 * t * h * n)
+        (xc, xt), (lc, ln), (wc, w) = r.randn(t, h), r.randn(h, std=0.1, mean=1.0), r.randn(n, h, std=0.02)
+        pc = torch.randint(0, 2048, (t,), generator=r.g)
+        cc = rope_table(d, 2048, 1e4)
+        pos, cache = pc.to(dev), cc.to(dev)
+        return Row(f"tinyllama_qkv_rope_t{t}", lambda: llama_attention_input(xt, ln, w, hq, hkv, 1e-5, pos, cache),
+                   t * h * 2 + h * 2 + n * h * 2 + t * n * 2 + t * 8 + t * d * 4, 2.0 * t * h * n,
+                   ref=lambda: cat3(_oracle().llama_attention_input(xc, lc, wc, hq, hkv, 1e-5, pc, cc)), got=cat3)
 
-    g, randn = gen(2)
-    cases += [tiny(t) for t in (1, 8, 512)]
+    r = _Gen(2, dev)
+    rows += [tiny(r, t) for t in (1, 8, 512)]
 
-    def qwen(t, h=1024, hq=16, hkv=8, d=128):
+    def qwen(r, t, h=1024, hq=16, hkv=8, d=128):
         n = (hq + 2 * hkv) * d
-        xt, w, ln = randn(t, h), randn(n, h, std=0.02), randn(h, std=0.1, mean=1.0)
-        qn = randn(d, std=0.1, mean=1.0)
-        kn = torch.exp(torch.empty(d).uniform_(-2.995732, 4.605170, generator=g)).to(bf).to(dev)
-        pos = torch.randint(0, 2048, (t,), generator=g).to(dev)
-        cache = rope_table(d, 40960, 1e6).to(dev)
-        return (f"qwen3_qkv_qknorm_rope_t{t}",
-                lambda: qwen3_attention_input(xt, ln, w, None, hq, hkv, 1e-6, pos, cache, qn, kn),
-                t * h * 2 + h * 2 + n * h * 2 + t * n * 2 + t * 8 + t * d * 4 + 2 * d * 2, 2.0 * t * h * n)
+        (xc, xt), (wc, w), (lc, ln) = r.randn(t, h), r.randn(n, h, std=0.02), r.randn(h, std=0.1, mean=1.0)
+        qc, qn = r.randn(d, std=0.1, mean=1.0)
+        kc = torch.exp(torch.empty(d).uniform_(-2.995732, 4.605170, generator=r.g)).to(bf)
+        kn = kc.to(dev)
+        pc = torch.randint(0, 2048, (t,), generator=r.g)
+        cc = rope_table(d, 40960, 1e6)
+        pos, cache = pc.to(dev), cc.to(dev)
+        return Row(f"qwen3_qkv_qknorm_rope_t{t}",
+                   lambda: qwen3_attention_input(xt, ln, w, None, hq, hkv, 1e-6, pos, cache, qn, kn),
+                   t * h * 2 + h * 2 + n * h * 2 + t * n * 2 + t * 8 + t * d * 4 + 2 * d * 2, 2.0 * t * h * n,
+                   ref=lambda: cat3(_oracle().qwen3_attention_input(xc, lc, wc, None, hq, hkv, 1e-6, pc, cc, qc, kc)),
+                   got=cat3)
 
-    g, randn = gen(3)
-    cases += [qwen(t) for t in (1, 2048)]
+    r = _Gen(3, dev)
+    rows += [qwen(r, t) for t in (1, 2048)]
 
-    g, randn = gen(4)
+    r = _Gen(4, dev)
     pages, hkv, ps, d = 256, 8, 16, 128
-    kv = randn(pages, 2, hkv, ps, d)
-    page_idx = torch.randperm(pages, generator=g).to(torch.int32).to(dev)
-    indptr = (torch.arange(17, dtype=torch.int32) * 16).to(dev)
-    delta = torch.randint(-4096, 4097, (16,), generator=g).to(dev)
-    last = torch.full((16,), ps, dtype=torch.int32, device=dev)
-    rcache = rope_table(d, 40960, 1e6).to(dev)
+    kvc, kv = r.randn(pages, 2, hkv, ps, d)
+    pic = torch.randperm(pages, generator=r.g).to(torch.int32)
+    ipc = torch.arange(17, dtype=torch.int32) * 16
+    dc = torch.randint(-4096, 4097, (16,), generator=r.g)
+    lpc = torch.full((16,), ps, dtype=torch.int32)
+    rcc = rope_table(d, 40960, 1e6)
+    page_idx, indptr, delta, last, rcache = (v.to(dev) for v in (pic, ipc, dc, lpc, rcc))
     rout = torch.empty(pages, ps, hkv, d, dtype=bf, device=dev)
-    cases.append(("rerotate_paged_k_4096tok",
-                  lambda: rerotate_paged_k(kv, page_idx, indptr, delta, last, rcache, out=rout),
-                  2 * pages * ps * hkv * d * 2, 0.0))
-    gu = randn(2048, 2 * 3072)
+    rows.append(Row("rerotate_paged_k_4096tok",
+                    lambda: rerotate_paged_k(kv, page_idx, indptr, delta, last, rcache, out=rout),
+                    2 * pages * ps * hkv * d * 2,
+                    ref=lambda: _oracle().rerotate_paged_k(kvc, pic, ipc, dc, lpc, rcc), exact=True))
+    guc, gu = r.randn(2048, 2 * 3072)
     silu = SiluAndMul()
-    cases.append(("swiglu_t2048_i3072", lambda: silu(gu), 3 * 2048 * 3072 * 2, 0.0))
+    rows.append(Row("swiglu_t2048_i3072", lambda: silu(gu), 3 * 2048 * 3072 * 2,
+                    ref=lambda: _oracle().silu_and_mul(guc)))
 
-    # paged KV append at Llama-3-8B kv geometry (8 heads x 128, page 16, HND):
-    # an 8192-token prefill into 512 of 1024 shuffled pages, and a 64-sequence
-    # decode batch (one new token each) in one batched launch
-    cases += kv_append_cases(dev)
-    cases += cascade_cases(dev)
-    cases += linear_cases(dev)
-    return cases
+    rows += kv_append_cases(dev)
+    rows += cascade_cases(dev)
+    rows += linear_cases(dev)
+    return rows
 
 
 def linear_cases(dev) -> list:
@@ -259,56 +317,69 @@ def linear_cases(dev) -> list:
     and o_proj + residual (4096 -> 4096), for an 8192-token prefill and a 64-token
     decode batch.  Algorithmic bytes: operand, weight, residual and output once."""
     from braidinfer_amd.layers import gate_up_silu_and_mul, linear_add_residual
-    g = torch.Generator().manual_seed(8)
-    bf = torch.bfloat16
+    r = _Gen(8, dev)
     h, inter = 4096, 14336
-
-    def randn(*shape, std=1.0):
-        return (torch.randn(*shape, generator=g) * std).to(bf).to(dev)
-
-    w_gu, w_down, w_o = randn(2 * inter, h, std=0.02), randn(h, inter, std=0.01), randn(h, h, std=0.02)
+    (guc, w_gu), (dnc, w_down), (oc, w_o) = r.randn(2 * inter, h, std=0.02), r.randn(h, inter, std=0.01), \
+        r.randn(h, h, std=0.02)
     out = []
     for t in (8192, 64):
-        x, xi, res = randn(t, h), randn(t, inter), randn(t, h)
+        (xc, x), (xic, xi), (rc, res) = r.randn(t, h), r.randn(t, inter), r.randn(t, h)
         out += [
-            (f"gate_up_silu_llama3_8b_t{t}", (lambda x=x: gate_up_silu_and_mul(x, w_gu)),
-             (t * h + 2 * inter * h + t * inter) * 2, 2.0 * t * h * 2 * inter),
-            (f"down_proj_residual_llama3_8b_t{t}", (lambda xi=xi, res=res: linear_add_residual(xi, w_down, res)),
-             (t * inter + inter * h + 2 * t * h) * 2, 2.0 * t * inter * h),
-            (f"o_proj_residual_llama3_8b_t{t}", (lambda x=x, res=res: linear_add_residual(x, w_o, res)),
-             (2 * t * h + h * h + t * h) * 2, 2.0 * t * h * h),
+            Row(f"gate_up_silu_llama3_8b_t{t}", (lambda x=x: gate_up_silu_and_mul(x, w_gu)),
+                (t * h + 2 * inter * h + t * inter) * 2, 2.0 * t * h * 2 * inter,
+                ref=lambda xc=xc: _oracle().gate_up_silu_and_mul(xc, guc)),
+            Row(f"down_proj_residual_llama3_8b_t{t}", (lambda xi=xi, res=res: linear_add_residual(xi, w_down, res)),
+                (t * inter + inter * h + 2 * t * h) * 2, 2.0 * t * inter * h,
+                ref=lambda xic=xic, rc=rc: _oracle().linear_add_residual(xic, dnc, rc)),
+            Row(f"o_proj_residual_llama3_8b_t{t}", (lambda x=x, res=res: linear_add_residual(x, w_o, res)),
+                (2 * t * h + h * h + t * h) * 2, 2.0 * t * h * h,
+                ref=lambda xc=xc, rc=rc: _oracle().linear_add_residual(xc, oc, rc)),
         ]
     return out
 
 
 def kv_append_cases(dev) -> list:
-    """Paged KV append cases (seed 6), own scope so the lambdas bind their own tensors."""
+    """Paged KV append at Llama-3-8B kv geometry (8 heads x 128, page 16, HND;
+    seed 6): an 8192-token prefill into 512 of 1024 shuffled pages, and a
+    64-sequence decode batch (one new token each) in one batched launch.  The
+    whole cache is compared bit for bit with the oracle's."""
     from braidinfer_amd.kernels import append_paged_kv_batch, append_to_paged_kv_cache_custom
-    g = torch.Generator().manual_seed(6)
-    bf = torch.bfloat16
-
-    def randn(*shape):
-        return torch.randn(*shape, generator=g).to(bf).to(dev)
-
+    r = _Gen(6, dev)
     hkv, d, ps, pages = 8, 128, 16, 1024
-    cache = randn(pages, 2, hkv, ps, d)
-    table = torch.randperm(pages, generator=g)[:512].to(torch.int32).to(dev)
-    kp, vp = randn(8192, hkv, d), randn(8192, hkv, d)
-    pp = torch.arange(8192, dtype=torch.int32, device=dev)
-    lens = torch.randint(0, 4000, (64,), generator=g)
-    perm = torch.randperm(pages, generator=g)
+    cc, cache = r.randn(pages, 2, hkv, ps, d)
+    tc = torch.randperm(pages, generator=r.g)[:512].to(torch.int32)
+    table = tc.to(dev)
+    (kpc, kp), (vpc, vp) = r.randn(8192, hkv, d), r.randn(8192, hkv, d)
+    ppc = torch.arange(8192, dtype=torch.int32)
+    pp = ppc.to(dev)
+    lens = torch.randint(0, 4000, (64,), generator=r.g)
+    perm = torch.randperm(pages, generator=r.g)
     # sequence s: a table of lens[s] // 16 + 1 entries whose last (the one written) is a
     # page of its own
     per = lens // ps + 1
-    ind = torch.cat([perm[s].repeat(int(per[s])) for s in range(64)]).to(torch.int32).to(dev)
-    indptr = torch.cat([torch.zeros(1, dtype=torch.int64), per.cumsum(0)]).to(torch.int32).to(dev)
-    bat = torch.arange(64, device=dev)
-    pd = lens.to(dev)
-    kd, vd = randn(64, hkv, d), randn(64, hkv, d)
-    return [("kv_append_t8192", lambda: append_to_paged_kv_cache_custom(kp, vp, cache, table, pp, ps),
-             4 * 8192 * hkv * d * 2 + 8192 * 4 + 512 * 4, 0.0),
-            ("kv_append_batch_b64", lambda: append_paged_kv_batch(kd, vd, cache, ind, indptr, bat, pd, ps),
-             4 * 64 * hkv * d * 2 + 64 * (8 + 8 + 4) + 65 * 4, 0.0)]
+    indc = torch.cat([perm[s].repeat(int(per[s])) for s in range(64)]).to(torch.int32)
+    iptc = torch.cat([torch.zeros(1, dtype=torch.int64), per.cumsum(0)]).to(torch.int32)
+    batc = torch.arange(64)
+    ind, indptr, bat, pd = indc.to(dev), iptc.to(dev), batc.to(dev), lens.to(dev)
+    (kdc, kd), (vdc, vd) = r.randn(64, hkv, d), r.randn(64, hkv, d)
+
+    cache_b = cache.clone()  # the batched append writes a cache of its own
+
+    def prefill():
+        append_to_paged_kv_cache_custom(kp, vp, cache, table, pp, ps)
+        return cache
+
+    def batch():
+        append_paged_kv_batch(kd, vd, cache_b, ind, indptr, bat, pd, ps)
+        return cache_b
+    # each append writes the same values on every call, so the cache after the
+    # timed repeats equals the oracle's single append into the initial cache
+    return [Row("kv_append_t8192", prefill, 4 * 8192 * hkv * d * 2 + 8192 * 4 + 512 * 4,
+                ref=lambda: _oracle().append_to_paged_kv_cache(kpc, vpc, cc, tc, ppc, ps)[0], exact=True,
+                note="whole cache compared"),
+            Row("kv_append_batch_b64", batch, 4 * 64 * hkv * d * 2 + 64 * (8 + 8 + 4) + 65 * 4,
+                ref=lambda: _oracle().append_paged_kv_batch(kdc, vdc, cc, indc, iptc, batc, lens, ps)[0],
+                exact=True, note="whole cache compared")]
 
 
 def cascade_cases(dev) -> list:
@@ -322,7 +393,8 @@ def cascade_cases(dev) -> list:
     g = torch.Generator().manual_seed(7)
     bf = torch.bfloat16
     hq, hkv, d, ps, pages = 16, 8, 128, 16, 512
-    kv = torch.randn(pages, 2, hkv, ps, d, generator=g).to(bf).to(dev)
+    kvc = torch.randn(pages, 2, hkv, ps, d, generator=g).to(bf)
+    kv = kvc.to(dev)
     perm = torch.randperm(pages, generator=g).tolist()
     deltas = torch.randint(-4096, 4097, (16,), generator=g).tolist()
     chunks = [SimpleNamespace(page_table=perm[16 * c:16 * c + 16], kv_length=256,
@@ -333,24 +405,28 @@ def cascade_cases(dev) -> list:
     rope = RotaryEmbedding(d, d, 40960, 1e6).to(dev)
     att = CascadeAttention(hq, d, d ** -0.5, hkv, ps, rotary_emb=rope)
     levels = att.create_cascade_levels(chunks)
+    cpu_levels = [SimpleNamespace(chunks=lv.chunks, kv_page_indices=lv.kv_page_indices.cpu(),
+                                  kv_page_indptr=lv.kv_page_indptr.cpu(),
+                                  kv_last_page_len=lv.kv_last_page_len.cpu()) for lv in levels]
+    knc = torch.exp(torch.empty(d).uniform_(_m.log(0.05), _m.log(100.0), generator=g)).to(bf)
     k_norm = RMSNorm(d, eps=1e-6).to(dev)
     with torch.no_grad():
-        k_norm.weight.data = torch.exp(torch.empty(d).uniform_(_m.log(0.05), _m.log(100.0), generator=g)).to(bf).to(dev)
+        k_norm.weight.data = knc.to(dev)
+    csc = rope.cos_sin_cache.cpu()
     kv_bytes = 4096 * hkv * d * 2 * 2
     out = []
     for t in (1, 256):
-        q = torch.randn(t, hq, d, generator=g).to(bf).to(dev)
-        qpos = torch.arange(4096 - t + 1, 4097, device=dev)
-        out.append((f"cascade_attention_qwen3_4096kv_t{t}",
-                    (lambda q=q, qpos=qpos: att.forward(q, qpos, kv, levels, 0, k_norm=k_norm)),
-                    kv_bytes + 2 * t * hq * d * 2, 4.0 * t * hq * 4096 * d))
+        qc = torch.randn(t, hq, d, generator=g).to(bf)
+        q = qc.to(dev)
+        qpc = torch.arange(4096 - t + 1, 4097)
+        qpos = qpc.to(dev)
+        out.append(Row(f"cascade_attention_qwen3_4096kv_t{t}",
+                       (lambda q=q, qpos=qpos: att.forward(q, qpos, kv, levels, 0, k_norm=k_norm)),
+                       kv_bytes + 2 * t * hq * d * 2, 4.0 * t * hq * 4096 * d,
+                       ref=lambda qc=qc, qpc=qpc: _oracle().cascade_attention(
+                           qc, qpc, kvc, cpu_levels, hq, hkv, d ** -0.5, ps, cos_sin_cache=csc,
+                           k_norm_weight=knc, k_norm_eps=1e-6)))
     return out
-
-
-def config_table(dev, iters: int) -> dict:
-    """Each case of config_cases graph-timed, with its roofline fractions."""
-    return {name: _roof_row(time_graph(fn, iters), nbytes, flops)
-            for name, fn, nbytes, flops in config_cases(dev)}
 
 
 def _capture(fn, reps: int) -> torch.cuda.CUDAGraph:
@@ -414,34 +490,18 @@ def time_cold(fn, iters: int, flush: torch.Tensor) -> float:
     return sum(s.elapsed_time(e) for s, e in pairs) / iters
 
 
-def cold_decode_table(dev, t: int, iters: int) -> dict:
-    """Decode-shape kernels streaming their operands from HBM (cache flushed)."""
-    c = Chain(t, dev)
-    flush = torch.empty(512 * 2**20 // 4, dtype=torch.float32, device=dev)
-    out = {}
-    for name, fn, nbytes in (
-        ("add_rms_norm", lambda: c.norm(c.x, c.residual), 4 * t * H * 2 + H * 2),
-        ("fused_rmsnorm_qkv_rope", c.qkv,
-         t * H * 2 + H * 2 + N * H * 2 + t * N * 2 + t * 8 + t * D * 4),
-        ("silu_and_mul", lambda: c.silu(c.gate_up), 3 * t * INTER * 2),
-    ):
-        ms = time_cold(fn, iters, flush)
-        gbs = nbytes / (ms * 1e-3) / 1e9
-        out[name] = {"us": round(ms * 1e3, 3), "gbs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
-    del c, flush
-    return out
-
-
 def chain_graph_us(c: Chain, steps: int, warmup: int) -> float:
     """Microseconds per chain step: `steps` steps captured into one HIP graph;
-    `warmup` untimed steps (whole replays of the graph, at least one), then
-    exactly `steps` timed steps between HIP events."""
+    `warmup` untimed steps (whole replays of the graph, at least one) and 0.3 s
+    of untimed replays for the clock to settle, then exactly `steps` timed steps
+    between HIP events."""
     graph = _capture(c.step, steps)
     done = 0
     while done < max(warmup, 1):
         graph.replay()
         done += steps
     torch.cuda.synchronize()
+    _settle(graph, 0.3)
     s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     s.record()
     graph.replay()
@@ -463,42 +523,96 @@ def chain_us(c: Chain, steps: int, warmup: int) -> float:
     return s.elapsed_time(e) / steps * 1e3
 
 
-def cpu_baseline(t_full: int, budget_s: float = 12.0) -> dict:
-    """The oracle's torch-CPU restatement of the same chain on a token sample,
-    scaled linearly to t_full tokens (rows of every op are independent)."""
-    from oracle import torch_ref as R
-    threads = len(os.sched_getaffinity(0))
-    torch.set_num_threads(threads)
-    ts = 256
-    g = torch.Generator().manual_seed(5)
-    bf = torch.bfloat16
-    x = torch.randn(ts, H, generator=g).to(bf)
-    res = torch.randn(ts, H, generator=g).to(bf)
-    w = (torch.randn(H, generator=g) * 0.1 + 1).to(bf)
-    wq = (torch.randn(N, H, generator=g) * 0.02).to(bf)
-    pos = torch.randint(0, MAXPOS, (ts,), generator=g)
-    cache = rope_table(D, MAXPOS, THETA)
-    gu = torch.randn(ts, 2 * INTER, generator=g).to(bf)
+def measure_rows(rows: list, iters: int, flush: torch.Tensor, cold_iters: int) -> dict:
+    """Warm (graph-replayed, settled clock, operands left in the caches by the
+    previous call) and cold (Infinity Cache flushed before each call) GPU time of
+    every row, with its roofline fractions."""
+    out = {}
+    for r in rows:
+        d = _roof_row(time_graph(r.fn, iters), r.nbytes, r.flops)
+        if cold_iters > 0:
+            cold_ms = time_cold(r.fn, cold_iters, flush)
+            d["us_cold"] = round(cold_ms * 1e3, 3)
+            d["hbm_frac_cold"] = round(r.nbytes / (cold_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
+        if r.note:
+            d["note"] = r.note
+        out[r.name] = d
+    return out
 
-    def step():
-        R.add_rms_forward(x, res, w, EPS)
-        R.llama_attention_input(x, w, wq, HQ, HKV, EPS, pos, cache)
-        R.silu_and_mul(gu)
 
-    step()
+def _bits(t: torch.Tensor) -> torch.Tensor:
+    t = t.contiguous()
+    return t.view({2: torch.int16, 4: torch.int32, 8: torch.int64}[t.element_size()])
+
+
+def compare(got: torch.Tensor, exp: torch.Tensor, exact: bool) -> dict:
+    """Error figures of a GPU result against the oracle's: bit-exact for the
+    integer/byte ops; otherwise max-abs, normwise relative error and the
+    elements outside |d| <= 2e-2 + 1e-2 |r| (the float tolerance; those are
+    the elements a documented rounding allowance of the parity tests covers)."""
+    got = got.detach().cpu()
+    if exact:
+        mism = int((_bits(got) != _bits(exp)).sum())
+        return {"bit_exact": mism == 0, "mismatches": mism, "numel": exp.numel()}
+    a, e = got.float(), exp.float()
+    fin = torch.isfinite(e)
+    same_pattern = bool(torch.equal(torch.isfinite(a), fin))
+    d = (a - e).abs()[fin]
+    ef = e[fin]
+    outside = int((d > 2e-2 + 1e-2 * ef.abs()).sum())
+    return {"max_abs": float(f"{d.max().item():.4g}") if d.numel() else 0.0,
+            "max_rel_normwise": float(f"{(d.norm() / ef.norm().clamp_min(1e-30)).item():.4g}"),
+            "allclose": same_pattern and outside == 0, "beyond_tol_elements": outside, "numel": exp.numel()}
+
+
+def time_cpu(fn, min_reps: int = 3, max_reps: int = 10, budget_s: float = 3.0):
+    """Median seconds of `fn` on the CPU over at least `min_reps` runs (more, up
+    to `max_reps`, while within `budget_s`), after one untimed run whose result
+    is returned."""
+    result = fn()
     times = []
     t0 = time.perf_counter()
-    while time.perf_counter() - t0 < budget_s and len(times) < 30:
+    while len(times) < max_reps and (len(times) < min_reps or time.perf_counter() - t0 < budget_s):
         s = time.perf_counter()
-        step()
+        fn()
         times.append(time.perf_counter() - s)
     times.sort()
-    med = times[len(times) // 2]
-    return {"value": round(med * 1e6 * t_full / ts, 1), "unit": "us/layer", "cores": threads,
-            "kind": "port",
-            "sample": f"oracle torch-CPU chain (add_rms_forward, llama attention input: minimal_f32 "
-                      f"QKV + RoPE, silu_and_mul) at {ts} tokens, median of {len(times)} runs, "
-                      f"scaled x{t_full / ts:g} to {t_full} tokens; torch {torch.__version__}"}
+    return times[len(times) // 2], len(times), result
+
+
+def cpu_info() -> dict:
+    model = "unknown"
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"model": model, "threads": len(os.sched_getaffinity(0)),
+            "parallel_info": torch.__config__.parallel_info()}
+
+
+def cpu_leg(groups: dict, tables: dict) -> None:
+    """The CPU baseline and check: each row's oracle (the torch-CPU restatement of
+    the reference) runs at the row's full size on the host cores -- timed,
+    median of >= 3 runs -- and the GPU result is compared with it.  Adds cpu_us,
+    cpu_reps and the error figures to the rows of `tables`."""
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    for gname, rows in groups.items():
+        for r in rows:
+            if r.ref is None:
+                continue
+            got = r.fn()
+            if r.got is not None:
+                got = r.got(got)
+            torch.cuda.synchronize()
+            sec, reps, exp = time_cpu(r.ref)
+            row = tables[gname][r.name]
+            row["cpu_us"] = round(sec * 1e6, 1)
+            row["cpu_reps"] = reps
+            row["vs_oracle"] = compare(got, exp, r.exact)
 
 
 def read_traffic(name: str):
@@ -516,7 +630,7 @@ def read_traffic(name: str):
 def profile_one(kernel: str, tokens: int, steps: int, dev) -> int:
     """Runs one kernel `steps` times on the chain's inputs (or one case of
     config_cases by name); prints its event-timed average."""
-    cases = {name: fn for name, fn, _, _ in config_cases(dev)} if kernel.startswith("case:") else {}
+    cases = {r.name: r.fn for r in config_cases(dev)} if kernel.startswith("case:") else {}
     if cases:
         ms = time_fn(cases[kernel[5:]], steps)
         print(json.dumps({"kernel": kernel, "calls": steps, "us": round(ms * 1e3, 3)}))
@@ -556,7 +670,7 @@ def main(argv=None) -> int:
     ap.add_argument("--tokens", type=int, default=8192)
     ap.add_argument("--decode-tokens", type=int, default=64)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--no-cold", action="store_true", help="skip the cold-cache decode table")
+    ap.add_argument("--no-cold", action="store_true", help="skip the cold-cache timings")
     ap.add_argument("--kernel", help="only run this kernel --steps times at --tokens (for "
                     "profilers): qkv_projection, qkv_operand, add_rms_norm, silu_and_mul, "
                     "embedding, copy, library_gemm (the projection's product through torch.mm), or "
@@ -581,25 +695,39 @@ def main(argv=None) -> int:
         print(f"bench: {stage}", file=sys.stderr, flush=True)
 
     progress(f"prefill chain, {args.tokens} tokens")
+    flush = torch.empty(512 * 2**20 // 4, dtype=torch.float32, device=dev)
     prefill = Chain(args.tokens, dev)
     us_eager = chain_us(prefill, args.steps, args.warmup)
     us = chain_graph_us(prefill, args.steps, args.warmup)
-    kp = kernel_table(prefill, dev, max(10, args.steps))
+    rows_p = chain_rows(prefill, dev, stages=True)
+    nc = 0 if args.no_cold else 1
+    kp = measure_rows(rows_p, max(10, args.steps), flush, 10 * nc)
     proj = kp["qkv_projection_rope"]
-    del prefill
-    torch.cuda.empty_cache()
 
     progress(f"decode chain, {args.decode_tokens} tokens")
     decode = Chain(args.decode_tokens, dev)
     us_dec_eager = chain_us(decode, max(args.steps, 100), args.warmup)
     us_dec = chain_graph_us(decode, max(args.steps, 100), max(args.warmup, 1000))
-    kd = kernel_table(decode, dev, max(50, args.steps))
-    del decode
-    torch.cuda.empty_cache()
-    cold = None if args.no_cold else cold_decode_table(dev, args.decode_tokens, 48)
+    rows_d = chain_rows(decode, dev, stages=False)
+    kd = measure_rows(rows_d, max(50, args.steps), flush, 48 * nc)
     progress("other configurations")
-    configs = config_table(dev, max(40, args.steps))
+    rows_c = config_cases(dev)
+    configs = measure_rows(rows_c, max(40, args.steps), flush, 24 * nc)
     _lib.check_device_status(dev)
+    tables = {"prefill": kp, "decode": kd, "configs": configs}
+    cpu = None
+    if not args.no_cpu:
+        progress("CPU baseline and checks against the oracle")
+        cpu_leg({"prefill": rows_p, "decode": rows_d, "configs": rows_c}, tables)
+        chain = ("add_rms_norm", "fused_rmsnorm_qkv_rope", "silu_and_mul")
+        cpu = {"value": round(sum(kp[k]["cpu_us"] for k in chain), 1), "unit": "us/layer",
+               "cores": len(os.sched_getaffinity(0)), "kind": "port",
+               "sample": f"the full {args.tokens}-token chain, not a sample: the oracle's torch-CPU "
+                         f"add_rms_forward, llama attention input (minimal_f32 QKV + RoPE) and "
+                         f"silu_and_mul at [{args.tokens}, 4096] / [{args.tokens}, 2x14336], each the "
+                         f"median of >= 3 runs (kernels_prefill.*.cpu_us); torch {torch.__version__}"}
+    del prefill, decode, flush
+    torch.cuda.empty_cache()
 
     line = {
         "metric": "us/layer + % HBM / % MFMA peak, fused norm+QKV+RoPE+SwiGLU, 1 MI355X",
@@ -622,17 +750,22 @@ def main(argv=None) -> int:
         "roofline": {"bound": "mfma", "kernel": "qkv_projection_rope",
                      "achieved": proj["tflops"], "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": proj["mfma_frac"],
-                     "traffic": read_traffic(f"traffic_qkv_projection_llama3_8b_t{args.tokens}")},
+                     "traffic": read_traffic(f"traffic_qkv_projection_llama3_8b_t{args.tokens}"),
+                     "traffic_source": f"profiles/traffic_qkv_projection_llama3_8b_t{args.tokens}.txt "
+                                       "(rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, calibrated on a device "
+                                       "copy; read from the file, not measured in this run)"},
         "kernels_prefill": kp,
         "eager_us_per_layer": round(us_eager, 2),
         "decode": {"tokens": args.decode_tokens, "us_per_layer": round(us_dec, 2),
-                   "eager_us_per_layer": round(us_dec_eager, 2),
-                   "kernels_warm": kd, "kernels_cold": cold},
+                   "eager_us_per_layer": round(us_dec_eager, 2), "kernels": kd},
         "configs": configs,
+        "timing": "us: graph-replayed HIP-event average after >= 0.2 s of settling replays (warm: "
+                  "operands in the caches from the previous call); us_cold: each call after a 512 MB "
+                  "read that flushes the 256 MB Infinity Cache",
+        "cpu": cpu_info() if not args.no_cpu else None,
     }
-    if not args.no_cpu:
-        progress("CPU baseline")
-        line["cpu_baseline"] = cpu_baseline(args.tokens)
+    if cpu is not None:
+        line["cpu_baseline"] = cpu
     print(json.dumps(line))
     return 0
 
