@@ -21,7 +21,7 @@ LIB_PATH = Path(__file__).resolve().parent / "lib" / "libbraidinfer_amd.so"
 ABI_VERSION = 1
 
 F32, F16, BF16, I32, I64 = 0, 1, 2, 3, 4
-_DTYPE_CODE = {
+DTYPE_CODE = _DTYPE_CODE = {
     torch.float32: F32,
     torch.float16: F16,
     torch.bfloat16: BF16,
@@ -138,11 +138,51 @@ def call(name: str, *args) -> int:
     if name.endswith("workspace_size"):
         return rc
     if rc < 0:
-        msg = lib.bfa_last_error().decode(errors="replace")
-        if rc == -1:
-            raise ValueError(msg)
-        raise BraidinferAMDError(msg)
+        raise_error(rc)
     return rc
+
+
+def entry(name: str):
+    """The bound ctypes function of entry point `name`, for hot paths that call
+    it directly and pass a negative return code to raise_error()."""
+    return getattr(load(), name)
+
+
+def raise_error(rc: int) -> None:
+    msg = load().bfa_last_error().decode(errors="replace")
+    if rc == -1:
+        raise ValueError(msg)
+    raise BraidinferAMDError(msg)
+
+
+def workspace_size(name: str, *args) -> int:
+    """`<name>(*args)` of a workspace-size entry point (not memoised: the plan
+    it reflects also follows the BFA_* measurement overrides of the process
+    environment)."""
+    return getattr(load(), name)(*args)
+
+
+_workspaces: dict = {}
+
+
+def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    """A device scratch buffer of at least `nbytes` (16-byte aligned) for a
+    kernel launched on the current stream.  Outside graph capture one buffer
+    per (device, stream) is kept and reused: launches on one stream are ordered,
+    so a call's kernels finish with it before the next call's start.  Under
+    graph capture a fresh allocation from the graph's pool is returned, so a
+    captured graph never shares (or outlives) the eager buffer."""
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    stream = stream_of(device)
+    if torch.cuda.is_current_stream_capturing():
+        return torch.empty(max(nbytes, 16), dtype=torch.uint8, device=device)
+    key = (idx, stream)
+    buf = _workspaces.get(key)
+    if buf is None or buf.numel() < nbytes:
+        buf = torch.empty(max(nbytes, 16, 0 if buf is None else 2 * buf.numel()), dtype=torch.uint8,
+                          device=device)
+        _workspaces[key] = buf
+    return buf
 
 
 def dtype_code(t: torch.Tensor | torch.dtype) -> int:
@@ -161,21 +201,22 @@ def ptr(t: torch.Tensor | None):
 
 def require_device(*tensors: torch.Tensor | None) -> torch.device:
     """All given tensors must live on one ROCm device; returns it."""
-    dev = None
+    first = None
+    idx = -1
     for t in tensors:
         if t is None:
             continue
-        if t.device.type != "cuda":
+        if not t.is_cuda:
             raise RuntimeError(
                 "braidinfer_amd ops run only on ROCm devices (got a tensor on "
                 f"{t.device}); there is no CPU path")
-        if dev is None:
-            dev = t.device
-        elif t.device != dev:
-            raise RuntimeError(f"braidinfer_amd: tensors on different devices ({dev}, {t.device})")
-    if dev is None:
+        if first is None:
+            first, idx = t, t.get_device()
+        elif t.get_device() != idx:
+            raise RuntimeError(f"braidinfer_amd: tensors on different devices ({first.device}, {t.device})")
+    if first is None:
         raise RuntimeError("braidinfer_amd: no device tensor given")
-    return dev
+    return first.device
 
 
 _raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)

@@ -59,16 +59,17 @@ def fused_rmsnorm_qkv(
     qkv_dim = qkv_weight.shape[0]
     if input.stride(-1) != 1 or input.data_ptr() % 16 != 0:
         input = input.contiguous()
-    norm_weight = norm_weight.contiguous()
+    if not norm_weight.is_contiguous():
+        norm_weight = norm_weight.contiguous()
     w = _matrix_weight(qkv_weight)
-    if qkv_bias is not None:
+    if qkv_bias is not None and not qkv_bias.is_contiguous():
         qkv_bias = qkv_bias.contiguous()
     dev = _lib.require_device(input, norm_weight, w, qkv_bias, q_norm_weight, k_norm_weight,
                               positions, cos_sin_cache)
     hd = head_dim_of(qkv_dim, num_q_heads, num_kv_heads)
-    if q_norm_weight is not None:
+    if q_norm_weight is not None and not q_norm_weight.is_contiguous():
         q_norm_weight = q_norm_weight.contiguous()
-    if k_norm_weight is not None:
+    if k_norm_weight is not None and not k_norm_weight.is_contiguous():
         k_norm_weight = k_norm_weight.contiguous()
     qn_dtype = (q_norm_weight if q_norm_weight is not None else k_norm_weight)
     if q_norm_weight is not None and k_norm_weight is not None and q_norm_weight.dtype != k_norm_weight.dtype:
@@ -78,26 +79,28 @@ def fused_rmsnorm_qkv(
             raise ValueError("RoPE needs positions")
         if cos_sin_cache.dtype != torch.float32:
             raise TypeError("cos_sin_cache must be float32")
-        cos_sin_cache = cos_sin_cache.contiguous()
+        if not cos_sin_cache.is_contiguous():
+            cos_sin_cache = cos_sin_cache.contiguous()
         if cos_sin_cache.shape[-1] != hd:
             raise ValueError(f"cos_sin_cache width {cos_sin_cache.shape[-1]} != head_dim {hd}")
-        positions = positions.reshape(-1)
+        if positions.dim() != 1:
+            positions = positions.reshape(-1)
         if positions.numel() != tokens:
             raise ValueError(f"{positions.numel()} positions for {tokens} tokens")
         if positions.dtype not in (torch.int64, torch.int32):
             positions = positions.long()
-        positions = positions.contiguous()
+        if not positions.is_contiguous():
+            positions = positions.contiguous()
     if out is None:
         out = torch.empty((tokens, qkv_dim), dtype=out_dtype, device=dev)
     if tokens == 0:
         return out
-    ws_bytes = _lib.call("bfa_fused_rmsnorm_qkv_workspace_size", tokens, hidden, qkv_dim, hd)
-    workspace = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=dev)
-    _lib.call(
-        "bfa_fused_rmsnorm_qkv",
-        _lib.ptr(input), _lib.dtype_code(input), tokens, hidden, input.stride(0),
-        _lib.ptr(norm_weight), _lib.dtype_code(norm_weight), float(eps), int(mixed_rounding),
-        _lib.ptr(w), _lib.dtype_code(w), qkv_dim, w.stride(0),
+    ws_bytes = _lib.workspace_size("bfa_fused_rmsnorm_qkv_workspace_size", tokens, hidden, qkv_dim, hd)
+    workspace = _lib.workspace(dev, ws_bytes)
+    rc = _FUSED()(
+        input.data_ptr(), _lib.dtype_code(input), tokens, hidden, input.stride(0),
+        norm_weight.data_ptr(), _lib.dtype_code(norm_weight), float(eps), int(mixed_rounding),
+        w.data_ptr(), _lib.dtype_code(w), qkv_dim, w.stride(0),
         _lib.ptr(qkv_bias), _lib.dtype_code(qkv_bias) if qkv_bias is not None else 0,
         num_q_heads, num_kv_heads, _lib.dtype_code(qkv_dtype),
         _lib.ptr(q_norm_weight), _lib.ptr(k_norm_weight),
@@ -105,11 +108,23 @@ def fused_rmsnorm_qkv(
         _lib.dtype_code(qk_norm_out_dtype or input.dtype),
         _lib.ptr(positions), _lib.dtype_code(positions) if positions is not None else 0,
         _lib.ptr(cos_sin_cache), cos_sin_cache.shape[0] if cos_sin_cache is not None else 0,
-        _lib.ptr(out), _lib.dtype_code(out), out.stride(0),
-        _lib.ptr(workspace), workspace.numel(),
-        _lib.ptr(_lib.status_word(dev)), _lib.stream_of(dev),
+        out.data_ptr(), _lib.dtype_code(out), out.stride(0),
+        workspace.data_ptr(), workspace.numel(),
+        _lib.status_word(dev).data_ptr(), _lib.stream_of(dev),
     )
+    if rc < 0:
+        _lib.raise_error(rc)
     return out
+
+
+_fused_fn = None
+
+
+def _FUSED():
+    global _fused_fn
+    if _fused_fn is None:
+        _fused_fn = _lib.entry("bfa_fused_rmsnorm_qkv")
+    return _fused_fn
 
 
 def split_heads(output: torch.Tensor, num_q_heads: int, num_kv_heads: int):

@@ -155,9 +155,9 @@ class CascadeAttention:
         qpos = qpos[:tokens].contiguous()
         if qpos.dtype not in (torch.int32, torch.int64):
             qpos = qpos.long()
-        ws_bytes = _lib.call("bfa_cascade_attention_workspace_size", tokens, self.num_heads, hkv, d,
-                             entries, self.page_size)
-        ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=dev)
+        ws_bytes = _lib.workspace_size("bfa_cascade_attention_workspace_size", tokens, self.num_heads, hkv, d,
+                                       entries, self.page_size)
+        ws = _lib.workspace(dev, ws_bytes)
         st = kv_cache.stride()
         _lib.call(
             "bfa_cascade_attention",

@@ -55,6 +55,16 @@ def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float, out: torch.Tenso
     return out
 
 
+_add_rms_fn = None
+
+
+def _ADD_RMS():
+    global _add_rms_fn
+    if _add_rms_fn is None:
+        _add_rms_fn = _lib.entry("bfa_add_rms_norm")
+    return _add_rms_fn
+
+
 class RMSNorm(nn.Module):
 
     def __init__(self, hidden_size: int, eps: float = 1e-6) -> None:
@@ -73,9 +83,29 @@ class RMSNorm(nn.Module):
         return rms_norm(x, self.weight, self.eps)
 
     def add_rms_forward(self, x: torch.Tensor, residual: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+        # common case first: 16-bit x and residual of one contiguous shape on one device
+        if (x.dtype != torch.float32 and x.is_cuda and x.is_contiguous() and residual.is_contiguous()
+                and residual.shape == x.shape and residual.dtype == x.dtype and residual.device == x.device):
+            weight = self.weight
+            if weight.is_cuda and weight.is_contiguous() and weight.device == x.device:
+                hidden = x.shape[-1]
+                y = torch.empty_like(x)
+                res_out = torch.empty_like(x)
+                code = _lib.DTYPE_CODE[x.dtype]
+                rc = _ADD_RMS()(x.data_ptr(), residual.data_ptr(), y.data_ptr(), res_out.data_ptr(),
+                                weight.data_ptr(), code, _lib.dtype_code(weight), x.numel() // hidden, hidden,
+                                hidden, hidden, hidden, hidden, float(self.eps), _lib.stream_of(x.device))
+                if rc < 0:
+                    _lib.raise_error(rc)
+                return y, res_out
         hidden = x.shape[-1]
-        weight = self.weight.contiguous()
-        dev = _lib.require_device(x, residual, weight)
+        weight = self.weight
+        if not weight.is_contiguous():
+            weight = weight.contiguous()
+        if x.is_cuda and residual.is_cuda and weight.is_cuda and x.device == residual.device == weight.device:
+            dev = x.device
+        else:
+            dev = _lib.require_device(x, residual, weight)
         inplace = x.dtype == torch.float32
         # 2-D row views (views of x itself when its layout allows, so the fp32
         # in-place form writes through to the caller's tensor)
@@ -97,10 +127,11 @@ class RMSNorm(nn.Module):
             return x, x
         y = torch.empty(x.shape, dtype=x.dtype, device=dev)
         res_out = torch.empty(x.shape, dtype=x.dtype, device=dev)
-        _lib.call("bfa_add_rms_norm", _lib.ptr(work), _lib.ptr(r2), _lib.ptr(y), _lib.ptr(res_out),
-                  _lib.ptr(weight), _lib.dtype_code(work), _lib.dtype_code(weight), rows, hidden,
-                  work.stride(0), r2.stride(0), hidden, hidden, float(self.eps),
-                  _lib.stream_of(dev))
+        rc = _ADD_RMS()(work.data_ptr(), r2.data_ptr(), y.data_ptr(), res_out.data_ptr(), weight.data_ptr(),
+                        _lib.dtype_code(work), _lib.dtype_code(weight), rows, hidden, work.stride(0),
+                        r2.stride(0), hidden, hidden, float(self.eps), _lib.stream_of(dev))
+        if rc < 0:
+            _lib.raise_error(rc)
         return y, res_out
 
     def forward(self, x: torch.Tensor, residual: torch.Tensor | None = None):

@@ -67,8 +67,8 @@ def _run(x: torch.Tensor, weight: torch.Tensor, n: int, mode: int, bias=None, re
         if bias.numel() != n:
             raise ValueError(f"bias has {bias.numel()} elements, the layer has {n} outputs")
         bias = bias.detach().contiguous()
-    ws_bytes = _lib.call("bfa_linear_workspace_size", tokens, k, n, mode)
-    ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=dev)
+    ws_bytes = _lib.workspace_size("bfa_linear_workspace_size", tokens, k, n, mode)
+    ws = _lib.workspace(dev, ws_bytes)
     _lib.call(
         "bfa_linear", _lib.ptr(x2), _lib.dtype_code(x2), tokens, k, x2.stride(0),
         _lib.ptr(weight), n, weight.stride(0), _lib.ptr(bias),
