@@ -236,7 +236,8 @@ def config_cases(dev) -> list:
       kv_append   paged KV append, 8 kv heads x 128, page 16: 8192-token prefill,
                   and a 64-sequence decode batch in one launch
       cascade     paged cascade attention over 4096 cached Qwen3 tokens (16 moved
-                  chunks, k_norm), 1 and 256 query tokens
+                  chunks, k_norm) and 2048 cached TinyLlama tokens (head_dim 64),
+                  1 and 256 query tokens
       linear      gate_up+SiluAndMul, down_proj+residual, o_proj+residual at
                   Llama-3-8B shapes, T 8192 and 64"""
     from braidinfer_amd.layers import llama_attention_input, qwen3_attention_input, rerotate_paged_k
@@ -386,43 +387,57 @@ def cascade_cases(dev) -> list:
     """Cascade attention at Qwen3-0.6B shape (seed 7): 4096 cached tokens in 16 chunks of
     256, shuffled 16-token HND pages, each chunk moved by a delta in [-4096, 4096]
     (theta 1e6, rotary table 40960), k_norm with log-uniform weights; 16 query heads
-    over 8 kv heads of 128.  A one-token decode step and a 256-token query chunk."""
+    over 8 kv heads of 128.  A one-token decode step and a 256-token query chunk.
+    The same at TinyLlama-1.1B shape (seed 9): 32 query heads over 4 kv heads of 64,
+    theta 1e4 (rotary table 4096), no k_norm, 2048 cached tokens in 8 chunks moved
+    by up to +-1024."""
+    return (_cascade_rows(dev, "qwen3", 7, 16, 8, 128, 4096, 1e6, 40960, True)
+            + _cascade_rows(dev, "tinyllama", 9, 32, 4, 64, 2048, 1e4, 4096, False))
+
+
+def _cascade_rows(dev, label, seed, hq, hkv, d, keys, theta, max_pos, knorm) -> list:
     import math as _m
     from types import SimpleNamespace
     from braidinfer_amd.layers import CascadeAttention, RMSNorm, RotaryEmbedding
-    g = torch.Generator().manual_seed(7)
+    g = torch.Generator().manual_seed(seed)
     bf = torch.bfloat16
-    hq, hkv, d, ps, pages = 16, 8, 128, 16, 512
+    ps = 16
+    nch = keys // 256
+    pages = 2 * keys // ps
     kvc = torch.randn(pages, 2, hkv, ps, d, generator=g).to(bf)
     kv = kvc.to(dev)
     perm = torch.randperm(pages, generator=g).tolist()
-    deltas = torch.randint(-4096, 4097, (16,), generator=g).tolist()
+    span = min(4096, max_pos // 4)
+    deltas = torch.randint(-span, span + 1, (nch,), generator=g).tolist()
+    start = 8192 if max_pos > 8192 else 0  # cached position of the first chunk
     chunks = [SimpleNamespace(page_table=perm[16 * c:16 * c + 16], kv_length=256,
-                              cached_position_start=8192 + 256 * c,
-                              global_position_start=8192 + 256 * c + deltas[c],
+                              cached_position_start=start + 256 * c,
+                              global_position_start=start + 256 * c + deltas[c],
                               chunk_type=SimpleNamespace(value="system_prompt" if c == 0 else "context"))
-              for c in range(16)]
-    rope = RotaryEmbedding(d, d, 40960, 1e6).to(dev)
+              for c in range(nch)]
+    rope = RotaryEmbedding(d, d, max_pos, theta).to(dev)
     att = CascadeAttention(hq, d, d ** -0.5, hkv, ps, rotary_emb=rope)
     levels = att.create_cascade_levels(chunks)
     cpu_levels = [SimpleNamespace(chunks=lv.chunks, kv_page_indices=lv.kv_page_indices.cpu(),
                                   kv_page_indptr=lv.kv_page_indptr.cpu(),
                                   kv_last_page_len=lv.kv_last_page_len.cpu()) for lv in levels]
-    knc = torch.exp(torch.empty(d).uniform_(_m.log(0.05), _m.log(100.0), generator=g)).to(bf)
-    k_norm = RMSNorm(d, eps=1e-6).to(dev)
-    with torch.no_grad():
-        k_norm.weight.data = knc.to(dev)
+    knc, k_norm = None, None
+    if knorm:
+        knc = torch.exp(torch.empty(d).uniform_(_m.log(0.05), _m.log(100.0), generator=g)).to(bf)
+        k_norm = RMSNorm(d, eps=1e-6).to(dev)
+        with torch.no_grad():
+            k_norm.weight.data = knc.to(dev)
     csc = rope.cos_sin_cache.cpu()
-    kv_bytes = 4096 * hkv * d * 2 * 2
+    kv_bytes = keys * hkv * d * 2 * 2
     out = []
     for t in (1, 256):
         qc = torch.randn(t, hq, d, generator=g).to(bf)
         q = qc.to(dev)
-        qpc = torch.arange(4096 - t + 1, 4097)
+        qpc = torch.arange(keys - t + 1, keys + 1)
         qpos = qpc.to(dev)
-        out.append(Row(f"cascade_attention_qwen3_4096kv_t{t}",
+        out.append(Row(f"cascade_attention_{label}_{keys}kv_t{t}",
                        (lambda q=q, qpos=qpos: att.forward(q, qpos, kv, levels, 0, k_norm=k_norm)),
-                       kv_bytes + 2 * t * hq * d * 2, 4.0 * t * hq * 4096 * d,
+                       kv_bytes + 2 * t * hq * d * 2, 4.0 * t * hq * keys * d,
                        ref=lambda qc=qc, qpc=qpc: _oracle().cascade_attention(
                            qc, qpc, kvc, cpu_levels, hq, hkv, d ** -0.5, ps, cos_sin_cache=csc,
                            k_norm_weight=knc, k_norm_eps=1e-6)))

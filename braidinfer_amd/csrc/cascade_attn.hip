@@ -156,11 +156,10 @@ struct CasArgs {
   int* status;
 };
 
-constexpr int CAS_D = 128;          // head_dim of the MFMA path
+constexpr int CAS_DMAX = 128;       // largest head_dim of the MFMA paths (64 and 128 are built)
 
 // a zeroed row that masked slots load from instead of the cache and the rotary table
-__device__ __align__(16) float cas_zero_row[CAS_D];
-constexpr int CAS_KP = CAS_D + 8;   // K row pitch in LDS (bf16): 272 bytes, conflict-free reads
+__device__ __align__(16) float cas_zero_row[CAS_DMAX];
 constexpr int CAS_VP = 32 + 8;      // V^T row pitch (bf16): 80 bytes
 
 // two floats rounded to the 16-bit type, packed low | high << 16
@@ -170,11 +169,87 @@ __device__ __forceinline__ uint32_t pack_pair(float lo, float hi) {
   return static_cast<uint32_t>(E::from_f32(lo)) | (static_cast<uint32_t>(E::from_f32(hi)) << 16);
 }
 
-template <bool BF16>
+// N consecutive 16-bit elements (N = 2, 4 or 8: 4, 8 or 16 bytes, aligned to
+// their size) as 32-bit words; NT: nontemporal load.
+typedef unsigned cas_u32x2_t __attribute__((ext_vector_type(2)));
+template <int N>
+struct Half16 {
+  uint32_t w[N / 2];
+};
+template <int N, bool NT>
+__device__ __forceinline__ Half16<N> ld16s(const uint16_t* p) {
+  Half16<N> r;
+  if constexpr (N == 8) {
+    const uint4 u = load16_nt<NT>(p);
+    r.w[0] = u.x; r.w[1] = u.y; r.w[2] = u.z; r.w[3] = u.w;
+  } else if constexpr (N == 4) {
+    cas_u32x2_t u;
+    if constexpr (NT) u = __builtin_nontemporal_load(reinterpret_cast<const cas_u32x2_t*>(p));
+    else u = *reinterpret_cast<const cas_u32x2_t*>(p);
+    r.w[0] = u.x; r.w[1] = u.y;
+  } else {
+    static_assert(N == 2, "2, 4 or 8 elements");
+    if constexpr (NT) r.w[0] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(p));
+    else r.w[0] = *reinterpret_cast<const uint32_t*>(p);
+  }
+  return r;
+}
+template <int N, class E>
+__device__ __forceinline__ void unpack_h(const Half16<N>& h, float (&x)[N]) {
+#pragma unroll
+  for (int i = 0; i < N / 2; ++i) {
+    x[2 * i] = E::to_f32(static_cast<uint16_t>(h.w[i] & 0xffffu));
+    x[2 * i + 1] = E::to_f32(static_cast<uint16_t>(h.w[i] >> 16));
+  }
+}
+// N fp32 values (N = 2, 4 or 8; 8- or 16-byte aligned)
+template <int N>
+__device__ __forceinline__ void ldf(const float* p, float (&v)[N]) {
+  if constexpr (N >= 4) {
+#pragma unroll
+    for (int c = 0; c < N / 4; ++c) {
+      const float4 f = reinterpret_cast<const float4*>(p)[c];
+      v[4 * c] = f.x; v[4 * c + 1] = f.y; v[4 * c + 2] = f.z; v[4 * c + 3] = f.w;
+    }
+  } else {
+    static_assert(N == 2, "2, 4 or 8 values");
+    const float2 f = *reinterpret_cast<const float2*>(p);
+    v[0] = f.x; v[1] = f.y;
+  }
+}
+// N elements of a vector of runtime dtype (fp32, bf16 or fp16) at element e
+template <int N>
+__device__ __forceinline__ void ld_any_n(const void* p, int dt, int64_t e, float (&v)[N]) {
+  if (dt == BFA_DTYPE_F32) {
+    ldf<N>(static_cast<const float*>(p) + e, v);
+  } else if (dt == BFA_DTYPE_BF16) {
+    unpack_h<N, Elem<BFA_DTYPE_BF16>>(ld16s<N, false>(static_cast<const uint16_t*>(p) + e), v);
+  } else {
+    unpack_h<N, Elem<BFA_DTYPE_F16>>(ld16s<N, false>(static_cast<const uint16_t*>(p) + e), v);
+  }
+}
+// N values stored as 16-bit elements (2, 4 or 8: one 4-, 8- or 16-byte store)
+template <int N, bool BF16>
+__device__ __forceinline__ void st16s(uint16_t* p, const float (&x)[N]) {
+  uint32_t w[N / 2];
+#pragma unroll
+  for (int i = 0; i < N / 2; ++i) w[i] = pack_pair<BF16>(x[2 * i], x[2 * i + 1]);
+  if constexpr (N == 8) *reinterpret_cast<uint4*>(p) = make_uint4(w[0], w[1], w[2], w[3]);
+  else if constexpr (N == 4) *reinterpret_cast<uint2*>(p) = make_uint2(w[0], w[1]);
+  else *reinterpret_cast<uint32_t*>(p) = w[0];
+}
+
+// D = head_dim (64 or 128).  Staging: key row tid / 8, 8 lanes per row, each
+// lane EL = D / 16 elements of each half (columns EL c .. and D / 2 + EL c ..,
+// the RoPE pairs).  S^T takes D / 32 MFMAs per 16 keys, O^T has D / 16 blocks.
+template <bool BF16, int D>
 __global__ __launch_bounds__(256) void cascade_attn_kernel(CasArgs a) {
   using E = Elem<BF16 ? BFA_DTYPE_BF16 : BFA_DTYPE_F16>;
-  __shared__ uint16_t ks[32 * CAS_KP];
-  __shared__ uint16_t vt[CAS_D * CAS_VP];
+  static_assert(D == 64 || D == 128, "head_dim 64 or 128");
+  constexpr int EL = D / 16, QJ = D / 32, OJ = D / 16;
+  constexpr int KP = D + 8;  // K row pitch in LDS (bf16): conflict-free fragment reads
+  __shared__ uint16_t ks[32 * KP];
+  __shared__ uint16_t vt[D * CAS_VP];
   __shared__ int64_t kpos_s[32];
   __shared__ int kval_s[32];
 
@@ -187,14 +262,14 @@ __global__ __launch_bounds__(256) void cascade_attn_kernel(CasArgs a) {
   int64_t step1 = min(step0 + a.steps_per_split, a.steps);
 
   // Q fragments (A operand, 16 rows x 32 head-dim per MFMA): lane holds row
-  // lane % 16 and head-dim 32 j + 8 (lane / 16) .. +7 for j = 0..3.
-  uint4 qf[4];
+  // lane % 16 and head-dim 32 j + 8 (lane / 16) .. +7 for j < D / 32.
+  uint4 qf[QJ];
   {
     const int64_t r = min(row0 + (lane & 15), rows - 1);
     const int64_t t = r / a.group, hh = g * a.group + (r - t * a.group);
     const uint16_t* qrow = a.q + t * a.q_st + hh * a.q_sh;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) qf[j] = *reinterpret_cast<const uint4*>(qrow + 32 * j + 8 * (lane >> 4));
+    for (int j = 0; j < QJ; ++j) qf[j] = *reinterpret_cast<const uint4*>(qrow + 32 * j + 8 * (lane >> 4));
   }
   // The matrix work is done transposed: S^T = K Q^T and O^T = V^T P^T, so a lane
   // owns one query row (lane % 16) throughout -- its scores, its running max and
@@ -206,31 +281,23 @@ __global__ __launch_bounds__(256) void cascade_attn_kernel(CasArgs a) {
 
   const float sl2 = a.scale * 1.4426950408889634f;  // scale x log2(e)
   float m = -INFINITY, l = 0.f;
-  cas_f32x4_t o[8];  // o[j][i] = O^T[head-dim 16 j + 4 (lane / 16) + i][query lane % 16]
+  cas_f32x4_t o[OJ];  // o[j][i] = O^T[head-dim 16 j + 4 (lane / 16) + i][query lane % 16]
 #pragma unroll
-  for (int j = 0; j < 8; ++j) o[j] = cas_f32x4_t{};
+  for (int j = 0; j < OJ; ++j) o[j] = cas_f32x4_t{};
 
-  // Staging roles: K -- key row tid / 8, head-dim pair chunk tid % 8 (columns
-  // 8c..8c+7 and 64+8c..64+8c+7, the RoPE pairs); V -- the same row, chunks c and
-  // c + 8 of 8 elements.  Loads run ahead of use: the K, V and cos/sin rows of
-  // step i+1 are issued before step i's matrix work, and the entry metadata of
-  // step i+2 right after them, raw, so that nothing waits on it before step i+1
-  // resolves its slots (the memory counter retires loads in issue order).
+  // Staging roles: K and V -- key row tid / 8, head-dim columns EL c .. and
+  // D / 2 + EL c .. (c = tid % 8; for K the RoPE pairs).  Loads run ahead of use:
+  // the K, V and cos/sin rows of step i+1 are issued before step i's matrix
+  // work, and the entry metadata of step i+2 right after them, raw, so that
+  // nothing waits on it before step i+1 resolves its slots (the memory counter
+  // retires loads in issue order).
   const int sk = tid >> 3, sc = tid & 7;
-  float kg1[8] = {1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f};  // k_norm weights of this lane's columns
-  float kg2[8] = {1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f};
+  float kg1[EL], kg2[EL];  // k_norm weights of this lane's columns
+#pragma unroll
+  for (int i = 0; i < EL; ++i) kg1[i] = kg2[i] = 1.f;
   if (a.knorm_w) {
-    const char* w = static_cast<const char*>(a.knorm_w);
-    if (a.knorm_dt == BFA_DTYPE_F32) {
-      load8<BFA_DTYPE_F32>(w + 4 * (8 * sc), kg1);
-      load8<BFA_DTYPE_F32>(w + 4 * (CAS_D / 2 + 8 * sc), kg2);
-    } else if (a.knorm_dt == BFA_DTYPE_BF16) {
-      load8<BFA_DTYPE_BF16>(w + 2 * (8 * sc), kg1);
-      load8<BFA_DTYPE_BF16>(w + 2 * (CAS_D / 2 + 8 * sc), kg2);
-    } else {
-      load8<BFA_DTYPE_F16>(w + 2 * (8 * sc), kg1);
-      load8<BFA_DTYPE_F16>(w + 2 * (CAS_D / 2 + 8 * sc), kg2);
-    }
+    ld_any_n<EL>(a.knorm_w, a.knorm_dt, EL * sc, kg1);
+    ld_any_n<EL>(a.knorm_w, a.knorm_dt, D / 2 + EL * sc, kg2);
   }
   struct Meta {  // an entry's metadata as loaded; used only by issue()
     int64_t kst, dpos, s;
@@ -255,8 +322,8 @@ __global__ __launch_bounds__(256) void cascade_attn_kernel(CasArgs a) {
     return mt;
   };
   struct Buf {
-    uint4 k1, k2, v0, v1;
-    float4 c0, c1, s0, s1;
+    Half16<EL> k1, k2, v0, v1;
+    float c[EL], sn[EL];
     bool valid, rot;
     int64_t kp;
   };
@@ -283,23 +350,14 @@ __global__ __launch_bounds__(256) void cascade_attn_kernel(CasArgs a) {
     const uint16_t* zero = reinterpret_cast<const uint16_t*>(cas_zero_row);
     const uint16_t* krow = b.valid ? a.cache + page * a.c_sp + g * a.c_sh + mt.s * a.c_ss : zero;
     const uint16_t* vrow = b.valid ? krow + a.c_skv : zero;
-    b.k1 = load16_nt(krow + 8 * sc);
-    b.k2 = load16_nt(krow + CAS_D / 2 + 8 * sc);
-    b.v0 = load16_nt(vrow + 8 * sc);
-    b.v1 = load16_nt(vrow + 64 + 8 * sc);
-    const float* csrow = b.rot ? a.cs + dpos * CAS_D : cas_zero_row;
-    const float4* cr = reinterpret_cast<const float4*>(csrow + 8 * sc);
-    const float4* sr = reinterpret_cast<const float4*>(csrow + CAS_D / 2 + 8 * sc);
-    b.c0 = cr[0]; b.c1 = cr[1]; b.s0 = sr[0]; b.s1 = sr[1];
+    b.k1 = ld16s<EL, true>(krow + EL * sc);
+    b.k2 = ld16s<EL, true>(krow + D / 2 + EL * sc);
+    b.v0 = ld16s<EL, true>(vrow + EL * sc);
+    b.v1 = ld16s<EL, true>(vrow + D / 2 + EL * sc);
+    const float* csrow = b.rot ? a.cs + dpos * D : cas_zero_row;
+    ldf<EL>(csrow + EL * sc, b.c);
+    ldf<EL>(csrow + D / 2 + EL * sc, b.sn);
     return b;
-  };
-  auto unpack8 = [](const uint4& u, float (&x)[8]) {
-    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      x[2 * i] = E::to_f32(static_cast<uint16_t>(w[i] & 0xffffu));
-      x[2 * i + 1] = E::to_f32(static_cast<uint16_t>(w[i] >> 16));
-    }
   };
 
   if (step0 >= step1) step1 = step0;  // an empty range (no entries): the loop below does not run
@@ -313,46 +371,42 @@ __global__ __launch_bounds__(256) void cascade_attn_kernel(CasArgs a) {
     // ---- K row (rotated, normalised) -> LDS
     // (a masked slot loaded zeros; its S column is masked below and its V row
     // must be zero, since 0 x a NaN would poison the sum)
-    float x1[8], x2[8];
-    unpack8(buf.k1, x1);
-    unpack8(buf.k2, x2);
+    float x1[EL], x2[EL];
+    unpack_h<EL, E>(buf.k1, x1);
+    unpack_h<EL, E>(buf.k2, x2);
     if (buf.rot) {
-      const float cs[8] = {buf.c0.x, buf.c0.y, buf.c0.z, buf.c0.w, buf.c1.x, buf.c1.y, buf.c1.z, buf.c1.w};
-      const float sn[8] = {buf.s0.x, buf.s0.y, buf.s0.z, buf.s0.w, buf.s1.x, buf.s1.y, buf.s1.z, buf.s1.w};
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {  // apply_rotary_emb: fp32, result in the cache dtype
+      for (int i = 0; i < EL; ++i) {  // apply_rotary_emb: fp32, result in the cache dtype
         const float u = x1[i], w = x2[i];
-        x1[i] = E::round(u * cs[i] - w * sn[i]);
-        x2[i] = E::round(w * cs[i] + u * sn[i]);
+        x1[i] = E::round(u * buf.c[i] - w * buf.sn[i]);
+        x2[i] = E::round(w * buf.c[i] + u * buf.sn[i]);
       }
     }
     if (a.knorm_w) {  // uniform: every lane joins the 8-lane sum (one key row per 8 lanes)
       float ss = 0.f;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) ss += x1[i] * x1[i] + x2[i] * x2[i];
+      for (int i = 0; i < EL; ++i) ss += x1[i] * x1[i] + x2[i] * x2[i];
       ss = group8_sum_dpp(ss);
-      const float r = 1.0f / sqrtf(ss / static_cast<float>(CAS_D) + a.knorm_eps);
+      const float r = 1.0f / sqrtf(ss / static_cast<float>(D) + a.knorm_eps);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
+      for (int i = 0; i < EL; ++i) {
         x1[i] = E::round(E::round(x1[i] * r) * kg1[i]);
         x2[i] = E::round(E::round(x2[i] * r) * kg2[i]);
       }
     }
-    store8<BF16 ? BFA_DTYPE_BF16 : BFA_DTYPE_F16>(ks + sk * CAS_KP + 8 * sc, x1);
-    store8<BF16 ? BFA_DTYPE_BF16 : BFA_DTYPE_F16>(ks + sk * CAS_KP + CAS_D / 2 + 8 * sc, x2);
+    st16s<EL, BF16>(ks + sk * KP + EL * sc, x1);
+    st16s<EL, BF16>(ks + sk * KP + D / 2 + EL * sc, x2);
     // ---- V row -> LDS transposed, in the PV product's key order: the score of
     //      key slot 16 b + 4 g + i sits in lane group g at position 4 b + i of its
     //      8-key B fragment, so that slot is V^T column 8 g + 4 b + i
     {
       const int kc = 8 * ((sk >> 2) & 3) + 4 * (sk >> 4) + (sk & 3);
-      const uint32_t w0[4] = {buf.v0.x, buf.v0.y, buf.v0.z, buf.v0.w};
-      const uint32_t w1[4] = {buf.v1.x, buf.v1.y, buf.v1.z, buf.v1.w};
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        vt[(8 * sc + 2 * i) * CAS_VP + kc] = static_cast<uint16_t>(w0[i] & 0xffffu);
-        vt[(8 * sc + 2 * i + 1) * CAS_VP + kc] = static_cast<uint16_t>(w0[i] >> 16);
-        vt[(64 + 8 * sc + 2 * i) * CAS_VP + kc] = static_cast<uint16_t>(w1[i] & 0xffffu);
-        vt[(64 + 8 * sc + 2 * i + 1) * CAS_VP + kc] = static_cast<uint16_t>(w1[i] >> 16);
+      for (int i = 0; i < EL / 2; ++i) {
+        vt[(EL * sc + 2 * i) * CAS_VP + kc] = static_cast<uint16_t>(buf.v0.w[i] & 0xffffu);
+        vt[(EL * sc + 2 * i + 1) * CAS_VP + kc] = static_cast<uint16_t>(buf.v0.w[i] >> 16);
+        vt[(D / 2 + EL * sc + 2 * i) * CAS_VP + kc] = static_cast<uint16_t>(buf.v1.w[i] & 0xffffu);
+        vt[(D / 2 + EL * sc + 2 * i + 1) * CAS_VP + kc] = static_cast<uint16_t>(buf.v1.w[i] >> 16);
       }
     }
     if (sc == 0) {
@@ -371,9 +425,9 @@ __global__ __launch_bounds__(256) void cascade_attn_kernel(CasArgs a) {
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
       sacc[b] = cas_f32x4_t{};
-      const uint16_t* kr = ks + (16 * b + (lane & 15)) * CAS_KP + 8 * (lane >> 4);
+      const uint16_t* kr = ks + (16 * b + (lane & 15)) * KP + 8 * (lane >> 4);
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
+      for (int j = 0; j < QJ; ++j)
         sacc[b] = mfma16x32<BF16>(*reinterpret_cast<const uint4*>(kr + 32 * j), qf[j], sacc[b]);
     }
     // ---- mask, running max / sum.  The running state is kept in base 2: scores
@@ -409,14 +463,14 @@ __global__ __launch_bounds__(256) void cascade_attn_kernel(CasArgs a) {
     m = m_new;
     if (__any(alpha != 1.0f)) {  // the running max moved for some query of the wave
 #pragma unroll
-      for (int j = 0; j < 8; ++j) o[j] *= alpha;
+      for (int j = 0; j < OJ; ++j) o[j] *= alpha;
     }
     // ---- O^T += V^T P^T (A: V^T rows 16 j + lane % 16, keys 8 (lane / 16) .. +7
     //      in the order V^T was written; B: this lane's 8 probabilities)
     const uint4 pf = make_uint4(pack_pair<BF16>(p[0][0], p[0][1]), pack_pair<BF16>(p[0][2], p[0][3]),
                                 pack_pair<BF16>(p[1][0], p[1][1]), pack_pair<BF16>(p[1][2], p[1][3]));
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
+    for (int j = 0; j < OJ; ++j) {
       const uint4 vf = *reinterpret_cast<const uint4*>(vt + (16 * j + (lane & 15)) * CAS_VP + 8 * (lane >> 4));
       o[j] = mfma16x32<BF16>(vf, pf, o[j]);
     }
@@ -430,19 +484,19 @@ __global__ __launch_bounds__(256) void cascade_attn_kernel(CasArgs a) {
     if (gridDim.z == 1) {
       const int64_t t = r / a.group, hh = g * a.group + (r - t * a.group);
       const float inv = 1.0f / fmaxf(l, 1e-12f);
-      uint16_t* orow = static_cast<uint16_t*>(a.out) + t * a.out_st + hh * CAS_D;
+      uint16_t* orow = static_cast<uint16_t*>(a.out) + t * a.out_st + hh * D;
 #pragma unroll
-      for (int j = 0; j < 8; ++j)
+      for (int j = 0; j < OJ; ++j)
         *reinterpret_cast<uint2*>(orow + 16 * j + d0) =
             make_uint2(pack_pair<BF16>(o[j][0] * inv, o[j][1] * inv), pack_pair<BF16>(o[j][2] * inv, o[j][3] * inv));
     } else {
-      float* pr = a.part + ((static_cast<int64_t>(blockIdx.z) * a.hkv + g) * rows + r) * (CAS_D + 2);
+      float* pr = a.part + ((static_cast<int64_t>(blockIdx.z) * a.hkv + g) * rows + r) * (D + 2);
       if (lane < 16) {
         pr[0] = m;
         pr[1] = l;
       }
 #pragma unroll
-      for (int j = 0; j < 8; ++j)
+      for (int j = 0; j < OJ; ++j)
 #pragma unroll
         for (int i = 0; i < 4; ++i) pr[2 + 16 * j + d0 + i] = o[j][i];
     }
@@ -477,30 +531,22 @@ __device__ __forceinline__ int pv_order(int k) {
   return (k & ~31) + 8 * ((sk >> 2) & 3) + 4 * (sk >> 4) + (sk & 3);
 }
 
-template <bool BF16>
+template <bool BF16, int D>
 __global__ __launch_bounds__(256) void cascade_flatten_kernel(CasArgs a, FlatArgs f) {
   using E = Elem<BF16 ? BFA_DTYPE_BF16 : BFA_DTYPE_F16>;
-  constexpr int DT = BF16 ? BFA_DTYPE_BF16 : BFA_DTYPE_F16;
-  __shared__ uint16_t vs[CAS_D * CAS_FVP];
+  constexpr int EL = D / 16;
+  __shared__ uint16_t vs[D * CAS_FVP];
   const int tid = threadIdx.x;
   const int64_t g = blockIdx.y;  // kv head
   const int64_t t0 = static_cast<int64_t>(blockIdx.x) * CAS_FT;
   const bool vrole = blockIdx.z == 1;  // z = 0: K (and the positions), z = 1: V^T
   const int sk = tid >> 3, sc = tid & 7;  // key row (and row + 32), column chunk
-  float kg1[8] = {1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f};
-  float kg2[8] = {1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f};
+  float kg1[EL], kg2[EL];
+#pragma unroll
+  for (int i = 0; i < EL; ++i) kg1[i] = kg2[i] = 1.f;
   if (a.knorm_w && !vrole) {
-    const char* w = static_cast<const char*>(a.knorm_w);
-    if (a.knorm_dt == BFA_DTYPE_F32) {
-      load8<BFA_DTYPE_F32>(w + 4 * (8 * sc), kg1);
-      load8<BFA_DTYPE_F32>(w + 4 * (CAS_D / 2 + 8 * sc), kg2);
-    } else if (a.knorm_dt == BFA_DTYPE_BF16) {
-      load8<BFA_DTYPE_BF16>(w + 2 * (8 * sc), kg1);
-      load8<BFA_DTYPE_BF16>(w + 2 * (CAS_D / 2 + 8 * sc), kg2);
-    } else {
-      load8<BFA_DTYPE_F16>(w + 2 * (8 * sc), kg1);
-      load8<BFA_DTYPE_F16>(w + 2 * (CAS_D / 2 + 8 * sc), kg2);
-    }
+    ld_any_n<EL>(a.knorm_w, a.knorm_dt, EL * sc, kg1);
+    ld_any_n<EL>(a.knorm_w, a.knorm_dt, D / 2 + EL * sc, kg2);
   }
 #pragma unroll
   for (int pass = 0; pass < 2; ++pass) {
@@ -538,26 +584,26 @@ __global__ __launch_bounds__(256) void cascade_flatten_kernel(CasArgs a, FlatArg
     const uint16_t* krow = valid ? a.cache + page * a.c_sp + g * a.c_sh + s * a.c_ss : zero;
     if (vrole) {  // V row -> LDS, transposed in the PV order
       const uint16_t* vrow = valid ? krow + a.c_skv : zero;
-      float v1[8], v2[8];
-      load8<DT>(vrow + 8 * sc, v1);
-      load8<DT>(vrow + CAS_D / 2 + 8 * sc, v2);
+      float v1[EL], v2[EL];
+      unpack_h<EL, E>(ld16s<EL, false>(vrow + EL * sc), v1);
+      unpack_h<EL, E>(ld16s<EL, false>(vrow + D / 2 + EL * sc), v2);
       const int kc = pv_order(kk);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        vs[(8 * sc + i) * CAS_FVP + kc] = E::from_f32(v1[i]);
-        vs[(CAS_D / 2 + 8 * sc + i) * CAS_FVP + kc] = E::from_f32(v2[i]);
+      for (int i = 0; i < EL; ++i) {
+        vs[(EL * sc + i) * CAS_FVP + kc] = E::from_f32(v1[i]);
+        vs[(D / 2 + EL * sc + i) * CAS_FVP + kc] = E::from_f32(v2[i]);
       }
       continue;
     }
-    float x1[8], x2[8];
-    load8<DT>(krow + 8 * sc, x1);
-    load8<DT>(krow + CAS_D / 2 + 8 * sc, x2);
+    float x1[EL], x2[EL];
+    unpack_h<EL, E>(ld16s<EL, false>(krow + EL * sc), x1);
+    unpack_h<EL, E>(ld16s<EL, false>(krow + D / 2 + EL * sc), x2);
     if (rot) {
-      float cs[8], sn[8];
-      load8<BFA_DTYPE_F32>(a.cs + dpos * CAS_D + 8 * sc, cs);
-      load8<BFA_DTYPE_F32>(a.cs + dpos * CAS_D + CAS_D / 2 + 8 * sc, sn);
+      float cs[EL], sn[EL];
+      ldf<EL>(a.cs + dpos * D + EL * sc, cs);
+      ldf<EL>(a.cs + dpos * D + D / 2 + EL * sc, sn);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {  // apply_rotary_emb: fp32, result in the cache dtype
+      for (int i = 0; i < EL; ++i) {  // apply_rotary_emb: fp32, result in the cache dtype
         const float u = x1[i], w = x2[i];
         x1[i] = E::round(u * cs[i] - w * sn[i]);
         x2[i] = E::round(w * cs[i] + u * sn[i]);
@@ -566,38 +612,49 @@ __global__ __launch_bounds__(256) void cascade_flatten_kernel(CasArgs a, FlatArg
     if (a.knorm_w) {  // uniform; a zero row stays zero
       float ss = 0.f;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) ss += x1[i] * x1[i] + x2[i] * x2[i];
+      for (int i = 0; i < EL; ++i) ss += x1[i] * x1[i] + x2[i] * x2[i];
       ss = group8_sum_dpp(ss);
-      const float r = 1.0f / sqrtf(ss / static_cast<float>(CAS_D) + a.knorm_eps);
+      const float r = 1.0f / sqrtf(ss / static_cast<float>(D) + a.knorm_eps);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
+      for (int i = 0; i < EL; ++i) {
         x1[i] = E::round(E::round(x1[i] * r) * kg1[i]);
         x2[i] = E::round(E::round(x2[i] * r) * kg2[i]);
       }
     }
-    uint16_t* kd = f.kf + (g * f.npad + slot) * CAS_D;
-    store8<DT>(kd + 8 * sc, x1);
-    store8<DT>(kd + CAS_D / 2 + 8 * sc, x2);
+    uint16_t* kd = f.kf + (g * f.npad + slot) * D;
+    st16s<EL, BF16>(kd + EL * sc, x1);
+    st16s<EL, BF16>(kd + D / 2 + EL * sc, x2);
     if (g == 0 && sc == 0) f.kpos[slot] = valid ? static_cast<int32_t>(kp) : INT32_MAX;
   }
   if (!vrole) return;  // uniform over the workgroup
   __syncthreads();
-  // V^T tile out: 128 head-dim rows of 64 keys, 16-byte granules
+  // V^T tile out: D head-dim rows of 64 keys, 16-byte granules
 #pragma unroll
-  for (int i = tid; i < CAS_D * 8; i += 256) {
+  for (int i = tid; i < D * 8; i += 256) {
     const int d = i >> 3, gr = i & 7;
-    *reinterpret_cast<uint4*>(f.vt + (g * CAS_D + d) * f.npad + t0 + 8 * gr) =
+    *reinterpret_cast<uint4*>(f.vt + (g * D + d) * f.npad + t0 + 8 * gr) =
         *reinterpret_cast<const uint4*>(vs + d * CAS_FVP + 8 * gr);
   }
 }
 
-template <bool BF16>
+// K tile slot of granule G of row r (rows of GK = D / 8 granules): 256-byte
+// rows (D = 128) at G ^ (r & 15), 128-byte rows (D = 64) at G ^ ((r / 2) & 7);
+// either way a 16-lane fragment read touches 16 distinct bank groups.
+template <int D>
+__device__ __forceinline__ int kslot(int r, int gr) {
+  if constexpr (D == 128) return gr ^ (r & 15);
+  else return gr ^ ((r >> 1) & 7);
+}
+
+template <bool BF16, int D>
 __global__ __launch_bounds__(256) void cascade_flat_kernel(CasArgs a, FlatArgs f) {
-  // K tile: 64 rows of 256 bytes, granule G of row r at slot G ^ (r & 15); V^T
-  // tile: 128 rows of 128 bytes, granule G of row r at slot G ^ ((r / 2) & 7).
-  // Both make a 16-lane fragment read touch 16 distinct bank groups.
-  __shared__ uint4 kbuf[2][CAS_FT * 16];
-  __shared__ uint4 vbuf[2][CAS_D * 8];
+  // K tile: 64 rows of D * 2 bytes (GK granules, slots by kslot); V^T tile: D
+  // rows of 128 bytes, granule G of row r at slot G ^ ((r / 2) & 7).
+  constexpr int GK = D / 8, QJ = D / 32, OJ = D / 16;
+  constexpr int KC = GK / 4;        // 1 KiB K copies per wave (each 64 / GK rows)
+  constexpr int VC = D / 32;        // 1 KiB V^T copies per wave (each 8 rows)
+  __shared__ uint4 kbuf[2][CAS_FT * GK];
+  __shared__ uint4 vbuf[2][D * 8];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -608,45 +665,48 @@ __global__ __launch_bounds__(256) void cascade_flat_kernel(CasArgs a, FlatArgs f
   const int64_t tl0 = static_cast<int64_t>(blockIdx.z) * f.tiles_per_split;
   const int64_t tl1 = min(tl0 + f.tiles_per_split, tiles);
 
-  uint4 qf[4];
+  uint4 qf[QJ];
   {
     const int64_t r = min(row0 + (lane & 15), rows - 1);
     const int64_t t = r / a.group, hh = g * a.group + (r - t * a.group);
     const uint16_t* qrow = a.q + t * a.q_st + hh * a.q_sh;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) qf[j] = *reinterpret_cast<const uint4*>(qrow + 32 * j + 8 * (lane >> 4));
+    for (int j = 0; j < QJ; ++j) qf[j] = *reinterpret_cast<const uint4*>(qrow + 32 * j + 8 * (lane >> 4));
   }
   const int64_t qt = min(row0 + (lane & 15), rows - 1) / a.group;
   const int64_t qp = a.qpos_i64 ? static_cast<const int64_t*>(a.qpos)[qt]
                                 : static_cast<const int32_t*>(a.qpos)[qt];
   const float sl2 = a.scale * 1.4426950408889634f;
   float m = -INFINITY, l = 0.f;
-  cas_f32x4_t o[8];
+  cas_f32x4_t o[OJ];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) o[j] = cas_f32x4_t{};
+  for (int j = 0; j < OJ; ++j) o[j] = cas_f32x4_t{};
 
-  // DMA roles, four 1 KiB copies of each tile per wave: K copy i moves rows
-  // 4 (4 i + wid) .. +3 (lane: row + lane / 16, slot lane % 16); V^T copy i moves
-  // rows 8 (4 i + wid) .. +7 (lane: row + lane / 8, slot lane % 8).  Offsets are
-  // in bytes from the tile's first element.
-  uint32_t koff[4], voff[4];
+  // DMA roles per wave: K copy i moves rows (64 / GK) (4 i + wid) .. (lane: row +
+  // lane / GK, slot lane % GK); V^T copy i moves rows 8 (4 i + wid) .. +7 (lane:
+  // row + lane / 8, slot lane % 8).  Offsets are in bytes from the tile's first
+  // element.
+  uint32_t koff[KC], voff[VC];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int kr = 4 * (4 * i + wid) + (lane >> 4);
-    koff[i] = static_cast<uint32_t>((kr * CAS_D + 8 * ((lane & 15) ^ (kr & 15))) * 2);
+  for (int i = 0; i < KC; ++i) {
+    const int kr = (64 / GK) * (4 * i + wid) + lane / GK;
+    koff[i] = static_cast<uint32_t>((kr * D + 8 * kslot<D>(kr, lane % GK)) * 2);
+  }
+#pragma unroll
+  for (int i = 0; i < VC; ++i) {
     const int vr = 8 * (4 * i + wid) + (lane >> 3);
     voff[i] = static_cast<uint32_t>((vr * f.npad + 8 * ((lane & 7) ^ ((vr >> 1) & 7))) * 2);
   }
-  const uint16_t* kbase = f.kf + g * f.npad * CAS_D;
-  const uint16_t* vbase = f.vt + g * CAS_D * f.npad;
+  const uint16_t* kbase = f.kf + g * f.npad * D;
+  const uint16_t* vbase = f.vt + g * D * f.npad;
   const uint32_t kl = lds_addr(kbuf), vl = lds_addr(vbuf);
   auto issue = [&](int64_t t, int b) {
-    const uint16_t* kt = kbase + t * CAS_FT * CAS_D;
+    const uint16_t* kt = kbase + t * CAS_FT * D;
     const uint16_t* vt = vbase + t * CAS_FT;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) dma16(kt, koff[i], kl + b * (CAS_FT * 256) + (4 * i + wid) * 1024);
+    for (int i = 0; i < KC; ++i) dma16(kt, koff[i], kl + b * (CAS_FT * GK * 16) + (4 * i + wid) * 1024);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) dma16(vt, voff[i], vl + b * (CAS_D * 128) + (4 * i + wid) * 1024);
+    for (int i = 0; i < VC; ++i) dma16(vt, voff[i], vl + b * (D * 128) + (4 * i + wid) * 1024);
   };
   // key positions of this lane's scores: slots 16 b + 4 (lane / 16) .. +3
   auto load_kp = [&](int64_t t, int4 (&kp)[4]) {
@@ -677,8 +737,8 @@ __global__ __launch_bounds__(256) void cascade_flat_kernel(CasArgs a, FlatArgs f
         sacc[c] = cas_f32x4_t{};
         const int kr = 16 * c + (lane & 15);
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-          sacc[c] = mfma16x32<BF16>(kb[kr * 16 + ((4 * j + (lane >> 4)) ^ (kr & 15))], qf[j], sacc[c]);
+        for (int j = 0; j < QJ; ++j)
+          sacc[c] = mfma16x32<BF16>(kb[kr * GK + kslot<D>(kr, 4 * j + (lane >> 4))], qf[j], sacc[c]);
       }
       float p[4][4];
       float mx = -INFINITY;
@@ -709,7 +769,7 @@ __global__ __launch_bounds__(256) void cascade_flat_kernel(CasArgs a, FlatArgs f
       m = m_new;
       if (__any(alpha != 1.0f)) {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) o[j] *= alpha;
+        for (int j = 0; j < OJ; ++j) o[j] *= alpha;
       }
       // O^T += V^T P^T over the two groups of 32 keys
       const uint4* vb = vbuf[b];
@@ -719,7 +779,7 @@ __global__ __launch_bounds__(256) void cascade_flat_kernel(CasArgs a, FlatArgs f
                                     pack_pair<BF16>(p[2 * h + 1][0], p[2 * h + 1][1]),
                                     pack_pair<BF16>(p[2 * h + 1][2], p[2 * h + 1][3]));
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
+        for (int j = 0; j < OJ; ++j) {
           const int vr = 16 * j + (lane & 15);
           o[j] = mfma16x32<BF16>(vb[vr * 8 + ((4 * h + (lane >> 4)) ^ ((vr >> 1) & 7))], pf, o[j]);
         }
@@ -737,19 +797,19 @@ __global__ __launch_bounds__(256) void cascade_flat_kernel(CasArgs a, FlatArgs f
     if (gridDim.z == 1) {
       const int64_t t = r / a.group, hh = g * a.group + (r - t * a.group);
       const float inv = 1.0f / fmaxf(l, 1e-12f);
-      uint16_t* orow = static_cast<uint16_t*>(a.out) + t * a.out_st + hh * CAS_D;
+      uint16_t* orow = static_cast<uint16_t*>(a.out) + t * a.out_st + hh * D;
 #pragma unroll
-      for (int j = 0; j < 8; ++j)
+      for (int j = 0; j < OJ; ++j)
         *reinterpret_cast<uint2*>(orow + 16 * j + d0) =
             make_uint2(pack_pair<BF16>(o[j][0] * inv, o[j][1] * inv), pack_pair<BF16>(o[j][2] * inv, o[j][3] * inv));
     } else {
-      float* pr = a.part + ((static_cast<int64_t>(blockIdx.z) * a.hkv + g) * rows + r) * (CAS_D + 2);
+      float* pr = a.part + ((static_cast<int64_t>(blockIdx.z) * a.hkv + g) * rows + r) * (D + 2);
       if (lane < 16) {
         pr[0] = m;
         pr[1] = l;
       }
 #pragma unroll
-      for (int j = 0; j < 8; ++j)
+      for (int j = 0; j < OJ; ++j)
 #pragma unroll
         for (int i = 0; i < 4; ++i) pr[2 + 16 * j + d0 + i] = o[j][i];
     }
@@ -758,23 +818,26 @@ __global__ __launch_bounds__(256) void cascade_flat_kernel(CasArgs a, FlatArgs f
 
 // Combines the splits' (m, l, acc) rows: one workgroup per (kv head, row).
 // Every wave finds the maximum over all splits (lanes over splits); wave w then
-// sums splits w, w + 4, ... -- each lane two head-dim columns, the weights
+// sums splits w, w + 4, ... -- each lane D / 64 head-dim columns, the weights
 // broadcast from the lanes that computed them, loads unrolled so they are in
 // flight together -- and the four partial sums meet in LDS.
-template <bool BF16>
+template <bool BF16, int D>
 __global__ __launch_bounds__(256) void cascade_merge_kernel(CasArgs a, int64_t splits) {
   using E = Elem<BF16 ? BFA_DTYPE_BF16 : BFA_DTYPE_F16>;
-  __shared__ float red[4][2 * 64 + 1];
+  constexpr int NC = D / 64;  // columns per lane
+  __shared__ float red[4][D + 1];
   const int64_t rows = a.tokens * a.group;
   const int64_t item = blockIdx.x;
   const int64_t g = item / rows, r = item - g * rows;
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-  const int64_t zstride = a.hkv * rows * (CAS_D + 2);
-  const float* base = a.part + (g * rows + r) * (CAS_D + 2);
+  const int64_t zstride = a.hkv * rows * (D + 2);
+  const float* base = a.part + (g * rows + r) * (D + 2);
   float mx = -INFINITY;
   for (int64_t z = lane; z < splits; z += 64) mx = fmaxf(mx, base[z * zstride]);
   mx = lanes4_max(group16_max_dpp(mx));  // DPP and lane swaps, no LDS round trips
-  float lsum = 0.f, o0 = 0.f, o1 = 0.f;
+  float lsum = 0.f, oc[NC];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) oc[c] = 0.f;
   // this wave's splits: z = wid + 4 k; lane k holds the weight of the k-th
   for (int64_t k0 = 0; 4 * k0 + wid < splits; k0 += 64) {
     const int64_t z = 4 * (k0 + lane) + wid;
@@ -794,84 +857,87 @@ __global__ __launch_bounds__(256) void cascade_merge_kernel(CasArgs a, int64_t s
         const float wj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), j0 + u));
         const int64_t zj = min<int64_t>(4 * (k0 + j0 + u) + wid, splits - 1);
         const float* pr = base + zj * zstride + 2;
-        o0 += wj * pr[lane];
-        o1 += wj * pr[64 + lane];
+#pragma unroll
+        for (int c = 0; c < NC; ++c) oc[c] += wj * pr[64 * c + lane];
       }
     }
   }
   lsum = group_sum<kWave>(lsum);
-  red[wid][lane] = o0;
-  red[wid][64 + lane] = o1;
-  if (lane == 0) red[wid][128] = lsum;
+#pragma unroll
+  for (int c = 0; c < NC; ++c) red[wid][64 * c + lane] = oc[c];
+  if (lane == 0) red[wid][D] = lsum;
   __syncthreads();
   if (wid != 0) return;
-  o0 = red[0][lane] + red[1][lane] + red[2][lane] + red[3][lane];
-  o1 = red[0][64 + lane] + red[1][64 + lane] + red[2][64 + lane] + red[3][64 + lane];
-  lsum = red[0][128] + red[1][128] + red[2][128] + red[3][128];
+  lsum = red[0][D] + red[1][D] + red[2][D] + red[3][D];
   const float inv = 1.0f / fmaxf(lsum, 1e-12f);
   const int64_t t = r / a.group, hh = g * a.group + (r - t * a.group);
-  uint16_t* orow = static_cast<uint16_t*>(a.out) + t * a.out_st + hh * CAS_D;
-  orow[lane] = E::from_f32(o0 * inv);
-  orow[64 + lane] = E::from_f32(o1 * inv);
+  uint16_t* orow = static_cast<uint16_t*>(a.out) + t * a.out_st + hh * D;
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const int col = 64 * c + lane;
+    orow[col] = E::from_f32((red[0][col] + red[1][col] + red[2][col] + red[3][col]) * inv);
+  }
 }
 
 // The same combination for at most 16 splits: one wave per (kv head, row), 4
-// rows per workgroup; every split's (m, l) and this lane's two columns are
+// rows per workgroup; every split's (m, l) and this lane's columns are
 // requested together (indices clamped, weights of absent splits zero).
-template <bool BF16>
+template <bool BF16, int D>
 __global__ __launch_bounds__(256) void cascade_merge_small_kernel(CasArgs a, int64_t splits) {
   using E = Elem<BF16 ? BFA_DTYPE_BF16 : BFA_DTYPE_F16>;
-  constexpr int ZMAX = 16;
+  constexpr int ZMAX = 16, NC = D / 64;
   const int64_t rows = a.tokens * a.group;
   const int64_t item = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
   if (item >= a.hkv * rows) return;
   const int64_t g = item / rows, r = item - g * rows;
   const int lane = threadIdx.x & 63;
-  const int64_t zstride = a.hkv * rows * (CAS_D + 2);
-  const float* base = a.part + (g * rows + r) * (CAS_D + 2);
-  float mz[ZMAX], lz[ZMAX], a0[ZMAX], a1[ZMAX];
+  const int64_t zstride = a.hkv * rows * (D + 2);
+  const float* base = a.part + (g * rows + r) * (D + 2);
+  float mz[ZMAX], lz[ZMAX], ac[ZMAX][NC];
 #pragma unroll
   for (int z = 0; z < ZMAX; ++z) {
     const float* pz = base + min<int64_t>(z, splits - 1) * zstride;
     mz[z] = pz[0];
     lz[z] = pz[1];
-    a0[z] = pz[2 + lane];
-    a1[z] = pz[2 + 64 + lane];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) ac[z][c] = pz[2 + 64 * c + lane];
   }
   float mx = -INFINITY;
 #pragma unroll
   for (int z = 0; z < ZMAX; ++z) mx = fmaxf(mx, z < splits ? mz[z] : -INFINITY);
   const float mref = mx == -INFINITY ? 0.f : mx;
-  float lsum = 0.f, o0 = 0.f, o1 = 0.f;
+  float lsum = 0.f, oc[NC];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) oc[c] = 0.f;
 #pragma unroll
   for (int z = 0; z < ZMAX; ++z) {
     const float w = z < splits ? __builtin_amdgcn_exp2f(mz[z] - mref) : 0.f;  // m in base 2; -inf -> 0
     lsum += w * lz[z];
-    o0 += w * a0[z];
-    o1 += w * a1[z];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) oc[c] += w * ac[z][c];
   }
   const float inv = 1.0f / fmaxf(lsum, 1e-12f);
   const int64_t t = r / a.group, hh = g * a.group + (r - t * a.group);
-  uint16_t* orow = static_cast<uint16_t*>(a.out) + t * a.out_st + hh * CAS_D;
-  orow[lane] = E::from_f32(o0 * inv);
-  orow[64 + lane] = E::from_f32(o1 * inv);
+  uint16_t* orow = static_cast<uint16_t*>(a.out) + t * a.out_st + hh * D;
+#pragma unroll
+  for (int c = 0; c < NC; ++c) orow[64 * c + lane] = E::from_f32(oc[c] * inv);
 }
 
 // Decode form (at most 4 query rows per kv head): scores on the VALU.  A
 // workgroup's 16 groups of 16 lanes walk its range of (entry, 16-slot block)
 // items; group kg takes slot 16 sb + kg of each item, lane j holds head-dim
-// 4j..4j+3 and 64+4j..64+4j+3 (the RoPE pairs), and each group keeps its own
-// online-softmax state for every row, so the walk needs no barrier.  The next
-// item's metadata and K / V / cos-sin rows load while the current one is
-// processed.  At the end the 16 group states meet in LDS and are combined into
-// the split's (m, l, acc) rows -- the layout the merge kernel reads -- or, with
-// one split, into the output.
-template <bool BF16, int R>
+// EH j .. and D / 2 + EH j .. (EH = D / 32 each: the RoPE pairs), and each group
+// keeps its own online-softmax state for every row, so the walk needs no
+// barrier.  The next item's metadata and K / V / cos-sin rows load while the
+// current one is processed.  At the end the 16 group states meet in LDS and are
+// combined into the split's (m, l, acc) rows -- the layout the merge kernel
+// reads -- or, with one split, into the output.
+template <bool BF16, int R, int D>
 __global__ __launch_bounds__(256) void cascade_decode_kernel(CasArgs a, int64_t items_per_split, int64_t nsb) {
   using E = Elem<BF16 ? BFA_DTYPE_BF16 : BFA_DTYPE_F16>;
-  constexpr int NG = 16;
+  constexpr int NG = 16, EH = D / 32;
   __shared__ float red_m[NG][R], red_l[NG][R];
-  __shared__ float red_a[NG][R][CAS_D];
+  __shared__ float red_a[NG][R][D];
   const int tid = threadIdx.x, j = tid & 15, kg = tid >> 4;
   const int64_t g = blockIdx.x;  // kv head
   const int64_t rows = a.tokens * a.group;
@@ -880,51 +946,32 @@ __global__ __launch_bounds__(256) void cascade_decode_kernel(CasArgs a, int64_t 
   const int64_t i1 = min(i0 + items_per_split, items);
 
   // queries (fp32 copies of the bf16 / fp16 values) and their positions
-  float q1[R][4], q2[R][4];
+  float q1[R][EH], q2[R][EH];
   int64_t qp[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     const int64_t rr = min<int64_t>(r, rows - 1);
     const int64_t t = rr / a.group, hh = g * a.group + (rr - t * a.group);
     const uint16_t* qrow = a.q + t * a.q_st + hh * a.q_sh;
-    const uint2 u1 = *reinterpret_cast<const uint2*>(qrow + 4 * j);
-    const uint2 u2 = *reinterpret_cast<const uint2*>(qrow + CAS_D / 2 + 4 * j);
-    q1[r][0] = E::to_f32(u1.x & 0xffffu); q1[r][1] = E::to_f32(u1.x >> 16);
-    q1[r][2] = E::to_f32(u1.y & 0xffffu); q1[r][3] = E::to_f32(u1.y >> 16);
-    q2[r][0] = E::to_f32(u2.x & 0xffffu); q2[r][1] = E::to_f32(u2.x >> 16);
-    q2[r][2] = E::to_f32(u2.y & 0xffffu); q2[r][3] = E::to_f32(u2.y >> 16);
+    unpack_h<EH, E>(ld16s<EH, false>(qrow + EH * j), q1[r]);
+    unpack_h<EH, E>(ld16s<EH, false>(qrow + D / 2 + EH * j), q2[r]);
     qp[r] = a.qpos_i64 ? static_cast<const int64_t*>(a.qpos)[t] : static_cast<const int32_t*>(a.qpos)[t];
   }
-  float kw1[4] = {1.f, 1.f, 1.f, 1.f}, kw2[4] = {1.f, 1.f, 1.f, 1.f};
-  if (a.knorm_w) {  // one uniform dtype branch, vector loads
-    if (a.knorm_dt == BFA_DTYPE_F32) {
-      const float4 w1 = *reinterpret_cast<const float4*>(static_cast<const float*>(a.knorm_w) + 4 * j);
-      const float4 w2 = *reinterpret_cast<const float4*>(static_cast<const float*>(a.knorm_w) + CAS_D / 2 + 4 * j);
-      kw1[0] = w1.x; kw1[1] = w1.y; kw1[2] = w1.z; kw1[3] = w1.w;
-      kw2[0] = w2.x; kw2[1] = w2.y; kw2[2] = w2.z; kw2[3] = w2.w;
-    } else {
-      const uint2 w1 = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(a.knorm_w) + 4 * j);
-      const uint2 w2 = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(a.knorm_w) + CAS_D / 2 + 4 * j);
-      const uint32_t u[4] = {w1.x, w1.y, w2.x, w2.y};
-      float f[8];
+  float kw1[EH], kw2[EH];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const uint16_t lo = static_cast<uint16_t>(u[i] & 0xffffu), hi = static_cast<uint16_t>(u[i] >> 16);
-        f[2 * i] = a.knorm_dt == BFA_DTYPE_BF16 ? Elem<BFA_DTYPE_BF16>::to_f32(lo) : Elem<BFA_DTYPE_F16>::to_f32(lo);
-        f[2 * i + 1] = a.knorm_dt == BFA_DTYPE_BF16 ? Elem<BFA_DTYPE_BF16>::to_f32(hi) : Elem<BFA_DTYPE_F16>::to_f32(hi);
-      }
-      kw1[0] = f[0]; kw1[1] = f[1]; kw1[2] = f[2]; kw1[3] = f[3];
-      kw2[0] = f[4]; kw2[1] = f[5]; kw2[2] = f[6]; kw2[3] = f[7];
-    }
+  for (int i = 0; i < EH; ++i) kw1[i] = kw2[i] = 1.f;
+  if (a.knorm_w) {  // one uniform dtype branch, vector loads
+    ld_any_n<EH>(a.knorm_w, a.knorm_dt, EH * j, kw1);
+    ld_any_n<EH>(a.knorm_w, a.knorm_dt, D / 2 + EH * j, kw2);
   }
   const float sl2 = a.scale * 1.4426950408889634f;
-  float m[R], l[R], acc1[R][4], acc2[R][4];
+  float m[R], l[R], acc1[R][EH], acc2[R][EH];
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     m[r] = -INFINITY;
     l[r] = 0.f;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) acc1[r][i] = acc2[r][i] = 0.f;
+    for (int i = 0; i < EH; ++i) acc1[r][i] = acc2[r][i] = 0.f;
   }
 
   // An item's metadata as loaded (used only by issue(), an item later), and the
@@ -936,8 +983,8 @@ __global__ __launch_bounds__(256) void cascade_decode_kernel(CasArgs a, int64_t 
     bool in;
   };
   struct Slot {
-    uint2 k1, k2, v1, v2;
-    float4 c, sn;
+    Half16<EH> k1, k2, v1, v2;
+    float c[EH], sn[EH];
     int64_t kp;
     bool valid, rot;
   };
@@ -978,13 +1025,13 @@ __global__ __launch_bounds__(256) void cascade_decode_kernel(CasArgs a, int64_t 
     const uint16_t* zero = reinterpret_cast<const uint16_t*>(cas_zero_row);
     const uint16_t* krow = b.valid ? a.cache + page * a.c_sp + g * a.c_sh + sl * a.c_ss : zero;
     const uint16_t* vrow = b.valid ? krow + a.c_skv : zero;
-    b.k1 = *reinterpret_cast<const uint2*>(krow + 4 * j);
-    b.k2 = *reinterpret_cast<const uint2*>(krow + CAS_D / 2 + 4 * j);
-    b.v1 = *reinterpret_cast<const uint2*>(vrow + 4 * j);
-    b.v2 = *reinterpret_cast<const uint2*>(vrow + CAS_D / 2 + 4 * j);
-    const float* csrow = b.rot ? a.cs + dpos * CAS_D : cas_zero_row;
-    b.c = *reinterpret_cast<const float4*>(csrow + 4 * j);
-    b.sn = *reinterpret_cast<const float4*>(csrow + CAS_D / 2 + 4 * j);
+    b.k1 = ld16s<EH, false>(krow + EH * j);
+    b.k2 = ld16s<EH, false>(krow + D / 2 + EH * j);
+    b.v1 = ld16s<EH, false>(vrow + EH * j);
+    b.v2 = ld16s<EH, false>(vrow + D / 2 + EH * j);
+    const float* csrow = b.rot ? a.cs + dpos * D : cas_zero_row;
+    ldf<EH>(csrow + EH * j, b.c);
+    ldf<EH>(csrow + D / 2 + EH * j, b.sn);
     return b;
   };
 
@@ -994,40 +1041,37 @@ __global__ __launch_bounds__(256) void cascade_decode_kernel(CasArgs a, int64_t 
     for (int64_t it = i0; it < i1; ++it) {
       const Slot nxt = issue(mn);  // item it + 1's rows fly while this item is processed,
       mn = load_meta(it + 2);      // and item it + 2's metadata
-      float x1[4] = {E::to_f32(cur.k1.x & 0xffffu), E::to_f32(cur.k1.x >> 16), E::to_f32(cur.k1.y & 0xffffu),
-                     E::to_f32(cur.k1.y >> 16)};
-      float x2[4] = {E::to_f32(cur.k2.x & 0xffffu), E::to_f32(cur.k2.x >> 16), E::to_f32(cur.k2.y & 0xffffu),
-                     E::to_f32(cur.k2.y >> 16)};
+      float x1[EH], x2[EH];
+      unpack_h<EH, E>(cur.k1, x1);
+      unpack_h<EH, E>(cur.k2, x2);
       if (cur.rot) {
-        const float cs[4] = {cur.c.x, cur.c.y, cur.c.z, cur.c.w}, sn[4] = {cur.sn.x, cur.sn.y, cur.sn.z, cur.sn.w};
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {  // apply_rotary_emb: fp32, result in the cache dtype
+        for (int i = 0; i < EH; ++i) {  // apply_rotary_emb: fp32, result in the cache dtype
           const float u = x1[i], w = x2[i];
-          x1[i] = E::round(u * cs[i] - w * sn[i]);
-          x2[i] = E::round(w * cs[i] + u * sn[i]);
+          x1[i] = E::round(u * cur.c[i] - w * cur.sn[i]);
+          x2[i] = E::round(w * cur.c[i] + u * cur.sn[i]);
         }
       }
       if (a.knorm_w) {  // uniform: every lane joins its group's 16-lane sum
         float ss = 0.f;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) ss += x1[i] * x1[i] + x2[i] * x2[i];
+        for (int i = 0; i < EH; ++i) ss += x1[i] * x1[i] + x2[i] * x2[i];
         ss = group16_sum_dpp(ss);
-        const float rn = 1.0f / sqrtf(ss / static_cast<float>(CAS_D) + a.knorm_eps);
+        const float rn = 1.0f / sqrtf(ss / static_cast<float>(D) + a.knorm_eps);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < EH; ++i) {
           x1[i] = E::round(E::round(x1[i] * rn) * kw1[i]);
           x2[i] = E::round(E::round(x2[i] * rn) * kw2[i]);
         }
       }
-      const float v1[4] = {E::to_f32(cur.v1.x & 0xffffu), E::to_f32(cur.v1.x >> 16), E::to_f32(cur.v1.y & 0xffffu),
-                           E::to_f32(cur.v1.y >> 16)};
-      const float v2[4] = {E::to_f32(cur.v2.x & 0xffffu), E::to_f32(cur.v2.x >> 16), E::to_f32(cur.v2.y & 0xffffu),
-                           E::to_f32(cur.v2.y >> 16)};
+      float v1[EH], v2[EH];
+      unpack_h<EH, E>(cur.v1, v1);
+      unpack_h<EH, E>(cur.v2, v2);
 #pragma unroll
       for (int r = 0; r < R; ++r) {
         float d = 0.f;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) d += q1[r][i] * x1[i] + q2[r][i] * x2[i];
+        for (int i = 0; i < EH; ++i) d += q1[r][i] * x1[i] + q2[r][i] * x2[i];
         d = group16_sum_dpp(d);
         const bool use = cur.valid && (!a.causal || cur.kp <= qp[r]);
         const float sc = use ? d * sl2 : -INFINITY;
@@ -1038,7 +1082,7 @@ __global__ __launch_bounds__(256) void cascade_decode_kernel(CasArgs a, int64_t 
         l[r] = l[r] * alpha + pr;
         m[r] = m_new;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < EH; ++i) {
           acc1[r][i] = acc1[r][i] * alpha + pr * v1[i];
           acc2[r][i] = acc2[r][i] * alpha + pr * v2[i];
         }
@@ -1054,14 +1098,14 @@ __global__ __launch_bounds__(256) void cascade_decode_kernel(CasArgs a, int64_t 
       red_l[kg][r] = l[r];
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      red_a[kg][r][4 * j + i] = acc1[r][i];
-      red_a[kg][r][CAS_D / 2 + 4 * j + i] = acc2[r][i];
+    for (int i = 0; i < EH; ++i) {
+      red_a[kg][r][EH * j + i] = acc1[r][i];
+      red_a[kg][r][D / 2 + EH * j + i] = acc2[r][i];
     }
   }
   __syncthreads();
-  for (int idx = tid; idx < R * CAS_D; idx += 256) {
-    const int r = idx / CAS_D, dcol = idx - r * CAS_D;
+  for (int idx = tid; idx < R * D; idx += 256) {
+    const int r = idx / D, dcol = idx - r * D;
     if (r >= rows) break;
     float mx = -INFINITY;
 #pragma unroll
@@ -1076,9 +1120,9 @@ __global__ __launch_bounds__(256) void cascade_decode_kernel(CasArgs a, int64_t 
     }
     if (gridDim.y == 1) {
       const int64_t t = r / a.group, hh = g * a.group + (r - t * a.group);
-      static_cast<uint16_t*>(a.out)[t * a.out_st + hh * CAS_D + dcol] = E::from_f32(asum / fmaxf(lsum, 1e-12f));
+      static_cast<uint16_t*>(a.out)[t * a.out_st + hh * D + dcol] = E::from_f32(asum / fmaxf(lsum, 1e-12f));
     } else {
-      float* pr = a.part + ((static_cast<int64_t>(blockIdx.y) * a.hkv + g) * rows + r) * (CAS_D + 2);
+      float* pr = a.part + ((static_cast<int64_t>(blockIdx.y) * a.hkv + g) * rows + r) * (D + 2);
       if (dcol == 0) {
         pr[0] = mx;
         pr[1] = lsum;
@@ -1110,15 +1154,28 @@ static DecodeSplit decode_split(int64_t hkv, int64_t num_entries, int64_t page_s
 
 static bool decode_form(int64_t rows) { return rows <= 4; }
 
+// Calls f(bf16 tag, head_dim tag) for the cache dtype and head_dim (64 or 128).
+template <class F>
+static void dispatch_dtype_hd(int dtype, int64_t head_dim, F&& f) {
+  using D64 = std::integral_constant<int, 64>;
+  using D128 = std::integral_constant<int, 128>;
+  if (dtype == BFA_DTYPE_BF16) {
+    if (head_dim == 64) f(std::true_type{}, D64{}); else f(std::true_type{}, D128{});
+  } else {
+    if (head_dim == 64) f(std::false_type{}, D64{}); else f(std::false_type{}, D128{});
+  }
+}
+
 // Split combination: a wave per row up to 16 splits, a workgroup per row above.
-template <bool BF16>
+template <bool BF16, int D>
 static void launch_merge(const CasArgs& a, int64_t rows, int64_t splits, hipStream_t s) {
   const int64_t items = a.hkv * rows;
   if (splits <= 16) {
-    hipLaunchKernelGGL(cascade_merge_small_kernel<BF16>, dim3(static_cast<unsigned>(cdiv(items, 4))), dim3(256), 0,
-                       s, a, splits);
+    hipLaunchKernelGGL((cascade_merge_small_kernel<BF16, D>), dim3(static_cast<unsigned>(cdiv(items, 4))), dim3(256),
+                       0, s, a, splits);
   } else {
-    hipLaunchKernelGGL(cascade_merge_kernel<BF16>, dim3(static_cast<unsigned>(items)), dim3(256), 0, s, a, splits);
+    hipLaunchKernelGGL((cascade_merge_kernel<BF16, D>), dim3(static_cast<unsigned>(items)), dim3(256), 0, s, a,
+                       splits);
   }
 }
 
@@ -1144,7 +1201,7 @@ struct FlatPlan {
 
 static int64_t align256c(int64_t v) { return (v + 255) / 256 * 256; }
 
-static FlatPlan flat_plan(int64_t rows, int64_t hkv, int64_t num_entries, int64_t page_size) {
+static FlatPlan flat_plan(int64_t rows, int64_t hkv, int64_t num_entries, int64_t page_size, int64_t d) {
   FlatPlan fp{};
   fp.npad = cdiv(num_entries * page_size, CAS_FT) * CAS_FT;
   fp.tiles = fp.npad / CAS_FT;
@@ -1160,8 +1217,8 @@ static FlatPlan flat_plan(int64_t rows, int64_t hkv, int64_t num_entries, int64_
   zs = std::max<int64_t>(1, zs);
   fp.tiles_per_split = std::max<int64_t>(1, cdiv(fp.tiles, zs));
   fp.splits = std::max<int64_t>(1, cdiv(fp.tiles, fp.tiles_per_split));
-  fp.part_bytes = fp.splits > 1 ? align256c(fp.splits * hkv * rows * (CAS_D + 2) * 4) : 0;
-  fp.kf_bytes = align256c(hkv * fp.npad * CAS_D * 2);
+  fp.part_bytes = fp.splits > 1 ? align256c(fp.splits * hkv * rows * (d + 2) * 4) : 0;
+  fp.kf_bytes = align256c(hkv * fp.npad * d * 2);
   fp.vt_bytes = fp.kf_bytes;
   fp.kp_bytes = align256c(fp.npad * 4);
   return fp;
@@ -1221,7 +1278,7 @@ extern "C" int64_t bfa_cascade_attention_workspace_size(int64_t tokens, int64_t 
   if (tokens <= 0 || num_kv_heads <= 0 || num_q_heads % num_kv_heads != 0 || page_size <= 0) return 0;
   const int64_t rows = tokens * (num_q_heads / num_kv_heads);
   if (!decode_form(rows) && flat_form(rows, num_entries))
-    return flat_plan(rows, num_kv_heads, num_entries, page_size).total();
+    return flat_plan(rows, num_kv_heads, num_entries, page_size, head_dim).total();
   const int64_t splits = decode_form(rows) ? decode_split(num_kv_heads, num_entries, page_size).splits
                                            : cascade_splits(rows, num_kv_heads, cdiv(num_entries * page_size, 32));
   return splits > 1 ? splits * num_kv_heads * rows * (head_dim + 2) * 4 : 0;
@@ -1240,7 +1297,7 @@ extern "C" int bfa_cascade_attention(
   const char* what = "bfa_cascade_attention";
   BFA_REQUIRE(dtype == BFA_DTYPE_BF16 || dtype == BFA_DTYPE_F16,
               "%s: query and cache must be bf16 or fp16", what);
-  BFA_REQUIRE(head_dim == CAS_D, "%s: head_dim %lld (this kernel covers 128)", what,
+  BFA_REQUIRE(head_dim == 128 || head_dim == 64, "%s: head_dim %lld (the kernels cover 64 and 128)", what,
               static_cast<long long>(head_dim));
   BFA_REQUIRE(qpos_dtype == BFA_DTYPE_I32 || qpos_dtype == BFA_DTYPE_I64, "%s: bad positions dtype", what);
   BFA_REQUIRE(num_tokens >= 0 && num_kv_heads > 0 && num_q_heads % num_kv_heads == 0 && page_size > 0 &&
@@ -1285,20 +1342,21 @@ extern "C" int bfa_cascade_attention(
     BFA_REQUIRE(ds.splits < 65536 && num_kv_heads < (int64_t{1} << 31), "%s: grid too large", what);
     const dim3 grid(static_cast<unsigned>(num_kv_heads), static_cast<unsigned>(ds.splits));
     const hipStream_t s = as_stream(stream);
-    auto launch = [&](auto bf) {
+    auto launch = [&](auto bf, auto dd) {
       constexpr bool B = decltype(bf)::value;
-      if (rows <= 1) hipLaunchKernelGGL((cascade_decode_kernel<B, 1>), grid, dim3(256), 0, s, a, ds.per_split, ds.nsb);
-      else if (rows <= 2) hipLaunchKernelGGL((cascade_decode_kernel<B, 2>), grid, dim3(256), 0, s, a, ds.per_split, ds.nsb);
-      else hipLaunchKernelGGL((cascade_decode_kernel<B, 4>), grid, dim3(256), 0, s, a, ds.per_split, ds.nsb);
-      if (ds.splits > 1) launch_merge<B>(a, rows, ds.splits, s);
+      constexpr int DD = decltype(dd)::value;
+      if (rows <= 1) hipLaunchKernelGGL((cascade_decode_kernel<B, 1, DD>), grid, dim3(256), 0, s, a, ds.per_split, ds.nsb);
+      else if (rows <= 2) hipLaunchKernelGGL((cascade_decode_kernel<B, 2, DD>), grid, dim3(256), 0, s, a, ds.per_split, ds.nsb);
+      else hipLaunchKernelGGL((cascade_decode_kernel<B, 4, DD>), grid, dim3(256), 0, s, a, ds.per_split, ds.nsb);
+      if (ds.splits > 1) launch_merge<B, DD>(a, rows, ds.splits, s);
     };
-    if (dtype == BFA_DTYPE_BF16) launch(std::true_type{}); else launch(std::false_type{});
+    dispatch_dtype_hd(dtype, head_dim, launch);
     return check_launch(what);
   }
   if (flat_form(rows, num_entries)) {
-    const FlatPlan fp = flat_plan(rows, num_kv_heads, num_entries, page_size);
+    const FlatPlan fp = flat_plan(rows, num_kv_heads, num_entries, page_size, head_dim);
     BFA_REQUIRE(workspace && workspace_bytes >= fp.total() && aligned16(workspace), "%s: workspace too small", what);
-    BFA_REQUIRE(fp.npad * CAS_D * 2 < (int64_t{1} << 31) && fp.tiles < (int64_t{1} << 31) &&
+    BFA_REQUIRE(fp.npad * head_dim * 2 < (int64_t{1} << 31) && fp.tiles < (int64_t{1} << 31) &&
                     cdiv(rows, 64) < (int64_t{1} << 31) && fp.splits < 65536 && num_kv_heads < 65536,
                 "%s: too many keys for the flat form", what);
     char* ws = static_cast<char*>(workspace);
@@ -1313,13 +1371,14 @@ extern "C" int bfa_cascade_attention(
     const dim3 pgrid(static_cast<unsigned>(fp.tiles), static_cast<unsigned>(num_kv_heads), 2);
     const dim3 grid(static_cast<unsigned>(cdiv(rows, 64)), static_cast<unsigned>(num_kv_heads),
                     static_cast<unsigned>(fp.splits));
-    auto launch = [&](auto bf) {
+    auto launch = [&](auto bf, auto dd) {
       constexpr bool B = decltype(bf)::value;
-      hipLaunchKernelGGL(cascade_flatten_kernel<B>, pgrid, dim3(256), 0, s, a, f);
-      hipLaunchKernelGGL(cascade_flat_kernel<B>, grid, dim3(256), 0, s, a, f);
-      if (fp.splits > 1) launch_merge<B>(a, rows, fp.splits, s);
+      constexpr int DD = decltype(dd)::value;
+      hipLaunchKernelGGL((cascade_flatten_kernel<B, DD>), pgrid, dim3(256), 0, s, a, f);
+      hipLaunchKernelGGL((cascade_flat_kernel<B, DD>), grid, dim3(256), 0, s, a, f);
+      if (fp.splits > 1) launch_merge<B, DD>(a, rows, fp.splits, s);
     };
-    if (dtype == BFA_DTYPE_BF16) launch(std::true_type{}); else launch(std::false_type{});
+    dispatch_dtype_hd(dtype, head_dim, launch);
     return check_launch(what);
   }
   a.steps = cdiv(num_entries * page_size, 32);
@@ -1337,12 +1396,12 @@ extern "C" int bfa_cascade_attention(
                   static_cast<unsigned>(zs));
   BFA_REQUIRE(zs == 1 || num_kv_heads * rows < (int64_t{1} << 31), "%s: grid too large", what);
   const hipStream_t s = as_stream(stream);
-  if (dtype == BFA_DTYPE_BF16) {
-    hipLaunchKernelGGL(cascade_attn_kernel<true>, grid, dim3(256), 0, s, a);
-    if (zs > 1) launch_merge<true>(a, rows, zs, s);
-  } else {
-    hipLaunchKernelGGL(cascade_attn_kernel<false>, grid, dim3(256), 0, s, a);
-    if (zs > 1) launch_merge<false>(a, rows, zs, s);
-  }
+  auto launch = [&](auto bf, auto dd) {
+    constexpr bool B = decltype(bf)::value;
+    constexpr int DD = decltype(dd)::value;
+    hipLaunchKernelGGL((cascade_attn_kernel<B, DD>), grid, dim3(256), 0, s, a);
+    if (zs > 1) launch_merge<B, DD>(a, rows, zs, s);
+  };
+  dispatch_dtype_hd(dtype, head_dim, launch);
   return check_launch(what);
 }

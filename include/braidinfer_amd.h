@@ -304,8 +304,9 @@ int bfa_online_softmax_update(const void* query, const void* key, const void* va
                               void* stream);
 
 /* CascadeAttention.forward — braidinfer/layers/cascade_attention.py:50-231 — in one
- * launch (plus a merge launch when the key range is split).  query [T, Hq, 128]
- * (bf16/fp16; token / head strides), query_positions [T]; kv_cache one layer of the
+ * launch (plus a merge launch when the key range is split).  query [T, Hq, D],
+ * D = head_dim = 64 or 128 (bf16/fp16; token / head strides), query_positions
+ * [T]; kv_cache one layer of the
  * paged cache, strides (page, K|V, head, slot), K at index 0.  The attended pages
  * are num_entries entries in the reference's walk order (levels, chunks, pages;
  * :112-224), each spanning page_size key positions:
@@ -317,12 +318,12 @@ int bfa_online_softmax_update(const void* query, const void* key, const void* va
  *   entry_delta[e]     global - cached position start of its chunk (:153-170),
  *   entry_info[e]      bits 0-15: tokens attended on the page (page_size, or
  *                      kv_last_page_len on a chunk's last page, :131-134), bit 16:
- *                      rotate K by cos_sin_cache[delta] (fp32 [max_position, 128];
+ *                      rotate K by cos_sin_cache[delta] (fp32 [max_position, D];
  *                      a negative delta wraps; out of range sets
  *                      BFA_STATUS_INDEX_OOB).
- * k_norm_weight [128] (optional) applies RMSNorm(eps) to K after the rotation
+ * k_norm_weight [D] (optional) applies RMSNorm(eps) to K after the rotation
  * (:175-178).  Query head h attends kv head h / (Hq / Hkv); causal masks keys
- * whose position exceeds the query's.  out [T, Hq * 128] (query dtype, token
+ * whose position exceeds the query's.  out [T, Hq * D] (query dtype, token
  * stride out_stride_token) = acc / max(l, 1e-12) (:226-231).  workspace:
  * bfa_cascade_attention_workspace_size bytes. */
 int64_t bfa_cascade_attention_workspace_size(int64_t tokens, int64_t num_q_heads,

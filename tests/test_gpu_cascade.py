@@ -72,7 +72,7 @@ def chunk(page_table, kv_length, cached=0, glob=0, kind="context"):
                            global_position_start=glob, chunk_type=SimpleNamespace(value=kind))
 
 
-def build_case(seed, hq, hkv, lengths, deltas, pages, ps=16, dtype=torch.bfloat16):
+def build_case(seed, hq, hkv, lengths, deltas, pages, ps=16, dtype=torch.bfloat16, d=128):
     """A system chunk and context chunks of the given token counts in shuffled pages,
     each moved by its delta; plus an empty chunk and one with pages but no tokens."""
     g = gen(seed)
@@ -86,7 +86,7 @@ def build_case(seed, hq, hkv, lengths, deltas, pages, ps=16, dtype=torch.bfloat1
         pos += n
     chunks.insert(2, chunk([], 0))
     chunks.insert(3, chunk(perm[used:used + 1], 0))
-    kv = randn(g, pages, 2, hkv, ps, 128, dtype=dtype)
+    kv = randn(g, pages, 2, hkv, ps, d, dtype=dtype)
     return chunks, kv, sum(lengths)
 
 
@@ -97,6 +97,19 @@ CASES = [
     ("qwen3 prefill chunk", 37, 16, 8, [48, 130, 64], [0, 77, -5], True, True),
     ("llama prefill", 300, 32, 8, [128, 700, 300], [0, 2048, 0], True, False),
     ("non-causal", 9, 16, 8, [33, 16, 1], [0, 5, 0], False, True),
+]
+
+
+# head_dim 64 (TinyLlama-1.1B: 32 query / 4 kv heads, theta 1e4), through the
+# decode form (up to 4 query rows per kv head: GQA 4 at one token, GQA 2 at
+# two), the fused kernel and the flat form (natural from 97 rows, forced below)
+CASES_D64 = [
+    ("tinyllama decode", 1, 32, 4, [100, 37, 516], [0, 4000, -77], True, False),
+    ("d64 decode form gqa4 k-norm", 1, 8, 2, [200, 17, 1000], [0, -4096, 3000], True, True),
+    ("d64 decode form gqa2 two tokens", 2, 16, 8, [64, 300, 5], [0, 0, 12], True, False),
+    ("tinyllama prefill chunk k-norm", 37, 32, 4, [48, 130, 64], [0, 77, -5], True, True),
+    ("tinyllama prefill", 300, 32, 4, [128, 700, 300], [0, 2048, 0], True, False),
+    ("d64 non-causal", 9, 16, 8, [33, 16, 1], [0, 5, 0], False, True),
 ]
 
 
@@ -115,12 +128,26 @@ def test_cascade_attention_flat_form(monkeypatch, name, tokens, hq, hkv, lengths
     _check_case(name, tokens, hq, hkv, lengths, deltas, causal, knorm)
 
 
-def _check_case(name, tokens, hq, hkv, lengths, deltas, causal, knorm):
+@pytest.mark.parametrize("name,tokens,hq,hkv,lengths,deltas,causal,knorm", CASES_D64)
+def test_cascade_attention_head_dim_64(monkeypatch, name, tokens, hq, hkv, lengths, deltas, causal, knorm):
+    monkeypatch.setenv("BFA_CASCADE_FLAT", "0")  # the fused kernel (or the decode form) for every case
+    _check_case(name, tokens, hq, hkv, lengths, deltas, causal, knorm, d=64, base=1e4)
+
+
+@pytest.mark.parametrize("name,tokens,hq,hkv,lengths,deltas,causal,knorm",
+                         [c for c in CASES_D64 if c[1] * c[2] // c[3] > 4])
+def test_cascade_attention_head_dim_64_flat_form(monkeypatch, name, tokens, hq, hkv, lengths, deltas, causal,
+                                                 knorm):
+    monkeypatch.setenv("BFA_CASCADE_FLAT", "1")
+    _check_case(name, tokens, hq, hkv, lengths, deltas, causal, knorm, d=64, base=1e4)
+
+
+def _check_case(name, tokens, hq, hkv, lengths, deltas, causal, knorm, d=128, base=1e6):
     seed = zlib.crc32(name.encode()) % 1000
     g = gen(seed)
-    d, ps, max_pos = 128, 16, 40960
-    chunks, kv, total = build_case(seed + 1, hq, hkv, lengths, deltas, pages=300)
-    rope = RotaryEmbedding(d, d, max_pos, 1e6).to(DEV)
+    ps, max_pos = 16, 40960
+    chunks, kv, total = build_case(seed + 1, hq, hkv, lengths, deltas, pages=300, d=d)
+    rope = RotaryEmbedding(d, d, max_pos, base).to(DEV)
     att = CascadeAttention(hq, d, d ** -0.5, hkv, ps, rotary_emb=rope)
     levels = att.create_cascade_levels(chunks)
     q = randn(g, tokens, hq, d)
@@ -141,16 +168,18 @@ def _check_case(name, tokens, hq, hkv, lengths, deltas, causal, knorm):
     assert_close(out, exp, what=name)
 
 
-@pytest.mark.parametrize("ps,tokens,dtype", [(8, 1, torch.bfloat16), (32, 2, torch.bfloat16), (16, 2, torch.float16),
-                                             (32, 1, torch.float16)])
-def test_cascade_decode_form_page_sizes(ps, tokens, dtype):
+@pytest.mark.parametrize("ps,tokens,dtype,d", [(8, 1, torch.bfloat16, 128), (32, 2, torch.bfloat16, 128),
+                                               (16, 2, torch.float16, 128), (32, 1, torch.float16, 128),
+                                               (8, 2, torch.bfloat16, 64), (32, 1, torch.float16, 64)])
+def test_cascade_decode_form_page_sizes(ps, tokens, dtype, d):
     """Up to 4 query rows per kv head run in the decode kernel, which walks
     (entry, 16-slot block) items: page size 8 leaves half the lane groups idle,
     32 takes two blocks per page.  Qwen3 geometry (16 / 8 heads), k_norm, moved
-    chunks, a partial last page."""
-    g = gen(90 + ps + tokens)
-    hq, hkv, d, max_pos = 16, 8, 128, 40960
-    chunks, kv, total = build_case(91 + ps, hq, hkv, [45, 130, 77], [0, 300, -41], pages=64, ps=ps, dtype=dtype)
+    chunks, a partial last page; head_dim 128 and 64."""
+    g = gen(90 + ps + tokens + d)
+    hq, hkv, max_pos = 16, 8, 40960
+    chunks, kv, total = build_case(91 + ps, hq, hkv, [45, 130, 77], [0, 300, -41], pages=64, ps=ps, dtype=dtype,
+                                   d=d)
     rope = RotaryEmbedding(d, d, max_pos, 1e6).to(DEV)
     att = CascadeAttention(hq, d, d ** -0.5, hkv, ps, rotary_emb=rope)
     levels = att.create_cascade_levels(chunks)
@@ -165,17 +194,18 @@ def test_cascade_decode_form_page_sizes(ps, tokens, dtype):
     braidinfer_amd.check_device_status()
     exp = R.cascade_attention(q, qpos, kv, cpu_levels(levels), hq, hkv, d ** -0.5, ps,
                               rope.cos_sin_cache.cpu(), kn_w, 1e-6, True)
-    assert_close(out, exp, what=f"decode form ps={ps} t={tokens} {dtype}")
+    assert_close(out, exp, what=f"decode form ps={ps} t={tokens} {dtype} d={d}")
 
 
-@pytest.mark.parametrize("ps,dtype", [(8, torch.bfloat16), (32, torch.float16)])
-def test_cascade_flat_form_page_sizes(monkeypatch, ps, dtype):
+@pytest.mark.parametrize("ps,dtype,d", [(8, torch.bfloat16, 128), (32, torch.float16, 128), (8, torch.float16, 64)])
+def test_cascade_flat_form_page_sizes(monkeypatch, ps, dtype, d):
     """Flat form with pages of 8 (8 pages per 64-key tile) and 32 slots, a
     partial last page and moved chunks, Qwen3 geometry with k_norm."""
     monkeypatch.setenv("BFA_CASCADE_FLAT", "1")
-    g = gen(95 + ps)
-    hq, hkv, d, max_pos, tokens = 16, 8, 128, 40960, 8
-    chunks, kv, total = build_case(96 + ps, hq, hkv, [45, 130, 77], [0, 300, -41], pages=64, ps=ps, dtype=dtype)
+    g = gen(95 + ps + d)
+    hq, hkv, max_pos, tokens = 16, 8, 40960, 8
+    chunks, kv, total = build_case(96 + ps, hq, hkv, [45, 130, 77], [0, 300, -41], pages=64, ps=ps, dtype=dtype,
+                                   d=d)
     rope = RotaryEmbedding(d, d, max_pos, 1e6).to(DEV)
     att = CascadeAttention(hq, d, d ** -0.5, hkv, ps, rotary_emb=rope)
     levels = att.create_cascade_levels(chunks)
@@ -190,7 +220,7 @@ def test_cascade_flat_form_page_sizes(monkeypatch, ps, dtype):
     braidinfer_amd.check_device_status()
     exp = R.cascade_attention(q, qpos, kv, cpu_levels(levels), hq, hkv, d ** -0.5, ps,
                               rope.cos_sin_cache.cpu(), kn_w, 1e-6, True)
-    assert_close(out, exp, what=f"flat form ps={ps} {dtype}")
+    assert_close(out, exp, what=f"flat form ps={ps} {dtype} d={d}")
 
 
 @pytest.mark.parametrize("flat", ["0", "1"])
