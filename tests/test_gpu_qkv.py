@@ -132,6 +132,40 @@ def test_decode_scale_after(t, heads, h, gdtype):
         assert_close(got, exp, what=f"scale-after with_bias {name} t={t}")
 
 
+@pytest.mark.parametrize("t,h,hq,hkv,d,strided,gdtype,sample", [
+    (65, 4096, 32, 8, 128, False, torch.bfloat16, 1),     # 128x128 tiles (32-deep stage ring)
+    (300, 2048, 32, 4, 64, True, torch.bfloat16, 1),      # head_dim 64, ragged rows, rows 2112 apart
+    (100, 256, 8, 4, 32, False, torch.bfloat16, 1),       # head_dim 32, four stages
+    (2048, 4096, 32, 8, 128, False, torch.bfloat16, 7),   # 128x256 tiles (64-deep stages)
+    (4096, 4096, 32, 8, 128, False, torch.bfloat16, 13),  # 256x256 tiles
+    (1024, 8192, 32, 8, 128, False, torch.bfloat16, 5),   # hidden 8192
+    (300, 2048, 32, 4, 64, False, torch.float32, 1),      # fp32 gamma
+])
+def test_prefill_fp32_variants(t, h, hq, hkv, d, strided, gdtype, sample):
+    """FusedRMSNormQKVMinimalF32 and FusedRMSNormQKVWithBias over the prefill
+    tile forms (operand pre-pass, then the GEMM with the fp32 epilogue): within
+    the tolerance of the oracle's (x / rms) * gamma operand in fp32, with
+    strided and ragged inputs; every `sample`-th row is checked at the large
+    sizes (rows of a GEMM are independent)."""
+    _, x, ln, w, b = make(217, t, h, hq, hkv, d)
+    ln = ln.to(gdtype)
+    xd = x.to(DEV)
+    if strided:
+        wide = torch.zeros(t, h + 64, dtype=x.dtype, device=DEV)
+        wide[:, :h] = xd
+        xd = wide[:, :h]
+    rows = torch.arange(0, t, sample)
+    got = FusedRMSNormQKVMinimalF32.forward(xd, ln.to(DEV), w.to(DEV), hq, hkv, eps=1e-5)
+    ref = R.split_qkv(R.qkv_minimal_f32(x[rows], ln, w, 1e-5), hq, hkv)
+    for g_, exp, name in zip(got, ref, "qkv"):
+        assert g_.dtype == torch.float32
+        assert_close(g_[rows.to(DEV)], exp, what=f"prefill minimal_f32 {name} t={t}")
+    got = FusedRMSNormQKVWithBias.forward(xd, ln.to(DEV), w.to(DEV), b.to(DEV), hq, hkv, eps=1e-5)
+    ref = R.split_qkv(R.qkv_with_bias(x[rows], ln, w, b, 1e-5), hq, hkv)
+    for g_, exp, name in zip(got, ref, "qkv"):
+        assert_close(g_[rows.to(DEV)], exp, what=f"prefill with_bias {name} t={t}")
+
+
 @pytest.mark.parametrize("t,h,dtype,strided", [
     (1, 4096, torch.bfloat16, False),   # Llama-3-8B batch-1 decode: eight 16-byte chunks per lane
     (3, 4096, torch.bfloat16, True),    # rows 4160 elements apart
