@@ -162,6 +162,61 @@ __device__ __forceinline__ void store4_sel(void* p, int dt, int64_t i, const flo
   }
 }
 
+// Epilogue dtype forms of the GEMM kernel.  EDT_RT reads every rounding and
+// store dtype from QkvEpi at run time (the branch-free selects above: each
+// rounds both ways and picks one).  The fixed forms compile the dtypes in for
+// the two combinations the decoders run, so a rounding is one conversion:
+//   EDT_F32_BF16  fp32 projection, no q/k norm, RoPE in fp32, bf16 store
+//                 (the Llama chain: minimal_f32 -> rotary_emb -> .to(bf16))
+//   EDT_BF16      every rounding point bf16 (the Qwen3 chain, the bf16 linears)
+enum { EDT_RT = 0, EDT_F32_BF16 = 1, EDT_BF16 = 2 };
+template <int EDT> struct EpiDt { static constexpr int Q = -1, N = -1, A = -1, O = -1, M = -1; };
+template <> struct EpiDt<EDT_F32_BF16> {
+  static constexpr int Q = BFA_DTYPE_F32, N = -1, A = BFA_DTYPE_F32, O = BFA_DTYPE_BF16, M = -1;
+};
+template <> struct EpiDt<EDT_BF16> {
+  static constexpr int Q = BFA_DTYPE_BF16, N = BFA_DTYPE_BF16, A = BFA_DTYPE_BF16,
+                       O = BFA_DTYPE_BF16, M = BFA_DTYPE_BF16;
+};
+
+// Rounding to DT (compile time) or to the run-time dtype dt when DT < 0.
+template <int DT>
+__device__ __forceinline__ float rnd(float v, int dt) {
+  if constexpr (DT < 0) return round_sel(v, dt);
+  else return Elem<DT>::round(v);
+}
+
+template <int DT>
+__device__ __forceinline__ void store4_dt(void* p, int dt, int64_t i, const float (&v)[4]) {
+  if constexpr (DT < 0) {
+    store4_sel(p, dt, i, v);
+  } else if constexpr (DT == BFA_DTYPE_F32) {
+    *reinterpret_cast<float4*>(static_cast<float*>(p) + i) = make_float4(v[0], v[1], v[2], v[3]);
+  } else {
+    using E = Elem<DT>;
+    *reinterpret_cast<uint2*>(static_cast<uint16_t*>(p) + i) =
+        make_uint2(E::from_f32(v[0]) | (static_cast<uint32_t>(E::from_f32(v[1])) << 16),
+                   E::from_f32(v[2]) | (static_cast<uint32_t>(E::from_f32(v[3])) << 16));
+  }
+}
+
+// 8 consecutive elements (column multiple of 8, 16-byte aligned row).
+template <int DT>
+__device__ __forceinline__ void store8_dt(void* p, int dt, int64_t i, const float (&y)[8]) {
+  if constexpr (DT >= 0) {
+    store8<DT>(static_cast<char*>(p) + i * (DT == BFA_DTYPE_F32 ? 4 : 2), y);
+  } else if (dt == BFA_DTYPE_F32) {
+    float4* q = reinterpret_cast<float4*>(static_cast<float*>(p) + i);
+    q[0] = make_float4(y[0], y[1], y[2], y[3]);
+    q[1] = make_float4(y[4], y[5], y[6], y[7]);
+  } else {
+    const bool bf = dt == BFA_DTYPE_BF16;
+    *reinterpret_cast<uint4*>(static_cast<uint16_t*>(p) + i) =
+        make_uint4(pack2_sel(y[0], y[1], bf), pack2_sel(y[2], y[3], bf),
+                   pack2_sel(y[4], y[5], bf), pack2_sel(y[6], y[7], bf));
+  }
+}
+
 // 0 = q head, 1 = k head, 2 = v head
 __device__ __forceinline__ int head_kind(const QkvEpi& e, int64_t head) {
   return head < e.hq ? 0 : (head < e.hq + e.hkv ? 1 : 2);
@@ -357,9 +412,11 @@ __device__ __forceinline__ void tile_store(uint4* buf, int gr, int gg, const uin
 // 4-wave workgroups, or one 8-wave workgroup, per CU.  BK is the depth of a DMA
 // stage: 32 (ring of NS stages, 16 rows x 64 bytes per copy) or 64 (two
 // buffers, 8 rows x 128 bytes per copy, full cache lines).
-template <int BM, int BN, int WM, int WN, bool BF16, int EPI, int HD, bool DIRECT, int NS, int BK>
+template <int BM, int BN, int WM, int WN, bool BF16, int EPI, int HD, bool DIRECT, int NS, int BK,
+          int EDT = EDT_RT>
 __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, (WM * WN <= 8192 ? 2 : 1)) void qkv_gemm_kernel(
     GemmArgs g, QkvEpi e) {
+  using DT = EpiDt<EDT>;
   constexpr int NWN = BN / WN;
   constexpr int NW = (BM / WM) * NWN;
   static_assert(NW == 4 || NW == 8, "four or eight waves per workgroup");
@@ -576,7 +633,6 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, (WM * WN <= 8192 ? 2 : 
     constexpr int CH = EPI == EPI_SWIGLU ? 1 : 2;  // 8-column chunks per lane
     const int c8 = lane & 7, r8 = lane >> 3;
     const int64_t ocol0 = EPI == EPI_SWIGLU ? n0 + wn * 64 : wcol0;  // first output column of the wave
-    const bool bf_out = e.out_dt == BFA_DTYPE_BF16;
     __syncthreads();  // the K loop's last LDS reads are done before the slices are reused
 #pragma unroll
     for (int i = 0; i < MB; ++i) {
@@ -607,8 +663,8 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, (WM * WN <= 8192 ? 2 : 
             const float uv[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
 #pragma unroll
             for (int t = 0; t < 8; ++t) {
-              const float gt = round_sel(av[t], e.qkv_dt), ut = round_sel(uv[t], e.qkv_dt);
-              y[t] = round_sel(round_sel(silu_fast(gt), e.qkv_dt) * ut, e.out_dt);
+              const float gt = rnd<DT::Q>(av[t], e.qkv_dt), ut = rnd<DT::Q>(uv[t], e.qkv_dt);
+              y[t] = rnd<DT::O>(rnd<DT::Q>(silu_fast(gt), e.qkv_dt) * ut, e.out_dt);
             }
           } else {
             float bv[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
@@ -630,19 +686,11 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, (WM * WN <= 8192 ? 2 : 
             }
 #pragma unroll
             for (int t = 0; t < 8; ++t)
-              y[t] = round_sel(round_sel(round_sel(av[t] + bv[t], e.qkv_dt) + rv[t], e.mid_dt), e.out_dt);
+              y[t] = rnd<DT::O>(rnd<DT::M>(rnd<DT::Q>(av[t] + bv[t], e.qkv_dt) + rv[t], e.mid_dt), e.out_dt);
           }
           if (row < g.m) {
             if (e.vec && col + 8 <= g.n) {
-              if (e.out_dt == BFA_DTYPE_F32) {
-                float4* q = reinterpret_cast<float4*>(static_cast<float*>(e.out) + row * e.ldo + col);
-                q[0] = make_float4(y[0], y[1], y[2], y[3]);
-                q[1] = make_float4(y[4], y[5], y[6], y[7]);
-              } else {
-                *reinterpret_cast<uint4*>(static_cast<uint16_t*>(e.out) + row * e.ldo + col) =
-                    make_uint4(pack2_sel(y[0], y[1], bf_out), pack2_sel(y[2], y[3], bf_out),
-                               pack2_sel(y[4], y[5], bf_out), pack2_sel(y[6], y[7], bf_out));
-              }
+              store8_dt<DT::O>(e.out, e.out_dt, row * e.ldo + col, y);
             } else {
 #pragma unroll
               for (int t = 0; t < 8; ++t)
@@ -747,8 +795,8 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, (WM * WN <= 8192 ? 2 : 
         }
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
-          x1[t] = round_sel(x1[t], e.qkv_dt);
-          x2[t] = round_sel(x2[t], e.qkv_dt);
+          x1[t] = rnd<DT::Q>(x1[t], e.qkv_dt);
+          x2[t] = rnd<DT::Q>(x2[t], e.qkv_dt);
         }
         if (any_norm) {
           float ss = 0.f;
@@ -759,8 +807,8 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, (WM * WN <= 8192 ? 2 : 
             const float r = 1.0f / sqrtf(ss / static_cast<float>(HD) + e.qk_eps);
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
-              x1[t] = round_sel((x1[t] * r) * g1[t], e.norm_dt);
-              x2[t] = round_sel((x2[t] * r) * g2[t], e.norm_dt);
+              x1[t] = rnd<DT::N>((x1[t] * r) * g1[t], e.norm_dt);
+              x2[t] = rnd<DT::N>((x2[t] * r) * g2[t], e.norm_dt);
             }
           }
         }
@@ -772,13 +820,13 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, (WM * WN <= 8192 ? 2 : 
 #pragma unroll
           for (int t = 0; t < 4; ++t) {
             const float u = x1[t], w = x2[t];
-            x1[t] = ok ? round_sel(u * c[t] - w * sn[t], dt_after) : 0.f;
-            x2[t] = ok ? round_sel(w * c[t] + u * sn[t], dt_after) : 0.f;
+            x1[t] = ok ? rnd<DT::A>(u * c[t] - w * sn[t], dt_after) : 0.f;
+            x2[t] = ok ? rnd<DT::A>(w * c[t] + u * sn[t], dt_after) : 0.f;
           }
         }
         if (row < g.m && colok) {
-          store4_sel(e.out, e.out_dt, row * e.ldo + gc1, x1);
-          store4_sel(e.out, e.out_dt, row * e.ldo + gc2, x2);
+          store4_dt<DT::O>(e.out, e.out_dt, row * e.ldo + gc1, x1);
+          store4_dt<DT::O>(e.out, e.out_dt, row * e.ldo + gc2, x2);
         }
       }
       if (bad && q == 0) flag_status(e.status, BFA_STATUS_INDEX_OOB);
@@ -1869,24 +1917,63 @@ static void launch_decode(const QkvPlan& p, const SplitArgs& s, hipStream_t st,
   else launch_decode_cpw<BF16, 2>(p, s, st);
 }
 
+// Epilogue dtype form for a launch: the fixed forms cover bf16 operands on the
+// DMA path; every other case keeps the run-time dtypes.
+static bool edt_forced_rt() {
+  const char* v = getenv("BFA_EDT_RT");  // measurement override: run-time dtypes only
+  return v && atoi(v) != 0;
+}
+
+static int fused_edt(const QkvEpi& e) {
+  if (edt_forced_rt()) return EDT_RT;
+  const bool norm = e.qn_w != nullptr || e.kn_w != nullptr;
+  if (e.qkv_dt == BFA_DTYPE_F32 && e.out_dt == BFA_DTYPE_BF16 && !norm) return EDT_F32_BF16;
+  if (e.qkv_dt == BFA_DTYPE_BF16 && e.out_dt == BFA_DTYPE_BF16 && (!norm || e.norm_dt == BFA_DTYPE_BF16))
+    return EDT_BF16;
+  return EDT_RT;
+}
+
+static int linear_edt(const QkvEpi& e) {
+  if (edt_forced_rt()) return EDT_RT;
+  return (e.qkv_dt == BFA_DTYPE_BF16 && e.mid_dt == BFA_DTYPE_BF16 && e.out_dt == BFA_DTYPE_BF16)
+             ? EDT_BF16 : EDT_RT;
+}
+
+template <int BM, int BN, int WM, int NS, int BK, bool BF16, bool DIRECT, int HD>
+static void launch_fused_edt(unsigned grid, dim3 block, int edt, const GemmArgs& g, const QkvEpi& e,
+                             hipStream_t st) {
+  if constexpr (BF16 && DIRECT && HD >= 64) {
+    if (edt == EDT_F32_BF16) {
+      hipLaunchKernelGGL((qkv_gemm_kernel<BM, BN, WM, 128, BF16, EPI_FUSED, HD, DIRECT, NS, BK, EDT_F32_BF16>),
+                         dim3(grid), block, 0, st, g, e);
+      return;
+    }
+    if (edt == EDT_BF16) {
+      hipLaunchKernelGGL((qkv_gemm_kernel<BM, BN, WM, 128, BF16, EPI_FUSED, HD, DIRECT, NS, BK, EDT_BF16>),
+                         dim3(grid), block, 0, st, g, e);
+      return;
+    }
+  }
+  hipLaunchKernelGGL((qkv_gemm_kernel<BM, BN, WM, 128, BF16, EPI_FUSED, HD, DIRECT, NS, BK>), dim3(grid),
+                     block, 0, st, g, e);
+}
+
 // BM x BN tile, waves of WM x 128 (the fused epilogue needs 128-column waves),
 // BK-deep DMA stages (NS of them when BK = 32).
 template <int BM, int BN, int WM, int NS, int BK, bool BF16, bool DIRECT>
 static void launch_prefill_tile(const QkvPlan& p, const GemmArgs& g, const QkvEpi& e, hipStream_t st) {
   const unsigned grid = static_cast<unsigned>(cdiv(g.m, BM) * cdiv(g.n, BN));
   const dim3 block((BM / WM) * (BN / 128) * 64);
+  const int edt = fused_edt(e);
   if (!p.fused_epi) {
     hipLaunchKernelGGL((qkv_gemm_kernel<BM, BN, WM, 128, BF16, EPI_RAW, 128, DIRECT, NS, BK>), dim3(grid),
                        block, 0, st, g, e);
   } else if (e.hd == 128) {
-    hipLaunchKernelGGL((qkv_gemm_kernel<BM, BN, WM, 128, BF16, EPI_FUSED, 128, DIRECT, NS, BK>),
-                       dim3(grid), block, 0, st, g, e);
+    launch_fused_edt<BM, BN, WM, NS, BK, BF16, DIRECT, 128>(grid, block, edt, g, e, st);
   } else if (e.hd == 64) {
-    hipLaunchKernelGGL((qkv_gemm_kernel<BM, BN, WM, 128, BF16, EPI_FUSED, 64, DIRECT, NS, BK>),
-                       dim3(grid), block, 0, st, g, e);
+    launch_fused_edt<BM, BN, WM, NS, BK, BF16, DIRECT, 64>(grid, block, edt, g, e, st);
   } else {
-    hipLaunchKernelGGL((qkv_gemm_kernel<BM, BN, WM, 128, BF16, EPI_FUSED, 32, DIRECT, NS, BK>),
-                       dim3(grid), block, 0, st, g, e);
+    launch_fused_edt<BM, BN, WM, NS, BK, BF16, DIRECT, 32>(grid, block, edt, g, e, st);
   }
 }
 
@@ -1896,6 +1983,17 @@ static void launch_linear_tile(const GemmArgs& g, const QkvEpi& e, bool swiglu, 
   const int64_t bno = swiglu ? BN / 2 : BN;
   const unsigned grid = static_cast<unsigned>(cdiv(g.m, BM) * cdiv(g.n, bno));
   const dim3 block((BM / WM) * (BN / 128) * 64);
+  if constexpr (BF16 && DIRECT) {
+    if (linear_edt(e) == EDT_BF16) {
+      if (swiglu)
+        hipLaunchKernelGGL((qkv_gemm_kernel<BM, BN, WM, 128, BF16, EPI_SWIGLU, 128, DIRECT, NS, BK, EDT_BF16>),
+                           dim3(grid), block, 0, st, g, e);
+      else
+        hipLaunchKernelGGL((qkv_gemm_kernel<BM, BN, WM, 128, BF16, EPI_LINEAR, 128, DIRECT, NS, BK, EDT_BF16>),
+                           dim3(grid), block, 0, st, g, e);
+      return;
+    }
+  }
   if (swiglu) {
     hipLaunchKernelGGL((qkv_gemm_kernel<BM, BN, WM, 128, BF16, EPI_SWIGLU, 128, DIRECT, NS, BK>),
                        dim3(grid), block, 0, st, g, e);
