@@ -1266,8 +1266,10 @@ __global__ __launch_bounds__(256) void qkv_decode_loop_kernel(DecodeArgs d, int 
         unpack8<BFA_DTYPE_BF16>(xv[i], xf);
         unpack8<BFA_DTYPE_BF16>(gam[i], gf);
         uint32_t o[4];
+        if (blockIdx.x == 0) {  // every column tile has the same sums; the first stores them
 #pragma unroll
-        for (int j = 0; j < 8; ++j) ssq[i] += xf[j] * xf[j];
+          for (int j = 0; j < 8; ++j) ssq[i] += xf[j] * xf[j];
+        }
 #pragma unroll
         for (int j = 0; j < 4; ++j)
           o[j] = static_cast<uint32_t>(f32_to_bf16_bits(xf[2 * j] * gf[2 * j])) |
@@ -1403,8 +1405,6 @@ __device__ __forceinline__ void decode_epilogue_item(const float4* part, int64_t
   // values masked) so that none waits behind a per-token or per-dtype branch.
   // absent inputs read a valid stand-in (the partials) and are masked after
   const void* posp = rope ? e.positions : part;
-  const void* biasp = e.bias ? e.bias : part;
-  const void* nwp = nw ? nw : part;
   int64_t raw[4];
   if (rope && e.pos_is_i64) {
 #pragma unroll
@@ -1413,46 +1413,33 @@ __device__ __forceinline__ void decode_epilogue_item(const float4* part, int64_t
 #pragma unroll
     for (int v = 0; v < 4; ++v) raw[v] = static_cast<const int32_t*>(posp)[min(tg * 4 + v, m - 1)];
   }
-  float4 a1[MAXP], a2[MAXP];
+  // scale-after sums of squares of the first 8 splits, requested before the
+  // partials (one memory round trip for both)
+  float sl[8][4];
+  {
+    const float* stp = e.stats ? e.stats : reinterpret_cast<const float*>(part);
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+        sl[u][v] = stp[e.stats ? min<int64_t>(u, splits - 1) * e.stat_rows + min(tg * 4 + v, m - 1) : 0];
+  }
+  // partials of the first 8 splits (indices clamped, masked when summed)
+  float4 l1[MAXP][8], l2[MAXP][8];
 #pragma unroll
   for (int pp = 0; pp < MAXP; ++pp) {
     const int64_t pc = min<int64_t>(lane + 64 * pp, half - 1);
     const float4* p1 = part + index(base + pc);
     const float4* p2 = part + index(base + half + pc);
-    a1[pp] = a2[pp] = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int64_t sp0 = 0; sp0 < splits; sp0 += 8) {
-      // up to 8 splits in flight, summed in split order
-      float4 l1[8], l2[8];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const int64_t sp = min(sp0 + u, splits - 1);
-        l1[u] = p1[sp * sstride];
-        l2[u] = p2[sp * sstride];
-      }
-      asm volatile("" ::: "memory");  // all 16 loads issue before the first sum waits
-#pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const float f = sp0 + u < splits ? 1.f : 0.f;
-        a1[pp].x += f * l1[u].x; a1[pp].y += f * l1[u].y; a1[pp].z += f * l1[u].z; a1[pp].w += f * l1[u].w;
-        a2[pp].x += f * l2[u].x; a2[pp].y += f * l2[u].y; a2[pp].z += f * l2[u].z; a2[pp].w += f * l2[u].w;
-      }
+    for (int u = 0; u < 8; ++u) {
+      const int64_t sp = min<int64_t>(u, splits - 1);
+      l1[pp][u] = p1[sp * sstride];
+      l2[pp][u] = p2[sp * sstride];
     }
   }
-  if (e.stats) {
-    // scale-after: r per token from the splits' sums of squares (split order)
-    float sq[4] = {0.f, 0.f, 0.f, 0.f};
-    for (int64_t sp = 0; sp < splits; ++sp)
-#pragma unroll
-      for (int v = 0; v < 4; ++v) sq[v] += e.stats[sp * e.stat_rows + min(tg * 4 + v, m - 1)];
-    float r[4];
-#pragma unroll
-    for (int v = 0; v < 4; ++v) r[v] = 1.0f / sqrtf(sq[v] / static_cast<float>(e.hidden) + e.stat_eps);
-#pragma unroll
-    for (int pp = 0; pp < MAXP; ++pp) {
-      a1[pp].x *= r[0]; a1[pp].y *= r[1]; a1[pp].z *= r[2]; a1[pp].w *= r[3];
-      a2[pp].x *= r[0]; a2[pp].y *= r[1]; a2[pp].z *= r[2]; a2[pp].w *= r[3];
-    }
-  }
+  // the cos/sin rows wait only for the positions (requested first), so they go
+  // out before the partials are summed
   int64_t pos[4];
   bool pok[4];
 #pragma unroll
@@ -1471,19 +1458,73 @@ __device__ __forceinline__ void decode_epilogue_item(const float4* part, int64_t
       const int64_t o = rope ? pos[v] * e.hd : 0;
       cs1[pp][v] = csp[o + pc];
       sn1[pp][v] = csp[o + half + pc];
-      if (!rope) cs1[pp][v] = 1.f, sn1[pp][v] = 0.f;
     }
   }
-  // bias and norm weights last: their dtype dispatch waits for the loads
-  // issued before them, which by now are all in flight
+  // bias and norm weights (uniform branches: nothing is read when absent)
   float b1[MAXP], b2[MAXP], g1[MAXP], g2[MAXP];
 #pragma unroll
   for (int pp = 0; pp < MAXP; ++pp) {
     const int64_t pc = min<int64_t>(lane + 64 * pp, half - 1);  // lanes past the head re-read its last pair
-    load2_any(biasp, e.bias ? e.bias_dtype : BFA_DTYPE_F32, base + pc, base + half + pc, b1[pp], b2[pp]);
-    load2_any(nwp, nw ? e.qk_w_dtype : BFA_DTYPE_F32, pc, half + pc, g1[pp], g2[pp]);
-    if (!e.bias) b1[pp] = b2[pp] = 0.f;
-    if (!nw) g1[pp] = g2[pp] = 1.f;
+    b1[pp] = b2[pp] = 0.f;
+    g1[pp] = g2[pp] = 1.f;
+    if (e.bias) load2_any(e.bias, e.bias_dtype, base + pc, base + half + pc, b1[pp], b2[pp]);
+    if (nw) load2_any(nw, e.qk_w_dtype, pc, half + pc, g1[pp], g2[pp]);
+  }
+  asm volatile("" ::: "memory");
+  float4 a1[MAXP], a2[MAXP];
+#pragma unroll
+  for (int pp = 0; pp < MAXP; ++pp) {
+    a1[pp] = a2[pp] = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const bool in = u < splits;
+      const float4 x = l1[pp][u], y = l2[pp][u];
+      a1[pp].x += in ? x.x : 0.f; a1[pp].y += in ? x.y : 0.f; a1[pp].z += in ? x.z : 0.f; a1[pp].w += in ? x.w : 0.f;
+      a2[pp].x += in ? y.x : 0.f; a2[pp].y += in ? y.y : 0.f; a2[pp].z += in ? y.z : 0.f; a2[pp].w += in ? y.w : 0.f;
+    }
+    if (splits > 8) {
+      const int64_t pc = min<int64_t>(lane + 64 * pp, half - 1);
+      const float4* p1 = part + index(base + pc);
+      const float4* p2 = part + index(base + half + pc);
+      for (int64_t sp0 = 8; sp0 < splits; sp0 += 8) {
+        float4 r1[8], r2[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const int64_t sp = min(sp0 + u, splits - 1);
+          r1[u] = p1[sp * sstride];
+          r2[u] = p2[sp * sstride];
+        }
+        asm volatile("" ::: "memory");  // all 16 loads issue before the first sum waits
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const bool in = sp0 + u < splits;
+          a1[pp].x += in ? r1[u].x : 0.f; a1[pp].y += in ? r1[u].y : 0.f;
+          a1[pp].z += in ? r1[u].z : 0.f; a1[pp].w += in ? r1[u].w : 0.f;
+          a2[pp].x += in ? r2[u].x : 0.f; a2[pp].y += in ? r2[u].y : 0.f;
+          a2[pp].z += in ? r2[u].z : 0.f; a2[pp].w += in ? r2[u].w : 0.f;
+        }
+      }
+    }
+  }
+  if (e.stats) {
+    // scale-after: r per token from the splits' sums of squares, in split order
+    // (the first 8 splits' values were requested with the partials)
+    float sq[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) sq[v] += u < splits ? sl[u][v] : 0.f;
+    for (int64_t sp = 8; sp < splits; ++sp)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) sq[v] += e.stats[sp * e.stat_rows + min(tg * 4 + v, m - 1)];
+    float r[4];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) r[v] = 1.0f / sqrtf(sq[v] / static_cast<float>(e.hidden) + e.stat_eps);
+#pragma unroll
+    for (int pp = 0; pp < MAXP; ++pp) {
+      a1[pp].x *= r[0]; a1[pp].y *= r[1]; a1[pp].z *= r[2]; a1[pp].w *= r[3];
+      a2[pp].x *= r[0]; a2[pp].y *= r[1]; a2[pp].z *= r[2]; a2[pp].w *= r[3];
+    }
   }
   float x1[MAXP][4], x2[MAXP][4];
   float ss[4] = {0.f, 0.f, 0.f, 0.f};
