@@ -240,6 +240,18 @@ __device__ __forceinline__ float group16_max_dpp(float v) {
   return fmaxf(v, dpp_f32<0x140>(v));
 }
 
+// Sum over aligned groups of L lanes (L = 1, 2, 4, 8, 16) on DPP; every lane of
+// a group gets the same bits.
+template <int L>
+__device__ __forceinline__ float group_sum_dpp(float v) {
+  static_assert(L == 1 || L == 2 || L == 4 || L == 8 || L == 16, "DPP row groups");
+  if constexpr (L >= 2) v += dpp_f32<0xB1>(v);
+  if constexpr (L >= 4) v += dpp_f32<0x4E>(v);
+  if constexpr (L >= 8) v += dpp_f32<0x141>(v);
+  if constexpr (L >= 16) v += dpp_f32<0x140>(v);
+  return v;
+}
+
 // Reductions over lanes l, l ^ 16, l ^ 32, l ^ 48 with the gfx950 lane swaps.
 // v_permlane16_swap x, y exchanges the odd 16-lane rows of x with the even rows
 // of y; with x = y = v on entry, each lane ends up holding its own value in one

@@ -405,6 +405,274 @@ __device__ __forceinline__ void tile_store(uint4* buf, int gr, int gg, const uin
   for (int i = 0; i < BG; ++i) buf[BM * 8 + swz(gr + 32 * i, gg)] = rb[i];
 }
 
+// Tile order: workgroups are dispatched round-robin over the 8 XCDs; remap so
+// that each XCD walks a contiguous range of tiles, and walk tiles column-major
+// inside groups of 8 row-tiles so that concurrently resident workgroups on one
+// XCD share operand rows and weight columns in its L2.  n0 is in output columns.
+template <int EPI, int BM, int BN>
+__device__ __forceinline__ void tile_origin(const GemmArgs& g, int64_t& m0, int64_t& n0) {
+  constexpr int BNO = out_cols<EPI, BN>();
+  const int64_t tiles_m = cdiv(g.m, BM), tiles_n = cdiv(g.n, BNO);
+  const int64_t ntiles = tiles_m * tiles_n;
+  int64_t bid = blockIdx.x;
+  if (ntiles % 8 == 0) bid = (bid % 8) * (ntiles / 8) + bid / 8;
+  constexpr int64_t GROUP_M = 8;
+  const int64_t group = bid / (GROUP_M * tiles_n);
+  const int64_t first_m = group * GROUP_M;
+  const int64_t gsize = min(tiles_m - first_m, GROUP_M);
+  const int64_t tm = first_m + (bid % (GROUP_M * tiles_n)) % gsize;
+  const int64_t tn = (bid % (GROUP_M * tiles_n)) / gsize;
+  m0 = tm * BM;
+  n0 = tn * BNO;
+}
+
+// ------------------------------------------------------------ GEMM epilogue
+// Shared by the GEMM kernels.  32x32 accumulator layout: lane holds column
+// (lane & 31) and rows 8*(v/4) + 4*(lane/32) + (v%4), v = 0..15, of each of the
+// wave's MB x NB 32x32 blocks; the wave tile starts at row m0 + wm * WM and
+// column n0 + wn * WN (n0 in output columns).  lds: at least NW x 32 x LDR
+// floats, free for the wave-private staging slices (the caller's barrier-free
+// LDS use must be over).  praw: the rows' raw positions when EARLY (one block
+// per wave, requested before the K loop).
+template <int EPI, int HD, int MB, int NB, int WM, int WN, int NW, int EDT, bool EARLY>
+__device__ __forceinline__ void gemm_epilogue(f32x16_t (&acc)[MB][NB], uint4* lds, const GemmArgs& g,
+                                              const QkvEpi& e, int64_t m0, int64_t n0, int wid, int wm,
+                                              int wn, int lane, const int64_t* praw) {
+  using DT = EpiDt<EDT>;
+  constexpr int LDR = 136;
+  constexpr bool EARLY_POS = EARLY;
+  const int frow = lane & 31, fhalf = lane >> 5;
+  const int64_t wcol0 = n0 + wn * WN;
+  const int64_t wrow0 = m0 + wm * WM;
+  if constexpr (EPI == EPI_RAW) {
+#pragma unroll
+    for (int i = 0; i < MB; ++i)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int64_t row = wrow0 + i * 32 + 8 * (v / 4) + 4 * fhalf + (v % 4);
+        if (row >= g.m) continue;
+#pragma unroll
+        for (int j = 0; j < NB; ++j) {
+          const int64_t col = wcol0 + j * 32 + frow;
+          if (col < g.n) g.raw[row * g.n + col] = acc[i][j][v];
+        }
+      }
+    return;
+  } else if constexpr (EPI == EPI_LINEAR || EPI == EPI_SWIGLU) {
+    static_assert(WN == 128, "the row epilogue maps 8 lanes x 16 columns onto 128 columns");
+    // Each 32-row accumulator block is staged through this wave's LDS slice;
+    // then 8 lanes per row each take 8 consecutive output columns (twice for
+    // EPI_LINEAR's 128), so residual reads and output writes are 16-byte rows.
+    float* et = reinterpret_cast<float*>(lds) + wid * (32 * LDR);
+    constexpr int CH = EPI == EPI_SWIGLU ? 1 : 2;  // 8-column chunks per lane
+    const int c8 = lane & 7, r8 = lane >> 3;
+    const int64_t ocol0 = EPI == EPI_SWIGLU ? n0 + wn * 64 : wcol0;  // first output column of the wave
+    __syncthreads();  // the K loop's last LDS reads are done before the slices are reused
+#pragma unroll
+    for (int i = 0; i < MB; ++i) {
+#pragma unroll
+      for (int j = 0; j < NB; ++j)
+#pragma unroll
+        for (int v = 0; v < 16; ++v)
+          et[(8 * (v / 4) + 4 * fhalf + (v % 4)) * LDR + j * 32 + frow] = acc[i][j][v];
+      __asm__ volatile("" ::: "memory");  // wave-private slice, LDS keeps a wave's order
+      // Kept rolled: unrolled over the 4 row groups the residual / store paths
+      // grew the kernel past the instruction cache, and the K loop of the other
+      // workgroup on the CU missed in it (o_proj 8192x4096x4096: 1320 vs 232 us).
+#pragma unroll 1
+      for (int it = 0; it < 4; ++it) {
+        const int rl = r8 + 8 * it;
+        const int64_t row = wrow0 + i * 32 + rl;
+#pragma unroll
+        for (int ch = 0; ch < CH; ++ch) {
+          const int lc = 64 * ch + 8 * c8;  // column inside the wave tile
+          const int64_t col = ocol0 + lc;
+          float y[8];
+          const float4 a0 = *reinterpret_cast<const float4*>(et + rl * LDR + lc);
+          const float4 a1 = *reinterpret_cast<const float4*>(et + rl * LDR + lc + 4);
+          const float av[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+          if constexpr (EPI == EPI_SWIGLU) {
+            const float4 u0 = *reinterpret_cast<const float4*>(et + rl * LDR + 64 + lc);
+            const float4 u1 = *reinterpret_cast<const float4*>(et + rl * LDR + 64 + lc + 4);
+            const float uv[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+              const float gt = rnd<DT::Q>(av[t], e.qkv_dt), ut = rnd<DT::Q>(uv[t], e.qkv_dt);
+              y[t] = rnd<DT::O>(rnd<DT::Q>(silu_fast(gt), e.qkv_dt) * ut, e.out_dt);
+            }
+          } else {
+            float bv[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+            if (e.bias) {
+#pragma unroll
+              for (int t = 0; t < 8; ++t) bv[t] = load_any(e.bias, e.bias_dtype, min(col + t, g.n - 1));
+            }
+            float rv[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+            if (e.res && row < g.m) {
+              if (e.vec && col + 8 <= g.n) {
+                if (e.res_dt == BFA_DTYPE_BF16) load8<BFA_DTYPE_BF16>(static_cast<const uint16_t*>(e.res) + row * e.ldr + col, rv);
+                else if (e.res_dt == BFA_DTYPE_F16) load8<BFA_DTYPE_F16>(static_cast<const uint16_t*>(e.res) + row * e.ldr + col, rv);
+                else load8<BFA_DTYPE_F32>(static_cast<const float*>(e.res) + row * e.ldr + col, rv);
+              } else {
+#pragma unroll
+                for (int t = 0; t < 8; ++t)
+                  if (col + t < g.n) rv[t] = load_any(e.res, e.res_dt, row * e.ldr + col + t);
+              }
+            }
+#pragma unroll
+            for (int t = 0; t < 8; ++t)
+              y[t] = rnd<DT::O>(rnd<DT::M>(rnd<DT::Q>(av[t] + bv[t], e.qkv_dt) + rv[t], e.mid_dt), e.out_dt);
+          }
+          if (row < g.m) {
+            if (e.vec && col + 8 <= g.n) {
+              store8_dt<DT::O>(e.out, e.out_dt, row * e.ldo + col, y);
+            } else {
+#pragma unroll
+              for (int t = 0; t < 8; ++t)
+                if (col + t < g.n) store_any(e.out, e.out_dt, row * e.ldo + col + t, y[t]);
+            }
+          }
+        }
+      }
+      __asm__ volatile("" ::: "memory");
+    }
+  } else {
+    static_assert(HD == 32 || HD == 64 || HD == 128, "fused epilogue covers head_dim 32/64/128");
+    static_assert(WN == 128, "the row epilogue maps 16 lanes x 8 columns onto 128 columns");
+    // Each 32-row accumulator block is staged through this wave's slice of the
+    // (now idle) LDS, then processed row by row: 16 lanes per row, each lane
+    // owning 4 RoPE pairs (columns j..j+3 and j+D/2..j+D/2+3 of one head), so
+    // the q/k norm is a butterfly over the D/8 lanes of a head and every store
+    // is a contiguous 4-element vector.
+    constexpr int LH = HD / 8;  // lanes per head
+    float* et = reinterpret_cast<float*>(lds) + wid * (32 * LDR);
+    const int l16 = lane & 15, rg = lane >> 4;
+    const int hloc = l16 / LH, q = l16 % LH;
+    const int c1 = hloc * HD + q * 4, c2 = c1 + HD / 2;  // columns inside the wave tile
+    const int64_t gc1 = wcol0 + c1, gc2 = wcol0 + c2;
+    const bool colok = gc1 < e.n;
+    const int64_t head = min(gc1, e.n - 1) / HD;
+    const int kd = head_kind(e, head);
+    const void* nw = kd == 0 ? e.qn_w : (kd == 1 ? e.kn_w : nullptr);
+    const bool any_norm = e.qn_w != nullptr || e.kn_w != nullptr;
+    const bool rope = e.cs != nullptr && kd != 2;
+    const bool has_bias = e.bias != nullptr;
+    float b1[4], b2[4], g1[4], g2[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      b1[t] = (e.bias && colok) ? load_any(e.bias, e.bias_dtype, gc1 + t) : 0.f;
+      b2[t] = (e.bias && colok) ? load_any(e.bias, e.bias_dtype, gc2 + t) : 0.f;
+      g1[t] = nw ? load_any(nw, e.qk_w_dtype, q * 4 + t) : 1.f;
+      g2[t] = nw ? load_any(nw, e.qk_w_dtype, HD / 2 + q * 4 + t) : 1.f;
+    }
+    const int dt_after = nw ? e.norm_dt : e.qkv_dt;  // dtype RoPE receives
+    // Positions of every row this lane will rotate, fetched up front (one
+    // batch of independent loads) so that each row iteration has a single
+    // dependent load level (its cos/sin) instead of two; -1 marks a position
+    // outside the table.
+    int32_t posv[MB][8];
+    if constexpr (EARLY_POS) {
+      if (rope) {
+#pragma unroll
+        for (int it = 0; it < 8; ++it) posv[0][it] = epi_pos_check(e, praw[it]);
+      }
+    } else if (rope) {
+      if (e.pos_is_i64) {
+#pragma unroll
+        for (int i = 0; i < MB; ++i)
+#pragma unroll
+          for (int it = 0; it < 8; ++it)
+            posv[i][it] = epi_pos_check(e, static_cast<const int64_t*>(e.positions)[min(wrow0 + i * 32 + rg + 4 * it, g.m - 1)]);
+      } else {
+#pragma unroll
+        for (int i = 0; i < MB; ++i)
+#pragma unroll
+          for (int it = 0; it < 8; ++it)
+            posv[i][it] = epi_pos_check(e, static_cast<const int32_t*>(e.positions)[min(wrow0 + i * 32 + rg + 4 * it, g.m - 1)]);
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < MB; ++i) {
+      // The cos/sin rows of the block's 8 rows are all requested before the
+      // accumulators are staged: in the row loop below each load would sit
+      // behind the previous row's stores (the table and the output may alias
+      // as far as the compiler knows), paying the table's L2 latency 8 times.
+      float4 cvv[8], svv[8];
+      if (rope) {
+#pragma unroll
+        for (int it = 0; it < 8; ++it) {
+          const int64_t p = posv[i][it] >= 0 ? posv[i][it] : 0;
+          cvv[it] = *reinterpret_cast<const float4*>(e.cs + p * HD + q * 4);
+          svv[it] = *reinterpret_cast<const float4*>(e.cs + p * HD + HD / 2 + q * 4);
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < NB; ++j)
+#pragma unroll
+        for (int v = 0; v < 16; ++v)
+          et[(8 * (v / 4) + 4 * fhalf + (v % 4)) * LDR + j * 32 + frow] = acc[i][j][v];
+      // The slice is private to this wave and LDS executes one wave's accesses
+      // in issue order, so the row reads below see these writes (and the next
+      // block's writes follow this block's reads) without a barrier; only the
+      // compiler's order must be kept.
+      __asm__ volatile("" ::: "memory");
+      bool bad = false;
+#pragma unroll
+      for (int it = 0; it < 8; ++it) {
+        const int rl = rg + 4 * it;
+        const int64_t row = wrow0 + i * 32 + rl;
+        const float4 a1 = *reinterpret_cast<const float4*>(et + rl * LDR + c1);
+        const float4 a2 = *reinterpret_cast<const float4*>(et + rl * LDR + c2);
+        float x1[4] = {a1.x, a1.y, a1.z, a1.w}, x2[4] = {a2.x, a2.y, a2.z, a2.w};
+        if (has_bias) {
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            x1[t] = x1[t] + b1[t];
+            x2[t] = x2[t] + b2[t];
+          }
+        }
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          x1[t] = rnd<DT::Q>(x1[t], e.qkv_dt);
+          x2[t] = rnd<DT::Q>(x2[t], e.qkv_dt);
+        }
+        if (any_norm) {
+          float ss = 0.f;
+#pragma unroll
+          for (int t = 0; t < 4; ++t) ss += x1[t] * x1[t] + x2[t] * x2[t];
+          ss = group_sum_dpp<LH>(ss);  // lanes of one head form an aligned group of a DPP row
+          if (nw) {
+            const float r = 1.0f / sqrtf(ss / static_cast<float>(HD) + e.qk_eps);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+              x1[t] = rnd<DT::N>((x1[t] * r) * g1[t], e.norm_dt);
+              x2[t] = rnd<DT::N>((x2[t] * r) * g2[t], e.norm_dt);
+            }
+          }
+        }
+        if (rope) {
+          const bool ok = posv[i][it] >= 0;
+          bad = bad || (!ok && row < g.m);
+          const float4 cv = cvv[it], sv = svv[it];
+          const float c[4] = {cv.x, cv.y, cv.z, cv.w}, sn[4] = {sv.x, sv.y, sv.z, sv.w};
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            const float u = x1[t], w = x2[t];
+            x1[t] = ok ? rnd<DT::A>(u * c[t] - w * sn[t], dt_after) : 0.f;
+            x2[t] = ok ? rnd<DT::A>(w * c[t] + u * sn[t], dt_after) : 0.f;
+          }
+        }
+        if (row < g.m && colok) {
+          store4_dt<DT::O>(e.out, e.out_dt, row * e.ldo + gc1, x1);
+          store4_dt<DT::O>(e.out, e.out_dt, row * e.ldo + gc2, x2);
+        }
+      }
+      if (bad && q == 0) flag_status(e.status, BFA_STATUS_INDEX_OOB);
+      __asm__ volatile("" ::: "memory");
+    }
+  }
+}
+
 // DIRECT: tiles go HBM -> LDS by DMA (K % 64 == 0, 16-byte aligned rows,
 // byte offsets below 4 GiB); otherwise HBM -> registers -> LDS with K masking.
 // NW = (BM / WM) (BN / WN) waves per workgroup (4 or 8).  Wave tiles of at most
@@ -416,7 +684,6 @@ template <int BM, int BN, int WM, int WN, bool BF16, int EPI, int HD, bool DIREC
           int EDT = EDT_RT>
 __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, (WM * WN <= 8192 ? 2 : 1)) void qkv_gemm_kernel(
     GemmArgs g, QkvEpi e) {
-  using DT = EpiDt<EDT>;
   constexpr int NWN = BN / WN;
   constexpr int NW = (BM / WM) * NWN;
   static_assert(NW == 4 || NW == 8, "four or eight waves per workgroup");
@@ -440,24 +707,29 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, (WM * WN <= 8192 ? 2 : 
   const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
   const int wm = wid / NWN, wn = wid % NWN;
 
-  // Tile order: workgroups are dispatched round-robin over the 8 XCDs; remap
-  // so that each XCD walks a contiguous range of tiles, and walk tiles
-  // column-major inside groups of 8 row-tiles so that concurrently resident
-  // workgroups on one XCD share operand rows and weight columns in its L2.
-  constexpr int BNO = out_cols<EPI, BN>();
-  const int64_t tiles_m = cdiv(g.m, BM), tiles_n = cdiv(g.n, BNO);
-  const int64_t ntiles = tiles_m * tiles_n;
-  int64_t bid = blockIdx.x;
-  if (ntiles % 8 == 0) bid = (bid % 8) * (ntiles / 8) + bid / 8;
-  constexpr int64_t GROUP_M = 8;
-  const int64_t group = bid / (GROUP_M * tiles_n);
-  const int64_t first_m = group * GROUP_M;
-  const int64_t gsize = min(tiles_m - first_m, GROUP_M);
-  const int64_t tm = first_m + (bid % (GROUP_M * tiles_n)) % gsize;
-  const int64_t tn = (bid % (GROUP_M * tiles_n)) / gsize;
-  const int64_t m0 = tm * BM, n0 = tn * BNO;
+  int64_t m0, n0;
+  tile_origin<EPI, BM, BN>(g, m0, n0);
   const int64_t KT = cdiv(g.k, 64);
   const int frow = lane & 31, fhalf = lane >> 5;
+
+  // Positions of the rows this lane rotates in the fused epilogue (rows
+  // lane / 16 + 4 it of each 32-row block).  With one block per wave they are
+  // requested here, before the K loop (16 registers), so that the epilogue's
+  // cos/sin loads do not wait a memory round trip for them.
+  constexpr bool EARLY_POS = EPI == EPI_FUSED && MB == 1;
+  int64_t praw[EARLY_POS ? 8 : 1];
+  if constexpr (EARLY_POS) {
+    const int64_t r0 = m0 + wm * WM + (lane >> 4);
+    if (e.cs != nullptr) {
+      if (e.pos_is_i64) {
+#pragma unroll
+        for (int it = 0; it < 8; ++it) praw[it] = static_cast<const int64_t*>(e.positions)[min(r0 + 4 * it, g.m - 1)];
+      } else {
+#pragma unroll
+        for (int it = 0; it < 8; ++it) praw[it] = static_cast<const int32_t*>(e.positions)[min(r0 + 4 * it, g.m - 1)];
+      }
+    }
+  }
 
   f32x16_t acc[MB][NB];
 #pragma unroll
@@ -604,235 +876,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, (WM * WN <= 8192 ? 2 : 
     }
   }
 
-  // ------------------------------------------------------------ epilogue
-  // 32x32 accumulator layout: lane holds column (lane & 31) and rows
-  // 8*(v/4) + 4*(lane/32) + (v%4), v = 0..15.
-  const int64_t wcol0 = n0 + wn * WN;
-  const int64_t wrow0 = m0 + wm * WM;
-  if constexpr (EPI == EPI_RAW) {
-#pragma unroll
-    for (int i = 0; i < MB; ++i)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int64_t row = wrow0 + i * 32 + 8 * (v / 4) + 4 * fhalf + (v % 4);
-        if (row >= g.m) continue;
-#pragma unroll
-        for (int j = 0; j < NB; ++j) {
-          const int64_t col = wcol0 + j * 32 + frow;
-          if (col < g.n) g.raw[row * g.n + col] = acc[i][j][v];
-        }
-      }
-    return;
-  } else if constexpr (EPI == EPI_LINEAR || EPI == EPI_SWIGLU) {
-    static_assert(WN == 128, "the row epilogue maps 8 lanes x 16 columns onto 128 columns");
-    // Each 32-row accumulator block is staged through this wave's LDS slice;
-    // then 8 lanes per row each take 8 consecutive output columns (twice for
-    // EPI_LINEAR's 128), so residual reads and output writes are 16-byte rows.
-    float* et = reinterpret_cast<float*>(lds) + wid * (32 * LDR);
-    static_assert(EPI_U4 <= LDS_U4, "epilogue staging fits");
-    constexpr int CH = EPI == EPI_SWIGLU ? 1 : 2;  // 8-column chunks per lane
-    const int c8 = lane & 7, r8 = lane >> 3;
-    const int64_t ocol0 = EPI == EPI_SWIGLU ? n0 + wn * 64 : wcol0;  // first output column of the wave
-    __syncthreads();  // the K loop's last LDS reads are done before the slices are reused
-#pragma unroll
-    for (int i = 0; i < MB; ++i) {
-#pragma unroll
-      for (int j = 0; j < NB; ++j)
-#pragma unroll
-        for (int v = 0; v < 16; ++v)
-          et[(8 * (v / 4) + 4 * fhalf + (v % 4)) * LDR + j * 32 + frow] = acc[i][j][v];
-      __asm__ volatile("" ::: "memory");  // wave-private slice, LDS keeps a wave's order
-      // Kept rolled: unrolled over the 4 row groups the residual / store paths
-      // grew the kernel past the instruction cache, and the K loop of the other
-      // workgroup on the CU missed in it (o_proj 8192x4096x4096: 1320 vs 232 us).
-#pragma unroll 1
-      for (int it = 0; it < 4; ++it) {
-        const int rl = r8 + 8 * it;
-        const int64_t row = wrow0 + i * 32 + rl;
-#pragma unroll
-        for (int ch = 0; ch < CH; ++ch) {
-          const int lc = 64 * ch + 8 * c8;  // column inside the wave tile
-          const int64_t col = ocol0 + lc;
-          float y[8];
-          const float4 a0 = *reinterpret_cast<const float4*>(et + rl * LDR + lc);
-          const float4 a1 = *reinterpret_cast<const float4*>(et + rl * LDR + lc + 4);
-          const float av[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
-          if constexpr (EPI == EPI_SWIGLU) {
-            const float4 u0 = *reinterpret_cast<const float4*>(et + rl * LDR + 64 + lc);
-            const float4 u1 = *reinterpret_cast<const float4*>(et + rl * LDR + 64 + lc + 4);
-            const float uv[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
-#pragma unroll
-            for (int t = 0; t < 8; ++t) {
-              const float gt = rnd<DT::Q>(av[t], e.qkv_dt), ut = rnd<DT::Q>(uv[t], e.qkv_dt);
-              y[t] = rnd<DT::O>(rnd<DT::Q>(silu_fast(gt), e.qkv_dt) * ut, e.out_dt);
-            }
-          } else {
-            float bv[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-            if (e.bias) {
-#pragma unroll
-              for (int t = 0; t < 8; ++t) bv[t] = load_any(e.bias, e.bias_dtype, min(col + t, g.n - 1));
-            }
-            float rv[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-            if (e.res && row < g.m) {
-              if (e.vec && col + 8 <= g.n) {
-                if (e.res_dt == BFA_DTYPE_BF16) load8<BFA_DTYPE_BF16>(static_cast<const uint16_t*>(e.res) + row * e.ldr + col, rv);
-                else if (e.res_dt == BFA_DTYPE_F16) load8<BFA_DTYPE_F16>(static_cast<const uint16_t*>(e.res) + row * e.ldr + col, rv);
-                else load8<BFA_DTYPE_F32>(static_cast<const float*>(e.res) + row * e.ldr + col, rv);
-              } else {
-#pragma unroll
-                for (int t = 0; t < 8; ++t)
-                  if (col + t < g.n) rv[t] = load_any(e.res, e.res_dt, row * e.ldr + col + t);
-              }
-            }
-#pragma unroll
-            for (int t = 0; t < 8; ++t)
-              y[t] = rnd<DT::O>(rnd<DT::M>(rnd<DT::Q>(av[t] + bv[t], e.qkv_dt) + rv[t], e.mid_dt), e.out_dt);
-          }
-          if (row < g.m) {
-            if (e.vec && col + 8 <= g.n) {
-              store8_dt<DT::O>(e.out, e.out_dt, row * e.ldo + col, y);
-            } else {
-#pragma unroll
-              for (int t = 0; t < 8; ++t)
-                if (col + t < g.n) store_any(e.out, e.out_dt, row * e.ldo + col + t, y[t]);
-            }
-          }
-        }
-      }
-      __asm__ volatile("" ::: "memory");
-    }
-  } else {
-    static_assert(HD == 32 || HD == 64 || HD == 128, "fused epilogue covers head_dim 32/64/128");
-    static_assert(WN == 128, "the row epilogue maps 16 lanes x 8 columns onto 128 columns");
-    // Each 32-row accumulator block is staged through this wave's slice of the
-    // (now idle) LDS, then processed row by row: 16 lanes per row, each lane
-    // owning 4 RoPE pairs (columns j..j+3 and j+D/2..j+D/2+3 of one head), so
-    // the q/k norm is a butterfly over the D/8 lanes of a head and every store
-    // is a contiguous 4-element vector.
-    constexpr int LH = HD / 8;  // lanes per head
-    float* et = reinterpret_cast<float*>(lds) + wid * (32 * LDR);
-    static_assert(EPI_U4 <= LDS_U4, "epilogue staging fits");
-    const int l16 = lane & 15, rg = lane >> 4;
-    const int hloc = l16 / LH, q = l16 % LH;
-    const int c1 = hloc * HD + q * 4, c2 = c1 + HD / 2;  // columns inside the wave tile
-    const int64_t gc1 = wcol0 + c1, gc2 = wcol0 + c2;
-    const bool colok = gc1 < e.n;
-    const int64_t head = min(gc1, e.n - 1) / HD;
-    const int kd = head_kind(e, head);
-    const void* nw = kd == 0 ? e.qn_w : (kd == 1 ? e.kn_w : nullptr);
-    const bool any_norm = e.qn_w != nullptr || e.kn_w != nullptr;
-    const bool rope = e.cs != nullptr && kd != 2;
-    const bool has_bias = e.bias != nullptr;
-    float b1[4], b2[4], g1[4], g2[4];
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      b1[t] = (e.bias && colok) ? load_any(e.bias, e.bias_dtype, gc1 + t) : 0.f;
-      b2[t] = (e.bias && colok) ? load_any(e.bias, e.bias_dtype, gc2 + t) : 0.f;
-      g1[t] = nw ? load_any(nw, e.qk_w_dtype, q * 4 + t) : 1.f;
-      g2[t] = nw ? load_any(nw, e.qk_w_dtype, HD / 2 + q * 4 + t) : 1.f;
-    }
-    const int dt_after = nw ? e.norm_dt : e.qkv_dt;  // dtype RoPE receives
-    // Positions of every row this lane will rotate, fetched up front (one
-    // batch of independent loads) so that each row iteration has a single
-    // dependent load level (its cos/sin) instead of two; -1 marks a position
-    // outside the table.
-    int32_t posv[MB][8];
-    if (rope) {
-      if (e.pos_is_i64) {
-#pragma unroll
-        for (int i = 0; i < MB; ++i)
-#pragma unroll
-          for (int it = 0; it < 8; ++it)
-            posv[i][it] = epi_pos_check(e, static_cast<const int64_t*>(e.positions)[min(wrow0 + i * 32 + rg + 4 * it, g.m - 1)]);
-      } else {
-#pragma unroll
-        for (int i = 0; i < MB; ++i)
-#pragma unroll
-          for (int it = 0; it < 8; ++it)
-            posv[i][it] = epi_pos_check(e, static_cast<const int32_t*>(e.positions)[min(wrow0 + i * 32 + rg + 4 * it, g.m - 1)]);
-      }
-    }
-    __syncthreads();
-#pragma unroll
-    for (int i = 0; i < MB; ++i) {
-      // The cos/sin rows of the block's 8 rows are all requested before the
-      // accumulators are staged: in the row loop below each load would sit
-      // behind the previous row's stores (the table and the output may alias
-      // as far as the compiler knows), paying the table's L2 latency 8 times.
-      float4 cvv[8], svv[8];
-      if (rope) {
-#pragma unroll
-        for (int it = 0; it < 8; ++it) {
-          const int64_t p = posv[i][it] >= 0 ? posv[i][it] : 0;
-          cvv[it] = *reinterpret_cast<const float4*>(e.cs + p * HD + q * 4);
-          svv[it] = *reinterpret_cast<const float4*>(e.cs + p * HD + HD / 2 + q * 4);
-        }
-      }
-#pragma unroll
-      for (int j = 0; j < NB; ++j)
-#pragma unroll
-        for (int v = 0; v < 16; ++v)
-          et[(8 * (v / 4) + 4 * fhalf + (v % 4)) * LDR + j * 32 + frow] = acc[i][j][v];
-      // The slice is private to this wave and LDS executes one wave's accesses
-      // in issue order, so the row reads below see these writes (and the next
-      // block's writes follow this block's reads) without a barrier; only the
-      // compiler's order must be kept.
-      __asm__ volatile("" ::: "memory");
-      bool bad = false;
-#pragma unroll
-      for (int it = 0; it < 8; ++it) {
-        const int rl = rg + 4 * it;
-        const int64_t row = wrow0 + i * 32 + rl;
-        const float4 a1 = *reinterpret_cast<const float4*>(et + rl * LDR + c1);
-        const float4 a2 = *reinterpret_cast<const float4*>(et + rl * LDR + c2);
-        float x1[4] = {a1.x, a1.y, a1.z, a1.w}, x2[4] = {a2.x, a2.y, a2.z, a2.w};
-        if (has_bias) {
-#pragma unroll
-          for (int t = 0; t < 4; ++t) {
-            x1[t] = x1[t] + b1[t];
-            x2[t] = x2[t] + b2[t];
-          }
-        }
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          x1[t] = rnd<DT::Q>(x1[t], e.qkv_dt);
-          x2[t] = rnd<DT::Q>(x2[t], e.qkv_dt);
-        }
-        if (any_norm) {
-          float ss = 0.f;
-#pragma unroll
-          for (int t = 0; t < 4; ++t) ss += x1[t] * x1[t] + x2[t] * x2[t];
-          ss = group_sum<LH>(ss);  // lanes of one head form an aligned group
-          if (nw) {
-            const float r = 1.0f / sqrtf(ss / static_cast<float>(HD) + e.qk_eps);
-#pragma unroll
-            for (int t = 0; t < 4; ++t) {
-              x1[t] = rnd<DT::N>((x1[t] * r) * g1[t], e.norm_dt);
-              x2[t] = rnd<DT::N>((x2[t] * r) * g2[t], e.norm_dt);
-            }
-          }
-        }
-        if (rope) {
-          const bool ok = posv[i][it] >= 0;
-          bad = bad || (!ok && row < g.m);
-          const float4 cv = cvv[it], sv = svv[it];
-          const float c[4] = {cv.x, cv.y, cv.z, cv.w}, sn[4] = {sv.x, sv.y, sv.z, sv.w};
-#pragma unroll
-          for (int t = 0; t < 4; ++t) {
-            const float u = x1[t], w = x2[t];
-            x1[t] = ok ? rnd<DT::A>(u * c[t] - w * sn[t], dt_after) : 0.f;
-            x2[t] = ok ? rnd<DT::A>(w * c[t] + u * sn[t], dt_after) : 0.f;
-          }
-        }
-        if (row < g.m && colok) {
-          store4_dt<DT::O>(e.out, e.out_dt, row * e.ldo + gc1, x1);
-          store4_dt<DT::O>(e.out, e.out_dt, row * e.ldo + gc2, x2);
-        }
-      }
-      if (bad && q == 0) flag_status(e.status, BFA_STATUS_INDEX_OOB);
-      __asm__ volatile("" ::: "memory");
-    }
-  }
+  gemm_epilogue<EPI, HD, MB, NB, WM, WN, NW, EDT, EARLY_POS>(acc, lds, g, e, m0, n0, wid, wm, wn, lane, praw);
 }
 
 // ======================================================== decode split-K
