@@ -307,6 +307,7 @@ def config_cases(dev) -> list:
                     ref=lambda: _oracle().silu_and_mul(guc)))
 
     rows += kv_append_cases(dev)
+    rows += fused_append_cases(dev)
     rows += cascade_cases(dev)
     rows += linear_cases(dev)
     return rows
@@ -381,6 +382,84 @@ def kv_append_cases(dev) -> list:
             Row("kv_append_batch_b64", batch, 4 * 64 * hkv * d * 2 + 64 * (8 + 8 + 4) + 65 * 4,
                 ref=lambda: _oracle().append_paged_kv_batch(kdc, vdc, cc, indc, iptc, batc, lens, ps)[0],
                 exact=True, note="whole cache compared")]
+
+
+def fused_append_cases(dev) -> list:
+    """Fused RMSNorm+QKV+RoPE with the paged KV append in its epilogue
+    (bfa_fused_rmsnorm_qkv_append) at Llama-3-8B shapes (seed 7), next to the two
+    separate calls it replaces (fused QKV, then append_to_paged_kv_cache_custom
+    or the batched append): an 8192-token prefill into 512 shuffled pages of a
+    1024-page HND cache (page 16), with and without the k/v columns in the QKV
+    output, and a 64-sequence decode batch (one token each, CSR page table).
+    Every row returns the cache, compared with the oracle's QKV + append."""
+    from braidinfer_amd.kernels import PagedKVAppend, append_paged_kv_batch, append_to_paged_kv_cache_custom
+    from braidinfer_amd.layers import llama_attention_input
+    r = _Gen(7, dev)
+    hkv, d, ps, pages = HKV, D, 16, 1024
+    kvb = 2 * HKV * D * 2  # k and v bytes per token
+    rows = []
+    for t in (8192, 64):
+        (xc, x), (lc, ln), (wc, w) = r.randn(t, H), r.randn(H, std=0.1, mean=1.0), r.randn(N, H, std=0.02)
+        pc = torch.randint(0, MAXPOS, (t,), generator=r.g)
+        pos, rope = pc.to(dev), rope_table(D, MAXPOS, THETA).to(dev)
+        rc_ = rope.cpu()
+        cc, cache = r.randn(pages, 2, hkv, ps, d)
+        if t == 8192:
+            tc = torch.randperm(pages, generator=r.g)[:512].to(torch.int32)
+            cpc = torch.arange(t, dtype=torch.int64)
+            extra = dict(kv_indptr=None, batch_indices=None)
+            ic = bc = None
+        else:
+            lens = torch.randint(0, 4000, (t,), generator=r.g)
+            perm = torch.randperm(pages, generator=r.g)
+            per = lens // ps + 1
+            tc = torch.cat([perm[s].repeat(int(per[s])) for s in range(t)]).to(torch.int32)
+            ic = torch.cat([torch.zeros(1, dtype=torch.int64), per.cumsum(0)]).to(torch.int32)
+            bc = torch.arange(t)
+            cpc = lens
+            extra = dict(kv_indptr=ic.to(dev), batch_indices=bc.to(dev))
+        table, cpos = tc.to(dev), cpc.to(dev)
+        caches = {k: cache.clone() for k in ("fused", "qonly", "sep")}
+        out = torch.empty(t, N, dtype=torch.bfloat16, device=dev)
+
+        def fused(kind, t=t, x=x, ln=ln, w=w, pos=pos, rope=rope, table=table, cpos=cpos, extra=extra,
+                  caches=caches, out=out):
+            pkv = PagedKVAppend(caches[kind], table, cpos, ps, write_kv_out=kind == "fused", **extra)
+            llama_attention_input(x, ln, w, HQ, HKV, EPS, pos, rope, paged_kv=pkv)
+            return caches[kind]
+
+        def separate(t=t, x=x, ln=ln, w=w, pos=pos, rope=rope, table=table, cpos=cpos, extra=extra,
+                     caches=caches):
+            _, k, v = llama_attention_input(x, ln, w, HQ, HKV, EPS, pos, rope)
+            k, v = k.view(t, HKV, D), v.view(t, HKV, D)
+            if extra["kv_indptr"] is None:
+                append_to_paged_kv_cache_custom(k, v, caches["sep"], table, cpos, ps)
+            else:
+                append_paged_kv_batch(k, v, caches["sep"], table, extra["kv_indptr"], extra["batch_indices"],
+                                      cpos, ps)
+            return caches["sep"]
+
+        def ref(t=t, xc=xc, lc=lc, wc=wc, pc=pc, rc_=rc_, cc=cc, tc=tc, cpc=cpc, ic=ic, bc=bc):
+            _, k, v = _oracle().llama_attention_input(xc, lc, wc, HQ, HKV, EPS, pc, rc_)
+            k, v = k.reshape(t, HKV, D), v.reshape(t, HKV, D)
+            if ic is None:
+                return _oracle().append_to_paged_kv_cache(k, v, cc, tc, cpc, ps)[0]
+            return _oracle().append_paged_kv_batch(k, v, cc, tc, ic, bc, cpc, ps)[0]
+
+        qkv_bytes = t * H * 2 + H * 2 + N * H * 2 + t * N * 2 + t * 8 + t * D * 4
+        meta = t * (8 + 8 + 4)  # cache positions, slot offsets, page entries
+        tag = "t8192" if t == 8192 else "b64"
+        rows += [Row(f"qkv_rope_append_llama3_8b_{tag}", lambda fused=fused: fused("fused"),
+                     qkv_bytes + t * kvb + meta, 2.0 * t * H * N, ref=ref,
+                     note="fused QKV + RoPE + paged KV append, one call; cache compared"),
+                 Row(f"qkv_rope_then_append_llama3_8b_{tag}", separate,
+                     qkv_bytes + 2 * t * kvb + meta, 2.0 * t * H * N, ref=ref,
+                     note="the two separate calls it replaces; cache compared")]
+        if t == 8192:
+            rows.append(Row(f"qkv_rope_append_q_only_llama3_8b_{tag}", lambda fused=fused: fused("qonly"),
+                            qkv_bytes - t * kvb + t * kvb + meta, 2.0 * t * H * N, ref=ref,
+                            note="write_kv_out=False: k/v only into the cache; cache compared"))
+    return rows
 
 
 def cascade_cases(dev) -> list:

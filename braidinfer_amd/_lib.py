@@ -78,6 +78,14 @@ _SIGNATURES = {
                                     c_int64, c_int64, c_int64, c_int64, _P, c_int, c_int64,
                                     _P, _P, c_int, c_int64,
                                     _P, c_int, c_int64, _P, _P]),
+    "bfa_fused_rmsnorm_qkv_append_workspace_size": (c_int64, [c_int64, c_int64, c_int64, c_int64]),
+    "bfa_fused_rmsnorm_qkv_append": (c_int, [_P, c_int, c_int64, c_int64, c_int64, _P, c_int,
+                                             c_float, c_int, _P, c_int, c_int64, c_int64, _P, c_int,
+                                             c_int64, c_int64, c_int, _P, _P, c_int, c_float, c_int,
+                                             _P, c_int, _P, c_int64, _P, c_int, c_int64, _P, c_int64,
+                                             _P, c_int, c_int64, c_int64, c_int64, c_int64, c_int64,
+                                             c_int64, _P, c_int, c_int64, _P, _P, c_int, c_int64,
+                                             _P, c_int, c_int64, c_int, _P, _P]),
     "bfa_online_softmax_update": (c_int, [_P, _P, _P, c_int, c_int, _P, _P, _P, _P, c_int, _P,
                                           c_int, c_int64, c_int64, c_int64, c_int64, c_int64,
                                           c_int64, c_int64, c_int64, c_int64, c_int64, c_int64,

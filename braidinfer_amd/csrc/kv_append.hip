@@ -26,79 +26,12 @@
 // slots, as every reference caller builds them (positions are an arange and a
 // page table holds distinct pages); for two tokens on one slot the reference
 // keeps the later token, and which one this kernel keeps is unspecified.
+#include "bfa_append.h"
 #include "bfa_device.h"
 #include "bfa_host.h"
+#include "bfa_internal.h"
 
 namespace bfa {
-
-struct AppendArgs {
-  const void* k;
-  const void* v;
-  int64_t k_st, k_sh, v_st, v_sh;  // token / head strides of k and v (elements)
-  uint32_t heads, head_dim;
-  void* cache;
-  int64_t c_sp, c_skv, c_sh, c_ss;  // page, K|V, head and slot strides (elements)
-  int64_t num_pages, cache_slots;   // pages in the cache, slots per cache page
-  int64_t page_size;                // divisor mapping a position to (page entry, slot)
-  const void* indices;
-  int idx_is_i64;
-  int64_t num_indices;
-  const int32_t* indptr;      // batched form: sequence s owns indices[indptr[s], indptr[s+1])
-  const void* batch;          // batched form: sequence of each token
-  int batch_is_i64;
-  int64_t num_seqs;
-  const void* positions;
-  int pos_is_i64;
-  FastDiv chunks_per_head;   // head_dim / 8 (vector kernel) or head_dim (scalar kernel)
-  FastDiv chunks_per_kv;     // heads * chunks_per_head
-  int* status;
-};
-
-// Destination (page, slot) of token t, or false when the token is not written
-// (the reason is flagged by the first lane of each wave that resolves t).
-__device__ __forceinline__ bool append_target(const AppendArgs& a, int64_t t, int64_t& page,
-                                              int64_t& slot) {
-  const int64_t pos = a.pos_is_i64 ? static_cast<const int64_t*>(a.positions)[t]
-                                   : static_cast<const int32_t*>(a.positions)[t];
-  int64_t off = pos / a.page_size, s = pos - off * a.page_size;
-  if (s < 0) {  // C truncates toward zero; Python floors
-    s += a.page_size;
-    off -= 1;
-  }
-  int bad = 0;
-  int64_t first = 0, len = a.num_indices;  // this token's page table
-  if (a.indptr) {
-    const int64_t sq = a.batch_is_i64 ? static_cast<const int64_t*>(a.batch)[t]
-                                      : static_cast<const int32_t*>(a.batch)[t];
-    if (sq < 0 || sq >= a.num_seqs) {
-      if ((threadIdx.x & 63) == 0) flag_status(a.status, BFA_STATUS_INDEX_OOB);
-      return false;
-    }
-    first = a.indptr[sq];
-    len = a.indptr[sq + 1] - first;
-  }
-  if (off >= len) {
-    bad = BFA_STATUS_APPEND_SKIPPED;
-  } else if (off < -len) {
-    bad = BFA_STATUS_INDEX_OOB;
-  } else {
-    if (off < 0) off += len;
-    off += first;
-    // a batched table slice must lie inside kv_indices (a malformed kv_indptr is an index error)
-    int64_t p = (off >= 0 && off < a.num_indices)
-                    ? (a.idx_is_i64 ? static_cast<const int64_t*>(a.indices)[off]
-                                    : static_cast<const int32_t*>(a.indices)[off])
-                    : a.num_pages;
-    if (p < -a.num_pages || p >= a.num_pages || s >= a.cache_slots) {
-      bad = BFA_STATUS_INDEX_OOB;
-    } else {
-      page = p < 0 ? p + a.num_pages : p;
-      slot = s;
-    }
-  }
-  if (bad && (threadIdx.x & 63) == 0) flag_status(a.status, bad);
-  return bad == 0;
-}
 
 // Copies 8 consecutive elements; a raw 16- or 32-byte copy for equal dtypes.
 template <int DTS, int DTD>
@@ -196,6 +129,62 @@ __global__ __launch_bounds__(256) void kv_append_scalar_kernel(AppendArgs a) {
   }
 }
 
+// Cache slot of every token for the QKV epilogues that append K and V
+// themselves: slot_off[t] = page * c_sp + slot * c_ss (elements), or -1 when the
+// token is not written (the reason is flagged in the status word).
+__global__ __launch_bounds__(256) void kv_slot_kernel(AppendArgs a, int64_t tokens, int64_t* slot_off) {
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (t >= tokens) return;
+  int64_t page = 0, slot = 0;
+  const int bad = append_target_code(a, t, page, slot);
+  if (bad) flag_status(a.status, bad);
+  slot_off[t] = bad ? -1 : page * a.c_sp + slot * a.c_ss;
+}
+
+void launch_kv_slots(const AppendArgs& a, int64_t tokens, int64_t* slot_off, hipStream_t s) {
+  hipLaunchKernelGGL(kv_slot_kernel, dim3(static_cast<unsigned>(cdiv(tokens, 256))), dim3(256), 0, s, a,
+                     tokens, slot_off);
+}
+
+int fill_append_args(const char* what, void* layer_cache, int cache_dtype, int64_t num_pages,
+                     int64_t cache_page_slots, int64_t stride_page, int64_t stride_kv,
+                     int64_t stride_head, int64_t stride_slot, const void* kv_indices,
+                     int kv_indices_dtype, int64_t num_indices, const int32_t* kv_indptr,
+                     const void* batch_indices, int batch_indices_dtype, int64_t num_seqs,
+                     const void* positions, int positions_dtype, int64_t page_size, int32_t* status,
+                     AppendArgs* out) {
+  BFA_REQUIRE(is_float_dtype(cache_dtype), "%s: bad cache dtype", what);
+  BFA_REQUIRE(kv_indices_dtype == BFA_DTYPE_I32 || kv_indices_dtype == BFA_DTYPE_I64,
+              "%s: kv_indices must be int32/int64", what);
+  BFA_REQUIRE(positions_dtype == BFA_DTYPE_I32 || positions_dtype == BFA_DTYPE_I64,
+              "%s: positions must be int32/int64", what);
+  BFA_REQUIRE(page_size > 0, "%s: page_size must be positive", what);
+  BFA_REQUIRE(num_pages >= 0 && cache_page_slots >= 0 && num_indices >= 0, "%s: bad geometry", what);
+  if (kv_indptr) {
+    BFA_REQUIRE(batch_indices && num_seqs >= 0, "%s: batched append needs batch_indices", what);
+    BFA_REQUIRE(batch_indices_dtype == BFA_DTYPE_I32 || batch_indices_dtype == BFA_DTYPE_I64,
+                "%s: batch_indices must be int32/int64", what);
+  }
+  AppendArgs a{};
+  a.cache = layer_cache;
+  a.c_sp = stride_page; a.c_skv = stride_kv; a.c_sh = stride_head; a.c_ss = stride_slot;
+  a.num_pages = num_pages;
+  a.cache_slots = cache_page_slots;
+  a.page_size = page_size;
+  a.indices = kv_indices;
+  a.idx_is_i64 = kv_indices_dtype == BFA_DTYPE_I64;
+  a.num_indices = num_indices;
+  a.indptr = kv_indptr;
+  a.batch = batch_indices;
+  a.batch_is_i64 = batch_indices_dtype == BFA_DTYPE_I64;
+  a.num_seqs = num_seqs;
+  a.positions = positions;
+  a.pos_is_i64 = positions_dtype == BFA_DTYPE_I64;
+  a.status = status;
+  *out = a;
+  return BFA_OK;
+}
+
 template <int DTS, int DTD>
 static void launch_append(AppendArgs a, int64_t tokens, bool vec, hipStream_t s) {
   a.chunks_per_head = FastDiv(vec ? a.head_dim / 8 : a.head_dim);
@@ -240,46 +229,24 @@ extern "C" int bfa_append_paged_kv(const void* k, const void* v, int kv_dtype, i
                                    const void* positions, int positions_dtype, int64_t page_size,
                                    int32_t* status, void* stream) {
   const char* what = "bfa_append_paged_kv";
-  BFA_REQUIRE(is_float_dtype(kv_dtype) && is_float_dtype(cache_dtype), "%s: bad dtype", what);
-  BFA_REQUIRE(kv_indices_dtype == BFA_DTYPE_I32 || kv_indices_dtype == BFA_DTYPE_I64,
-              "%s: kv_indices must be int32/int64", what);
-  BFA_REQUIRE(positions_dtype == BFA_DTYPE_I32 || positions_dtype == BFA_DTYPE_I64,
-              "%s: positions must be int32/int64", what);
-  BFA_REQUIRE(page_size > 0, "%s: page_size must be positive", what);
-  BFA_REQUIRE(num_tokens >= 0 && num_kv_heads >= 0 && head_dim >= 0 && num_pages >= 0 &&
-                  cache_page_slots >= 0 && num_indices >= 0,
-              "%s: bad geometry", what);
+  BFA_REQUIRE(is_float_dtype(kv_dtype), "%s: bad dtype", what);
+  BFA_REQUIRE(num_tokens >= 0 && num_kv_heads >= 0 && head_dim >= 0, "%s: bad geometry", what);
   BFA_REQUIRE(num_tokens < (int64_t{1} << 31), "%s: too many tokens", what);
   BFA_REQUIRE(num_kv_heads * head_dim < (int64_t{1} << 30), "%s: head block too large", what);
+  AppendArgs a{};
+  int rc = fill_append_args(what, layer_cache, cache_dtype, num_pages, cache_page_slots, stride_page,
+                            stride_kv, stride_head, stride_slot, kv_indices, kv_indices_dtype,
+                            num_indices, kv_indptr, batch_indices, batch_indices_dtype, num_seqs,
+                            positions, positions_dtype, page_size, status, &a);
+  if (rc != BFA_OK) return rc;
   if (num_tokens == 0 || num_kv_heads == 0 || head_dim == 0) return BFA_OK;
   BFA_REQUIRE(k && v && layer_cache && positions, "%s: null pointer", what);
   BFA_REQUIRE(num_indices == 0 || kv_indices, "%s: null kv_indices", what);
-  if (kv_indptr) {
-    BFA_REQUIRE(batch_indices && num_seqs >= 0, "%s: batched append needs batch_indices", what);
-    BFA_REQUIRE(batch_indices_dtype == BFA_DTYPE_I32 || batch_indices_dtype == BFA_DTYPE_I64,
-                "%s: batch_indices must be int32/int64", what);
-  }
-  AppendArgs a{};
   a.k = k; a.v = v;
   a.k_st = k_stride_token; a.k_sh = k_stride_head;
   a.v_st = v_stride_token; a.v_sh = v_stride_head;
   a.heads = static_cast<uint32_t>(num_kv_heads);
   a.head_dim = static_cast<uint32_t>(head_dim);
-  a.cache = layer_cache;
-  a.c_sp = stride_page; a.c_skv = stride_kv; a.c_sh = stride_head; a.c_ss = stride_slot;
-  a.num_pages = num_pages;
-  a.cache_slots = cache_page_slots;
-  a.page_size = page_size;
-  a.indices = kv_indices;
-  a.idx_is_i64 = kv_indices_dtype == BFA_DTYPE_I64;
-  a.num_indices = num_indices;
-  a.indptr = kv_indptr;
-  a.batch = batch_indices;
-  a.batch_is_i64 = batch_indices_dtype == BFA_DTYPE_I64;
-  a.num_seqs = num_seqs;
-  a.positions = positions;
-  a.pos_is_i64 = positions_dtype == BFA_DTYPE_I64;
-  a.status = status;
   const auto m8 = [](int64_t x) { return x % 8 == 0; };
   const bool vec = head_dim % 8 == 0 && m8(k_stride_token) && m8(k_stride_head) &&
                    m8(v_stride_token) && m8(v_stride_head) && m8(stride_page) && m8(stride_kv) &&

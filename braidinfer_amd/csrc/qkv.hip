@@ -34,6 +34,7 @@
 #include <cstdlib>
 #include <mutex>
 
+#include "bfa_append.h"
 #include "bfa_device.h"
 #include "bfa_host.h"
 #include "bfa_internal.h"
@@ -103,6 +104,20 @@ struct QkvEpi {
   int64_t stat_rows;
   int64_t hidden;
   float stat_eps;
+  // Paged-KV append in the epilogue (bfa_fused_rmsnorm_qkv_append): the k and v
+  // heads of row t also go to cache + slot_off[t] + (V ? c_skv : 0) + (head -
+  // first head of its kind) * c_sh + column in the head, as cache_dt (from the
+  // value rounded to out_dt); slot_off[t] < 0 skips the row.  skip_kv_out = 1
+  // leaves the k/v columns of `out` unwritten.
+  void* cache;
+  int cache_dt;
+  int64_t c_skv, c_sh;
+  const int64_t* slot_off;
+  int skip_kv_out;
+  // app_in_kernel = 1: the prefill GEMM resolves its rows' cache slots itself
+  // (before the K loop, from `app`), and slot_off is not used
+  int app_in_kernel;
+  AppendArgs app;
 };
 
 __device__ __forceinline__ float round_to(float v, int dt) {
@@ -433,8 +448,9 @@ __device__ __forceinline__ void tile_origin(const GemmArgs& g, int64_t& m0, int6
 // column n0 + wn * WN (n0 in output columns).  lds: at least NW x 32 x LDR
 // floats, free for the wave-private staging slices (the caller's barrier-free
 // LDS use must be over).  praw: the rows' raw positions when EARLY (one block
-// per wave, requested before the K loop).
-template <int EPI, int HD, int MB, int NB, int WM, int WN, int NW, int EDT, bool EARLY>
+// per wave, requested before the K loop).  SLOT_U4: uint4 offset in lds of the
+// fused KV append's slot table (MB x 32 int64 per wave).
+template <int EPI, int HD, int MB, int NB, int WM, int WN, int NW, int EDT, bool EARLY, int SLOT_U4>
 __device__ __forceinline__ void gemm_epilogue(f32x16_t (&acc)[MB][NB], uint4* lds, const GemmArgs& g,
                                               const QkvEpi& e, int64_t m0, int64_t n0, int wid, int wm,
                                               int wn, int lane, const int64_t* praw) {
@@ -565,6 +581,13 @@ __device__ __forceinline__ void gemm_epilogue(f32x16_t (&acc)[MB][NB], uint4* ld
       g2[t] = nw ? load_any(nw, e.qk_w_dtype, HD / 2 + q * 4 + t) : 1.f;
     }
     const int dt_after = nw ? e.norm_dt : e.qkv_dt;  // dtype RoPE receives
+    // fused KV append: this wave's rows' cache slots, in a wave-private LDS
+    // table after the staging slices (filled after the barrier below)
+    const bool app = e.cache != nullptr && kd != 0;
+    const bool out_ok = kd == 0 || !e.skip_kv_out;
+    int64_t* const stab = reinterpret_cast<int64_t*>(lds + SLOT_U4) + wid * (MB * 32);
+    const int64_t hk = head - e.hq - (kd == 2 ? e.hkv : 0);  // head index within the k or v heads
+    const int64_t cbase = (kd == 2 ? e.c_skv : 0) + hk * e.c_sh + q * 4;
     // Positions of every row this lane will rotate, fetched up front (one
     // batch of independent loads) so that each row iteration has a single
     // dependent load level (its cos/sin) instead of two; -1 marks a position
@@ -591,6 +614,11 @@ __device__ __forceinline__ void gemm_epilogue(f32x16_t (&acc)[MB][NB], uint4* ld
       }
     }
     __syncthreads();
+    if (e.cache != nullptr && !e.app_in_kernel) {
+      // rows past m read the last row's slot; their stores are masked
+      for (int r = lane; r < MB * 32; r += 64) stab[r] = e.slot_off[min(wrow0 + r, g.m - 1)];
+      __asm__ volatile("" ::: "memory");  // the wave's own LDS writes precede its reads below
+    }
 #pragma unroll
     for (int i = 0; i < MB; ++i) {
       // The cos/sin rows of the block's 8 rows are all requested before the
@@ -663,8 +691,23 @@ __device__ __forceinline__ void gemm_epilogue(f32x16_t (&acc)[MB][NB], uint4* ld
           }
         }
         if (row < g.m && colok) {
-          store4_dt<DT::O>(e.out, e.out_dt, row * e.ldo + gc1, x1);
-          store4_dt<DT::O>(e.out, e.out_dt, row * e.ldo + gc2, x2);
+          if (out_ok) {
+            store4_dt<DT::O>(e.out, e.out_dt, row * e.ldo + gc1, x1);
+            store4_dt<DT::O>(e.out, e.out_dt, row * e.ldo + gc2, x2);
+          }
+          if (app) {
+            const int64_t so = stab[i * 32 + rl];
+            if (so >= 0) {
+              float y1[4], y2[4];
+#pragma unroll
+              for (int t = 0; t < 4; ++t) {
+                y1[t] = rnd<DT::O>(x1[t], e.out_dt);
+                y2[t] = rnd<DT::O>(x2[t], e.out_dt);
+              }
+              store4_sel(e.cache, e.cache_dt, so + cbase, y1);
+              store4_sel(e.cache, e.cache_dt, so + cbase + HD / 2, y2);
+            }
+          }
         }
       }
       if (bad && q == 0) flag_status(e.status, BFA_STATUS_INDEX_OOB);
@@ -698,7 +741,11 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, (WM * WN <= 8192 ? 2 : 
   constexpr int STAGE_U4 = (BM + BN) * BK / 8;
   constexpr int EPI_U4 = NW * 32 * LDR / 4;
   constexpr int MAIN_U4 = DIRECT ? (BK == 32 ? NS : 2) * STAGE_U4 : 2 * (BM + BN) * 8;
-  constexpr int LDS_U4 = MAIN_U4 > EPI_U4 ? MAIN_U4 : EPI_U4;
+  // the fused KV append's per-wave slot table (MB x 32 int64) lies past both the
+  // K loop's buffers and the epilogue's staging slices: it is filled before the
+  // K loop and read in the epilogue
+  constexpr int SLOT_U4 = MAIN_U4 > EPI_U4 ? MAIN_U4 : EPI_U4;
+  constexpr int LDS_U4 = SLOT_U4 + (EPI == EPI_FUSED ? NW * MB * 32 / 2 : 0);
   __shared__ uint4 lds[LDS_U4];
   uint4* const lds0 = lds;
   uint4* const lds1 = lds + (BM + BN) * 8;
@@ -711,6 +758,23 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, (WM * WN <= 8192 ? 2 : 
   tile_origin<EPI, BM, BN>(g, m0, n0);
   const int64_t KT = cdiv(g.k, 64);
   const int frow = lane & 31, fhalf = lane >> 5;
+
+  // Fused KV append: the cache slots of this wave's rows go to its slot table.
+  // Called right after the K loop's first loads are issued, so that the
+  // page-table lookups wait together with those loads, not ahead of them.
+  auto resolve_slots = [&]() {
+    if constexpr (EPI == EPI_FUSED) {
+      if (e.cache != nullptr && e.app_in_kernel) {
+        int64_t* stab = reinterpret_cast<int64_t*>(lds + SLOT_U4) + wid * (MB * 32);
+        for (int r = lane; r < MB * 32; r += 64) {
+          int64_t page = 0, slot = 0;
+          const int bad = append_target_code(e.app, min(m0 + wm * WM + r, g.m - 1), page, slot);
+          if (bad) flag_status(e.app.status, bad);
+          stab[r] = bad ? -1 : page * e.app.c_sp + slot * e.app.c_ss;
+        }
+      }
+    }
+  };
 
   // Positions of the rows this lane rotates in the fused epilogue (rows
   // lane / 16 + 4 it of each 32-row block).  With one block per wave they are
@@ -767,6 +831,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, (WM * WN <= 8192 ? 2 : 
 #pragma unroll
     for (int st = 0; st < NS; ++st)
       if (st < nst) issue_stage<ADPW, BDPW, BM, 32, NW>(g.a, g.w, st, aoff, boff, lbase + st * SB);
+    resolve_slots();
     wait_stages<DPW, NS>(min<int64_t>(NS - 1, nst - 1));
     __syncthreads();
     uint4 fa0[MB], fb0[NB], fa1[MB], fb1[NB];
@@ -808,6 +873,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, (WM * WN <= 8192 ? 2 : 
     const uint32_t l0 = lds_addr(lds0) + wid * 1024, l1 = lds_addr(lds1) + wid * 1024;
     uint4 fa0[MB], fb0[NB], fa1[MB], fb1[NB];
     issue_stage<ADPW, BDPW, BM, 64, NW>(g.a, g.w, 0, aoff, boff, l0);
+    resolve_slots();
     wait_vmem();
     __syncthreads();
     load_frags<MB, NB, BM, WM, WN>(lds0, 0, wm, wn, frow, fhalf, fa0, fb0);
@@ -847,6 +913,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, (WM * WN <= 8192 ? 2 : 
     uint4 ra2[AG], rb2[BG];
     uint4 fa0[MB], fb0[NB], fa1[MB], fb1[NB];
     tile_load<AG, BG, false>(g.a, g.w, aoff, boff, 0, gg, g.k, ra, rb);
+    resolve_slots();
     tile_store<AG, BG, BM>(lds0, gr, gg, ra, rb);
     if (KT > 1) tile_load<AG, BG, false>(g.a, g.w, aoff, boff, 1, gg, g.k, ra, rb);
     if (KT > 2) tile_load<AG, BG, false>(g.a, g.w, aoff, boff, 2, gg, g.k, ra2, rb2);
@@ -876,7 +943,8 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, (WM * WN <= 8192 ? 2 : 
     }
   }
 
-  gemm_epilogue<EPI, HD, MB, NB, WM, WN, NW, EDT, EARLY_POS>(acc, lds, g, e, m0, n0, wid, wm, wn, lane, praw);
+  gemm_epilogue<EPI, HD, MB, NB, WM, WN, NW, EDT, EARLY_POS, SLOT_U4>(acc, lds, g, e, m0, n0, wid, wm, wn,
+                                                                    lane, praw);
 }
 
 // ======================================================== decode split-K
@@ -1449,6 +1517,13 @@ __device__ __forceinline__ void decode_epilogue_item(const float4* part, int64_t
   // values masked) so that none waits behind a per-token or per-dtype branch.
   // absent inputs read a valid stand-in (the partials) and are masked after
   const void* posp = rope ? e.positions : part;
+  // fused KV append: cache slots of the 4 tokens (first load level)
+  const bool app = e.cache != nullptr && kd != 0;
+  int64_t so[4] = {-1, -1, -1, -1};
+  if (app) {
+#pragma unroll
+    for (int v = 0; v < 4; ++v) so[v] = e.slot_off[min(tg * 4 + v, m - 1)];
+  }
   int64_t raw[4];
   if (rope && e.pos_is_i64) {
 #pragma unroll
@@ -1620,8 +1695,16 @@ __device__ __forceinline__ void decode_epilogue_item(const float4* part, int64_t
         a = pok[v] ? round_to(u * c - w * sn, dt) : 0.f;
         b = pok[v] ? round_to(w * c + u * sn, dt) : 0.f;
       }
-      store_any(e.out, e.out_dt, t * e.ldo + base + p, a);
-      store_any(e.out, e.out_dt, t * e.ldo + base + half + p, b);
+      if (kd == 0 || !e.skip_kv_out) {
+        store_any(e.out, e.out_dt, t * e.ldo + base + p, a);
+        store_any(e.out, e.out_dt, t * e.ldo + base + half + p, b);
+      }
+      if (app && so[v] >= 0) {
+        const int64_t hk = h - e.hq - (kd == 2 ? e.hkv : 0);
+        const int64_t cb = so[v] + (kd == 2 ? e.c_skv : 0) + hk * e.c_sh;
+        store_any(e.cache, e.cache_dt, cb + p, round_to(a, e.out_dt));
+        store_any(e.cache, e.cache_dt, cb + half + p, round_to(b, e.out_dt));
+      }
     }
   }
 }
@@ -1728,6 +1811,9 @@ __device__ __forceinline__ void row_epilogue_item(const float* part, int64_t spl
   float x1[MAXP], x2[MAXP];
   int dt = e.qkv_dt;
   float ss = 0.f;
+  // fused KV append: this token's cache slot
+  const bool app = e.cache != nullptr && kd != 0;
+  const int64_t so = app ? e.slot_off[t] : -1;
 #pragma unroll
   for (int p = 0; p < MAXP; ++p) {
     const int64_t j = lane + 64 * p;
@@ -1791,12 +1877,19 @@ __device__ __forceinline__ void row_epilogue_item(const float* part, int64_t spl
       }
     }
   }
+  const int64_t cb = so + (kd == 2 ? e.c_skv : 0) + (h - e.hq - (kd == 2 ? e.hkv : 0)) * e.c_sh;
 #pragma unroll
   for (int p = 0; p < MAXP; ++p) {
     const int64_t j = lane + 64 * p;
     if (j < half) {
-      store_any(e.out, e.out_dt, t * e.ldo + base + j, x1[p]);
-      store_any(e.out, e.out_dt, t * e.ldo + base + half + j, x2[p]);
+      if (kd == 0 || !e.skip_kv_out) {
+        store_any(e.out, e.out_dt, t * e.ldo + base + j, x1[p]);
+        store_any(e.out, e.out_dt, t * e.ldo + base + half + j, x2[p]);
+      }
+      if (app && so >= 0) {
+        store_any(e.cache, e.cache_dt, cb + j, round_to(x1[p], e.out_dt));
+        store_any(e.cache, e.cache_dt, cb + half + j, round_to(x2[p], e.out_dt));
+      }
     }
   }
 }
@@ -2149,6 +2242,16 @@ extern "C" int64_t bfa_fused_rmsnorm_qkv_workspace_size(int64_t tokens, int64_t 
   return p.operand_bytes + p.part_bytes;
 }
 
+// Host side of the fused KV append's QkvEpi fields.
+struct CacheEpi {
+  void* cache;
+  int cache_dt;
+  int64_t c_skv, c_sh;
+  const int64_t* slot_off;  // resolved slots (decode and raw-epilogue paths)
+  int skip_kv_out;
+  const AppendArgs* app;    // the prefill GEMM's fused epilogue resolves its own
+};
+
 // The projection with its epilogue; `operand` rows are `lda` apart.  With a
 // fold (decode, one to four tokens) `operand` is the raw input x and the decode
 // kernel normalises it itself.
@@ -2162,7 +2265,8 @@ static int qkv_projection_impl(const void* operand, int64_t lda, const OperandFo
                                   const void* positions, int positions_dtype,
                                   const float* cos_sin_cache, int64_t max_position, void* out,
                                   int out_dtype, int64_t out_stride, void* part_workspace,
-                                  int64_t part_workspace_bytes, int32_t* status, void* stream) {
+                                  int64_t part_workspace_bytes, int32_t* status, void* stream,
+                                  const CacheEpi* ce = nullptr) {
   const char* what = fold ? "bfa_fused_rmsnorm_qkv" : "bfa_qkv_projection";
   BFA_REQUIRE(w_dtype == BFA_DTYPE_BF16 || w_dtype == BFA_DTYPE_F16, "%s: weight must be bf16/fp16", what);
   BFA_REQUIRE(is_float_dtype(qkv_dtype) && is_float_dtype(out_dtype) && is_float_dtype(qk_norm_out_dtype),
@@ -2207,6 +2311,16 @@ static int qkv_projection_impl(const void* operand, int64_t lda, const OperandFo
   e.out = out; e.ldo = out_stride; e.status = status;
   if (fold && fold->stats) {
     e.stats = fold->stats; e.stat_rows = 16 * p.mt; e.hidden = hidden; e.stat_eps = fold->eps;
+  }
+  if (ce) {
+    e.cache = ce->cache; e.cache_dt = ce->cache_dt; e.c_skv = ce->c_skv; e.c_sh = ce->c_sh;
+    e.slot_off = ce->slot_off; e.skip_kv_out = ce->skip_kv_out;
+    if (!p.decode && p.fused_epi) {
+      e.app_in_kernel = 1;
+      e.app = *ce->app;
+    } else {
+      BFA_REQUIRE(ce->slot_off != nullptr, "%s: cache slots not resolved", what);
+    }
   }
 
   const hipStream_t st = as_stream(stream);
@@ -2269,18 +2383,15 @@ extern "C" int bfa_qkv_projection(const void* operand, int64_t tokens, int64_t h
                              out_stride, part_workspace, part_workspace_bytes, status, stream);
 }
 
-extern "C" int bfa_fused_rmsnorm_qkv(const void* x, int x_dtype, int64_t tokens, int64_t hidden,
-                                     int64_t x_stride, const void* norm_weight, int nw_dtype,
-                                     float eps, int mixed_rounding, const void* qkv_weight,
-                                     int w_dtype, int64_t qkv_dim, int64_t w_stride,
-                                     const void* bias, int bias_dtype, int64_t num_q_heads,
-                                     int64_t num_kv_heads, int qkv_dtype,
-                                     const void* q_norm_weight, const void* k_norm_weight,
-                                     int qk_norm_dtype, float qk_eps, int qk_norm_out_dtype,
-                                     const void* positions, int positions_dtype,
-                                     const float* cos_sin_cache, int64_t max_position, void* out,
-                                     int out_dtype, int64_t out_stride, void* workspace,
-                                     int64_t workspace_bytes, int32_t* status, void* stream) {
+static int fused_impl(const void* x, int x_dtype, int64_t tokens, int64_t hidden, int64_t x_stride,
+                      const void* norm_weight, int nw_dtype, float eps, int mixed_rounding,
+                      const void* qkv_weight, int w_dtype, int64_t qkv_dim, int64_t w_stride,
+                      const void* bias, int bias_dtype, int64_t num_q_heads, int64_t num_kv_heads,
+                      int qkv_dtype, const void* q_norm_weight, const void* k_norm_weight,
+                      int qk_norm_dtype, float qk_eps, int qk_norm_out_dtype, const void* positions,
+                      int positions_dtype, const float* cos_sin_cache, int64_t max_position, void* out,
+                      int out_dtype, int64_t out_stride, void* workspace, int64_t workspace_bytes,
+                      int32_t* status, void* stream, const CacheEpi* ce) {
   const char* what = "bfa_fused_rmsnorm_qkv";
   BFA_REQUIRE(x && norm_weight && qkv_weight, "%s: null pointer", what);
   if (tokens == 0) return BFA_OK;
@@ -2320,7 +2431,7 @@ extern "C" int bfa_fused_rmsnorm_qkv(const void* x, int x_dtype, int64_t tokens,
                                bias, bias_dtype, num_q_heads, num_kv_heads, qkv_dtype, q_norm_weight,
                                k_norm_weight, qk_norm_dtype, qk_eps, qk_norm_out_dtype, positions,
                                positions_dtype, cos_sin_cache, max_position, out, out_dtype, out_stride,
-                               ws + p.operand_bytes, workspace_bytes - p.operand_bytes, status, stream);
+                               ws + p.operand_bytes, workspace_bytes - p.operand_bytes, status, stream, ce);
   }
   if (fold) {
     const OperandFold f{norm_weight, nw_dtype, mixed_rounding != 0, eps, fold_rows, nullptr};
@@ -2328,17 +2439,99 @@ extern "C" int bfa_fused_rmsnorm_qkv(const void* x, int x_dtype, int64_t tokens,
                                bias, bias_dtype, num_q_heads, num_kv_heads, qkv_dtype, q_norm_weight,
                                k_norm_weight, qk_norm_dtype, qk_eps, qk_norm_out_dtype, positions,
                                positions_dtype, cos_sin_cache, max_position, out, out_dtype, out_stride,
-                               ws + p.operand_bytes, workspace_bytes - p.operand_bytes, status, stream);
+                               ws + p.operand_bytes, workspace_bytes - p.operand_bytes, status, stream, ce);
   }
   int rc = launch_qkv_operand(x, x_dtype, tokens, hidden, x_stride, norm_weight, nw_dtype,
                               mixed_rounding != 0, ws, w_dtype, eps, as_stream(stream));
   if (rc != BFA_OK) return rc;
-  return bfa_qkv_projection(ws, tokens, hidden, qkv_weight, w_dtype, qkv_dim, w_stride, bias,
-                            bias_dtype, num_q_heads, num_kv_heads, qkv_dtype, q_norm_weight,
-                            k_norm_weight, qk_norm_dtype, qk_eps, qk_norm_out_dtype, positions,
-                            positions_dtype, cos_sin_cache, max_position, out, out_dtype,
-                            out_stride, ws + p.operand_bytes, workspace_bytes - p.operand_bytes,
-                            status, stream);
+  return qkv_projection_impl(ws, hidden, nullptr, tokens, hidden, qkv_weight, w_dtype, qkv_dim, w_stride,
+                             bias, bias_dtype, num_q_heads, num_kv_heads, qkv_dtype, q_norm_weight,
+                             k_norm_weight, qk_norm_dtype, qk_eps, qk_norm_out_dtype, positions,
+                             positions_dtype, cos_sin_cache, max_position, out, out_dtype, out_stride,
+                             ws + p.operand_bytes, workspace_bytes - p.operand_bytes, status, stream, ce);
+}
+
+extern "C" int bfa_fused_rmsnorm_qkv(const void* x, int x_dtype, int64_t tokens, int64_t hidden,
+                                     int64_t x_stride, const void* norm_weight, int nw_dtype,
+                                     float eps, int mixed_rounding, const void* qkv_weight,
+                                     int w_dtype, int64_t qkv_dim, int64_t w_stride,
+                                     const void* bias, int bias_dtype, int64_t num_q_heads,
+                                     int64_t num_kv_heads, int qkv_dtype,
+                                     const void* q_norm_weight, const void* k_norm_weight,
+                                     int qk_norm_dtype, float qk_eps, int qk_norm_out_dtype,
+                                     const void* positions, int positions_dtype,
+                                     const float* cos_sin_cache, int64_t max_position, void* out,
+                                     int out_dtype, int64_t out_stride, void* workspace,
+                                     int64_t workspace_bytes, int32_t* status, void* stream) {
+  return fused_impl(x, x_dtype, tokens, hidden, x_stride, norm_weight, nw_dtype, eps, mixed_rounding,
+                    qkv_weight, w_dtype, qkv_dim, w_stride, bias, bias_dtype, num_q_heads, num_kv_heads,
+                    qkv_dtype, q_norm_weight, k_norm_weight, qk_norm_dtype, qk_eps, qk_norm_out_dtype,
+                    positions, positions_dtype, cos_sin_cache, max_position, out, out_dtype, out_stride,
+                    workspace, workspace_bytes, status, stream, nullptr);
+}
+
+// ------------------------------------------------ fused QKV + paged KV append
+// bfa_fused_rmsnorm_qkv, then bfa_append_paged_kv of its k and v heads (as
+// [tokens, num_kv_heads, head_dim] views of `out`), in the projection's own
+// epilogue: a small kernel first resolves every token's cache slot into the
+// workspace tail (tokens x 8 bytes), then each epilogue writes the finished k/v
+// head rows to the cache as well (and, with write_kv_out = 0, only there).
+extern "C" int64_t bfa_fused_rmsnorm_qkv_append_workspace_size(int64_t tokens, int64_t hidden,
+                                                               int64_t qkv_dim, int64_t head_dim) {
+  if (tokens <= 0) return 0;
+  return bfa_fused_rmsnorm_qkv_workspace_size(tokens, hidden, qkv_dim, head_dim) + align256(tokens * 8);
+}
+
+extern "C" int bfa_fused_rmsnorm_qkv_append(
+    const void* x, int x_dtype, int64_t tokens, int64_t hidden, int64_t x_stride, const void* norm_weight,
+    int nw_dtype, float eps, int mixed_rounding, const void* qkv_weight, int w_dtype, int64_t qkv_dim,
+    int64_t w_stride, const void* bias, int bias_dtype, int64_t num_q_heads, int64_t num_kv_heads,
+    int qkv_dtype, const void* q_norm_weight, const void* k_norm_weight, int qk_norm_dtype, float qk_eps,
+    int qk_norm_out_dtype, const void* positions, int positions_dtype, const float* cos_sin_cache,
+    int64_t max_position, void* out, int out_dtype, int64_t out_stride, void* workspace,
+    int64_t workspace_bytes, void* layer_cache, int cache_dtype, int64_t num_pages,
+    int64_t cache_page_slots, int64_t stride_page, int64_t stride_kv, int64_t stride_head,
+    int64_t stride_slot, const void* kv_indices, int kv_indices_dtype, int64_t num_indices,
+    const int32_t* kv_indptr, const void* batch_indices, int batch_indices_dtype, int64_t num_seqs,
+    const void* cache_positions, int cache_positions_dtype, int64_t page_size, int write_kv_out,
+    int32_t* status, void* stream) {
+  const char* what = "bfa_fused_rmsnorm_qkv_append";
+  AppendArgs a{};
+  int rc = fill_append_args(what, layer_cache, cache_dtype, num_pages, cache_page_slots, stride_page,
+                            stride_kv, stride_head, stride_slot, kv_indices, kv_indices_dtype, num_indices,
+                            kv_indptr, batch_indices, batch_indices_dtype, num_seqs, cache_positions,
+                            cache_positions_dtype, page_size, status, &a);
+  if (rc != BFA_OK) return rc;
+  BFA_REQUIRE(tokens >= 0 && tokens < (int64_t{1} << 31), "%s: bad token count", what);
+  if (tokens == 0) return BFA_OK;
+  BFA_REQUIRE(layer_cache && cache_positions, "%s: null cache or positions", what);
+  BFA_REQUIRE(num_indices == 0 || kv_indices, "%s: null kv_indices", what);
+  // the prefill epilogue writes 4 consecutive elements per store
+  BFA_REQUIRE(stride_page % 4 == 0 && stride_kv % 4 == 0 && stride_head % 4 == 0 && stride_slot % 4 == 0 &&
+                  aligned16(layer_cache),
+              "%s: cache strides must be multiples of 4 elements and the cache 16-byte aligned", what);
+  const int64_t heads = num_q_heads + 2 * num_kv_heads;
+  BFA_REQUIRE(heads > 0 && qkv_dim % heads == 0, "%s: bad head geometry", what);
+  const int64_t fsize = bfa_fused_rmsnorm_qkv_workspace_size(tokens, hidden, qkv_dim, qkv_dim / heads);
+  BFA_REQUIRE(workspace && aligned16(workspace) && workspace_bytes >= fsize + align256(tokens * 8),
+              "%s: workspace too small (%lld < %lld bytes)", what, (long long)workspace_bytes,
+              (long long)(fsize + align256(tokens * 8)));
+  // the prefill GEMM with the fused epilogue resolves the slots itself; every
+  // other path reads them from the workspace tail, filled by a small kernel
+  const QkvPlan p = make_plan(tokens, qkv_dim, hidden, qkv_dim / heads);
+  int64_t* slot_off = nullptr;
+  if (p.decode || !p.fused_epi) {
+    slot_off = reinterpret_cast<int64_t*>(static_cast<char*>(workspace) + fsize);
+    launch_kv_slots(a, tokens, slot_off, as_stream(stream));
+    rc = check_launch(what);
+    if (rc != BFA_OK) return rc;
+  }
+  const CacheEpi ce{layer_cache, cache_dtype, stride_kv, stride_head, slot_off, write_kv_out ? 0 : 1, &a};
+  return fused_impl(x, x_dtype, tokens, hidden, x_stride, norm_weight, nw_dtype, eps, mixed_rounding,
+                    qkv_weight, w_dtype, qkv_dim, w_stride, bias, bias_dtype, num_q_heads, num_kv_heads,
+                    qkv_dtype, q_norm_weight, k_norm_weight, qk_norm_dtype, qk_eps, qk_norm_out_dtype,
+                    positions, positions_dtype, cos_sin_cache, max_position, out, out_dtype, out_stride,
+                    workspace, fsize, status, stream, &ce);
 }
 
 // ------------------------------------------------ allocation-free variant

@@ -4,7 +4,7 @@ from .fused_rmsnorm_qkv_minimal_f32 import FusedRMSNormQKVMinimalF32
 from .fused_rmsnorm_qkv_mixed_precision import FusedRMSNormQKVMixedPrecision
 from .fused_rmsnorm_qkv_production import FusedRMSNormQKV
 from .fused_rmsnorm_qkv_with_bias import FusedRMSNormQKVWithBias
-from .kv_cache_utils import (append_paged_kv_batch, append_to_paged_kv_cache_custom,
+from .kv_cache_utils import (PagedKVAppend, append_paged_kv_batch, append_to_paged_kv_cache_custom,
                              build_paged_kv_indices)
 from .online_softmax import online_softmax_update
 from .rmsnorm_f32 import RMSNormF32
@@ -15,6 +15,7 @@ __all__ = [
     "FusedRMSNormQKVMinimalF32",
     "FusedRMSNormQKVMixedPrecision",
     "FusedRMSNormQKVWithBias",
+    "PagedKVAppend",
     "RMSNormF32",
     "append_paged_kv_batch",
     "attention_output",

@@ -51,9 +51,12 @@ def fused_rmsnorm_qkv(
     positions: torch.Tensor | None = None,
     cos_sin_cache: torch.Tensor | None = None,
     out: torch.Tensor | None = None,
+    paged_kv=None,
 ) -> torch.Tensor:
     """Runs RMSNorm -> x @ W^T (+bias) [-> q/k RMSNorm] [-> RoPE] and returns the
-    [tokens, qkv_dim] result (q | k | v columns) in `out_dtype`."""
+    [tokens, qkv_dim] result (q | k | v columns) in `out_dtype`.  With
+    ``paged_kv`` (a kv_cache_utils.PagedKVAppend) the k and v heads are also
+    appended to that paged cache by the same call."""
     assert input.dim() == 2, f"Expected 2D input, got {input.dim()}D"
     tokens, hidden = input.shape
     qkv_dim = qkv_weight.shape[0]
@@ -93,7 +96,30 @@ def fused_rmsnorm_qkv(
             positions = positions.contiguous()
     if out is None:
         out = torch.empty((tokens, qkv_dim), dtype=out_dtype, device=dev)
+    if paged_kv is not None:
+        cache_args = paged_kv.c_args(tokens, num_kv_heads, hd)
     if tokens == 0:
+        return out
+    if paged_kv is not None:
+        ws_bytes = _lib.workspace_size("bfa_fused_rmsnorm_qkv_append_workspace_size", tokens, hidden,
+                                       qkv_dim, hd)
+        workspace = _lib.workspace(dev, ws_bytes)
+        _lib.call(
+            "bfa_fused_rmsnorm_qkv_append",
+            input.data_ptr(), _lib.dtype_code(input), tokens, hidden, input.stride(0),
+            norm_weight.data_ptr(), _lib.dtype_code(norm_weight), float(eps), int(mixed_rounding),
+            w.data_ptr(), _lib.dtype_code(w), qkv_dim, w.stride(0),
+            _lib.ptr(qkv_bias), _lib.dtype_code(qkv_bias) if qkv_bias is not None else 0,
+            num_q_heads, num_kv_heads, _lib.dtype_code(qkv_dtype),
+            _lib.ptr(q_norm_weight), _lib.ptr(k_norm_weight),
+            _lib.dtype_code(qn_dtype) if qn_dtype is not None else 0, float(qk_norm_eps),
+            _lib.dtype_code(qk_norm_out_dtype or input.dtype),
+            _lib.ptr(positions), _lib.dtype_code(positions) if positions is not None else 0,
+            _lib.ptr(cos_sin_cache), cos_sin_cache.shape[0] if cos_sin_cache is not None else 0,
+            out.data_ptr(), _lib.dtype_code(out), out.stride(0),
+            workspace.data_ptr(), workspace.numel(), *cache_args,
+            _lib.status_word(dev).data_ptr(), _lib.stream_of(dev),
+        )
         return out
     ws_bytes = _lib.workspace_size("bfa_fused_rmsnorm_qkv_workspace_size", tokens, hidden, qkv_dim, hd)
     workspace = _lib.workspace(dev, ws_bytes)

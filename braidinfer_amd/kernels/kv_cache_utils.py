@@ -4,11 +4,14 @@
 loop (two ``.item()`` host syncs and two slice assignments per token,
 kernels/kv_cache_utils.py:9-78) with one launch of ``bfa_append_paged_kv``.
 ``build_paged_kv_indices`` is the reference's host-side CSR builder
-(kernels/kv_cache_utils.py:81-118), restated.
+(kernels/kv_cache_utils.py:81-118), restated.  ``PagedKVAppend`` names where a
+fused RMSNorm+QKV call (``fused_rmsnorm_qkv(..., paged_kv=...)``) appends its k
+and v heads itself, in the projection's epilogue.
 """
 from __future__ import annotations
 
-from typing import List, Tuple
+from dataclasses import dataclass
+from typing import List, Optional, Tuple
 
 import torch
 
@@ -125,6 +128,82 @@ def _append(k, v, layer_cache, kv_indices, kv_indptr, batch_indices, positions, 
         _lib.ptr(positions), _lib.dtype_code(positions), int(page_size),
         _lib.ptr(_lib.status_word(dev)), _lib.stream_of(dev),
     )
+
+
+@dataclass
+class PagedKVAppend:
+    """The cache side of append_to_paged_kv_cache_custom (or, with ``kv_indptr``
+    and ``batch_indices``, of append_paged_kv_batch) for a fused QKV call that
+    appends its own k and v heads: the appended rows are the call's k and v
+    outputs ([tokens, num_kv_heads, head_dim] in its output dtype), at
+    ``positions`` (the tokens' positions in their sequences).  With
+    ``write_kv_out=False`` the call leaves the k/v columns of its output
+    unwritten and only the cache receives them."""
+
+    layer_cache: torch.Tensor
+    kv_indices: torch.Tensor
+    positions: torch.Tensor
+    page_size: int
+    kv_layout: str = "HND"
+    kv_indptr: Optional[torch.Tensor] = None
+    batch_indices: Optional[torch.Tensor] = None
+    write_kv_out: bool = True
+
+    def c_args(self, num_tokens: int, num_kv_heads: int, head_dim: int) -> tuple:
+        """Checks the cache against the call's kv heads and returns the cache
+        arguments of bfa_fused_rmsnorm_qkv_append (layer_cache .. write_kv_out)."""
+        cache = self.layer_cache
+        if self.kv_layout not in _LAYOUT_DIMS:
+            raise ValueError(f"Unknown kv_layout: {self.kv_layout}")
+        if cache.dim() != 5 or cache.shape[1] != 2:
+            raise ValueError("layer_cache must be [num_pages, 2, ...] with 5 dimensions")
+        hdim, sdim = _LAYOUT_DIMS[self.kv_layout]
+        if cache.shape[hdim] != num_kv_heads or cache.shape[4] != head_dim:
+            raise RuntimeError(f"layer_cache holds {cache.shape[hdim]} heads x {cache.shape[4]}, the "
+                               f"call's k/v rows are {num_kv_heads} x {head_dim}")
+        if cache.stride(-1) != 1:
+            raise ValueError("layer_cache must have unit stride along head_dim")
+        if num_tokens and self.page_size == 0:
+            raise ZeroDivisionError("integer division or modulo by zero")
+        if self.page_size < 0:
+            raise ValueError("page_size must be positive")
+        positions = self.positions.reshape(-1)
+        if positions.numel() < num_tokens:
+            raise IndexError(f"{positions.numel()} positions for {num_tokens} tokens")
+        positions = positions[:num_tokens]
+        if positions.dtype not in (torch.int32, torch.int64):
+            positions = positions.long()
+        if self.kv_indices.dim() > 1:
+            raise ValueError("kv_indices must be one-dimensional")
+        kv_indices = self.kv_indices.reshape(-1)
+        if kv_indices.dtype not in (torch.int32, torch.int64):
+            kv_indices = kv_indices.long()
+        kv_indptr = batch_indices = None
+        if self.kv_indptr is not None:
+            if self.batch_indices is None:
+                raise ValueError("a batched append needs batch_indices")
+            kv_indptr = self.kv_indptr.reshape(-1).to(torch.int32).contiguous()
+            batch_indices = self.batch_indices.reshape(-1)
+            if batch_indices.dtype not in (torch.int32, torch.int64):
+                batch_indices = batch_indices.long()
+            if batch_indices.numel() < num_tokens:
+                raise IndexError(f"{batch_indices.numel()} batch indices for {num_tokens} tokens")
+            batch_indices = batch_indices[:num_tokens].contiguous()
+        # keep the converted tensors alive until the call has been queued
+        self._keep = (positions.contiguous(), kv_indices.contiguous(), kv_indptr, batch_indices)
+        positions, kv_indices = self._keep[0], self._keep[1]
+        _lib.require_device(cache, kv_indices, positions, kv_indptr, batch_indices)
+        st = cache.stride()
+        return (
+            _lib.ptr(cache), _lib.dtype_code(cache), cache.shape[0], cache.shape[sdim],
+            st[0], st[1], st[hdim], st[sdim],
+            _lib.ptr(kv_indices), _lib.dtype_code(kv_indices), kv_indices.numel(),
+            _lib.ptr(kv_indptr), _lib.ptr(batch_indices),
+            _lib.dtype_code(batch_indices) if batch_indices is not None else 0,
+            kv_indptr.numel() - 1 if kv_indptr is not None else 0,
+            _lib.ptr(positions), _lib.dtype_code(positions), int(self.page_size),
+            int(bool(self.write_kv_out)),
+        )
 
 
 def build_paged_kv_indices(

@@ -12,6 +12,9 @@ and the attention call:
 
 Both return (q_flat, k_flat, v_flat) of shapes [T, Hq*D], [T, Hkv*D],
 [T, Hkv*D] in the hidden-state dtype, as views of one [T, qkv_dim] buffer.
+With ``paged_kv`` (kernels.kv_cache_utils.PagedKVAppend) the same call also
+appends k and v to the layer's paged cache, which the reference's attention
+layer does next (layers/attention.py:191-205 -> kernels/kv_cache_utils.py:9-78).
 """
 from __future__ import annotations
 
@@ -30,24 +33,24 @@ def qwen3_attention_input(hidden_states: torch.Tensor, layernorm_weight: torch.T
                           num_heads: int, num_kv_heads: int, rms_norm_eps: float,
                           positions: torch.Tensor, cos_sin_cache: torch.Tensor,
                           q_norm_weight: torch.Tensor, k_norm_weight: torch.Tensor,
-                          qk_norm_eps: float | None = None):
+                          qk_norm_eps: float | None = None, paged_kv=None):
     dtype = hidden_states.dtype
     out = fused_rmsnorm_qkv(
         hidden_states, layernorm_weight, qkv_weight, num_heads, num_kv_heads, rms_norm_eps,
         mixed_rounding=True, qkv_dtype=torch.bfloat16, out_dtype=dtype, qkv_bias=qkv_bias,
         q_norm_weight=q_norm_weight, k_norm_weight=k_norm_weight,
         qk_norm_eps=rms_norm_eps if qk_norm_eps is None else qk_norm_eps,
-        qk_norm_out_dtype=dtype, positions=positions, cos_sin_cache=cos_sin_cache)
+        qk_norm_out_dtype=dtype, positions=positions, cos_sin_cache=cos_sin_cache, paged_kv=paged_kv)
     return _split_flat(out, num_heads, num_kv_heads)
 
 
 def llama_attention_input(hidden_states: torch.Tensor, layernorm_weight: torch.Tensor,
                           qkv_weight: torch.Tensor, num_heads: int, num_kv_heads: int,
                           rms_norm_eps: float, positions: torch.Tensor,
-                          cos_sin_cache: torch.Tensor):
+                          cos_sin_cache: torch.Tensor, paged_kv=None):
     dtype = hidden_states.dtype
     out = fused_rmsnorm_qkv(
         hidden_states, layernorm_weight, qkv_weight, num_heads, num_kv_heads, rms_norm_eps,
         mixed_rounding=False, qkv_dtype=torch.float32, out_dtype=dtype,
-        positions=positions, cos_sin_cache=cos_sin_cache)
+        positions=positions, cos_sin_cache=cos_sin_cache, paged_kv=paged_kv)
     return _split_flat(out, num_heads, num_kv_heads)

@@ -282,6 +282,37 @@ int bfa_append_paged_kv(const void* k, const void* v, int kv_dtype, int64_t num_
                         const void* positions, int positions_dtype, int64_t page_size,
                         int32_t* status, void* stream);
 
+/* bfa_fused_rmsnorm_qkv followed by bfa_append_paged_kv of its k and v heads,
+ * in one call whose projection epilogue writes the cache itself --
+ * kernels/kv_cache_utils.py:9-78 fused into the QKV epilogue, as the page
+ * manager appends each layer's k/v right after its QKV projection
+ * (engine/page_manager.py:159-218, layers/attention.py:191-205).  No single
+ * reference function does both; the result is what the two calls produce:
+ * out as bfa_fused_rmsnorm_qkv, then k = out[:, Hq*D : (Hq+Hkv)*D] and
+ * v = out[:, (Hq+Hkv)*D :] (as [tokens, Hkv, D], rounded to out_dtype) appended
+ * by the rule of bfa_append_paged_kv with `cache_positions` (the tokens'
+ * positions in their sequences, which may differ from the RoPE positions).
+ * write_kv_out = 0 leaves the k/v columns of out unwritten (q only).  Cache
+ * strides must be multiples of 4 elements and the cache 16-byte aligned.
+ * workspace: bfa_fused_rmsnorm_qkv_append_workspace_size() bytes (the fused
+ * workspace plus tokens x 8 bytes of resolved cache slots). */
+int64_t bfa_fused_rmsnorm_qkv_append_workspace_size(int64_t tokens, int64_t hidden,
+                                                    int64_t qkv_dim, int64_t head_dim);
+int bfa_fused_rmsnorm_qkv_append(
+    const void* x, int x_dtype, int64_t tokens, int64_t hidden, int64_t x_stride,
+    const void* norm_weight, int nw_dtype, float eps, int mixed_rounding, const void* qkv_weight,
+    int w_dtype, int64_t qkv_dim, int64_t w_stride, const void* bias, int bias_dtype,
+    int64_t num_q_heads, int64_t num_kv_heads, int qkv_dtype, const void* q_norm_weight,
+    const void* k_norm_weight, int qk_norm_dtype, float qk_eps, int qk_norm_out_dtype,
+    const void* positions, int positions_dtype, const float* cos_sin_cache, int64_t max_position,
+    void* out, int out_dtype, int64_t out_stride, void* workspace, int64_t workspace_bytes,
+    void* layer_cache, int cache_dtype, int64_t num_pages, int64_t cache_page_slots,
+    int64_t stride_page, int64_t stride_kv, int64_t stride_head, int64_t stride_slot,
+    const void* kv_indices, int kv_indices_dtype, int64_t num_indices, const int32_t* kv_indptr,
+    const void* batch_indices, int batch_indices_dtype, int64_t num_seqs,
+    const void* cache_positions, int cache_positions_dtype, int64_t page_size, int write_kv_out,
+    int32_t* status, void* stream);
+
 /* ------------------------------------------------------ cascade attention --
  * online_softmax_update — braidinfer/kernels/online_softmax.py:214-297 (kernel
  * :14-211): updates the running state (m_i [H, B], l_i [H, B], acc_i [H, B, D],
