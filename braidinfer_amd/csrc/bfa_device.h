@@ -22,6 +22,13 @@ __device__ __forceinline__ float bf16_bits_to_f32(uint32_t b) {
 __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
   return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
 }
+// two floats -> two bf16 (round to nearest even) in one word, low element in
+// the low half: a single v_cvt_pk_bf16_f32
+typedef __bf16 bfa_bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float bfa_f32x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((bfa_f32x2_t){lo, hi}, bfa_bf16x2_t));
+}
 __device__ __forceinline__ float f16_bits_to_f32(uint32_t b) {
   return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(b)));
 }
@@ -195,6 +202,17 @@ __device__ __forceinline__ void dma16(const void* base, uint32_t voff, uint32_t 
   const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(b >> 32)));
   const uint64_t bu = (static_cast<uint64_t>(hi) << 32) | lo;
   asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(__builtin_amdgcn_readfirstlane(m0)),
+               "v"(voff), "s"(reinterpret_cast<const void*>(bu))
+               : "memory");
+}
+
+// 4-byte form of dma16: lane i's dword at base + voff goes to LDS m0 + 4 i.
+__device__ __forceinline__ void dma4(const void* base, uint32_t voff, uint32_t m0) {
+  const uint64_t b = reinterpret_cast<uint64_t>(base);
+  const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(b)));
+  const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(b >> 32)));
+  const uint64_t bu = (static_cast<uint64_t>(hi) << 32) | lo;
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, %2" ::"s"(__builtin_amdgcn_readfirstlane(m0)),
                "v"(voff), "s"(reinterpret_cast<const void*>(bu))
                : "memory");
 }

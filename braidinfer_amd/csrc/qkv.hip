@@ -31,6 +31,12 @@
 //  * qkv_decode_epilogue_kernel / qkv_epilogue_kernel sum the split-K partials (or
 //    read the raw fp32 projection for head_dim the GEMM epilogue does not cover)
 //    and apply bias / q-k norm / RoPE / rounding per (token, head) row.
+//  * qkv_decode_pair_kernel  17-64 decode tokens without q/k norm: a workgroup
+//    owns 16 RoPE column pairs for the whole of K (its waves split K, each
+//    streaming its segments by LDS DMA through a private ring), so the projection,
+//    the fp32 variants' RMSNorm (gamma on the weight fragments, row sums of
+//    squares from the operand fragments), bias, RoPE and the KV append run in
+//    one launch with no partials.
 #include <cstdlib>
 #include <mutex>
 
@@ -1798,6 +1804,293 @@ __global__ __launch_bounds__(256) void qkv_decode_epilogue_kernel(const float4* 
   decode_epilogue_item<MAXP>(part, splits, ntiles, mt, m, e, tg, item - tg * heads, threadIdx.x & 63);
 }
 
+// ================================== decode: whole-K column-pair tiles
+// 17-64 tokens, head_dim a multiple of 32, no q/k norm.  A workgroup owns 32
+// output columns -- 16 of the first half of a head, h D + c0 + [0, 16), and the
+// 16 that RoPE pairs with them, + D/2 -- for every token and the whole of K, so
+// the projection never leaves the workgroup: no split-K partials, no reduction
+// kernel.  The four waves split K: wave w takes the 64-deep segment w of every
+// 256-deep chunk and streams it on its own, with no barrier until the end.  Per
+// chunk the wave DMAs its operand segment (rows x 128 B) and its weight segment
+// (32 rows x 128 B: the 16 first-half columns, then their pairs), whole cache
+// lines, into a slot of its private LDS ring (granule g of row r at slot
+// g ^ (r/2 & 7)), and reads 16x16x32 fragments from there.  The loop issues no
+// other memory request, so the one wait per chunk is exact: before chunk c the
+// wave waits for vmcnt(PER x chunks already requested after c), and chunk
+// c + R goes into c's slot as soon as c's fragments are in registers.
+// At the end the four partial tiles are summed through LDS in wave order and
+// wave i finishes the rows of 16-token block i: a lane holds the pair (p, p + D/2)
+// of four rows in its two accumulators, so RoPE needs no exchange.
+//
+// SA (scale-after, the fp32 variants, bf16 x and gamma): the operand is the raw
+// x and gamma goes onto the weight fragments (bf16(w * gamma): every weight
+// element is used by one workgroup only, where x * gamma would be redone by every
+// column tile; the segment's 64 gamma values come with the chunk, one 8-lane
+// DMA); the rows' sums of squares come from one more MFMA of each operand
+// fragment with itself (the diagonal of the 16x16 Gram block), and the epilogue
+// multiplies the projection by r = 1 / sqrt(sum / hidden + eps) before the bias.
+// No pass over x and no other launch.
+
+template <int MT> struct PairRing { static constexpr int R = MT == 2 ? 4 : 3; };  // slots within 160 KiB
+
+template <int MT, bool SA, int EDT>
+__global__ __launch_bounds__(256) void qkv_decode_pair_kernel(DecodeArgs d, QkvEpi e, int nch) {
+  using DT = EpiDt<EDT>;
+  constexpr int R = PairRing<MT>::R;
+  constexpr int ROWS = MT * 16;
+  constexpr int DX = ROWS / 8;          // operand DMAs per wave per chunk (8 rows x 128 B)
+  constexpr int PER = DX + 4 + (SA ? 1 : 0);  // + 4 weight DMAs (+ gamma)
+  constexpr int XS = ROWS * 8;          // uint4 of the operand part of a slot
+  constexpr int GS = XS + 32 * 8;       // + the weight part; then 8 uint4 of gamma
+  constexpr int SLOT = GS + (SA ? 8 : 0);
+  static_assert(MT >= 2 && MT <= 4, "two to four token blocks");
+  static_assert((R - 1) * PER < 64 && R <= 4, "vmcnt range");
+  __shared__ uint4 ring[4 * R * SLOT];
+  __shared__ uint32_t posl[4][32];  // per wave: the raw positions of its 16 epilogue rows
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lr = lane & 15, lq = lane >> 4;
+  const int64_t tph = e.hd / 32;  // pair tiles per head
+  const int64_t head = blockIdx.x / tph;
+  const int64_t c0 = (blockIdx.x - head * tph) * 16;  // first pair of the tile inside the head
+  const int64_t half = e.hd / 2;
+  const int64_t cola = head * e.hd + c0;  // columns cola + [0, 16) and cola + half + [0, 16)
+
+  // DMA j of a 128-byte-row block covers its rows 8 j .. 8 j + 7: lane l fills
+  // slot l % 8 of row 8 j + l / 8, i.e. logical granule (l % 8) ^ (row / 2 & 7).
+  // Operand rows past m re-read row m - 1; weight row 8 j + l / 8 of the tile is
+  // column cola + row (rows < 16) or cola + half + row - 16.
+  uint32_t aoff[DX], woff[4];
+#pragma unroll
+  for (int j = 0; j < DX; ++j) {
+    const int row = 8 * j + (lane >> 3);
+    const int g = (lane & 7) ^ ((row >> 1) & 7);
+    aoff[j] = static_cast<uint32_t>((min<int64_t>(row, d.m - 1) * d.lda + wid * 64 + g * 8) * 2);
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int row = 8 * j + (lane >> 3);
+    const int g = (lane & 7) ^ ((row >> 1) & 7);
+    const int64_t col = cola + (row < 16 ? row : half + row - 16);
+    woff[j] = static_cast<uint32_t>((col * d.ldw + wid * 64 + g * 8) * 2);
+  }
+  const uint32_t lring = lds_addr(ring) + static_cast<uint32_t>(wid * R * SLOT * 16);
+  const uint32_t goff = static_cast<uint32_t>((wid * 64 + lane * 8) * 2);
+  // Each workgroup walks the chunks from its own starting point (workgroups of
+  // one XCD, i = xcd + 8 j, start at chunk j mod nch): rows are a power of two
+  // apart, so in lockstep every workgroup would read the same 512-byte column
+  // band of x and W, which sits in a few L2 channels.
+  const int rot = static_cast<int>((blockIdx.x >> 3) % static_cast<unsigned>(nch));
+  auto kchunk = [&](int c) { return c + rot < nch ? c + rot : c + rot - nch; };
+  auto issue = [&](int c) {
+    const uint32_t ls = lring + static_cast<uint32_t>((c % R) * SLOT * 16);
+    const int64_t kc = kchunk(c);
+    const uint16_t* ab = d.a + kc * 256;
+    const uint16_t* wb = d.w + kc * 256;
+#pragma unroll
+    for (int j = 0; j < DX; ++j) dma16(ab, aoff[j], ls + j * 1024);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) dma16(wb, woff[j], ls + (XS + j * 64) * 16);
+    if constexpr (SA) {
+      // lanes 0-7: the segment's 64 gamma values
+      if (lane < 8) dma16(static_cast<const uint16_t*>(d.gamma) + kc * 256, goff, ls + GS * 16);
+    }
+  };
+
+  // this lane finishes rows 16 wid + 4 lq + v of columns cola + lr, + half (wid < MT)
+  const int kd = head_kind(e, head);
+  const bool rope = kd != 2 && e.cs != nullptr;
+  // Epilogue inputs.  The compiler waits for a load it issued by counting only
+  // its own requests, so a use of one inside the loop would wait for every DMA
+  // in flight: the positions come by DMA into LDS instead (one 4-byte request
+  // per lane, ahead of the ring, so chunk 0's wait covers them) and the cos/sin
+  // rows are requested once chunk 0 has landed; the bias and the cache slots
+  // need nothing and go out first.  All of them are used after the loop.
+  const int psh = e.pos_is_i64 ? 1 : 0;
+  if (rope && wid < MT && lane < (16 << psh)) {
+    const int64_t t = min<int64_t>(wid * 16 + (lane >> psh), d.m - 1);
+    dma4(e.positions, static_cast<uint32_t>(((t << psh) + (lane & psh)) * 4), lds_addr(posl[wid]));
+  }
+  float cs[4] = {1.f, 1.f, 1.f, 1.f}, sn[4] = {0.f, 0.f, 0.f, 0.f};
+  uint32_t bw[4] = {0, 0, 0, 0};
+  int64_t so[4] = {-1, -1, -1, -1};
+  bool pok[4] = {true, true, true, true};
+  const bool app = e.cache != nullptr && kd != 0;
+  const int64_t p = c0 + lr;  // this lane's pair inside the head
+  if (wid < MT) {
+    if (e.bias) {
+      // 16-bit words (an fp32 bias element is two), combined after the loop
+      const uint16_t* bp = static_cast<const uint16_t*>(e.bias);
+      const int sh = e.bias_dtype == BFA_DTYPE_F32 ? 1 : 0;
+      const int64_t ia = (cola + lr) << sh, ib = (cola + half + lr) << sh;
+      bw[0] = bp[ia]; bw[1] = bp[ia + sh]; bw[2] = bp[ib]; bw[3] = bp[ib + sh];
+    }
+    if (app) {
+#pragma unroll
+      for (int v = 0; v < 4; ++v) so[v] = e.slot_off[min<int64_t>(wid * 16 + lq * 4 + v, d.m - 1)];
+    }
+  }
+  auto rope_loads = [&]() {
+    if (wid >= MT || !rope) return;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int r = lq * 4 + v;
+      const int64_t raw = psh ? static_cast<int64_t>((static_cast<uint64_t>(posl[wid][2 * r + 1]) << 32) |
+                                                     posl[wid][2 * r])
+                              : static_cast<int64_t>(static_cast<int32_t>(posl[wid][r]));
+      const int32_t c = epi_pos_check(e, raw);
+      pok[v] = c >= 0;
+      const int64_t o = static_cast<int64_t>(pok[v] ? c : 0) * e.hd;
+      cs[v] = e.cs[o + p];
+      sn[v] = e.cs[o + half + p];
+    }
+  };
+  // ring prologue: every slot
+#pragma unroll
+  for (int c = 0; c < R; ++c)
+    if (c < nch) issue(c);
+
+  f32x4_t acc[MT][2], gacc[SA ? MT : 1];
+#pragma unroll
+  for (int i = 0; i < MT; ++i) {
+    acc[i][0] = acc[i][1] = f32x4_t{};
+    if constexpr (SA) gacc[i] = f32x4_t{};
+  }
+  for (int c = 0; c < nch; ++c) {
+    const int later = min(R - 1, nch - 1 - c);  // chunks requested after c
+    if (later >= 3) wait_vm<(R > 3 ? 3 : 0) * PER>();
+    else if (later == 2) wait_vm<(R > 2 ? 2 : 0) * PER>();
+    else if (later == 1) wait_vm<PER>();
+    else wait_vm<0>();
+    asm volatile("" ::: "memory");  // no LDS read of the chunk moves above its wait
+    if (c == 0) rope_loads();
+    const uint4* xs = ring + (wid * R + c % R) * SLOT;
+    const uint4* wsl = xs + XS;
+    uint4 wf[2][2], af[MT][2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) wf[j][h] = wsl[wslot(j * 16 + lr, h * 4 + lq)];
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) af[i][h] = xs[wslot(i * 16 + lr, h * 4 + lq)];
+    if constexpr (SA) {
+      // this lane's k range of fragment half h: h 32 + lq 8 .. + 8 of the segment
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        float gf[8];
+        unpack8<BFA_DTYPE_BF16>(xs[GS + h * 4 + lq], gf);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          float w8[8];
+          unpack8<BFA_DTYPE_BF16>(wf[j][h], w8);
+          uint32_t o[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) o[q] = pack_bf16x2(w8[2 * q] * gf[2 * q], w8[2 * q + 1] * gf[2 * q + 1]);
+          wf[j][h] = make_uint4(o[0], o[1], o[2], o[3]);
+        }
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < MT; ++i) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        acc[i][0] = mfma16<true>(af[i][h], wf[0][h], acc[i][0]);
+        acc[i][1] = mfma16<true>(af[i][h], wf[1][h], acc[i][1]);
+        if constexpr (SA) gacc[i] = mfma16<true>(af[i][h], af[i][h], gacc[i]);
+      }
+    }
+    // chunk c + R reuses this slot: its DMAs go out once every fragment read of
+    // chunk c has returned
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    if (c + R < nch) issue(c + R);
+  }
+
+  // the four partial tiles (and Gram diagonals) through each wave's own ring
+  float4* mine = reinterpret_cast<float4*>(ring + wid * R * SLOT);
+#pragma unroll
+  for (int i = 0; i < MT; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      mine[(i * 2 + j) * 64 + lane] = make_float4(acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]);
+  if constexpr (SA) {
+    float* st = reinterpret_cast<float*>(mine + MT * 2 * 64);
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+      if ((lr >> 2) == lq) st[i * 16 + lr] = gacc[i][lr & 3];
+  }
+  __syncthreads();
+  if (wid >= MT) return;
+  const int i = wid;
+  float a[4] = {0.f, 0.f, 0.f, 0.f}, b[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int wv = 0; wv < 4; ++wv) {
+    const float4* t = reinterpret_cast<const float4*>(ring + wv * R * SLOT);
+    const float4 x = t[(i * 2) * 64 + lane], y = t[(i * 2 + 1) * 64 + lane];
+    a[0] += x.x; a[1] += x.y; a[2] += x.z; a[3] += x.w;
+    b[0] += y.x; b[1] += y.y; b[2] += y.z; b[3] += y.w;
+  }
+  if constexpr (SA) {
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      float s = 0.f;
+#pragma unroll
+      for (int wv = 0; wv < 4; ++wv)
+        s += reinterpret_cast<const float*>(reinterpret_cast<const float4*>(ring + wv * R * SLOT) +
+                                            MT * 2 * 64)[i * 16 + lq * 4 + v];
+      const float r = 1.0f / sqrtf(s / static_cast<float>(d.k) + d.eps);
+      a[v] *= r;
+      b[v] *= r;
+    }
+  }
+  if (rope && head == 0 && c0 == 0 && lr == 0) {
+#pragma unroll
+    for (int v = 0; v < 4; ++v)
+      if (!pok[v] && i * 16 + lq * 4 + v < d.m) flag_status(e.status, BFA_STATUS_INDEX_OOB);
+  }
+  float ba = 0.f, bb = 0.f;
+  if (e.bias) {
+    if (e.bias_dtype == BFA_DTYPE_F32) {
+      ba = __builtin_bit_cast(float, (bw[1] << 16) | bw[0]);
+      bb = __builtin_bit_cast(float, (bw[3] << 16) | bw[2]);
+    } else if (e.bias_dtype == BFA_DTYPE_BF16) {
+      ba = Elem<BFA_DTYPE_BF16>::to_f32(static_cast<uint16_t>(bw[0]));
+      bb = Elem<BFA_DTYPE_BF16>::to_f32(static_cast<uint16_t>(bw[2]));
+    } else {
+      ba = Elem<BFA_DTYPE_F16>::to_f32(static_cast<uint16_t>(bw[0]));
+      bb = Elem<BFA_DTYPE_F16>::to_f32(static_cast<uint16_t>(bw[2]));
+    }
+  }
+  const int64_t hk = head - e.hq - (kd == 2 ? e.hkv : 0);
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    const int64_t t = i * 16 + lq * 4 + v;
+    if (t >= d.m) continue;
+    float x1 = rnd<DT::Q>(a[v] + ba, e.qkv_dt), x2 = rnd<DT::Q>(b[v] + bb, e.qkv_dt);
+    if (rope) {
+      const float u = x1, w = x2;
+      x1 = pok[v] ? rnd<DT::Q>(u * cs[v] - w * sn[v], e.qkv_dt) : 0.f;
+      x2 = pok[v] ? rnd<DT::Q>(w * cs[v] + u * sn[v], e.qkv_dt) : 0.f;
+    }
+    if (kd == 0 || !e.skip_kv_out) {
+      if constexpr (DT::O >= 0) {
+        store1<DT::O>(e.out, t * e.ldo + cola + lr, x1);
+        store1<DT::O>(e.out, t * e.ldo + cola + half + lr, x2);
+      } else {
+        store_any(e.out, e.out_dt, t * e.ldo + cola + lr, x1);
+        store_any(e.out, e.out_dt, t * e.ldo + cola + half + lr, x2);
+      }
+    }
+    if (app && so[v] >= 0) {
+      const int64_t cbase = so[v] + (kd == 2 ? e.c_skv : 0) + hk * e.c_sh;
+      store_any(e.cache, e.cache_dt, cbase + p, rnd<DT::O>(x1, e.out_dt));
+      store_any(e.cache, e.cache_dt, cbase + half + p, rnd<DT::O>(x2, e.out_dt));
+    }
+  }
+}
+
 // ============================================== reduction + row epilogue
 // One wave per (token, head).  v = sum over splits of part[s, t, col] (+bias),
 // then the same rounding / norm / RoPE chain as the in-register epilogue.
@@ -2224,6 +2517,56 @@ static void launch_prefill(const QkvPlan& p, const GemmArgs& g, const QkvEpi& e,
   else launch_prefill_t<BF16, false>(p, g, e, st);
 }
 
+// Whole-K column-pair decode kernel (qkv_decode_pair_kernel): 17-64 tokens,
+// bf16 operand and weight, head_dim a multiple of 32, no q/k norm, K a multiple
+// of 256, and at least 128 column tiles, so that the weight stream still covers
+// most CUs.  BFA_DECODE_PAIR=0 keeps the
+// split-K kernels, =1 drops the tile minimum (measurements and tests).
+static bool pair_ok(const QkvPlan& p, int64_t n, int64_t hd, int64_t k, bool qk_norm, bool bf16,
+                    int64_t lda, const void* operand, int64_t m, int64_t ldw) {
+  if (!p.decode || !p.stream || p.mt < 2 || !bf16 || qk_norm) return false;
+  if (hd % 32 != 0 || n % 32 != 0 || k % 256 != 0) return false;
+  // 32-bit DMA offsets for the operand and weight rows
+  if (lda % 8 != 0 || !aligned16(operand) || m * lda * 2 >= (int64_t(1) << 32) ||
+      n * ldw * 2 >= (int64_t(1) << 32))
+    return false;
+  int mode = -1;
+  if (const char* v = getenv("BFA_DECODE_PAIR")) mode = atoi(v);
+  if (mode == 0) return false;
+  return mode == 1 || n / 32 >= 128;
+}
+
+// epilogue dtype forms of the pair kernel (no q/k norm): the scale-after form is
+// an fp32 projection, so it has the Llama chain's form or the run-time one
+template <int MT>
+static void launch_pair_mt(bool sa, int edt, dim3 grid, const DecodeArgs& d, const QkvEpi& e, int nch,
+                           hipStream_t st) {
+  if (sa) {
+    if (edt == EDT_F32_BF16)
+      hipLaunchKernelGGL((qkv_decode_pair_kernel<MT, true, EDT_F32_BF16>), grid, dim3(256), 0, st, d, e, nch);
+    else
+      hipLaunchKernelGGL((qkv_decode_pair_kernel<MT, true, EDT_RT>), grid, dim3(256), 0, st, d, e, nch);
+    return;
+  }
+  if (edt == EDT_F32_BF16)
+    hipLaunchKernelGGL((qkv_decode_pair_kernel<MT, false, EDT_F32_BF16>), grid, dim3(256), 0, st, d, e, nch);
+  else if (edt == EDT_BF16)
+    hipLaunchKernelGGL((qkv_decode_pair_kernel<MT, false, EDT_BF16>), grid, dim3(256), 0, st, d, e, nch);
+  else
+    hipLaunchKernelGGL((qkv_decode_pair_kernel<MT, false, EDT_RT>), grid, dim3(256), 0, st, d, e, nch);
+}
+
+static void launch_pair(const QkvPlan& p, const DecodeArgs& d, const QkvEpi& e, bool sa, hipStream_t st) {
+  const dim3 grid(static_cast<unsigned>(d.n / 32));
+  const int nch = static_cast<int>(d.k / 256);
+  const int edt = fused_edt(e);
+  switch (p.mt) {
+    case 2: launch_pair_mt<2>(sa, edt, grid, d, e, nch, st); break;
+    case 3: launch_pair_mt<3>(sa, edt, grid, d, e, nch, st); break;
+    default: launch_pair_mt<4>(sa, edt, grid, d, e, nch, st); break;
+  }
+}
+
 static void launch_epilogue(const float* part, int64_t splits, int64_t m, const QkvEpi& e,
                             hipStream_t st) {
   const int64_t items = m * (e.hq + 2 * e.hkv);
@@ -2326,6 +2669,24 @@ static int qkv_projection_impl(const void* operand, int64_t lda, const OperandFo
   const hipStream_t st = as_stream(stream);
   const bool bf16 = w_dtype == BFA_DTYPE_BF16;
   float* part = static_cast<float*>(part_workspace);
+  if (p.decode && pair_ok(p, qkv_dim, hd, hidden, q_norm_weight || k_norm_weight, bf16, lda, operand, tokens,
+                         w_stride)) {
+    DecodeArgs d{};
+    d.a = static_cast<const uint16_t*>(operand);
+    d.w = static_cast<const uint16_t*>(qkv_weight);
+    d.m = tokens; d.n = qkv_dim; d.k = hidden; d.lda = lda; d.ldw = w_stride;
+    const bool sa = fold && fold->stats;
+    if (sa) {
+      BFA_REQUIRE(fold->gamma_dt == BFA_DTYPE_BF16 && aligned16(fold->gamma),
+                  "%s: scale-after needs a 16-byte aligned bf16 norm weight", what);
+      d.gamma = fold->gamma; d.gamma_dt = fold->gamma_dt; d.eps = fold->eps;
+    }
+    e.stats = nullptr;
+    launch_pair(p, d, e, sa, st);
+    return check_launch(what);
+  }
+  // the scale-after fold outside the pair kernel is the deep-K kernel's
+  BFA_REQUIRE(!(fold && fold->stats) || (p.decode && p.nch > 0), "%s: scale-after fold without a kernel", what);
   if (p.decode) {
     SplitArgs s{};
     s.a = static_cast<const uint16_t*>(operand);
@@ -2416,15 +2777,19 @@ static int fused_impl(const void* x, int x_dtype, int64_t tokens, int64_t hidden
   const bool fold = !no_fold && fold_rows > 0 && p.decode && p.stream && p.mt == 1 && x_dtype == w_dtype &&
                     (w_dtype == BFA_DTYPE_BF16 || w_dtype == BFA_DTYPE_F16) && hidden % 8 == 0 &&
                     x_stride % 8 == 0 && aligned16(x) && aligned16(norm_weight) && is_float_dtype(nw_dtype);
-  // 17 to 64 decode tokens of the fp32 variants (operand (x / rms) * gamma):
-  // the deep-K kernel projects bf16(x * gamma) and returns each split's sums of
-  // x^2, and the reduction kernel applies 1 / rms -- no operand pre-pass.  bf16
-  // only: x * gamma without the row scale could leave the fp16 range.
-  const bool scale_after = !no_fold && p.decode && p.stream && p.nch > 0 && mixed_rounding == 0 &&
+  // 17 to 64 decode tokens of the fp32 variants (operand (x / rms) * gamma): the
+  // row scale 1 / rms comes out of the sum, so no operand pre-pass.  The
+  // column-pair kernel projects x onto bf16(w * gamma) and sums the rows'
+  // squares itself; the deep-K kernel projects bf16(x * gamma), returns each
+  // split's sums of x^2 and the reduction kernel applies 1 / rms.  bf16 only:
+  // x * gamma without the row scale could leave the fp16 range.
+  const bool pair = pair_ok(p, qkv_dim, qkv_dim / heads, hidden, q_norm_weight || k_norm_weight,
+                            x_dtype == BFA_DTYPE_BF16 && w_dtype == BFA_DTYPE_BF16, x_stride, x, tokens, w_stride);
+  const bool scale_after = !no_fold && p.decode && p.stream && mixed_rounding == 0 &&
                            qkv_dtype == BFA_DTYPE_F32 && x_dtype == BFA_DTYPE_BF16 &&
                            w_dtype == BFA_DTYPE_BF16 && nw_dtype == BFA_DTYPE_BF16 && hidden % 8 == 0 &&
                            x_stride % 8 == 0 && aligned16(x) && aligned16(norm_weight) &&
-                           p.splits * 16 * p.mt * 4 <= p.operand_bytes;
+                           (pair || (p.nch > 0 && p.splits * 16 * p.mt * 4 <= p.operand_bytes));
   if (scale_after) {
     const OperandFold f{norm_weight, nw_dtype, false, eps, 0, reinterpret_cast<float*>(ws)};
     return qkv_projection_impl(x, x_stride, &f, tokens, hidden, qkv_weight, w_dtype, qkv_dim, w_stride,
