@@ -1813,11 +1813,13 @@ __global__ __launch_bounds__(256) void qkv_decode_epilogue_kernel(const float4* 
 // 256-deep chunk and streams it on its own, with no barrier until the end.  Per
 // chunk the wave DMAs its operand segment (rows x 128 B) and its weight segment
 // (32 rows x 128 B: the 16 first-half columns, then their pairs), whole cache
-// lines, into a slot of its private LDS ring (granule g of row r at slot
-// g ^ (r/2 & 7)), and reads 16x16x32 fragments from there.  The loop issues no
-// other memory request, so the one wait per chunk is exact: before chunk c the
-// wave waits for vmcnt(PER x chunks already requested after c), and chunk
-// c + R goes into c's slot as soon as c's fragments are in registers.
+// lines, into slots of its private LDS rings (granule g of row r at slot
+// g ^ (r/2 & 7)), and reads 16x16x32 fragments from there.  The weight ring is
+// deeper than the operand ring (HBM against L2 latency).  The loop issues no
+// other memory request, so the one wait per chunk is exact (the requests issued
+// after the chunk's operand DMAs may stay in flight), and the chunks that reuse
+// c's slots are requested as soon as c's fragments are in registers, before
+// c's arithmetic.
 // At the end the four partial tiles are summed through LDS in wave order and
 // wave i finishes the rows of 16-token block i: a lane holds the pair (p, p + D/2)
 // of four rows in its two accumulators, so RoPE needs no exchange.
@@ -1831,21 +1833,43 @@ __global__ __launch_bounds__(256) void qkv_decode_epilogue_kernel(const float4* 
 // multiplies the projection by r = 1 / sqrt(sum / hidden + eps) before the bias.
 // No pass over x and no other launch.
 
-template <int MT> struct PairRing { static constexpr int R = MT == 2 ? 4 : 3; };  // slots within 160 KiB
+// Ring slots per wave: RX operand segments, RW weight (+ gamma) segments.  At
+// 64 tokens, Llama-3-8B shape, the K loop took 10.0 us with (3, 2) and (4, 1),
+// 10.3 with (3, 3), 11.4-11.6 with (2, 3) and (2, 5): the operand (read by every
+// workgroup, 512 KiB at 64 tokens) wants the depth; past that the loop is bound
+// by the LDS (every byte DMA'd in and read out as a fragment), not by latency.
+template <int MT> struct PairRing {
+  static constexpr int RX = 3;
+  static constexpr int RW = 2;
+};
+
+// s_waitcnt vmcnt(n) for a run-time n in [LO, HI] (a binary search over constant waits)
+template <int LO, int HI>
+__device__ __forceinline__ void wait_vm_dyn(int n) {
+  if constexpr (LO >= HI) {
+    wait_vm<LO>();
+  } else {
+    constexpr int MID = (LO + HI + 1) / 2;
+    if (n >= MID) wait_vm_dyn<MID, HI>(n);
+    else wait_vm_dyn<LO, MID - 1>(n);
+  }
+}
 
 template <int MT, bool SA, int EDT>
 __global__ __launch_bounds__(256) void qkv_decode_pair_kernel(DecodeArgs d, QkvEpi e, int nch) {
   using DT = EpiDt<EDT>;
-  constexpr int R = PairRing<MT>::R;
+  constexpr int RX = PairRing<MT>::RX, RW = PairRing<MT>::RW;
   constexpr int ROWS = MT * 16;
-  constexpr int DX = ROWS / 8;          // operand DMAs per wave per chunk (8 rows x 128 B)
-  constexpr int PER = DX + 4 + (SA ? 1 : 0);  // + 4 weight DMAs (+ gamma)
-  constexpr int XS = ROWS * 8;          // uint4 of the operand part of a slot
-  constexpr int GS = XS + 32 * 8;       // + the weight part; then 8 uint4 of gamma
-  constexpr int SLOT = GS + (SA ? 8 : 0);
+  constexpr int XN = ROWS / 8;          // operand DMAs per wave per chunk (8 rows x 128 B)
+  constexpr int WN = 4 + (SA ? 1 : 0);  // weight DMAs (+ gamma)
+  constexpr int XS = ROWS * 8;          // uint4 per operand slot
+  constexpr int WS = 32 * 8 + (SA ? 8 : 0);  // uint4 per weight slot: 32 rows, then 64 gamma values
+  constexpr int WAVE_U4 = RX * XS + RW * WS;
+  // requests issued after the later of a chunk's operand and weight requests
+  constexpr int YMAX = RX < RW ? WN + (RX - 1) * (XN + WN) : (RW - 1) * (XN + WN);
   static_assert(MT >= 2 && MT <= 4, "two to four token blocks");
-  static_assert((R - 1) * PER < 64 && R <= 4, "vmcnt range");
-  __shared__ uint4 ring[4 * R * SLOT];
+  static_assert(YMAX < 64, "ring shape");
+  __shared__ uint4 ring[4 * WAVE_U4];
   __shared__ uint32_t posl[4][32];  // per wave: the raw positions of its 16 epilogue rows
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -1861,9 +1885,9 @@ __global__ __launch_bounds__(256) void qkv_decode_pair_kernel(DecodeArgs d, QkvE
   // slot l % 8 of row 8 j + l / 8, i.e. logical granule (l % 8) ^ (row / 2 & 7).
   // Operand rows past m re-read row m - 1; weight row 8 j + l / 8 of the tile is
   // column cola + row (rows < 16) or cola + half + row - 16.
-  uint32_t aoff[DX], woff[4];
+  uint32_t aoff[XN], woff[4];
 #pragma unroll
-  for (int j = 0; j < DX; ++j) {
+  for (int j = 0; j < XN; ++j) {
     const int row = 8 * j + (lane >> 3);
     const int g = (lane & 7) ^ ((row >> 1) & 7);
     aoff[j] = static_cast<uint32_t>((min<int64_t>(row, d.m - 1) * d.lda + wid * 64 + g * 8) * 2);
@@ -1875,7 +1899,7 @@ __global__ __launch_bounds__(256) void qkv_decode_pair_kernel(DecodeArgs d, QkvE
     const int64_t col = cola + (row < 16 ? row : half + row - 16);
     woff[j] = static_cast<uint32_t>((col * d.ldw + wid * 64 + g * 8) * 2);
   }
-  const uint32_t lring = lds_addr(ring) + static_cast<uint32_t>(wid * R * SLOT * 16);
+  const uint32_t lring = lds_addr(ring) + static_cast<uint32_t>(wid * WAVE_U4 * 16);
   const uint32_t goff = static_cast<uint32_t>((wid * 64 + lane * 8) * 2);
   // Each workgroup walks the chunks from its own starting point (workgroups of
   // one XCD, i = xcd + 8 j, start at chunk j mod nch): rows are a power of two
@@ -1883,19 +1907,42 @@ __global__ __launch_bounds__(256) void qkv_decode_pair_kernel(DecodeArgs d, QkvE
   // band of x and W, which sits in a few L2 channels.
   const int rot = static_cast<int>((blockIdx.x >> 3) % static_cast<unsigned>(nch));
   auto kchunk = [&](int c) { return c + rot < nch ? c + rot : c + rot - nch; };
-  auto issue = [&](int c) {
-    const uint32_t ls = lring + static_cast<uint32_t>((c % R) * SLOT * 16);
+  // Requests, in issue order: at step v (v < 0: the prologue) the operand of
+  // chunk v + RX, then the weight of chunk v + RW, each while it exists.  Before
+  // chunk c the wave waits for its operand (issued at step c - RX, after the
+  // weight of c), i.e. for vmcnt(requests issued after it): younger(c).
+  auto issue_x = [&](int c) {
+    const uint32_t ls = lring + static_cast<uint32_t>((c % RX) * XS * 16);
+    const uint16_t* ab = d.a + static_cast<int64_t>(kchunk(c)) * 256;
+#pragma unroll
+    for (int j = 0; j < XN; ++j) dma16(ab, aoff[j], ls + j * 1024);
+  };
+  auto issue_w = [&](int c) {
+    const uint32_t ls = lring + static_cast<uint32_t>((RX * XS + (c % RW) * WS) * 16);
     const int64_t kc = kchunk(c);
-    const uint16_t* ab = d.a + kc * 256;
     const uint16_t* wb = d.w + kc * 256;
 #pragma unroll
-    for (int j = 0; j < DX; ++j) dma16(ab, aoff[j], ls + j * 1024);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) dma16(wb, woff[j], ls + (XS + j * 64) * 16);
+    for (int j = 0; j < 4; ++j) dma16(wb, woff[j], ls + j * 1024);
     if constexpr (SA) {
       // lanes 0-7: the segment's 64 gamma values
-      if (lane < 8) dma16(static_cast<const uint16_t*>(d.gamma) + kc * 256, goff, ls + GS * 16);
+      if (lane < 8) dma16(static_cast<const uint16_t*>(d.gamma) + kc * 256, goff, ls + 256 * 16);
     }
+  };
+  auto step_issue = [&](int v) {
+    if (v + RX >= 0 && v + RX < nch) issue_x(v + RX);
+    if (v + RW >= 0 && v + RW < nch) issue_w(v + RW);
+  };
+  auto younger = [&](int c) {
+    // the later of chunk c's requests: its operand (step c - RX) when RX < RW,
+    // else its weight (step c - RW, the last request of that step)
+    constexpr int RL = RX < RW ? RX : RW;
+    int n = RX < RW && c - RX + RW < nch ? WN : 0;
+#pragma unroll
+    for (int i = 1; i < RL; ++i) {
+      const int v = c - RL + i;
+      n += (v + RX < nch ? XN : 0) + (v + RW < nch ? WN : 0);
+    }
+    return n;
   };
 
   // this lane finishes rows 16 wid + 4 lq + v of columns cola + lr, + half (wid < MT)
@@ -1946,10 +1993,9 @@ __global__ __launch_bounds__(256) void qkv_decode_pair_kernel(DecodeArgs d, QkvE
       sn[v] = e.cs[o + half + p];
     }
   };
-  // ring prologue: every slot
+  // ring prologue: steps -max(RX, RW) .. -1
 #pragma unroll
-  for (int c = 0; c < R; ++c)
-    if (c < nch) issue(c);
+  for (int v = -(RX > RW ? RX : RW); v < 0; ++v) step_issue(v);
 
   f32x4_t acc[MT][2], gacc[SA ? MT : 1];
 #pragma unroll
@@ -1958,30 +2004,39 @@ __global__ __launch_bounds__(256) void qkv_decode_pair_kernel(DecodeArgs d, QkvE
     if constexpr (SA) gacc[i] = f32x4_t{};
   }
   for (int c = 0; c < nch; ++c) {
-    const int later = min(R - 1, nch - 1 - c);  // chunks requested after c
-    if (later >= 3) wait_vm<(R > 3 ? 3 : 0) * PER>();
-    else if (later == 2) wait_vm<(R > 2 ? 2 : 0) * PER>();
-    else if (later == 1) wait_vm<PER>();
-    else wait_vm<0>();
+    wait_vm_dyn<0, YMAX>(younger(c));
     asm volatile("" ::: "memory");  // no LDS read of the chunk moves above its wait
     if (c == 0) rope_loads();
-    const uint4* xs = ring + (wid * R + c % R) * SLOT;
-    const uint4* wsl = xs + XS;
+    const uint4* xs = ring + wid * WAVE_U4 + (c % RX) * XS;
+    const uint4* wsl = ring + wid * WAVE_U4 + RX * XS + (c % RW) * WS;
     uint4 wf[2][2], af[MT][2];
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int h = 0; h < 2; ++h) wf[j][h] = wsl[wslot(j * 16 + lr, h * 4 + lq)];
 #pragma unroll
     for (int i = 0; i < MT; ++i)
 #pragma unroll
       for (int h = 0; h < 2; ++h) af[i][h] = xs[wslot(i * 16 + lr, h * 4 + lq)];
-    if constexpr (SA) {
-      // this lane's k range of fragment half h: h 32 + lq 8 .. + 8 of the segment
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) wf[j][h] = wsl[wslot(j * 16 + lr, h * 4 + lq)];
+    uint4 gw[2] = {};
+    if constexpr (SA) {
+      gw[0] = wsl[256 + lq];
+      gw[1] = wsl[256 + 4 + lq];
+    }
+    // chunk c + RX (c + RW) reuses this operand (weight) slot: its DMAs go out
+    // as soon as every read of chunk c has returned, and the conversion and
+    // MFMAs below run from registers while they are in flight
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    step_issue(c);
+    if constexpr (SA) {
+      // bf16(w * gamma) for fragment half h (this lane's k range: h 32 + lq 8
+      // .. + 8 of the segment).  Three scheduling regions put the conversion
+      // under the matrix cores: (A) the Gram MFMAs with the conversion of half
+      // 0, (B) half 0's MFMAs with the conversion of half 1, (C) half 1's MFMAs;
+      // inside A and B one MFMA alternates with six VALU instructions.
+      auto convert = [&](int h) {
         float gf[8];
-        unpack8<BFA_DTYPE_BF16>(xs[GS + h * 4 + lq], gf);
+        unpack8<BFA_DTYPE_BF16>(gw[h], gf);
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
           float w8[8];
@@ -1991,25 +2046,48 @@ __global__ __launch_bounds__(256) void qkv_decode_pair_kernel(DecodeArgs d, QkvE
           for (int q = 0; q < 4; ++q) o[q] = pack_bf16x2(w8[2 * q] * gf[2 * q], w8[2 * q + 1] * gf[2 * q + 1]);
           wf[j][h] = make_uint4(o[0], o[1], o[2], o[3]);
         }
+      };
+      auto interleave = [&]() {
+#pragma unroll
+        for (int q = 0; q < 2 * MT; ++q) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+          __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);  // six VALU
+        }
+      };
+#pragma unroll
+      for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) gacc[i] = mfma16<true>(af[i][h], af[i][h], gacc[i]);
+      convert(0);
+      interleave();
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 0; i < MT; ++i) {
+        acc[i][0] = mfma16<true>(af[i][0], wf[0][0], acc[i][0]);
+        acc[i][1] = mfma16<true>(af[i][0], wf[1][0], acc[i][1]);
+      }
+      convert(1);
+      interleave();
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 0; i < MT; ++i) {
+        acc[i][0] = mfma16<true>(af[i][1], wf[0][1], acc[i][0]);
+        acc[i][1] = mfma16<true>(af[i][1], wf[1][1], acc[i][1]);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < MT; ++i) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          acc[i][0] = mfma16<true>(af[i][h], wf[0][h], acc[i][0]);
+          acc[i][1] = mfma16<true>(af[i][h], wf[1][h], acc[i][1]);
+        }
       }
     }
-#pragma unroll
-    for (int i = 0; i < MT; ++i) {
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        acc[i][0] = mfma16<true>(af[i][h], wf[0][h], acc[i][0]);
-        acc[i][1] = mfma16<true>(af[i][h], wf[1][h], acc[i][1]);
-        if constexpr (SA) gacc[i] = mfma16<true>(af[i][h], af[i][h], gacc[i]);
-      }
-    }
-    // chunk c + R reuses this slot: its DMAs go out once every fragment read of
-    // chunk c has returned
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    if (c + R < nch) issue(c + R);
   }
 
   // the four partial tiles (and Gram diagonals) through each wave's own ring
-  float4* mine = reinterpret_cast<float4*>(ring + wid * R * SLOT);
+  float4* mine = reinterpret_cast<float4*>(ring + wid * WAVE_U4);
 #pragma unroll
   for (int i = 0; i < MT; ++i)
 #pragma unroll
@@ -2027,7 +2105,7 @@ __global__ __launch_bounds__(256) void qkv_decode_pair_kernel(DecodeArgs d, QkvE
   float a[4] = {0.f, 0.f, 0.f, 0.f}, b[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int wv = 0; wv < 4; ++wv) {
-    const float4* t = reinterpret_cast<const float4*>(ring + wv * R * SLOT);
+    const float4* t = reinterpret_cast<const float4*>(ring + wv * WAVE_U4);
     const float4 x = t[(i * 2) * 64 + lane], y = t[(i * 2 + 1) * 64 + lane];
     a[0] += x.x; a[1] += x.y; a[2] += x.z; a[3] += x.w;
     b[0] += y.x; b[1] += y.y; b[2] += y.z; b[3] += y.w;
@@ -2038,7 +2116,7 @@ __global__ __launch_bounds__(256) void qkv_decode_pair_kernel(DecodeArgs d, QkvE
       float s = 0.f;
 #pragma unroll
       for (int wv = 0; wv < 4; ++wv)
-        s += reinterpret_cast<const float*>(reinterpret_cast<const float4*>(ring + wv * R * SLOT) +
+        s += reinterpret_cast<const float*>(reinterpret_cast<const float4*>(ring + wv * WAVE_U4) +
                                             MT * 2 * 64)[i * 16 + lq * 4 + v];
       const float r = 1.0f / sqrtf(s / static_cast<float>(d.k) + d.eps);
       a[v] *= r;
