@@ -748,7 +748,7 @@ def profile_one(kernel: str, tokens: int, steps: int, dev) -> int:
         ms = time_fn(lambda: torch.mm(c.hidden, wt, out=out), steps)
         print(json.dumps({"kernel": kernel, "tokens": tokens, "calls": steps, "us": round(ms * 1e3, 3)}))
         return 0
-    fn = {"qkv_projection": st.projection, "qkv_operand": st.operand,
+    fn = {"qkv_projection": st.projection, "qkv_operand": st.operand, "fused_qkv": c.qkv,
           "add_rms_norm": lambda: c.norm(c.x, c.residual), "silu_and_mul": lambda: c.silu(c.gate_up),
           "embedding": lambda: embedding(c.ids, table)}[kernel]
     ms = time_fn(fn, steps)
@@ -766,7 +766,8 @@ def main(argv=None) -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-cold", action="store_true", help="skip the cold-cache timings")
     ap.add_argument("--kernel", help="only run this kernel --steps times at --tokens (for "
-                    "profilers): qkv_projection, qkv_operand, add_rms_norm, silu_and_mul, "
+                    "profilers): qkv_projection, qkv_operand, fused_qkv (the whole fused "
+                    "RMSNorm+QKV+RoPE op), add_rms_norm, silu_and_mul, "
                     "embedding, copy, library_gemm (the projection's product through torch.mm), or "
                     "case:<name> for a case of the configuration table")
     args = ap.parse_args(argv)
