@@ -83,12 +83,23 @@ __device__ __forceinline__ void load8(const void* p, float (&v)[8]) {
   }
 }
 
-template <int DT>
+// NT: the nontemporal hint, for large outputs that are not read again soon
+// (see stream_output below).
+template <int DT, bool NT = false>
 __device__ __forceinline__ void store8(void* p, const float (&v)[8]) {
+  typedef unsigned u32x4_nt_t __attribute__((ext_vector_type(4)));
   if constexpr (DT == BFA_DTYPE_F32) {
-    float4* q = reinterpret_cast<float4*>(p);
-    q[0] = make_float4(v[0], v[1], v[2], v[3]);
-    q[1] = make_float4(v[4], v[5], v[6], v[7]);
+    if constexpr (NT) {
+      u32x4_nt_t* q = reinterpret_cast<u32x4_nt_t*>(p);
+      __builtin_nontemporal_store(u32x4_nt_t{__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]),
+                                             __float_as_uint(v[3])}, q);
+      __builtin_nontemporal_store(u32x4_nt_t{__float_as_uint(v[4]), __float_as_uint(v[5]), __float_as_uint(v[6]),
+                                             __float_as_uint(v[7])}, q + 1);
+    } else {
+      float4* q = reinterpret_cast<float4*>(p);
+      q[0] = make_float4(v[0], v[1], v[2], v[3]);
+      q[1] = make_float4(v[4], v[5], v[6], v[7]);
+    }
   } else {
     uint32_t w[4];
 #pragma unroll
@@ -96,9 +107,23 @@ __device__ __forceinline__ void store8(void* p, const float (&v)[8]) {
       w[i] = static_cast<uint32_t>(Elem<DT>::from_f32(v[2 * i])) |
              (static_cast<uint32_t>(Elem<DT>::from_f32(v[2 * i + 1])) << 16);
     }
-    *reinterpret_cast<uint4*>(p) = make_uint4(w[0], w[1], w[2], w[3]);
+    if constexpr (NT) {
+      __builtin_nontemporal_store(u32x4_nt_t{w[0], w[1], w[2], w[3]}, reinterpret_cast<u32x4_nt_t*>(p));
+    } else {
+      *reinterpret_cast<uint4*>(p) = make_uint4(w[0], w[1], w[2], w[3]);
+    }
   }
 }
+
+// Stores carry the nontemporal hint when an output is this large (SiLU*mul's
+// activation, add+RMSNorm's residual): such an output cannot stay in the 256 MB
+// Infinity Cache for its consumer anyway, and streaming it past the cache keeps
+// what the next kernels read there.  SiLU*mul at 8192 x 14336 alone slows from
+// 103 to 111 us with it, while the Llama-3-8B 8192-token layer chain
+// (add+RMSNorm, fused QKV, SiLU*mul) goes from 546 to 515 us.  Smaller outputs
+// (decode batches) keep plain stores, so their consumers find them cached.
+constexpr int64_t kStreamOutputBytes = int64_t(64) << 20;
+inline bool stream_output(int64_t bytes) { return bytes >= kStreamOutputBytes; }
 
 // Streaming forms: 16-byte loads with the nontemporal hint, for operands that
 // are read exactly once (activations of the memory-bound kernels, gathered
@@ -106,8 +131,7 @@ __device__ __forceinline__ void store8(void* p, const float (&v)[8]) {
 // SiLU*mul kernel from 5.6 to 6.8 TB/s at 8192 x 2 x 14336, and in the
 // Llama-3-8B 8192-token layer chain add+RMSNorm from 70 to 51 us (a kernel
 // repeated on the same input in isolation reads faster with plain loads, which
-// keep the input in the Infinity Cache between repeats).  Nontemporal stores
-// were slower, so stores stay plain.
+// keep the input in the Infinity Cache between repeats).
 typedef unsigned bfa_u32x4_t __attribute__((ext_vector_type(4)));
 
 template <bool NT = true>

@@ -74,7 +74,9 @@ __device__ __forceinline__ float norm_inv(float ss, int64_t hidden, float eps) {
   return 1.0f / sqrtf(ss / static_cast<float>(hidden) + eps);
 }
 
-template <int DT_IN, int DT_OUT, int MODE, int L, int MAXC>
+// NTR (kAddRms): residual_out is stored with the nontemporal hint (a large
+// residual is not read again until after the attention block).
+template <int DT_IN, int DT_OUT, int MODE, int L, int MAXC, bool NTR = false>
 __global__ __launch_bounds__(256) void norm_vec_kernel(NormArgs a) {
   using TIN = typename Elem<DT_IN>::T;
   using TOUT = typename Elem<DT_OUT>::T;
@@ -101,7 +103,7 @@ __global__ __launch_bounds__(256) void norm_vec_kernel(NormArgs a) {
         load8_nt<DT_IN>(static_cast<const TIN*>(a.res) + row * a.r_s + ch * 8, r);
 #pragma unroll
         for (int i = 0; i < 8; ++i) v[c][i] = v[c][i] + r[i];
-        if (a.res_out) store8<DT_IN>(static_cast<TIN*>(a.res_out) + row * a.ro_s + ch * 8, v[c]);
+        if (a.res_out) store8<DT_IN, NTR>(static_cast<TIN*>(a.res_out) + row * a.ro_s + ch * 8, v[c]);
       }
 #pragma unroll
       for (int i = 0; i < 8; ++i) ss += v[c][i] * v[c][i];
@@ -171,6 +173,13 @@ template <int DT_IN, int DT_OUT, int MODE, int L, int MAXC>
 static void launch_vec(const NormArgs& a, hipStream_t s) {
   constexpr int RPW = (L >= 256) ? 1 : 256 / L;
   const int64_t grid = cdiv(a.rows, RPW);
+  if constexpr (MODE == kAddRms) {
+    if (a.res_out && stream_output(a.rows * a.hidden * static_cast<int64_t>(sizeof(typename Elem<DT_IN>::T)))) {
+      hipLaunchKernelGGL((norm_vec_kernel<DT_IN, DT_OUT, MODE, L, MAXC, true>), dim3(grid), dim3(256), 0,
+                         s, a);
+      return;
+    }
+  }
   hipLaunchKernelGGL((norm_vec_kernel<DT_IN, DT_OUT, MODE, L, MAXC>), dim3(grid), dim3(256), 0,
                      s, a);
 }

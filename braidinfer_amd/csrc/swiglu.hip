@@ -28,7 +28,7 @@ struct SwigluArgs {
 
 constexpr int kSwigluPerLane = 2;  // 8-column chunks per lane
 
-template <int DT>
+template <int DT, bool NT>
 __global__ __launch_bounds__(256) void silu_mul_vec_kernel(SwigluArgs a) {
   constexpr int U = kSwigluPerLane;
   using T = typename Elem<DT>::T;
@@ -54,7 +54,7 @@ __global__ __launch_bounds__(256) void silu_mul_vec_kernel(SwigluArgs a) {
     float o[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) o[i] = Elem<DT>::round(silu_fast(g[c][i])) * u[c][i];
-    store8<DT>(static_cast<T*>(a.y) + yoff[c], o);
+    store8<DT, NT>(static_cast<T*>(a.y) + yoff[c], o);
   }
 }
 
@@ -76,7 +76,10 @@ template <int DT>
 static void launch_silu(const SwigluArgs& a, bool vec, hipStream_t s) {
   if (vec) {
     const int64_t grid = std::max<int64_t>(1, cdiv(a.total, 256 * kSwigluPerLane));
-    hipLaunchKernelGGL((silu_mul_vec_kernel<DT>), dim3(grid), dim3(256), 0, s, a);
+    if (stream_output(a.rows * a.inter * static_cast<int64_t>(sizeof(typename Elem<DT>::T))))
+      hipLaunchKernelGGL((silu_mul_vec_kernel<DT, true>), dim3(grid), dim3(256), 0, s, a);
+    else
+      hipLaunchKernelGGL((silu_mul_vec_kernel<DT, false>), dim3(grid), dim3(256), 0, s, a);
   } else {
     // grid-stride: enough workgroups to cover the tensor once, capped so that
     // each lane loops a few times on large tensors (256 CUs x 16 workgroups)
