@@ -625,21 +625,27 @@ __device__ __forceinline__ void gemm_epilogue(f32x16_t (&acc)[MB][NB], uint4* ld
       for (int r = lane; r < MB * 32; r += 64) stab[r] = e.slot_off[min(wrow0 + r, g.m - 1)];
       __asm__ volatile("" ::: "memory");  // the wave's own LDS writes precede its reads below
     }
+    // The cos/sin rows of a block's 8 rows are all requested before its row
+    // loop: there each load would sit behind the previous row's stores (the
+    // table and the output may alias as far as the compiler knows), paying the
+    // table's L2 latency 8 times.  Block i+1's rows are requested once block i's
+    // accumulators are staged (their registers are free) and before block i's
+    // stores: requested after them, their wait would also wait for every store
+    // of block i, which all CUs issue at once.
+    float4 cvv[2][8], svv[2][8];
+    auto load_cs = [&](int i, float4 (&cv)[8], float4 (&sv)[8]) {
+#pragma unroll
+      for (int it = 0; it < 8; ++it) {
+        const int64_t p = posv[i][it] >= 0 ? posv[i][it] : 0;
+        cv[it] = *reinterpret_cast<const float4*>(e.cs + p * HD + q * 4);
+        sv[it] = *reinterpret_cast<const float4*>(e.cs + p * HD + HD / 2 + q * 4);
+      }
+    };
+    if (rope) load_cs(0, cvv[0], svv[0]);
 #pragma unroll
     for (int i = 0; i < MB; ++i) {
-      // The cos/sin rows of the block's 8 rows are all requested before the
-      // accumulators are staged: in the row loop below each load would sit
-      // behind the previous row's stores (the table and the output may alias
-      // as far as the compiler knows), paying the table's L2 latency 8 times.
-      float4 cvv[8], svv[8];
-      if (rope) {
-#pragma unroll
-        for (int it = 0; it < 8; ++it) {
-          const int64_t p = posv[i][it] >= 0 ? posv[i][it] : 0;
-          cvv[it] = *reinterpret_cast<const float4*>(e.cs + p * HD + q * 4);
-          svv[it] = *reinterpret_cast<const float4*>(e.cs + p * HD + HD / 2 + q * 4);
-        }
-      }
+      float4 (&cvv_i)[8] = cvv[i & 1];
+      float4 (&svv_i)[8] = svv[i & 1];
 #pragma unroll
       for (int j = 0; j < NB; ++j)
 #pragma unroll
@@ -650,6 +656,7 @@ __device__ __forceinline__ void gemm_epilogue(f32x16_t (&acc)[MB][NB], uint4* ld
       // block's writes follow this block's reads) without a barrier; only the
       // compiler's order must be kept.
       __asm__ volatile("" ::: "memory");
+      if (rope && i + 1 < MB) load_cs(i + 1, cvv[(i + 1) & 1], svv[(i + 1) & 1]);
       bool bad = false;
 #pragma unroll
       for (int it = 0; it < 8; ++it) {
@@ -687,7 +694,7 @@ __device__ __forceinline__ void gemm_epilogue(f32x16_t (&acc)[MB][NB], uint4* ld
         if (rope) {
           const bool ok = posv[i][it] >= 0;
           bad = bad || (!ok && row < g.m);
-          const float4 cv = cvv[it], sv = svv[it];
+          const float4 cv = cvv_i[it], sv = svv_i[it];
           const float c[4] = {cv.x, cv.y, cv.z, cv.w}, sn[4] = {sv.x, sv.y, sv.z, sv.w};
 #pragma unroll
           for (int t = 0; t < 4; ++t) {
