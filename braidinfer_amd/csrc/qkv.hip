@@ -683,7 +683,7 @@ __device__ __forceinline__ void gemm_epilogue(f32x16_t (&acc)[MB][NB], uint4* ld
           for (int t = 0; t < 4; ++t) ss += x1[t] * x1[t] + x2[t] * x2[t];
           ss = group_sum_dpp<LH>(ss);  // lanes of one head form an aligned group of a DPP row
           if (nw) {
-            const float r = 1.0f / sqrtf(ss / static_cast<float>(HD) + e.qk_eps);
+            const float r = __builtin_amdgcn_rsqf(ss / static_cast<float>(HD) + e.qk_eps);
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
               x1[t] = rnd<DT::N>((x1[t] * r) * g1[t], e.norm_dt);
@@ -1679,7 +1679,7 @@ __device__ __forceinline__ void decode_epilogue_item(const float4* part, int64_t
     if (nw) {
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
-        const float r = 1.0f / sqrtf(ss[v] / static_cast<float>(e.hd) + e.qk_eps);
+        const float r = __builtin_amdgcn_rsqf(ss[v] / static_cast<float>(e.hd) + e.qk_eps);
 #pragma unroll
         for (int pp = 0; pp < MAXP; ++pp) {
           x1[pp][v] = round_to((x1[pp][v] * r) * g1[pp], e.norm_dt);
@@ -2228,7 +2228,7 @@ __device__ __forceinline__ void row_epilogue_item(const float* part, int64_t spl
   if (kd != 2 && (e.qn_w || e.kn_w)) {
     ss = wave_sum_dpp(ss);
     if (nw) {
-      const float r = 1.0f / sqrtf(ss / static_cast<float>(e.hd) + e.qk_eps);
+      const float r = __builtin_amdgcn_rsqf(ss / static_cast<float>(e.hd) + e.qk_eps);
 #pragma unroll
       for (int p = 0; p < MAXP; ++p) {
         const int64_t j = lane + 64 * p;
