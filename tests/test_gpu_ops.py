@@ -359,6 +359,37 @@ def test_silu_and_mul_8192_tokens():
     assert_close(y[rows.to(DEV)], R.silu_and_mul(xs), what="silu_and_mul, 8192 x 2*14336 (sampled rows)")
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_streamed_outputs_equal_cached_stores(dtype):
+    """Outputs of 64 MiB and more are stored with the nontemporal hint, smaller
+    ones plainly; the hint must not change a value.  A call whose output is just
+    over 64 MiB and a call on its first rows (well under it) agree bit for bit on
+    those rows: SiLU*mul, and add+RMSNorm's y and residual."""
+    esz = torch.tensor([], dtype=dtype).element_size()
+    dg = torch.Generator(device=DEV).manual_seed(131)
+    inter = 4096
+    rows = (64 << 20) // (inter * esz) + 8
+    xd = torch.randn(rows, 2 * inter, device=DEV, generator=dg).to(dtype)
+    y_full = SiluAndMul()(xd)
+    for lo in (0, rows - 64):
+        y_part = SiluAndMul()(xd[lo:lo + 64].contiguous())
+        assert torch.equal(bits(y_full[lo:lo + 64]), bits(y_part)), f"silu_and_mul rows {lo}.."
+    h = 4096
+    rows = (64 << 20) // (h * esz) + 8
+    x = torch.randn(rows, h, device=DEV, generator=dg).to(dtype)
+    r = torch.randn(rows, h, device=DEV, generator=dg).to(dtype)
+    w = (torch.randn(h, device=DEV, generator=dg) * 0.1 + 1.0).to(dtype)
+    norm = RMSNorm(h, eps=1e-5).to(DEV)
+    with torch.no_grad():
+        norm.weight.data = w
+    y_full, r_full = norm(x.clone(), r.clone())  # fp32 normalises in place: work on copies
+    y_full, r_full = y_full.clone(), r_full.clone()
+    for lo in (0, rows - 64):
+        y_part, r_part = norm(x[lo:lo + 64].clone(), r[lo:lo + 64].clone())
+        assert torch.equal(bits(y_full[lo:lo + 64]), bits(y_part)), f"add_rms y rows {lo}.."
+        assert torch.equal(bits(r_full[lo:lo + 64]), bits(r_part)), f"add_rms residual rows {lo}.."
+
+
 def test_embedding_full_llama3_table_8192_ids():
     """The gather over the whole [128256, 4096] table with 8192 ids (about a
     quarter of them repeated), bit for bit against indexing a host copy."""
