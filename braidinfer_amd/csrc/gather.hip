@@ -85,6 +85,51 @@ __global__ __launch_bounds__(256) void gather_vec_kernel(GatherArgs a) {
   }
 }
 
+// Many ids: RB rows per workgroup (grid.y * grid.z cover the row blocks).  The
+// ids of all RB rows are read first, then every chunk load of the RB rows goes
+// out before the first store, so a workgroup waits for one id round trip and
+// one row round trip for all of its rows, not one of each per row.
+template <typename IdT, int DT, bool SCALE, int CPT, int RB>
+__global__ __launch_bounds__(256) void gather_rows_kernel(GatherArgs a) {
+  const int64_t t0 = (static_cast<int64_t>(blockIdx.y) + static_cast<int64_t>(blockIdx.z) * gridDim.y) * RB;
+  if (t0 >= a.num_ids) return;
+  int64_t id[RB];
+  bool in[RB], ok[RB];
+#pragma unroll
+  for (int r = 0; r < RB; ++r) {
+    in[r] = t0 + r < a.num_ids;
+    id[r] = in[r] ? fetch_id<IdT>(a.ids, t0 + r) : 0;
+    ok[r] = in[r] && id[r] >= 0 && id[r] < a.num_embeddings;
+    if (in[r] && !ok[r] && blockIdx.x == 0 && threadIdx.x == 0) flag_status(a.status, BFA_STATUS_INDEX_OOB);
+  }
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * (256 * CPT) + threadIdx.x;
+  uint4 v[RB][CPT];
+#pragma unroll
+  for (int r = 0; r < RB; ++r) {
+    const uint4* src = reinterpret_cast<const uint4*>(a.table + (ok[r] ? id[r] : 0) * a.table_stride_b);
+#pragma unroll
+    for (int c = 0; c < CPT; ++c) {
+      const int64_t ch = base + c * 256;
+      if (in[r] && ch < a.row_chunks) v[r][c] = ok[r] ? load16_nt(src + ch) : make_uint4(0, 0, 0, 0);
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < RB; ++r) {
+    uint4* dst = reinterpret_cast<uint4*>(a.out + (t0 + r) * a.out_stride_b);
+#pragma unroll
+    for (int c = 0; c < CPT; ++c) {
+      const int64_t ch = base + c * 256;
+      if (in[r] && ch < a.row_chunks) {
+        if constexpr (SCALE) {
+          dst[ch] = scale_chunk<DT>(v[r][c], a.scale);
+        } else {
+          dst[ch] = v[r][c];
+        }
+      }
+    }
+  }
+}
+
 // Element-granular fallback (unaligned rows or row bytes not a multiple of 16).
 template <typename IdT, typename E, int DT, bool SCALE>
 __global__ __launch_bounds__(256) void gather_scalar_kernel(GatherArgs a) {
@@ -116,6 +161,13 @@ static dim3 token_grid(int64_t gx, int64_t n) {
 template <typename IdT, int DT, bool SCALE>
 static void launch_gather(GatherArgs a, bool vec, int esize, hipStream_t s) {
   if (vec) {
+    if (a.num_ids >= 4096 && a.row_chunks <= 256 * 2) {
+      // rows of up to 8 KiB, four per workgroup (8192 ids of the Llama-3-8B
+      // table: 24.8 -> 24.2 us against one row per workgroup)
+      const dim3 g = token_grid(1, cdiv(a.num_ids, 4));
+      hipLaunchKernelGGL((gather_rows_kernel<IdT, DT, SCALE, 2, 4>), g, dim3(256), 0, s, a);
+      return;
+    }
     if (a.num_ids >= 1024) {
       const dim3 g = token_grid(cdiv(a.row_chunks, 256 * 4), a.num_ids);
       hipLaunchKernelGGL((gather_vec_kernel<IdT, DT, SCALE, 4>), g, dim3(256), 0, s, a);

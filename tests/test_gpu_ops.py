@@ -166,6 +166,33 @@ def test_embedding_bit_exact(v, h, ids_shape, idt):
     braidinfer_amd.check_device_status()
 
 
+@pytest.mark.parametrize("idt", [torch.int32, torch.int64])
+def test_embedding_many_ids_four_rows_per_workgroup(idt):
+    """From 4096 ids, rows of up to 8 KiB are gathered four per workgroup: a
+    count that leaves a partial last block, out-of-range ids (zero rows and
+    IndexError) inside a block, and the scaled (Qwen3) form."""
+    g = gen(123)
+    v, h, t = 3000, 2048, 4099
+    table = randn(g, v, h, std=0.02)
+    ids = torch.randint(0, v, (t,), generator=g, dtype=idt)
+    out = embedding(ids.to(DEV), table.to(DEV))
+    assert torch.equal(bits(out), bits(R.embedding(ids.long(), table)))
+    braidinfer_amd.check_device_status()
+    outs = embedding(ids.to(DEV), table.to(DEV), scale=1.0 / (h ** 0.5))
+    assert torch.equal(bits(outs), bits(R.embedding_scaled(ids.long(), table, h)))
+    bad = ids.clone()
+    bad[4097] = v          # in the partial last block
+    bad[5] = -1
+    out = embedding(bad.to(DEV), table.to(DEV))
+    with pytest.raises(IndexError):
+        braidinfer_amd.check_device_status()
+    keep = torch.ones(t, dtype=torch.bool)
+    keep[[5, 4097]] = False
+    assert out[5].eq(0).all() and out[4097].eq(0).all()
+    assert torch.equal(bits(out[keep.to(DEV)]), bits(R.embedding(ids.long(), table)[keep]))
+    braidinfer_amd.check_device_status()  # cleared
+
+
 def test_embedding_scaled_matches_qwen3_glue():
     g = gen(108)
     table = randn(g, 4000, 2048, std=0.02)
