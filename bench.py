@@ -16,7 +16,9 @@ Prints one JSON line.  `value` is microseconds per layer (lower is better):
 K chain steps captured into one HIP graph and replayed between HIP events
 after the clock has settled, i.e. the GPU time of the three kernels back to
 back without Python launch gaps; `eager_us_per_layer` is the same chain
-launched eagerly.  Every (kernel, workload) row -- kernels_prefill,
+launched eagerly; `rotating_weights_us_per_layer` is the graph-replayed chain
+with the QKV weight taken from four copies in turn, as a model's consecutive
+layers would (the repeated chain keeps its one weight in the Infinity Cache).  Every (kernel, workload) row -- kernels_prefill,
 decode.kernels, configs -- carries:
     us, gbs / tflops, hbm_frac / mfma_frac   warm, graph-replayed
     us_cold, hbm_frac_cold                   Infinity Cache flushed before each call
@@ -584,12 +586,12 @@ def time_cold(fn, iters: int, flush: torch.Tensor) -> float:
     return sum(s.elapsed_time(e) for s, e in pairs) / iters
 
 
-def chain_graph_us(c: Chain, steps: int, warmup: int) -> float:
+def chain_graph_us(c: Chain, steps: int, warmup: int, step=None) -> float:
     """Microseconds per chain step: `steps` steps captured into one HIP graph;
     `warmup` untimed steps (whole replays of the graph, at least one) and 0.3 s
     of untimed replays for the clock to settle, then exactly `steps` timed steps
     between HIP events."""
-    graph = _capture(c.step, steps)
+    graph = _capture(step or c.step, steps)
     done = 0
     while done < max(warmup, 1):
         graph.replay()
@@ -602,6 +604,23 @@ def chain_graph_us(c: Chain, steps: int, warmup: int) -> float:
     e.record()
     torch.cuda.synchronize()
     return s.elapsed_time(e) / steps * 1e3
+
+
+def chain_graph_rotating_us(c: Chain, steps: int, warmup: int, nw: int = 4) -> float:
+    """As chain_graph_us, with the QKV weight taken from `nw` copies in turn (one
+    per captured step), as consecutive layers of a model use different weights:
+    the repeated chain otherwise finds its 50 MB weight in the Infinity Cache."""
+    ws = [c.w_qkv] + [c.w_qkv.clone() for _ in range(nw - 1)]
+    turn = [0]
+
+    def step():
+        c.w_qkv = ws[turn[0] % nw]
+        turn[0] += 1
+        c.step()
+    try:
+        return chain_graph_us(c, -(-steps // nw) * nw, warmup, step)
+    finally:
+        c.w_qkv = ws[0]
 
 
 def chain_us(c: Chain, steps: int, warmup: int) -> float:
@@ -794,6 +813,7 @@ def main(argv=None) -> int:
     prefill = Chain(args.tokens, dev)
     us_eager = chain_us(prefill, args.steps, args.warmup)
     us = chain_graph_us(prefill, args.steps, args.warmup)
+    us_rot = chain_graph_rotating_us(prefill, args.steps, args.warmup)
     rows_p = chain_rows(prefill, dev, stages=True)
     nc = 0 if args.no_cold else 1
     kp = measure_rows(rows_p, max(10, args.steps), flush, 10 * nc)
@@ -851,6 +871,7 @@ def main(argv=None) -> int:
                                        "copy; read from the file, not measured in this run)"},
         "kernels_prefill": kp,
         "eager_us_per_layer": round(us_eager, 2),
+        "rotating_weights_us_per_layer": round(us_rot, 2),
         "decode": {"tokens": args.decode_tokens, "us_per_layer": round(us_dec, 2),
                    "eager_us_per_layer": round(us_dec_eager, 2), "kernels": kd},
         "configs": configs,

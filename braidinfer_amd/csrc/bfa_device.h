@@ -8,6 +8,7 @@
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include <cstdlib>
 
 #include "braidinfer_amd.h"
 
@@ -122,8 +123,15 @@ __device__ __forceinline__ void store8(void* p, const float (&v)[8]) {
 // 103 to 111 us with it, while the Llama-3-8B 8192-token layer chain
 // (add+RMSNorm, fused QKV, SiLU*mul) goes from 546 to 515 us.  Smaller outputs
 // (decode batches) keep plain stores, so their consumers find them cached.
+// BFA_STREAM_STORES=0 keeps every store plain (measurement override).
 constexpr int64_t kStreamOutputBytes = int64_t(64) << 20;
-inline bool stream_output(int64_t bytes) { return bytes >= kStreamOutputBytes; }
+inline bool stream_output(int64_t bytes) {
+  static const bool off = [] {
+    const char* v = getenv("BFA_STREAM_STORES");
+    return v != nullptr && atoi(v) == 0;
+  }();
+  return !off && bytes >= kStreamOutputBytes;
+}
 
 // Streaming forms: 16-byte loads with the nontemporal hint, for operands that
 // are read exactly once (activations of the memory-bound kernels, gathered
