@@ -121,8 +121,11 @@ __device__ __forceinline__ void store8(void* p, const float (&v)[8]) {
 // Infinity Cache for its consumer anyway, and streaming it past the cache keeps
 // what the next kernels read there.  SiLU*mul at 8192 x 14336 alone slows from
 // 103 to 111 us with it, while the Llama-3-8B 8192-token layer chain
-// (add+RMSNorm, fused QKV, SiLU*mul) goes from 546 to 515 us.  Smaller outputs
-// (decode batches) keep plain stores, so their consumers find them cached.
+// (add+RMSNorm, fused QKV, SiLU*mul) goes from 542 to 507 us when one layer is
+// repeated (its QKV weight then stays cached), and from 543 to 531.5 us with
+// the weight rotating over four copies, as consecutive layers would.  Smaller
+// outputs (decode batches) keep plain stores, so their consumers find them
+// cached.
 // BFA_STREAM_STORES=0 keeps every store plain (measurement override).
 constexpr int64_t kStreamOutputBytes = int64_t(64) << 20;
 inline bool stream_output(int64_t bytes) {
