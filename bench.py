@@ -813,7 +813,6 @@ def main(argv=None) -> int:
     prefill = Chain(args.tokens, dev)
     us_eager = chain_us(prefill, args.steps, args.warmup)
     us = chain_graph_us(prefill, args.steps, args.warmup)
-    us_rot = chain_graph_rotating_us(prefill, args.steps, args.warmup)
     rows_p = chain_rows(prefill, dev, stages=True)
     nc = 0 if args.no_cold else 1
     kp = measure_rows(rows_p, max(10, args.steps), flush, 10 * nc)
@@ -828,6 +827,9 @@ def main(argv=None) -> int:
     progress("other configurations")
     rows_c = config_cases(dev)
     configs = measure_rows(rows_c, max(40, args.steps), flush, 24 * nc)
+    # after every per-kernel row, so that its heat does not reach them
+    progress("prefill chain with rotating QKV weights")
+    us_rot = chain_graph_rotating_us(prefill, args.steps, args.warmup)
     _lib.check_device_status(dev)
     tables = {"prefill": kp, "decode": kd, "configs": configs}
     cpu = None
