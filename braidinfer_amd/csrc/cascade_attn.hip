@@ -387,7 +387,7 @@ __global__ __launch_bounds__(256) void cascade_attn_kernel(CasArgs a) {
 #pragma unroll
       for (int i = 0; i < EL; ++i) ss += x1[i] * x1[i] + x2[i] * x2[i];
       ss = group8_sum_dpp(ss);
-      const float r = 1.0f / sqrtf(ss / static_cast<float>(D) + a.knorm_eps);
+      const float r = __builtin_amdgcn_rsqf(ss / static_cast<float>(D) + a.knorm_eps);
 #pragma unroll
       for (int i = 0; i < EL; ++i) {
         x1[i] = E::round(E::round(x1[i] * r) * kg1[i]);
@@ -614,7 +614,7 @@ __global__ __launch_bounds__(256) void cascade_flatten_kernel(CasArgs a, FlatArg
 #pragma unroll
       for (int i = 0; i < EL; ++i) ss += x1[i] * x1[i] + x2[i] * x2[i];
       ss = group8_sum_dpp(ss);
-      const float r = 1.0f / sqrtf(ss / static_cast<float>(D) + a.knorm_eps);
+      const float r = __builtin_amdgcn_rsqf(ss / static_cast<float>(D) + a.knorm_eps);
 #pragma unroll
       for (int i = 0; i < EL; ++i) {
         x1[i] = E::round(E::round(x1[i] * r) * kg1[i]);
@@ -992,7 +992,12 @@ __global__ __launch_bounds__(256) void cascade_decode_kernel(CasArgs a, int64_t 
     Meta mt;
     const int64_t e = it / nsb, sb = it - e * nsb;
     mt.in = it < i1;
-    const int64_t ec = mt.in ? e : 0;
+    // the entry index in a vector register: its loads are then vector loads,
+    // which complete in order, so the wait for an item's metadata (two items
+    // ahead) does not also wait for later ones, as out-of-order scalar loads
+    // would (Qwen3 decode over 4096 keys 13.6 -> 13.35 us)
+    int64_t ec = mt.in ? e : 0;
+    asm volatile("" : "+v"(ec));
     mt.pg = a.pages[ec];
     mt.kst = a.kstart[ec];
     mt.dpos = a.delta[ec];
@@ -1057,7 +1062,7 @@ __global__ __launch_bounds__(256) void cascade_decode_kernel(CasArgs a, int64_t 
 #pragma unroll
         for (int i = 0; i < EH; ++i) ss += x1[i] * x1[i] + x2[i] * x2[i];
         ss = group16_sum_dpp(ss);
-        const float rn = 1.0f / sqrtf(ss / static_cast<float>(D) + a.knorm_eps);
+        const float rn = __builtin_amdgcn_rsqf(ss / static_cast<float>(D) + a.knorm_eps);
 #pragma unroll
         for (int i = 0; i < EH; ++i) {
           x1[i] = E::round(E::round(x1[i] * rn) * kw1[i]);
