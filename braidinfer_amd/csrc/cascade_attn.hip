@@ -967,7 +967,7 @@ __global__ __launch_bounds__(256) void cascade_merge_small_kernel(CasArgs a, int
 template <bool BF16, int R, int D>
 __global__ __launch_bounds__(256) void cascade_decode_kernel(CasArgs a, int64_t items_per_split, int64_t nsb) {
   using E = Elem<BF16 ? BFA_DTYPE_BF16 : BFA_DTYPE_F16>;
-  constexpr int NG = 16, EH = D / 32;
+  constexpr int NG = 16, EH = D / 32, NU = 4;  // NU: most items per workgroup taken at once
   __shared__ float red_m[NG][R], red_l[NG][R];
   __shared__ float red_a[NG][R][D];
   const int tid = threadIdx.x, j = tid & 15, kg = tid >> 4;
@@ -1072,59 +1072,81 @@ __global__ __launch_bounds__(256) void cascade_decode_kernel(CasArgs a, int64_t 
     return b;
   };
 
+  // one item into the group's online-softmax states
+  auto consume = [&](const Slot& cur) {
+    float x1[EH], x2[EH];
+    unpack_h<EH, E>(cur.k1, x1);
+    unpack_h<EH, E>(cur.k2, x2);
+    if (cur.rot) {
+#pragma unroll
+      for (int i = 0; i < EH; ++i) {  // apply_rotary_emb: fp32, result in the cache dtype
+        const float u = x1[i], w = x2[i];
+        x1[i] = E::round(u * cur.c[i] - w * cur.sn[i]);
+        x2[i] = E::round(w * cur.c[i] + u * cur.sn[i]);
+      }
+    }
+    if (a.knorm_w) {  // uniform: every lane joins its group's 16-lane sum
+      float ss = 0.f;
+#pragma unroll
+      for (int i = 0; i < EH; ++i) ss += x1[i] * x1[i] + x2[i] * x2[i];
+      ss = group16_sum_dpp(ss);
+      const float rn = __builtin_amdgcn_rsqf(ss / static_cast<float>(D) + a.knorm_eps);
+#pragma unroll
+      for (int i = 0; i < EH; ++i) {
+        x1[i] = E::round(E::round(x1[i] * rn) * kw1[i]);
+        x2[i] = E::round(E::round(x2[i] * rn) * kw2[i]);
+      }
+    }
+    float v1[EH], v2[EH];
+    unpack_h<EH, E>(cur.v1, v1);
+    unpack_h<EH, E>(cur.v2, v2);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      float d = 0.f;
+#pragma unroll
+      for (int i = 0; i < EH; ++i) d += q1[r][i] * x1[i] + q2[r][i] * x2[i];
+      d = group16_sum_dpp(d);
+      const bool use = cur.valid && (!a.causal || cur.kp <= qp[r]);
+      const float sc = use ? d * sl2 : -INFINITY;
+      const float m_new = fmaxf(m[r], sc);
+      const float mref = m_new == -INFINITY ? 0.f : m_new;  // nothing seen yet: stay at zero
+      const float alpha = __builtin_amdgcn_exp2f(m[r] - mref);
+      const float pr = __builtin_amdgcn_exp2f(sc - mref);
+      l[r] = l[r] * alpha + pr;
+      m[r] = m_new;
+#pragma unroll
+      for (int i = 0; i < EH; ++i) {
+        acc1[r][i] = acc1[r][i] * alpha + pr * v1[i];
+        acc2[r][i] = acc2[r][i] * alpha + pr * v2[i];
+      }
+    }
+  };
+
   if (i0 < i1) {
-    Slot cur = issue(load_meta(i0));
-    Meta mn = load_meta(i0 + 1);
-    for (int64_t it = i0; it < i1; ++it) {
-      const Slot nxt = issue(mn);  // item it + 1's rows fly while this item is processed,
-      mn = load_meta(it + 2);      // and item it + 2's metadata
-      float x1[EH], x2[EH];
-      unpack_h<EH, E>(cur.k1, x1);
-      unpack_h<EH, E>(cur.k2, x2);
-      if (cur.rot) {
+    if (items_per_split > 1 && items_per_split <= NU) {
+      // Few items: every item's metadata, then every item's rows, requested
+      // at once -- two memory round trips in all, where the pipelined walk
+      // waits about one per item.  Slots past i1 load the zeroed row and are
+      // not consumed (a uniform branch).  Qwen3 decode over 4096 keys: 4 items
+      // per workgroup, 12.1 -> 11.6 us.
+      Meta mt[NU];
 #pragma unroll
-        for (int i = 0; i < EH; ++i) {  // apply_rotary_emb: fp32, result in the cache dtype
-          const float u = x1[i], w = x2[i];
-          x1[i] = E::round(u * cur.c[i] - w * cur.sn[i]);
-          x2[i] = E::round(w * cur.c[i] + u * cur.sn[i]);
-        }
+      for (int u = 0; u < NU; ++u) mt[u] = load_meta(i0 + u);
+      Slot sv[NU];
+#pragma unroll
+      for (int u = 0; u < NU; ++u) sv[u] = issue(mt[u]);
+#pragma unroll
+      for (int u = 0; u < NU; ++u)
+        if (i0 + u < i1) consume(sv[u]);
+    } else {
+      Slot cur = issue(load_meta(i0));
+      Meta mn = load_meta(i0 + 1);
+      for (int64_t it = i0; it < i1; ++it) {
+        const Slot nxt = issue(mn);  // item it + 1's rows fly while this item is processed,
+        mn = load_meta(it + 2);      // and item it + 2's metadata
+        consume(cur);
+        cur = nxt;
       }
-      if (a.knorm_w) {  // uniform: every lane joins its group's 16-lane sum
-        float ss = 0.f;
-#pragma unroll
-        for (int i = 0; i < EH; ++i) ss += x1[i] * x1[i] + x2[i] * x2[i];
-        ss = group16_sum_dpp(ss);
-        const float rn = __builtin_amdgcn_rsqf(ss / static_cast<float>(D) + a.knorm_eps);
-#pragma unroll
-        for (int i = 0; i < EH; ++i) {
-          x1[i] = E::round(E::round(x1[i] * rn) * kw1[i]);
-          x2[i] = E::round(E::round(x2[i] * rn) * kw2[i]);
-        }
-      }
-      float v1[EH], v2[EH];
-      unpack_h<EH, E>(cur.v1, v1);
-      unpack_h<EH, E>(cur.v2, v2);
-#pragma unroll
-      for (int r = 0; r < R; ++r) {
-        float d = 0.f;
-#pragma unroll
-        for (int i = 0; i < EH; ++i) d += q1[r][i] * x1[i] + q2[r][i] * x2[i];
-        d = group16_sum_dpp(d);
-        const bool use = cur.valid && (!a.causal || cur.kp <= qp[r]);
-        const float sc = use ? d * sl2 : -INFINITY;
-        const float m_new = fmaxf(m[r], sc);
-        const float mref = m_new == -INFINITY ? 0.f : m_new;  // nothing seen yet: stay at zero
-        const float alpha = __builtin_amdgcn_exp2f(m[r] - mref);
-        const float pr = __builtin_amdgcn_exp2f(sc - mref);
-        l[r] = l[r] * alpha + pr;
-        m[r] = m_new;
-#pragma unroll
-        for (int i = 0; i < EH; ++i) {
-          acc1[r][i] = acc1[r][i] * alpha + pr * v1[i];
-          acc2[r][i] = acc2[r][i] * alpha + pr * v2[i];
-        }
-      }
-      cur = nxt;
     }
   }
   // ---- the 16 group states -> one state per row

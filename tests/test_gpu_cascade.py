@@ -197,6 +197,29 @@ def test_cascade_decode_form_page_sizes(ps, tokens, dtype, d):
     assert_close(out, exp, what=f"decode form ps={ps} t={tokens} {dtype} d={d}")
 
 
+@pytest.mark.parametrize("target", [8, 64, 256, 1024, 8192])
+def test_cascade_decode_split_merges(monkeypatch, target):
+    """The decode kernel's split count follows the workgroup target; every
+    combination form is taken over about 3000 keys (about 190 pages) at 8 kv
+    heads: one split (no merge), 8 (a wave per row), 32 (one round trip, 16
+    splits per wave), about 95 and about 190 (the looped merge)."""
+    monkeypatch.setenv("BFA_CASCADE_DECODE_WG", str(target))
+    g = gen(120 + target)
+    hq, hkv, d, ps, max_pos = 32, 8, 128, 16, 40960
+    chunks, kv, total = build_case(121, hq, hkv, [1500, 900, 601], [0, 2000, -700], pages=200, ps=ps, d=d)
+    rope = RotaryEmbedding(d, d, max_pos, 1e6).to(DEV)
+    att = CascadeAttention(hq, d, d ** -0.5, hkv, ps, rotary_emb=rope)
+    levels = att.create_cascade_levels(chunks)
+    q = randn(g, 1, hq, d)
+    qpos = torch.tensor([total])
+    out = att.forward(q.to(DEV), qpos.to(DEV), kv.to(DEV), levels, 0)
+    torch.cuda.synchronize()
+    braidinfer_amd.check_device_status()
+    exp = R.cascade_attention(q, qpos, kv, cpu_levels(levels), hq, hkv, d ** -0.5, ps,
+                              rope.cos_sin_cache.cpu(), None, 1e-6, True)
+    assert_close(out, exp, what=f"decode splits, target {target}")
+
+
 @pytest.mark.parametrize("ps,dtype,d", [(8, torch.bfloat16, 128), (32, torch.float16, 128), (8, torch.float16, 64)])
 def test_cascade_flat_form_page_sizes(monkeypatch, ps, dtype, d):
     """Flat form with pages of 8 (8 pages per 64-key tile) and 32 slots, a
