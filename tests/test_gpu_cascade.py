@@ -197,12 +197,13 @@ def test_cascade_decode_form_page_sizes(ps, tokens, dtype, d):
     assert_close(out, exp, what=f"decode form ps={ps} t={tokens} {dtype} d={d}")
 
 
-@pytest.mark.parametrize("target", [8, 64, 256, 1024, 8192])
+@pytest.mark.parametrize("target", [8, 32, 64, 96, 256, 1024, 8192])
 def test_cascade_decode_split_merges(monkeypatch, target):
     """The decode kernel's split count follows the workgroup target; every
     combination form is taken over about 3000 keys (about 190 pages) at 8 kv
-    heads: one split (no merge), 8 (a wave per row), 32 (one round trip, 16
-    splits per wave), about 95 and about 190 (the looped merge)."""
+    heads: one split (no merge), 4, 8 and 12 (a wave per row, sized for 4, 8
+    and 16 splits), 32 (one round trip, 16 splits per wave), about 95 and
+    about 190 (the looped merge)."""
     monkeypatch.setenv("BFA_CASCADE_DECODE_WG", str(target))
     g = gen(120 + target)
     hq, hkv, d, ps, max_pos = 32, 8, 128, 16, 40960
