@@ -25,7 +25,13 @@ decode.kernels, configs -- carries:
     cpu_us, cpu_reps                         the oracle's torch-CPU restatement of the
                                              reference at the row's full size, median
     vs_oracle                                bit-exact, or max_abs / max_rel_normwise /
-                                             allclose / beyond_tol_elements
+                                             allclose / beyond_tol_elements against the
+                                             oracle (the reference's own rounding points)
+    vs_fp32, oracle_vs_fp32                  float rows: the same figures against the fp32
+                                             mode of the oracle (every op chain in fp32,
+                                             one rounding: the "fp32 reference after bf16
+                                             rounding" of the accuracy target), for the GPU
+                                             result and for the reference's own rounding
 `roofline` is for the dominant kernel (the QKV projection at 8192 tokens):
 its algorithmic FLOPs / its own average event-timed duration against the
 2.5 PFLOP/s dense-bf16 peak.  `cpu_baseline` is the sum of the three chain
@@ -159,9 +165,10 @@ class Row:
     the same inputs on the CPU, and `got` maps fn's output to the tensor(s)
     compared with it.  exact: integer/byte ops compared bit for bit."""
 
-    def __init__(self, name, fn, nbytes, flops=0.0, ref=None, got=None, exact=False, note=None):
+    def __init__(self, name, fn, nbytes, flops=0.0, ref=None, got=None, exact=False, note=None, ref32=None):
         self.name, self.fn, self.nbytes, self.flops = name, fn, nbytes, flops
         self.ref, self.got, self.exact, self.note = ref, got, exact, note
+        self.ref32 = ref32  # the fp32 mode of the oracle (float rows)
 
 
 def chain_rows(c: Chain, dev, stages: bool) -> list:
@@ -169,7 +176,8 @@ def chain_rows(c: Chain, dev, stages: bool) -> list:
     fused QKV op (operand pre-pass, projection) as rows of their own."""
     t = c.t
     rows = [Row("add_rms_norm", lambda: c.norm(c.x, c.residual)[0], 4 * t * H * 2 + H * 2,
-                ref=lambda: _oracle().add_rms_forward(c.cpu["x"], c.cpu["residual"], c.cpu["norm_w"], EPS)[0])]
+                ref=lambda: _oracle().add_rms_forward(c.cpu["x"], c.cpu["residual"], c.cpu["norm_w"], EPS)[0],
+                ref32=lambda: _oracle32().add_rms_forward(c.cpu["x"], c.cpu["residual"], c.cpu["norm_w"], EPS)[0])]
     if stages:
         st = QkvStages(c, dev)
         rows += [Row("qkv_operand_prepass", st.operand, 2 * t * H * 2 + H * 2, note="stage of the fused op"),
@@ -177,14 +185,15 @@ def chain_rows(c: Chain, dev, stages: bool) -> list:
                      t * H * 2 + N * H * 2 + t * N * 2 + t * 8 + t * D * 4, 2.0 * t * H * N,
                      note="stage of the fused op (operand from the pre-pass)")]
 
-    def llama_ref():
-        q, k, v = _oracle().llama_attention_input(c.cpu["hidden"], c.cpu["ln_w"], c.cpu["w_qkv"], HQ, HKV, EPS,
-                                                  c.cpu["positions"], c.cpu["cache"])
+    def llama_ref(o=_oracle):
+        q, k, v = o().llama_attention_input(c.cpu["hidden"], c.cpu["ln_w"], c.cpu["w_qkv"], HQ, HKV, EPS,
+                                            c.cpu["positions"], c.cpu["cache"])
         return torch.cat([q, k, v], 1)
     rows += [Row("fused_rmsnorm_qkv_rope", c.qkv, t * H * 2 + H * 2 + N * H * 2 + t * N * 2 + t * 8 + t * D * 4,
-                 2.0 * t * H * N, ref=llama_ref),
+                 2.0 * t * H * N, ref=llama_ref, ref32=lambda: llama_ref(_oracle32)),
              Row("silu_and_mul", lambda: c.silu(c.gate_up), 3 * t * INTER * 2,
-                 ref=lambda: _oracle().silu_and_mul(c.cpu["gate_up"]))]
+                 ref=lambda: _oracle().silu_and_mul(c.cpu["gate_up"]),
+                 ref32=lambda: _oracle32().silu_and_mul(c.cpu["gate_up"]))]
     table = torch.empty(VOCAB, H, dtype=torch.bfloat16, device=dev).normal_(0, 0.02)
     host = {}
 
@@ -212,6 +221,12 @@ def _oracle():
     leg, which times it and checks the GPU results against it."""
     from oracle import torch_ref
     return torch_ref
+
+
+def _oracle32():
+    """The fp32 mode of the oracle (oracle/fp32_ref.py), for the vs_fp32 figures."""
+    from oracle import fp32_ref
+    return fp32_ref
 
 
 class _Gen:
@@ -253,7 +268,8 @@ def config_cases(dev) -> list:
     with torch.no_grad():
         norm.weight.data = w
     rows.append(Row("rmsnorm_t128_h2048", lambda: norm(x), 2 * 128 * 2048 * 2 + 2048 * 2,
-                    ref=lambda: _oracle().rms_forward(xc, wc, 1e-5)))
+                    ref=lambda: _oracle().rms_forward(xc, wc, 1e-5),
+                    ref32=lambda: _oracle32().rms_forward(xc, wc, 1e-5)))
 
     def cat3(qkv):
         return torch.cat([t.reshape(t.shape[0], -1) for t in qkv], 1)
@@ -266,7 +282,8 @@ def config_cases(dev) -> list:
         pos, cache = pc.to(dev), cc.to(dev)
         return Row(f"tinyllama_qkv_rope_t{t}", lambda: llama_attention_input(xt, ln, w, hq, hkv, 1e-5, pos, cache),
                    t * h * 2 + h * 2 + n * h * 2 + t * n * 2 + t * 8 + t * d * 4, 2.0 * t * h * n,
-                   ref=lambda: cat3(_oracle().llama_attention_input(xc, lc, wc, hq, hkv, 1e-5, pc, cc)), got=cat3)
+                   ref=lambda: cat3(_oracle().llama_attention_input(xc, lc, wc, hq, hkv, 1e-5, pc, cc)), got=cat3,
+                   ref32=lambda: cat3(_oracle32().llama_attention_input(xc, lc, wc, hq, hkv, 1e-5, pc, cc)))
 
     r = _Gen(2, dev)
     rows += [tiny(r, t) for t in (1, 8, 512)]
@@ -284,7 +301,9 @@ def config_cases(dev) -> list:
                    lambda: qwen3_attention_input(xt, ln, w, None, hq, hkv, 1e-6, pos, cache, qn, kn),
                    t * h * 2 + h * 2 + n * h * 2 + t * n * 2 + t * 8 + t * d * 4 + 2 * d * 2, 2.0 * t * h * n,
                    ref=lambda: cat3(_oracle().qwen3_attention_input(xc, lc, wc, None, hq, hkv, 1e-6, pc, cc, qc, kc)),
-                   got=cat3)
+                   got=cat3,
+                   ref32=lambda: cat3(_oracle32().qwen3_attention_input(xc, lc, wc, None, hq, hkv, 1e-6, pc, cc,
+                                                                        qc, kc)))
 
     r = _Gen(3, dev)
     rows += [qwen(r, t) for t in (1, 2048)]
@@ -306,7 +325,7 @@ def config_cases(dev) -> list:
     guc, gu = r.randn(2048, 2 * 3072)
     silu = SiluAndMul()
     rows.append(Row("swiglu_t2048_i3072", lambda: silu(gu), 3 * 2048 * 3072 * 2,
-                    ref=lambda: _oracle().silu_and_mul(guc)))
+                    ref=lambda: _oracle().silu_and_mul(guc), ref32=lambda: _oracle32().silu_and_mul(guc)))
 
     rows += kv_append_cases(dev)
     rows += fused_append_cases(dev)
@@ -331,13 +350,16 @@ def linear_cases(dev) -> list:
         out += [
             Row(f"gate_up_silu_llama3_8b_t{t}", (lambda x=x: gate_up_silu_and_mul(x, w_gu)),
                 (t * h + 2 * inter * h + t * inter) * 2, 2.0 * t * h * 2 * inter,
-                ref=lambda xc=xc: _oracle().gate_up_silu_and_mul(xc, guc)),
+                ref=lambda xc=xc: _oracle().gate_up_silu_and_mul(xc, guc),
+                ref32=lambda xc=xc: _oracle32().gate_up_silu_and_mul(xc, guc)),
             Row(f"down_proj_residual_llama3_8b_t{t}", (lambda xi=xi, res=res: linear_add_residual(xi, w_down, res)),
                 (t * inter + inter * h + 2 * t * h) * 2, 2.0 * t * inter * h,
-                ref=lambda xic=xic, rc=rc: _oracle().linear_add_residual(xic, dnc, rc)),
+                ref=lambda xic=xic, rc=rc: _oracle().linear_add_residual(xic, dnc, rc),
+                ref32=lambda xic=xic, rc=rc: _oracle32().linear(xic, dnc, residual=rc)),
             Row(f"o_proj_residual_llama3_8b_t{t}", (lambda x=x, res=res: linear_add_residual(x, w_o, res)),
                 (2 * t * h + h * h + t * h) * 2, 2.0 * t * h * h,
-                ref=lambda xc=xc, rc=rc: _oracle().linear_add_residual(xc, oc, rc)),
+                ref=lambda xc=xc, rc=rc: _oracle().linear_add_residual(xc, oc, rc),
+                ref32=lambda xc=xc, rc=rc: _oracle32().linear(xc, oc, residual=rc)),
         ]
     return out
 
@@ -441,8 +463,8 @@ def fused_append_cases(dev) -> list:
                                       cpos, ps)
             return caches["sep"]
 
-        def ref(t=t, xc=xc, lc=lc, wc=wc, pc=pc, rc_=rc_, cc=cc, tc=tc, cpc=cpc, ic=ic, bc=bc):
-            _, k, v = _oracle().llama_attention_input(xc, lc, wc, HQ, HKV, EPS, pc, rc_)
+        def ref(t=t, xc=xc, lc=lc, wc=wc, pc=pc, rc_=rc_, cc=cc, tc=tc, cpc=cpc, ic=ic, bc=bc, qkv=_oracle):
+            _, k, v = qkv().llama_attention_input(xc, lc, wc, HQ, HKV, EPS, pc, rc_)
             k, v = k.reshape(t, HKV, D), v.reshape(t, HKV, D)
             if ic is None:
                 return _oracle().append_to_paged_kv_cache(k, v, cc, tc, cpc, ps)[0]
@@ -451,15 +473,16 @@ def fused_append_cases(dev) -> list:
         qkv_bytes = t * H * 2 + H * 2 + N * H * 2 + t * N * 2 + t * 8 + t * D * 4
         meta = t * (8 + 8 + 4)  # cache positions, slot offsets, page entries
         tag = "t8192" if t == 8192 else "b64"
+        ref32 = (lambda ref=ref: ref(qkv=_oracle32))
         rows += [Row(f"qkv_rope_append_llama3_8b_{tag}", lambda fused=fused: fused("fused"),
-                     qkv_bytes + t * kvb + meta, 2.0 * t * H * N, ref=ref,
+                     qkv_bytes + t * kvb + meta, 2.0 * t * H * N, ref=ref, ref32=ref32,
                      note="fused QKV + RoPE + paged KV append, one call; cache compared"),
                  Row(f"qkv_rope_then_append_llama3_8b_{tag}", separate,
-                     qkv_bytes + 2 * t * kvb + meta, 2.0 * t * H * N, ref=ref,
+                     qkv_bytes + 2 * t * kvb + meta, 2.0 * t * H * N, ref=ref, ref32=ref32,
                      note="the two separate calls it replaces; cache compared")]
         if t == 8192:
             rows.append(Row(f"qkv_rope_append_q_only_llama3_8b_{tag}", lambda fused=fused: fused("qonly"),
-                            qkv_bytes - t * kvb + t * kvb + meta, 2.0 * t * H * N, ref=ref,
+                            qkv_bytes - t * kvb + t * kvb + meta, 2.0 * t * H * N, ref=ref, ref32=ref32,
                             note="write_kv_out=False: k/v only into the cache; cache compared"))
     return rows
 
@@ -521,7 +544,12 @@ def _cascade_rows(dev, label, seed, hq, hkv, d, keys, theta, max_pos, knorm) -> 
                        kv_bytes + 2 * t * hq * d * 2, 4.0 * t * hq * keys * d,
                        ref=lambda qc=qc, qpc=qpc: _oracle().cascade_attention(
                            qc, qpc, kvc, cpu_levels, hq, hkv, d ** -0.5, ps, cos_sin_cache=csc,
-                           k_norm_weight=knc, k_norm_eps=1e-6)))
+                           k_norm_weight=knc, k_norm_eps=1e-6),
+                       # fp32 mode: the same op chain on fp32 copies of the bf16 inputs
+                       # (no intermediate rounding), rounded once to bf16
+                       ref32=lambda qc=qc, qpc=qpc: _oracle().cascade_attention(
+                           qc.float(), qpc, kvc.float(), cpu_levels, hq, hkv, d ** -0.5, ps, cos_sin_cache=csc,
+                           k_norm_weight=None if knc is None else knc.float(), k_norm_eps=1e-6).to(bf)))
     return out
 
 
@@ -658,11 +686,12 @@ def _bits(t: torch.Tensor) -> torch.Tensor:
     return t.view({2: torch.int16, 4: torch.int32, 8: torch.int64}[t.element_size()])
 
 
-def compare(got: torch.Tensor, exp: torch.Tensor, exact: bool) -> dict:
+def compare(got: torch.Tensor, exp: torch.Tensor, exact: bool, brief: bool = False) -> dict:
     """Error figures of a GPU result against the oracle's: bit-exact for the
     integer/byte ops; otherwise max-abs, normwise relative error and the
     elements outside |d| <= 2e-2 + 1e-2 |r| (the float tolerance; those are
-    the elements a documented rounding allowance of the parity tests covers)."""
+    the elements a documented rounding allowance of the parity tests covers).
+    brief: without allclose and numel (the vs_fp32 figures)."""
     got = got.detach().cpu()
     if exact:
         mism = int((_bits(got) != _bits(exp)).sum())
@@ -673,9 +702,12 @@ def compare(got: torch.Tensor, exp: torch.Tensor, exact: bool) -> dict:
     d = (a - e).abs()[fin]
     ef = e[fin]
     outside = int((d > 2e-2 + 1e-2 * ef.abs()).sum())
-    return {"max_abs": float(f"{d.max().item():.4g}") if d.numel() else 0.0,
-            "max_rel_normwise": float(f"{(d.norm() / ef.norm().clamp_min(1e-30)).item():.4g}"),
-            "allclose": same_pattern and outside == 0, "beyond_tol_elements": outside, "numel": exp.numel()}
+    out = {"max_abs": float(f"{d.max().item():.4g}") if d.numel() else 0.0,
+           "max_rel_normwise": float(f"{(d.norm() / ef.norm().clamp_min(1e-30)).item():.4g}"),
+           "beyond_tol_elements": outside}
+    if not brief:
+        out.update({"allclose": same_pattern and outside == 0, "numel": exp.numel()})
+    return out
 
 
 def time_cpu(fn, min_reps: int = 3, max_reps: int = 10, budget_s: float = 3.0):
@@ -726,6 +758,10 @@ def cpu_leg(groups: dict, tables: dict) -> None:
             row["cpu_us"] = round(sec * 1e6, 1)
             row["cpu_reps"] = reps
             row["vs_oracle"] = compare(got, exp, r.exact)
+            if r.ref32 is not None:
+                exp32 = r.ref32()
+                row["vs_fp32"] = compare(got, exp32, False, brief=True)
+                row["oracle_vs_fp32"] = compare(exp, exp32, False, brief=True)
 
 
 def read_traffic(name: str):
@@ -864,6 +900,16 @@ def main(argv=None) -> int:
                                f"-> SiLU*mul [{args.tokens},2x14336]",
                    "tokens": args.tokens, "hidden": H, "q_heads": HQ, "kv_heads": HKV,
                    "head_dim": D, "intermediate": INTER},
+        "configs": configs,
+        "timing": "us: graph-replayed HIP-event average after >= 0.2 s of settling replays (warm: "
+                  "operands in the caches from the previous call); us_cold: each call after a 512 MB "
+                  "read that flushes the 256 MB Infinity Cache",
+        "cpu": cpu_info() if not args.no_cpu else None,
+        "kernels_prefill": kp,
+        "decode": {"tokens": args.decode_tokens, "us_per_layer": round(us_dec, 2),
+                   "eager_us_per_layer": round(us_dec_eager, 2), "kernels": kd},
+        "eager_us_per_layer": round(us_eager, 2),
+        "rotating_weights_us_per_layer": round(us_rot, 2),
         "roofline": {"bound": "mfma", "kernel": "qkv_projection_rope",
                      "achieved": proj["tflops"], "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": proj["mfma_frac"],
@@ -871,16 +917,6 @@ def main(argv=None) -> int:
                      "traffic_source": f"profiles/traffic_qkv_projection_llama3_8b_t{args.tokens}.txt "
                                        "(rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, calibrated on a device "
                                        "copy; read from the file, not measured in this run)"},
-        "kernels_prefill": kp,
-        "eager_us_per_layer": round(us_eager, 2),
-        "rotating_weights_us_per_layer": round(us_rot, 2),
-        "decode": {"tokens": args.decode_tokens, "us_per_layer": round(us_dec, 2),
-                   "eager_us_per_layer": round(us_dec_eager, 2), "kernels": kd},
-        "configs": configs,
-        "timing": "us: graph-replayed HIP-event average after >= 0.2 s of settling replays (warm: "
-                  "operands in the caches from the previous call); us_cold: each call after a 512 MB "
-                  "read that flushes the 256 MB Infinity Cache",
-        "cpu": cpu_info() if not args.no_cpu else None,
     }
     if cpu is not None:
         line["cpu_baseline"] = cpu

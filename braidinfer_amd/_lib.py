@@ -38,6 +38,8 @@ _P = c_void_p
 _SIGNATURES = {
     "bfa_abi_version": (c_int, []),
     "bfa_last_error": (ctypes.c_char_p, []),
+    "bfa_set_tuning": (c_int, [c_int, c_int]),
+    "bfa_get_tuning": (c_int, [c_int]),
     "bfa_rms_norm": (c_int, [_P, _P, _P, c_int, c_int, c_int64, c_int64, c_int64,
                              c_int64, c_int64, c_int64, c_int64, c_float, _P]),
     "bfa_add_rms_norm": (c_int, [_P, _P, _P, _P, _P, c_int, c_int, c_int64, c_int64,
@@ -165,9 +167,29 @@ def raise_error(rc: int) -> None:
 
 def workspace_size(name: str, *args) -> int:
     """`<name>(*args)` of a workspace-size entry point (not memoised: the plan
-    it reflects also follows the BFA_* measurement overrides of the process
-    environment)."""
+    it reflects also follows the planner overrides, see set_tuning)."""
     return getattr(load(), name)(*args)
+
+
+# Planner overrides (BFA_TUNE_* of include/braidinfer_amd.h).  The library reads
+# each from its environment variable (BFA_<NAME>) once, when it is loaded;
+# set_tuning changes it afterwards.  For measurements and tests only.
+TUNING_KEYS = {
+    "DECODE_KS": 0, "DECODE_WG": 1, "DECODE_SPLITS": 2, "QKV_TILE": 3, "EDT_RT": 4,
+    "DECODE_PAIR": 5, "NO_OPERAND_FOLD": 6, "CASCADE_DECODE_WG": 7, "CASCADE_FLAT": 8,
+    "CASCADE_FLAT_WG": 9, "STREAM_STORES": 10,
+}
+
+
+def set_tuning(name: str, value: int | None) -> None:
+    """Sets planner override `name` (a TUNING_KEYS key); None or -1 unsets it."""
+    call("bfa_set_tuning", TUNING_KEYS[name], -1 if value is None else int(value))
+
+
+def get_tuning(name: str) -> int | None:
+    """Current value of planner override `name`, None when unset."""
+    v = load().bfa_get_tuning(TUNING_KEYS[name])
+    return None if v < 0 else v
 
 
 _workspaces: dict = {}
@@ -191,6 +213,24 @@ def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
                           device=device)
         _workspaces[key] = buf
     return buf
+
+
+def clear_workspaces(device: torch.device | int | None = None) -> int:
+    """Releases the reused scratch buffers of workspace() (all devices, or one)
+    back to torch's caching allocator and returns the bytes released.  A buffer
+    grows to the largest call made on its stream and is otherwise kept for the
+    life of the process; call this after a one-off large call (an 8192-token
+    cascade prefill, say) to give that memory back.  Safe while kernels that use
+    a buffer are still queued: each buffer was allocated on the stream it serves,
+    so the allocator reuses its memory only in that stream's order."""
+    idx = None
+    if device is not None:
+        idx = device if isinstance(device, int) else (
+            device.index if device.index is not None else torch.cuda.current_device())
+    freed = 0
+    for key in [k for k in _workspaces if idx is None or k[0] == idx]:
+        freed += _workspaces.pop(key).numel()
+    return freed
 
 
 def dtype_code(t: torch.Tensor | torch.dtype) -> int:

@@ -126,14 +126,12 @@ __device__ __forceinline__ void store8(void* p, const float (&v)[8]) {
 // the weight rotating over four copies, as consecutive layers would.  Smaller
 // outputs (decode batches) keep plain stores, so their consumers find them
 // cached.
-// BFA_STREAM_STORES=0 keeps every store plain (measurement override).
+// Planner override BFA_TUNE_STREAM_STORES = 0 keeps every store plain (for
+// measurements).
+int tuning(int key);  // capi.hip
 constexpr int64_t kStreamOutputBytes = int64_t(64) << 20;
 inline bool stream_output(int64_t bytes) {
-  static const bool off = [] {
-    const char* v = getenv("BFA_STREAM_STORES");
-    return v != nullptr && atoi(v) == 0;
-  }();
-  return !off && bytes >= kStreamOutputBytes;
+  return tuning(BFA_TUNE_STREAM_STORES) != 0 && bytes >= kStreamOutputBytes;
 }
 
 // Streaming forms: 16-byte loads with the nontemporal hint, for operands that
@@ -226,7 +224,12 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 // Asynchronous 16-byte-per-lane copy global -> LDS (global_load_lds_dwordx4):
 // lane i's 16 bytes at base + voff land at LDS byte m0 + 16*i.  Issued as
 // inline assembly so the compiler does not serialise consecutive copies; the
-// caller waits (wait_vmem) and barriers before the LDS is read.
+// caller waits (wait_vmem) and barriers before the LDS is read.  m0 is a
+// register the compiler reserves and assumes unchanged across an asm statement
+// (listing it as clobbered has no effect), so the statement saves it and puts
+// it back after the copy is issued (the copy reads m0 at issue).  The s_nop is
+// the one wait state the ISA requires between an SALU write of m0 and a global
+// load with the LDS bit.
 __device__ __forceinline__ void dma16(const void* base, uint32_t voff, uint32_t m0) {
   // the base is wave-uniform; readfirstlane lets the compiler see that when the
   // pointer came through a path it cannot prove uniform (an SGPR operand).  The
@@ -236,19 +239,24 @@ __device__ __forceinline__ void dma16(const void* base, uint32_t voff, uint32_t 
   const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(b)));
   const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(b >> 32)));
   const uint64_t bu = (static_cast<uint64_t>(hi) << 32) | lo;
-  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(__builtin_amdgcn_readfirstlane(m0)),
-               "v"(voff), "s"(reinterpret_cast<const void*>(bu))
+  uint32_t saved;
+  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %2, %3\n\ts_mov_b32 m0, %0"
+               : "=&s"(saved)
+               : "s"(__builtin_amdgcn_readfirstlane(m0)), "v"(voff), "s"(reinterpret_cast<const void*>(bu))
                : "memory");
 }
 
-// 4-byte form of dma16: lane i's dword at base + voff goes to LDS m0 + 4 i.
+// 4-byte form of dma16: lane i's dword at base + voff goes to LDS m0 + 4 i
+// (m0 saved and restored, and the wait state, as there).
 __device__ __forceinline__ void dma4(const void* base, uint32_t voff, uint32_t m0) {
   const uint64_t b = reinterpret_cast<uint64_t>(base);
   const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(b)));
   const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(b >> 32)));
   const uint64_t bu = (static_cast<uint64_t>(hi) << 32) | lo;
-  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, %2" ::"s"(__builtin_amdgcn_readfirstlane(m0)),
-               "v"(voff), "s"(reinterpret_cast<const void*>(bu))
+  uint32_t saved;
+  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %2, %3\n\ts_mov_b32 m0, %0"
+               : "=&s"(saved)
+               : "s"(__builtin_amdgcn_readfirstlane(m0)), "v"(voff), "s"(reinterpret_cast<const void*>(bu))
                : "memory");
 }
 

@@ -17,6 +17,9 @@ int set_error(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3
 // Checks hipGetLastError() after a launch; BFA_OK or BFA_ERR_LAUNCH.
 int check_launch(const char* what);
 
+// Current value of planner override `key` (BFA_TUNE_*), -1 when unset.
+int tuning(int key);
+
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }

@@ -1205,7 +1205,7 @@ static DecodeSplit decode_split(int64_t hkv, int64_t num_entries, int64_t page_s
   d.nsb = cdiv(page_size, 16);
   d.items = num_entries * d.nsb;
   int64_t target = 512;
-  if (const char* v = getenv("BFA_CASCADE_DECODE_WG")) target = std::max(1, atoi(v));  // measurement override
+  if (tuning(BFA_TUNE_CASCADE_DECODE_WG) >= 1) target = tuning(BFA_TUNE_CASCADE_DECODE_WG);  // planner override
   const int64_t want = std::max<int64_t>(1, std::min<int64_t>(d.items, cdiv(target, hkv)));
   d.per_split = std::max<int64_t>(1, cdiv(d.items, want));
   d.splits = d.items > 0 ? cdiv(d.items, d.per_split) : 1;
@@ -1249,7 +1249,7 @@ static void launch_merge(const CasArgs& a, int64_t rows, int64_t splits, hipStre
 }
 
 // The flat form, from more than CAS_FLAT_ROWS query rows per kv head (or as
-// BFA_CASCADE_FLAT = 0 / 1 forces, for measurements).  At Qwen3 shape over 4096
+// override BFA_TUNE_CASCADE_FLAT = 0 / 1 forces, for measurements).  At Qwen3 shape over 4096
 // keys it is slower than the fused kernel up to 64 rows (26.3 against 25.3 us)
 // and faster from 128 (28.5 against 32.7; 42.3 against 79.4 at 512 rows).
 // Workspace after the split partials: K and V^T copies of the attended keys and
@@ -1258,7 +1258,8 @@ constexpr int64_t CAS_FLAT_ROWS = 96;
 
 static bool flat_form(int64_t rows, int64_t num_entries) {
   if (num_entries <= 0) return false;
-  if (const char* v = getenv("BFA_CASCADE_FLAT")) return atoi(v) != 0 && rows > 4;
+  const int forced = tuning(BFA_TUNE_CASCADE_FLAT);  // planner override
+  if (forced >= 0) return forced != 0 && rows > 4;
   return rows > CAS_FLAT_ROWS;
 }
 
@@ -1277,11 +1278,11 @@ static FlatPlan flat_plan(int64_t rows, int64_t hkv, int64_t num_entries, int64_
   // Split the keys until about 512 workgroups run (two per CU), or four per
   // 64-row block up to 1024 when there are many blocks: Qwen3 over 4096 keys,
   // 256 queries run best at 8 splits (43 us against 51 at 4 and 52 at 16),
-  // 1024 queries at 4 (98 against 126 unsplit).  BFA_CASCADE_FLAT_WG sets the
-  // workgroup target instead, for measurements.
+  // 1024 queries at 4 (98 against 126 unsplit).  Override
+  // BFA_TUNE_CASCADE_FLAT_WG sets the workgroup target instead.
   const int64_t blocks = cdiv(rows, 64) * hkv;
   int64_t target = std::min<int64_t>(std::max<int64_t>(512, 4 * blocks), 1024);
-  if (const char* v = getenv("BFA_CASCADE_FLAT_WG")) target = std::max(1, atoi(v));
+  if (tuning(BFA_TUNE_CASCADE_FLAT_WG) >= 1) target = tuning(BFA_TUNE_CASCADE_FLAT_WG);
   int64_t zs = std::min<int64_t>(cdiv(target, blocks), fp.tiles);
   zs = std::max<int64_t>(1, zs);
   fp.tiles_per_split = std::max<int64_t>(1, cdiv(fp.tiles, zs));

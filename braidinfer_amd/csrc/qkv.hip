@@ -2315,9 +2315,9 @@ static QkvPlan make_plan(int64_t m, int64_t n, int64_t k, int64_t hd) {
       int ks = 1;
       for (int c = 8; c >= 1; --c)
         if (segs % c == 0 && ntile * (segs / c) >= 256) { ks = c; break; }
-      // BFA_DECODE_KS (1..8, dividing k / 64) overrides the depth for measurements
-      if (const char* v = getenv("BFA_DECODE_KS")) {
-        const int c = atoi(v);
+      // planner override BFA_TUNE_DECODE_KS (1..8, dividing k / 64) sets the depth
+      {
+        const int c = tuning(BFA_TUNE_DECODE_KS);
         if (c >= 1 && c <= 8 && segs % c == 0) ks = c;
       }
       p.ks = ks;
@@ -2326,18 +2326,18 @@ static QkvPlan make_plan(int64_t m, int64_t n, int64_t k, int64_t hd) {
       p.cpw = 2;
       // From two token blocks up the partial tiles cost more than the extra
       // workgroups gain: the deep-K form takes the fewest splits of 256-deep
-      // chunks that still give BFA_DECODE_WG (default 192) workgroups, with at
-      // least two chunks per split.  BFA_DECODE_SPLITS (dividing the chunk
-      // count) overrides the split count for measurements.
+      // chunks that still give 192 workgroups (override BFA_TUNE_DECODE_WG),
+      // with at least two chunks per split.  Override BFA_TUNE_DECODE_SPLITS
+      // (dividing the chunk count) sets the split count.
       const int64_t chunks = segs / LOOP_KS;
       if (p.mt > 1 && segs % LOOP_KS == 0 && chunks >= 2) {
         int64_t target = 192;
-        if (const char* v = getenv("BFA_DECODE_WG")) target = std::max(1, atoi(v));
+        if (tuning(BFA_TUNE_DECODE_WG) >= 1) target = tuning(BFA_TUNE_DECODE_WG);
         int64_t sp = chunks;
         for (int64_t c = 1; c <= chunks; ++c)
           if (chunks % c == 0 && ntile * c >= target) { sp = c; break; }
-        if (const char* v = getenv("BFA_DECODE_SPLITS")) {
-          const int64_t c = atoi(v);
+        {
+          const int64_t c = tuning(BFA_TUNE_DECODE_SPLITS);
           if (c >= 1 && chunks % c == 0) sp = c;
         }
         if (chunks / sp >= 2) {
@@ -2370,13 +2370,13 @@ static QkvPlan make_plan(int64_t m, int64_t n, int64_t k, int64_t hd) {
     // Largest tile that still fills the CUs: 256x256 with 8 waves (two per
     // SIMD, full-line 64-deep DMA stages) from one tile per CU; else 128x256
     // with 8 waves from 192 tiles; else 128x128 with 4 waves (two workgroups
-    // per CU).  BFA_QKV_TILE (2: 256x256 8 waves, 3: 128x256 8 waves, 1:
-    // 128x256 4 waves, 128: 128x128) overrides the choice for measurements.
+    // per CU).  Override BFA_TUNE_QKV_TILE (2: 256x256 8 waves, 3: 128x256 8
+    // waves, 1: 128x256 4 waves, 128: 128x128) sets the tile.
     if (cdiv(m, 256) * cdiv(n, 256) >= 256) p.tile = 2;
     else if (cdiv(m, 128) * cdiv(n, 256) >= 192) p.tile = 3;
     else p.tile = 128;
-    if (const char* t = getenv("BFA_QKV_TILE")) {
-      const int v = atoi(t);
+    {
+      const int v = tuning(BFA_TUNE_QKV_TILE);
       if ((v >= 1 && v <= 3) || v == 128) p.tile = v;
     }
     p.splits = 1;
@@ -2476,8 +2476,7 @@ static void launch_decode(const QkvPlan& p, const SplitArgs& s, hipStream_t st,
 // Epilogue dtype form for a launch: the fixed forms cover bf16 operands on the
 // DMA path; every other case keeps the run-time dtypes.
 static bool edt_forced_rt() {
-  const char* v = getenv("BFA_EDT_RT");  // measurement override: run-time dtypes only
-  return v && atoi(v) != 0;
+  return tuning(BFA_TUNE_EDT_RT) > 0;  // planner override: run-time dtypes only
 }
 
 static int fused_edt(const QkvEpi& e) {
@@ -2605,8 +2604,8 @@ static void launch_prefill(const QkvPlan& p, const GemmArgs& g, const QkvEpi& e,
 // Whole-K column-pair decode kernel (qkv_decode_pair_kernel): 17-64 tokens,
 // bf16 operand and weight, head_dim a multiple of 32, no q/k norm, K a multiple
 // of 256, and at least 128 column tiles, so that the weight stream still covers
-// most CUs.  BFA_DECODE_PAIR=0 keeps the
-// split-K kernels, =1 drops the tile minimum (measurements and tests).
+// most CUs.  Override BFA_TUNE_DECODE_PAIR = 0 keeps the split-K kernels, = 1
+// drops the tile minimum (measurements and tests).
 static bool pair_ok(const QkvPlan& p, int64_t n, int64_t hd, int64_t k, bool qk_norm, bool bf16,
                     int64_t lda, const void* operand, int64_t m, int64_t ldw) {
   if (!p.decode || !p.stream || p.mt < 2 || !bf16 || qk_norm) return false;
@@ -2615,8 +2614,7 @@ static bool pair_ok(const QkvPlan& p, int64_t n, int64_t hd, int64_t k, bool qk_
   if (lda % 8 != 0 || !aligned16(operand) || m * lda * 2 >= (int64_t(1) << 32) ||
       n * ldw * 2 >= (int64_t(1) << 32))
     return false;
-  int mode = -1;
-  if (const char* v = getenv("BFA_DECODE_PAIR")) mode = atoi(v);
+  const int mode = tuning(BFA_TUNE_DECODE_PAIR);
   if (mode == 0) return false;
   return mode == 1 || n / 32 >= 128;
 }
@@ -2853,9 +2851,8 @@ static int fused_impl(const void* x, int x_dtype, int64_t tokens, int64_t hidden
   // row per wave up to 4 tokens (hidden <= 4096), two up to 8 (hidden <= 2048),
   // four up to 16 (hidden <= 1024); beyond that the reads of the rows cost more
   // than the launch (TinyLlama, 16 tokens: 11.2 against 10.1 us with the
-  // pre-pass).  BFA_NO_OPERAND_FOLD=1 keeps the pre-pass (for measurements).
-  const char* nf = getenv("BFA_NO_OPERAND_FOLD");
-  const bool no_fold = nf && atoi(nf) != 0;
+  // pre-pass).  Override BFA_TUNE_NO_OPERAND_FOLD > 0 keeps the pre-pass.
+  const bool no_fold = tuning(BFA_TUNE_NO_OPERAND_FOLD) > 0;
   const int fold_rows = (tokens <= 4 && hidden <= 4096) ? 1
                         : (tokens <= 8 && hidden <= 2048) ? 2
                         : (tokens <= 16 && hidden <= 1024) ? 4 : 0;

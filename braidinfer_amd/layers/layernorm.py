@@ -84,7 +84,8 @@ class RMSNorm(nn.Module):
 
     def add_rms_forward(self, x: torch.Tensor, residual: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
         # common case first: 16-bit x and residual of one contiguous shape on one device
-        if (x.dtype != torch.float32 and x.is_cuda and x.is_contiguous() and residual.is_contiguous()
+        if ((x.dtype == torch.bfloat16 or x.dtype == torch.float16) and x.is_cuda and x.is_contiguous()
+                and residual.is_contiguous()
                 and residual.shape == x.shape and residual.dtype == x.dtype and residual.device == x.device):
             weight = self.weight
             if weight.is_cuda and weight.is_contiguous() and weight.device == x.device:

@@ -48,6 +48,35 @@ extern "C" {
 int bfa_abi_version(void);
 const char* bfa_last_error(void);
 
+/* ------------------------------------------------------ planner overrides --
+ * No counterpart in the reference (its Triton launchers have fixed grids).
+ * The kernel planners pick a kernel form and a grid from the shapes alone; the
+ * keys below override one choice each, for measurements and for tests that
+ * reach a form the planner would not pick at that shape.  A serving process
+ * leaves them unset.  Each key starts from the environment variable named
+ * beside it, read ONCE when the library is loaded (an integer; absent = unset);
+ * afterwards only bfa_set_tuning changes it, so no entry point reads the
+ * environment on a call.  value -1 = unset (the planner's own choice).
+ * bfa_set_tuning returns BFA_OK, or BFA_ERR_INVALID for an unknown key;
+ * bfa_get_tuning returns the value, -1 when unset or the key is unknown.
+ * The table is process-wide and not synchronised: set it between calls. */
+#define BFA_TUNE_DECODE_KS 0         /* BFA_DECODE_KS: 64-deep K segments per decode split (1..8) */
+#define BFA_TUNE_DECODE_WG 1         /* BFA_DECODE_WG: workgroup target of the deep-K decode form */
+#define BFA_TUNE_DECODE_SPLITS 2     /* BFA_DECODE_SPLITS: split count of the deep-K decode form */
+#define BFA_TUNE_QKV_TILE 3          /* BFA_QKV_TILE: prefill tile, 1 2 3 or 128 */
+#define BFA_TUNE_EDT_RT 4            /* BFA_EDT_RT: non-zero = run-time epilogue dtypes only */
+#define BFA_TUNE_DECODE_PAIR 5       /* BFA_DECODE_PAIR: 0 = never the column-pair decode
+                                        kernel, 1 = at any shape it supports */
+#define BFA_TUNE_NO_OPERAND_FOLD 6   /* BFA_NO_OPERAND_FOLD: non-zero = keep the decode pre-pass */
+#define BFA_TUNE_CASCADE_DECODE_WG 7 /* BFA_CASCADE_DECODE_WG: cascade decode workgroup target */
+#define BFA_TUNE_CASCADE_FLAT 8      /* BFA_CASCADE_FLAT: 0 = fused cascade kernel, non-zero =
+                                        flat form from 5 query rows */
+#define BFA_TUNE_CASCADE_FLAT_WG 9   /* BFA_CASCADE_FLAT_WG: flat-form workgroup target */
+#define BFA_TUNE_STREAM_STORES 10    /* BFA_STREAM_STORES: 0 = no nontemporal stores */
+#define BFA_TUNE_COUNT 11
+int bfa_set_tuning(int key, int value);
+int bfa_get_tuning(int key);
+
 /* ------------------------------------------------------------------ norms --
  * Row geometry shared by the norm entry points: `rows` rows of `hidden`
  * contiguous elements; row r lives at  (r / rows_inner) * stride_outer

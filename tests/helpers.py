@@ -10,6 +10,15 @@ ATOL = 2e-2
 RTOL = 1e-2
 
 
+# Every use of a documented rounding allowance, for the session summary that
+# tests/conftest.py prints: (what, elements beyond the strict bound, elements).
+ALLOWANCE_LOG: list = []
+
+
+def record_allowance(what: str, used: int, numel: int) -> None:
+    ALLOWANCE_LOG.append((what, int(used), int(numel)))
+
+
 def gen(seed: int) -> torch.Generator:
     return torch.Generator().manual_seed(seed)
 
@@ -36,6 +45,7 @@ def assert_close(actual: torch.Tensor, expected: torch.Tensor, atol=ATOL, rtol=R
         strict = bound[fin]
         bound = bound + slack.detach().float().cpu().reshape(e.shape)
         used = int((diff > strict).sum())
+        record_allowance(what, used, diff.numel())
         assert used <= max_slack_frac * diff.numel(), (
             f"{what}: {used}/{diff.numel()} elements need the rounding allowance (> {max_slack_frac:g})")
     bound = bound[fin]

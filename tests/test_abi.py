@@ -53,7 +53,7 @@ def test_workspace_size_plan():
     assert ws == (300 * 512 * 2 + 255) // 256 * 256 + (300 * 800 * 4 + 255) // 256 * 256
 
 
-def test_cascade_workspace_size_plan(monkeypatch):
+def test_cascade_workspace_size_plan(tuning):
     """Cascade attention's workspace: split partials (m, l and 128 accumulators
     per row) for the decode form and the fused kernel; from 97 query rows per kv
     head also the flat form's K and V^T copies of the padded keys and their
@@ -70,7 +70,7 @@ def test_cascade_workspace_size_plan(monkeypatch):
     # 48 queries = 96 rows: the fused kernel, 2 x 8 row blocks split 32 ways, no copies
     assert _lib.call("bfa_cascade_attention_workspace_size", 48, hq, hkv, d, entries, ps) == part(32, 96)
     # forcing the fused kernel drops the copies (256 queries: 8 x 8 blocks, 8 splits)
-    monkeypatch.setenv("BFA_CASCADE_FLAT", "0")
+    tuning("CASCADE_FLAT", 0)
     assert _lib.call("bfa_cascade_attention_workspace_size", 256, hq, hkv, d, entries, ps) == part(8, 512)
     # no attended pages: nothing to copy or merge
     assert _lib.call("bfa_cascade_attention_workspace_size", 256, hq, hkv, d, 0, ps) == 0

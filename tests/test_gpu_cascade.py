@@ -10,7 +10,7 @@ bf16 for the P.V matrix product (a relative error of at most 2^-9 per weight).
 Three kernel forms serve a call: the decode form (up to 4 query rows per kv
 head), the fused kernel, and from 97 rows the flat form (K rotated and
 normalised once by a pre-pass, DMA'd tiles); the oracle cases run through the
-fused kernel and, forced by BFA_CASCADE_FLAT=1, through the flat form."""
+fused kernel and, forced by the CASCADE_FLAT planner override, through the flat form."""
 from __future__ import annotations
 
 import math
@@ -120,25 +120,25 @@ def test_cascade_attention(name, tokens, hq, hkv, lengths, deltas, causal, knorm
 
 @pytest.mark.parametrize("name,tokens,hq,hkv,lengths,deltas,causal,knorm",
                          [c for c in CASES if c[1] * c[2] // c[3] > 4])
-def test_cascade_attention_flat_form(monkeypatch, name, tokens, hq, hkv, lengths, deltas, causal, knorm):
+def test_cascade_attention_flat_form(tuning, name, tokens, hq, hkv, lengths, deltas, causal, knorm):
     """The same oracle cases through the flat form (K rotated / normalised once
     by a pre-pass, DMA'd tiles), which runs by itself only from 97 rows per kv
     head: forced here for every case above 4 rows."""
-    monkeypatch.setenv("BFA_CASCADE_FLAT", "1")
+    tuning("CASCADE_FLAT", 1)
     _check_case(name, tokens, hq, hkv, lengths, deltas, causal, knorm)
 
 
 @pytest.mark.parametrize("name,tokens,hq,hkv,lengths,deltas,causal,knorm", CASES_D64)
-def test_cascade_attention_head_dim_64(monkeypatch, name, tokens, hq, hkv, lengths, deltas, causal, knorm):
-    monkeypatch.setenv("BFA_CASCADE_FLAT", "0")  # the fused kernel (or the decode form) for every case
+def test_cascade_attention_head_dim_64(tuning, name, tokens, hq, hkv, lengths, deltas, causal, knorm):
+    tuning("CASCADE_FLAT", 0)  # the fused kernel (or the decode form) for every case
     _check_case(name, tokens, hq, hkv, lengths, deltas, causal, knorm, d=64, base=1e4)
 
 
 @pytest.mark.parametrize("name,tokens,hq,hkv,lengths,deltas,causal,knorm",
                          [c for c in CASES_D64 if c[1] * c[2] // c[3] > 4])
-def test_cascade_attention_head_dim_64_flat_form(monkeypatch, name, tokens, hq, hkv, lengths, deltas, causal,
+def test_cascade_attention_head_dim_64_flat_form(tuning, name, tokens, hq, hkv, lengths, deltas, causal,
                                                  knorm):
-    monkeypatch.setenv("BFA_CASCADE_FLAT", "1")
+    tuning("CASCADE_FLAT", 1)
     _check_case(name, tokens, hq, hkv, lengths, deltas, causal, knorm, d=64, base=1e4)
 
 
@@ -198,13 +198,13 @@ def test_cascade_decode_form_page_sizes(ps, tokens, dtype, d):
 
 
 @pytest.mark.parametrize("target", [8, 32, 64, 96, 256, 1024, 8192])
-def test_cascade_decode_split_merges(monkeypatch, target):
+def test_cascade_decode_split_merges(tuning, target):
     """The decode kernel's split count follows the workgroup target; every
     combination form is taken over about 3000 keys (about 190 pages) at 8 kv
     heads: one split (no merge), 4, 8 and 12 (a wave per row, sized for 4, 8
     and 16 splits), 32 (one round trip, 16 splits per wave), about 95 and
     about 190 (the looped merge)."""
-    monkeypatch.setenv("BFA_CASCADE_DECODE_WG", str(target))
+    tuning("CASCADE_DECODE_WG", target)
     g = gen(120 + target)
     hq, hkv, d, ps, max_pos = 32, 8, 128, 16, 40960
     chunks, kv, total = build_case(121, hq, hkv, [1500, 900, 601], [0, 2000, -700], pages=200, ps=ps, d=d)
@@ -222,10 +222,10 @@ def test_cascade_decode_split_merges(monkeypatch, target):
 
 
 @pytest.mark.parametrize("ps,dtype,d", [(8, torch.bfloat16, 128), (32, torch.float16, 128), (8, torch.float16, 64)])
-def test_cascade_flat_form_page_sizes(monkeypatch, ps, dtype, d):
+def test_cascade_flat_form_page_sizes(tuning, ps, dtype, d):
     """Flat form with pages of 8 (8 pages per 64-key tile) and 32 slots, a
     partial last page and moved chunks, Qwen3 geometry with k_norm."""
-    monkeypatch.setenv("BFA_CASCADE_FLAT", "1")
+    tuning("CASCADE_FLAT", 1)
     g = gen(95 + ps + d)
     hq, hkv, max_pos, tokens = 16, 8, 40960, 8
     chunks, kv, total = build_case(96 + ps, hq, hkv, [45, 130, 77], [0, 300, -41], pages=64, ps=ps, dtype=dtype,
@@ -248,8 +248,8 @@ def test_cascade_flat_form_page_sizes(monkeypatch, ps, dtype, d):
 
 
 @pytest.mark.parametrize("flat", ["0", "1"])
-def test_cascade_attention_fp16_query_before_keys_and_empty(monkeypatch, flat):
-    monkeypatch.setenv("BFA_CASCADE_FLAT", flat)
+def test_cascade_attention_fp16_query_before_keys_and_empty(tuning, flat):
+    tuning("CASCADE_FLAT", int(flat))
     g = gen(70)
     hq, hkv, d, ps = 16, 8, 128, 16
     chunks, kv, total = build_case(71, hq, hkv, [20, 40], [0, 3], pages=20, dtype=torch.float16)
@@ -283,10 +283,10 @@ def test_cascade_attention_delta_out_of_table_raises():
         braidinfer_amd.check_device_status()
 
 
-def test_cascade_flat_form_delta_out_of_table_raises(monkeypatch):
+def test_cascade_flat_form_delta_out_of_table_raises(tuning):
     """The flat form's pre-pass reports a delta outside the rotary table the
     same way."""
-    monkeypatch.setenv("BFA_CASCADE_FLAT", "1")
+    tuning("CASCADE_FLAT", 1)
     hq, hkv, d, ps = 16, 8, 128, 16
     chunks, kv, total = build_case(76, hq, hkv, [20, 40], [0, -5000], pages=20)
     rope = RotaryEmbedding(d, d, 4096, 1e6).to(DEV)
@@ -299,7 +299,7 @@ def test_cascade_flat_form_delta_out_of_table_raises(monkeypatch):
         braidinfer_amd.check_device_status()
 
 
-def test_cascade_flat_form_matches_fused_kernel(monkeypatch):
+def test_cascade_flat_form_matches_fused_kernel(tuning):
     """The flat form (pre-pass + DMA'd tiles) and the fused kernel agree on a
     256-query Qwen3 call with k_norm and moved chunks (the oracle check of both
     is in test_cascade_attention)."""
@@ -313,9 +313,9 @@ def test_cascade_flat_form_matches_fused_kernel(monkeypatch):
     qpos = torch.arange(total - 255, total + 1, device=DEV)
     k_norm = RMSNorm(d, eps=1e-6).to(DEV)
     kv = kv.to(DEV)
-    monkeypatch.setenv("BFA_CASCADE_FLAT", "1")
+    tuning("CASCADE_FLAT", 1)
     flat = att.forward(q, qpos, kv, levels, 0, k_norm=k_norm).clone()
-    monkeypatch.setenv("BFA_CASCADE_FLAT", "0")
+    tuning("CASCADE_FLAT", 0)
     fused = att.forward(q, qpos, kv, levels, 0, k_norm=k_norm)
     torch.cuda.synchronize()
     braidinfer_amd.check_device_status()

@@ -8,7 +8,7 @@ kernels/fused_rmsnorm_qkv_production.py, kernels/kv_cache_utils.py:9-78).
 
 The library takes this kernel by itself from 128 column tiles up (Llama-3-8B at
 64 tokens, test_gpu_qkv.py's llama chain and scale-after cases); here
-BFA_DECODE_PAIR=1 forces it on smaller shapes, so that every token-block count
+The DECODE_PAIR planner override forces it on smaller shapes, so that every token-block count
 (2-4), head_dim 64 and 128, bias, RoPE with in- and out-of-range positions, the
 bf16 variants (operand from the pre-pass) and the fp32 ones (scale-after) and
 the fused KV append each run it.  Tolerance as the other QKV tests
@@ -33,8 +33,8 @@ DEV = "cuda"
 
 
 @pytest.fixture(autouse=True)
-def force_pair(monkeypatch):
-    monkeypatch.setenv("BFA_DECODE_PAIR", "1")
+def force_pair(tuning):
+    tuning("DECODE_PAIR", 1)
 
 
 def make(seed, t, h, hq, hkv, d):

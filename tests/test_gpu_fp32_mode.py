@@ -6,12 +6,19 @@ The accuracy target is stated against that fp32 reference: |d| <= 2e-2 +
 The reference's own rounding points already move some results away from it:
 for the Qwen3 k heads after k_norm weights up to 100 (values near 100, where a
 bf16 ulp is 0.5) the reference itself leaves about 4 % of elements outside
-that bound.  So every case asserts that the GPU path is no further from the
-fp32 reference than the reference's rounding is -- at most 1e-4 of the
-elements more outside the bound, and a normwise relative error below 5e-3
-(half the relative bound) or within 1.5x of the reference's own where that is
-larger -- so the cases where the reference itself is within the bound assert
-the bound outright (up to that 1e-4 fraction).  The fp32 variants (minimal_f32,
+that bound.  So every case asserts:
+
+* where the reference's rounding keeps every element inside the bound (the
+  norms, SiLU*mul, the Llama chains, the v heads, the linear fusions), the GPU
+  path keeps every element inside it too -- the north-star bound, outright;
+* elsewhere (the Qwen3 q/k heads after the extreme k_norm weights), that the
+  GPU path is no further from the fp32 reference than the reference's rounding
+  is: at most 1e-4 of the elements more outside the bound (the count is
+  recorded as a rounding allowance in the session summary);
+* in both cases a normwise relative error below 5e-3 (half the relative bound)
+  or within 1.5x of the reference's own where that is larger.
+
+The fp32 variants (minimal_f32,
 with_bias) round their operand to bf16 for the matrix cores where the
 reference's fp32 dot product runs at TF32 on its GPUs; their normwise error
 (about 2e-3) comes from that and stays inside the bound.
@@ -28,7 +35,7 @@ from braidinfer_amd.layers import RMSNorm, SiluAndMul, llama_attention_input, qw
 from braidinfer_amd.layers.linear import gate_up_silu_and_mul, linear_add_residual
 from oracle import fp32_ref as F
 from oracle import torch_ref as R
-from tests.helpers import ATOL, RTOL, gen, randn
+from tests.helpers import ATOL, RTOL, gen, randn, record_allowance
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -49,7 +56,11 @@ def check_vs_fp32(gpu, ref_mode, fp32_mode, what):
     print(f"{what}: vs fp32 mode max_abs {g_abs:.3e} normwise {g_nw:.3e} outside {g_out}/{n}; "
           f"reference rounding: max_abs {r_abs:.3e} normwise {r_nw:.3e} outside {r_out}", flush=True)
     assert torch.isfinite(gpu).all(), f"{what}: non-finite output"
-    assert g_out <= r_out + slack, f"{what}: {g_out} elements outside the bound (reference {r_out})"
+    if r_out == 0:
+        assert g_out == 0, f"{what}: {g_out} elements outside the bound where the reference has none"
+    else:
+        record_allowance(f"{what} (vs fp32; reference itself {r_out} outside)", max(0, g_out - r_out), n)
+        assert g_out <= r_out + slack, f"{what}: {g_out} elements outside the bound (reference {r_out})"
     assert g_nw <= max(1.5 * r_nw, 5e-3) + 1e-4, f"{what}: normwise {g_nw:.3e} against the reference's {r_nw:.3e}"
 
 

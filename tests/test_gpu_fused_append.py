@@ -113,8 +113,8 @@ def test_fused_append_every_epilogue(model, tokens):
 
 
 @pytest.mark.parametrize("tile", ["2", "3", "1", "128"])
-def test_fused_append_tile_forms(monkeypatch, tile):
-    monkeypatch.setenv("BFA_QKV_TILE", tile)
+def test_fused_append_tile_forms(tuning, tile):
+    tuning("QKV_TILE", int(tile))
     c = make_case(50 + int(tile), 300, **LLAMA)
     check(c, f"tile {tile}")
     c = make_case(60 + int(tile), 300, **QWEN)

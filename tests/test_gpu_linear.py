@@ -76,11 +76,11 @@ def test_linear_add_residual(shape):
 
 
 @pytest.mark.parametrize("splits,t", [("4", 64), ("1", 48), ("2", 20), ("3", 33)])
-def test_deep_k_chunk_counts(monkeypatch, splits, t):
+def test_deep_k_chunk_counts(tuning, splits, t):
     """The deep-K decode form with the split count forced (K = 3072: 12 chunks of
     256): 3, 12, 6 and 4 chunks per split, two to four 16-token blocks, against
     the oracle."""
-    monkeypatch.setenv("BFA_DECODE_SPLITS", splits)
+    tuning("DECODE_SPLITS", int(splits))
     g = gen(900 + t)
     k, n = 3072, 2048
     x, w, b = randn(g, t, k), randn(g, n, k, std=0.03), randn(g, n, std=0.5)
@@ -107,6 +107,30 @@ def test_gate_up_silu_and_mul(shape):
     with torch.no_grad():
         layer.weight.copy_(w.to(DEV))
     assert torch.equal(layer.forward_silu_and_mul(x.to(DEV)), got)
+
+
+def test_gate_up_silu_and_mul_8192_tokens_sampled_rows():
+    """Llama-3-8B gate_up_proj + SiluAndMul at the 8192-token prefill (4096 ->
+    2 x 14336, 256x256 tiles over the full grid): the rows of a GEMM are
+    independent, so 128 rows sampled across the whole range (both ends, every
+    row tile's neighbourhood) are checked against the oracle, with the same
+    one-ulp flip allowance as above, and against the fp32 mode of the oracle."""
+    from oracle import fp32_ref as F
+    g = gen(8192)
+    t, k, inter = 8192, 4096, 14336
+    x = randn(g, t, k)
+    w = randn(g, 2 * inter, k, std=0.02)
+    got = gate_up_silu_and_mul(x.to(DEV), w.to(DEV))
+    rows = torch.cat([torch.tensor([0, 1, 255, 256, t - 2, t - 1]),
+                      torch.randperm(t, generator=g)[:122]]).sort().values
+    sub = got[rows.to(DEV)].cpu()
+    exp = R.gate_up_silu_and_mul(x[rows], w)
+    assert_close(sub, exp, what="gate_up silu t=8192 (128 sampled rows)", slack=2.0 ** -6 * exp.float().abs(),
+                 max_slack_frac=1e-4)
+    f32 = F.gate_up_silu_and_mul(x[rows], w)
+    d = (sub.float() - f32.float()).abs()
+    assert ((d - (2e-2 + 1e-2 * f32.float().abs())) > 0).sum().item() <= 1e-4 * d.numel()
+    assert (d.norm() / f32.float().norm()).item() < 5e-3
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])

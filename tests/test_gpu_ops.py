@@ -107,6 +107,15 @@ def test_add_rms_forward_fp32_aliases():
     assert_close(a, ry, atol=1e-5, rtol=1e-5)
 
 
+def test_add_rms_forward_unsupported_dtype_raises_type_error():
+    """float64 (which no kernel takes) raises the library's dtype error, not a
+    bare KeyError from the 16-bit fast path."""
+    norm = RMSNorm(64).to(DEV)
+    x = torch.randn(4, 64, dtype=torch.float64, device=DEV)
+    with pytest.raises(TypeError, match="unsupported dtype"):
+        norm(x, torch.randn_like(x))
+
+
 def test_rmsnorm_f32_reference_tests():
     """The checks of tests/test_rmsnorm_f32.py, run on the HIP kernel."""
     g = gen(106)

@@ -810,6 +810,99 @@ def test_fp32_mode_closed_forms():
                                rtol=1e-6, atol=1e-6)
 
 
+def test_fp32_mode_linear_closed_forms():
+    """fp32_ref.linear / gate_up_silu_and_mul pinned without restating them:
+    integer-valued operands make every product and sum exact in fp32 and in
+    float64, so a brute-force triple loop in float64 fixes the result bit for
+    bit; identity and selection weights fix the operand order (W is [N, K])."""
+    from oracle import fp32_ref as F
+    g = gen(44)
+    t, k, n = 3, 5, 4
+    xi = torch.randint(-4, 5, (t, k), generator=g).to(torch.bfloat16)
+    wi = torch.randint(-3, 4, (n, k), generator=g).to(torch.bfloat16)
+    bi = torch.randint(-8, 9, (n,), generator=g).to(torch.bfloat16)
+    ri = torch.randint(-8, 9, (t, n), generator=g).to(torch.bfloat16)
+    brute = torch.zeros(t, n, dtype=torch.float64)
+    for i in range(t):
+        for j in range(n):
+            acc = 0.0
+            for c in range(k):
+                acc += float(xi[i, c]) * float(wi[j, c])
+            brute[i, j] = acc
+    assert torch.equal(F.linear(xi, wi), brute.to(torch.bfloat16))
+    assert torch.equal(F.linear(xi, wi, bi), (brute + bi.double()).to(torch.bfloat16))
+    assert torch.equal(F.linear(xi, wi, bi, residual=ri), (brute + bi.double() + ri.double()).to(torch.bfloat16))
+    # one rounding: x + b with both bf16 is formed in fp32 and rounded once
+    x, b = randn(g, 6, 16), randn(g, 16)
+    eye = torch.eye(16, dtype=torch.bfloat16)
+    assert torch.equal(F.linear(x, eye), x)
+    assert torch.equal(F.linear(x, eye, b), (x.float() + b.float()).bfloat16())
+    # a selection weight picks input columns in its row order
+    sel = eye[[3, 0, 7]]
+    assert torch.equal(F.linear(x, sel), x[:, [3, 0, 7]])
+    # gate_up: [gate rows; up rows].  W = [I; I]: silu(x) * x in fp32, one rounding
+    xs = randn(g, 4, 16)
+    xf = xs.double()
+    want = (xf * torch.sigmoid(xf) * xf).to(torch.bfloat16)
+    got = F.gate_up_silu_and_mul(xs, torch.cat([eye, eye]))
+    assert (got.float() - want.float()).abs().le(want.float().abs() * 2.0 ** -8 + 1e-30).all()
+    zero = torch.zeros_like(eye)
+    assert F.gate_up_silu_and_mul(xs, torch.cat([eye, zero])).eq(0).all()  # up = 0
+    assert F.gate_up_silu_and_mul(xs, torch.cat([zero, eye])).eq(0).all()  # silu(0) = 0
+    # the gate is the first half: a large gate leaves silu(g) * u = g * u; with
+    # the halves swapped the result is silu(u) * g, not the same
+    big = torch.full((4, 16), 40.0, dtype=torch.bfloat16)
+    gate_sel = torch.cat([eye, zero], 1)  # picks the first 16 of 32 input columns
+    up_sel = torch.cat([zero, eye], 1)
+    xin = torch.cat([big, xs], 1)
+    y = F.gate_up_silu_and_mul(xin, torch.cat([gate_sel, up_sel]))
+    assert torch.equal(y, (big.float() * xs.float()).bfloat16())
+    y_swapped = F.gate_up_silu_and_mul(xin, torch.cat([up_sel, gate_sel]))
+    assert not torch.equal(y_swapped, y)
+
+
+def test_planted_fp32_linear_mistakes_are_caught():
+    """Copies of fp32_ref.linear / gate_up_silu_and_mul with a planted mistake
+    (transposed weight, bias dropped, halves swapped, silu on the up half, a
+    bf16 rounding of the projection) fail the closed forms above."""
+    g = gen(45)
+    x = randn(g, 4, 16)
+    eye = torch.eye(16, dtype=torch.bfloat16)
+    sel = eye[[3, 0, 7]]
+    b = randn(g, 16)
+
+    def transposed(x, w):
+        return (x.float() @ w.float()).bfloat16()
+    with pytest.raises(RuntimeError):  # [4, 16] @ [3, 16] does not even compose
+        transposed(x, sel)
+    perm = torch.randperm(16, generator=g)
+    assert not torch.equal(transposed(x, eye[perm]), x[:, perm])
+
+    def no_bias(x, w, bias=None):
+        return (x.float() @ w.float().t()).bfloat16()
+    assert not torch.equal(no_bias(x, eye, b), (x.float() + b.float()).bfloat16())
+
+    def two_roundings(x, w, bias):
+        return ((x.float() @ w.float().t()).bfloat16().float() + bias.float()).bfloat16()
+    # W = I + shift: out_j = x_j + x_(j+1), not representable in bf16 in general
+    xr, br = randn(g, 64, 16), randn(g, 16, std=0.01)
+    w2 = eye + eye.roll(1, 1)
+    once = (xr.double() + xr.double().roll(-1, 1) + br.double()).to(torch.bfloat16)
+    from oracle import fp32_ref as F
+    assert torch.equal(F.linear(xr, w2, br), once)
+    assert not torch.equal(two_roundings(xr, w2, br), once)
+
+    def silu_on_up(x, w):
+        gu = x.float() @ w.float().t()
+        gg, u = gu.chunk(2, -1)
+        return (gg * u * torch.sigmoid(u)).bfloat16()
+    zero = torch.zeros_like(eye)
+    big = torch.full((4, 16), 40.0, dtype=torch.bfloat16)
+    xin = torch.cat([big, x], 1)
+    w = torch.cat([torch.cat([eye, zero], 1), torch.cat([zero, eye], 1)])
+    assert not torch.equal(silu_on_up(xin, w), (big.float() * x.float()).bfloat16())
+
+
 def test_fp32_mode_chains_match_the_pinned_fp32_pieces():
     """The attention-input chains of fp32_ref equal their pieces composed from
     the ref-rounding oracle's fp32 forms: rotary_forward on fp32 q/k (it rounds
