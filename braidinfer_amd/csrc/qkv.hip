@@ -431,11 +431,16 @@ __device__ __forceinline__ void tile_store(uint4* buf, int gr, int gg, const uin
 // inside groups of 8 row-tiles so that concurrently resident workgroups on one
 // XCD share operand rows and weight columns in its L2.  n0 is in output columns.
 template <int EPI, int BM, int BN>
-__device__ __forceinline__ void tile_origin(const GemmArgs& g, int64_t& m0, int64_t& n0) {
+__device__ __forceinline__ int64_t tile_count(const GemmArgs& g) {
+  return cdiv(g.m, BM) * cdiv(g.n, out_cols<EPI, BN>());
+}
+
+template <int EPI, int BM, int BN>
+__device__ __forceinline__ void tile_origin(const GemmArgs& g, int64_t tile, int64_t& m0, int64_t& n0) {
   constexpr int BNO = out_cols<EPI, BN>();
   const int64_t tiles_m = cdiv(g.m, BM), tiles_n = cdiv(g.n, BNO);
   const int64_t ntiles = tiles_m * tiles_n;
-  int64_t bid = blockIdx.x;
+  int64_t bid = tile;
   if (ntiles % 8 == 0) bid = (bid % 8) * (ntiles / 8) + bid / 8;
   constexpr int64_t GROUP_M = 8;
   const int64_t group = bid / (GROUP_M * tiles_n);
@@ -767,8 +772,15 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, (WM * WN <= 8192 ? 2 : 
   const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
   const int wm = wid / NWN, wn = wid % NWN;
 
+  // A grid smaller than the tile count loops: workgroup b takes tiles b,
+  // b + gridDim.x, ... (the same XCD each time, since tile t and workgroup b
+  // agree modulo 8).  The barrier keeps the next tile's first copies out of
+  // the LDS that the previous tile's epilogue may still be reading.
+  const int64_t ntiles = tile_count<EPI, BM, BN>(g);
+  for (int64_t tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
+  if (tile != blockIdx.x) __syncthreads();
   int64_t m0, n0;
-  tile_origin<EPI, BM, BN>(g, m0, n0);
+  tile_origin<EPI, BM, BN>(g, tile, m0, n0);
   const int64_t KT = cdiv(g.k, 64);
   const int frow = lane & 31, fhalf = lane >> 5;
 
@@ -958,6 +970,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, (WM * WN <= 8192 ? 2 : 
 
   gemm_epilogue<EPI, HD, MB, NB, WM, WN, NW, EDT, EARLY_POS, SLOT_U4>(acc, lds, g, e, m0, n0, wid, wm, wn,
                                                                     lane, praw);
+  }
 }
 
 // ======================================================== decode split-K
@@ -2513,11 +2526,19 @@ static void launch_fused_edt(unsigned grid, dim3 block, int edt, const GemmArgs&
                      block, 0, st, g, e);
 }
 
+// Workgroups of a prefill GEMM launch: one per tile, or with the planner
+// override BFA_TUNE_QKV_PERSIST = c > 0 at most c per CU, each looping over tiles.
+static unsigned persistent_grid(int64_t tiles) {
+  const int c = tuning(BFA_TUNE_QKV_PERSIST);
+  if (c > 0) tiles = std::min<int64_t>(tiles, int64_t(256) * c);
+  return static_cast<unsigned>(tiles);
+}
+
 // BM x BN tile, waves of WM x 128 (the fused epilogue needs 128-column waves),
 // BK-deep DMA stages (NS of them when BK = 32).
 template <int BM, int BN, int WM, int NS, int BK, bool BF16, bool DIRECT>
 static void launch_prefill_tile(const QkvPlan& p, const GemmArgs& g, const QkvEpi& e, hipStream_t st) {
-  const unsigned grid = static_cast<unsigned>(cdiv(g.m, BM) * cdiv(g.n, BN));
+  const unsigned grid = persistent_grid(cdiv(g.m, BM) * cdiv(g.n, BN));
   const dim3 block((BM / WM) * (BN / 128) * 64);
   const int edt = fused_edt(e);
   if (!p.fused_epi) {
@@ -2536,7 +2557,7 @@ static void launch_prefill_tile(const QkvPlan& p, const GemmArgs& g, const QkvEp
 template <int BM, int BN, int WM, int NS, int BK, bool BF16, bool DIRECT>
 static void launch_linear_tile(const GemmArgs& g, const QkvEpi& e, bool swiglu, hipStream_t st) {
   const int64_t bno = swiglu ? BN / 2 : BN;
-  const unsigned grid = static_cast<unsigned>(cdiv(g.m, BM) * cdiv(g.n, bno));
+  const unsigned grid = persistent_grid(cdiv(g.m, BM) * cdiv(g.n, bno));
   const dim3 block((BM / WM) * (BN / 128) * 64);
   if constexpr (BF16 && DIRECT) {
     if (linear_edt(e) == EDT_BF16) {

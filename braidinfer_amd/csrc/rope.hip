@@ -288,6 +288,199 @@ __global__ __launch_bounds__(256) void rerotate_kernel(RerotArgs a) {
   }
 }
 
+// One workgroup per page-list entry, covering every kv head of the page.  The
+// page's K half (Hkv x page_size rows of D elements, contiguous) is requested
+// as soon as the page id has arrived, while the chunk search and the delta ->
+// cos/sin lookups (one row for the whole entry) are still in flight.  Rows are
+// walked in passes of 256 / LPR: a row belongs to an aligned group of LPR
+// lanes (LPR the power of two >= D / 16; lanes q >= D / 16 idle), lane q taking
+// the granule pair at columns 8q and D/2 + 8q, and U passes are in flight at
+// once.  Same arithmetic and outputs as rerotate_kernel.
+template <int LPR>
+__device__ __forceinline__ float row_group_sum(float v) {
+  if constexpr (LPR <= 16) return group_sum_dpp<LPR>(v);
+  else return group_sum<LPR>(v);
+}
+
+// 8 elements as raw bits (16-bit types: one 16-byte word; fp32: two), so that
+// loads can be issued unconditionally and converted after the data is in.
+template <int DT>
+struct Raw8 {
+  uint4 w[DT == BFA_DTYPE_F32 ? 2 : 1];
+  __device__ __forceinline__ void load(const void* p) {
+    w[0] = load16_nt(p);
+    if constexpr (DT == BFA_DTYPE_F32) w[1] = load16_nt(static_cast<const float*>(p) + 4);
+  }
+  __device__ __forceinline__ void to_f32(float (&v)[8]) const {
+    if constexpr (DT == BFA_DTYPE_F32) {
+      const uint32_t u[8] = {w[0].x, w[0].y, w[0].z, w[0].w, w[1].x, w[1].y, w[1].z, w[1].w};
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[i] = __uint_as_float(u[i]);
+    } else {
+      const uint32_t u[4] = {w[0].x, w[0].y, w[0].z, w[0].w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        v[2 * i] = Elem<DT>::to_f32(static_cast<uint16_t>(u[i] & 0xffffu));
+        v[2 * i + 1] = Elem<DT>::to_f32(static_cast<uint16_t>(u[i] >> 16));
+      }
+    }
+  }
+};
+
+template <int DT, bool NORM, int LPR, bool ONE_BLOCK>
+__global__ __launch_bounds__(256) void rerotate_entry_kernel(RerotArgs a) {
+  using T = typename Elem<DT>::T;
+  static_assert(LPR >= 1 && LPR <= 64, "a row stays inside one wave");
+  constexpr int RPP = 256 / LPR;                         // rows per pass
+  constexpr int U = LPR >= 8 ? 4 : (LPR >= 2 ? 2 : 1);  // passes per batch
+  const int64_t g = blockIdx.x;
+  const int tid = threadIdx.x, wl = tid & (kWave - 1);
+  const int q = tid % LPR, rsub = tid / LPR, j = q * 8;
+  const int64_t D = a.head_dim, half = D / 2;
+  const bool act = j < half;  // lane q < D / 16
+  const int32_t page32 = a.page_indices[g];  // widened after the barrier below
+  // Chunk owning entry g: the last c with indptr[c] <= g.  Lane l requests
+  // indptr[l] together with the page id and, when there are fewer than 64
+  // chunks, chunk l's delta and last-page length too, so that the chunk's
+  // figures come out of that one round trip by lane reads.
+  // (loads are unconditional, at clamped indices, so that none waits for
+  // another; ONE_BLOCK: fewer than 64 chunks, chosen by the host, so that the
+  // code has no join where the compiler would wait for every load)
+  constexpr bool one_block = ONE_BLOCK;
+  const int64_t wi = min<int64_t>(wl, a.num_chunks);      // indptr has num_chunks + 1 entries
+  const int64_t wc = min<int64_t>(wl, a.num_chunks - 1);  // num_chunks >= 1
+  int32_t v0 = a.chunk_indptr[wi];
+  // delta as 32-bit words at a computed offset: no branch between the loads
+  const int32_t* dw = static_cast<const int32_t*>(a.delta);
+  int32_t dlo = dw[a.delta_is_i64 ? 2 * wc : wc];
+  int32_t dhi = dw[a.delta_is_i64 ? 2 * wc + 1 : wc];
+  int32_t vlast = a.last_page_len[wc];
+  // keep the page id's wait (its first use is below) after these loads' issue
+  __builtin_amdgcn_sched_barrier(0);
+  const int64_t page = page32;
+  // no branch before every load is issued: an out-of-range page id reads
+  // page 0 and leaves once the loads are out
+  const bool page_ok = page >= 0 && page < a.num_cache_pages;
+  const int64_t rows = a.hkv * a.page_size;
+  const T* kpage = static_cast<const T*>(a.cache) + (page_ok ? page : 0) * a.page_elems;
+  Raw8<DT> k1[U], k2[U];
+  const int jc = act ? j : 0;
+  auto load_batch = [&](int64_t r0) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t row = min(r0 + u * RPP + rsub, rows - 1);
+      k1[u].load(kpage + row * D + jc);
+      k2[u].load(kpage + row * D + half + jc);
+    }
+  };
+  load_batch(0);  // in flight during the chunk search and the delta -> cos/sin lookups
+  // the chunk figures are taken from these registers by lane reads; the empty
+  // asm keeps the compiler from turning each lane read back into a load of
+  // its own, issued only once the chunk is known
+  __asm__ volatile("" : "+v"(v0), "+v"(dlo), "+v"(dhi), "+v"(vlast));
+  if (!page_ok) {
+    if (tid == 0) flag_status(a.status, BFA_STATUS_INDEX_OOB);
+    return;
+  }
+  int32_t v = wl <= a.num_chunks ? v0 : 0x7fffffff;
+  const int64_t vdelta = a.delta_is_i64 ? static_cast<int64_t>((static_cast<uint64_t>(static_cast<uint32_t>(dhi)) << 32) |
+                                                                static_cast<uint32_t>(dlo))
+                                        : static_cast<int64_t>(dlo);
+  int64_t c = 0, delta;
+  int32_t next, lpl;
+  if constexpr (one_block) {
+    const uint64_t m = __ballot(wl < a.num_chunks && v <= g);
+    c = m ? __popcll(m) - 1 : 0;
+    const int ci = static_cast<int>(c);
+    next = __builtin_amdgcn_readlane(v, ci + 1);
+    lpl = __builtin_amdgcn_readlane(vlast, ci);
+    const uint32_t dlo = __builtin_amdgcn_readlane(static_cast<uint32_t>(vdelta), ci);
+    const uint32_t dhi = __builtin_amdgcn_readlane(static_cast<uint32_t>(static_cast<uint64_t>(vdelta) >> 32), ci);
+    delta = static_cast<int64_t>((static_cast<uint64_t>(dhi) << 32) | dlo);
+  } else {
+    for (int64_t base = 0;;) {
+      const uint64_t m = __ballot(base + wl < a.num_chunks && v <= g);
+      if (m) c = base + __popcll(m) - 1;
+      if ((m >> (kWave - 1)) == 0) break;  // the prefix ended inside this block
+      base += kWave;
+      if (base >= a.num_chunks) break;
+      v = base + wl < a.num_chunks ? a.chunk_indptr[base + wl] : 0x7fffffff;
+    }
+    next = a.chunk_indptr[c + 1];
+    lpl = a.last_page_len[c];
+    delta = a.delta_is_i64 ? static_cast<const int64_t*>(a.delta)[c] : static_cast<const int32_t*>(a.delta)[c];
+  }
+  bool ok = true;
+  const int64_t p = wrap_position(delta, a.max_pos, ok);
+  if (!ok) {
+    if (tid == 0) flag_status(a.status, BFA_STATUS_INDEX_OOB);
+    return;
+  }
+  const bool rotate = delta != 0;
+  if (!rotate && a.out == nullptr) return;  // in place, nothing to do
+  const int64_t ntok =
+      g == next - 1 ? max(int64_t(0), min(static_cast<int64_t>(lpl), a.page_size)) : a.page_size;
+  float cs[8], sn[8];
+  load_cs8(a.cs_cache + p * D, half, jc, cs, sn);  // (row p = 0 when delta is 0: unused)
+  float g1[8], g2[8];
+  if constexpr (NORM) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      g1[i] = load_any(a.norm_w, a.norm_w_dtype, jc + i);
+      g2[i] = load_any(a.norm_w, a.norm_w_dtype, half + jc + i);
+    }
+  }
+  for (int64_t r0 = 0; r0 < rows; r0 += U * RPP) {
+    if (r0 > 0) load_batch(r0);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t row = r0 + u * RPP + rsub;
+      if (row >= rows) continue;  // uniform over the row's lanes
+      const int64_t h = row / a.page_size, tok = row - h * a.page_size;
+      float x1[8], x2[8];
+      k1[u].to_f32(x1);
+      k2[u].to_f32(x2);
+      if (tok >= ntok) {
+        if (a.out != nullptr && act) {
+          T* dst = static_cast<T*>(a.out) + ((g * a.page_size + tok) * a.hkv + h) * D;
+          const float z[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+          store8<DT>(dst + j, z);
+          store8<DT>(dst + half + j, z);
+        }
+        continue;
+      }
+      if (rotate && act) {
+        rotate8(x1, x2, cs, sn);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {  // apply_rotary_emb returns x.dtype
+          x1[i] = Elem<DT>::round(x1[i]);
+          x2[i] = Elem<DT>::round(x2[i]);
+        }
+      }
+      if constexpr (NORM) {
+        float ss = 0.f;
+        if (act) {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) ss += x1[i] * x1[i] + x2[i] * x2[i];
+        }
+        ss = row_group_sum<LPR>(ss);  // every lane of the row group takes part
+        const float r = 1.0f / sqrtf(ss / static_cast<float>(D) + a.norm_eps);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          x1[i] = Elem<DT>::round(x1[i] * r) * g1[i];
+          x2[i] = Elem<DT>::round(x2[i] * r) * g2[i];
+        }
+      }
+      if (act) {
+        T* dst = a.out == nullptr ? const_cast<T*>(kpage) + row * D
+                                  : static_cast<T*>(a.out) + ((g * a.page_size + tok) * a.hkv + h) * D;
+        store8<DT>(dst + j, x1);
+        store8<DT>(dst + half + j, x2);
+      }
+    }
+  }
+}
+
 }  // namespace bfa
 
 using namespace bfa;
@@ -384,12 +577,45 @@ extern "C" int bfa_rerotate_paged_k(void* kv_cache, int dtype, int64_t num_cache
   a.norm_eps = k_norm_eps;
   a.out = out;
   a.status = status;
-  const dim3 grid(static_cast<unsigned>(num_entries), static_cast<unsigned>(num_kv_heads));
   const hipStream_t s = as_stream(stream);
   const bool norm = k_norm_weight != nullptr;
-#define BFA_RR(DT)                                                                          \
-  if (norm) hipLaunchKernelGGL((rerotate_kernel<DT, true>), grid, dim3(256), 0, s, a);     \
-  else hipLaunchKernelGGL((rerotate_kernel<DT, false>), grid, dim3(256), 0, s, a);
+  // head_dim up to 1024: one workgroup per entry, a row on an aligned group of
+  // LPR lanes (the power of two >= head_dim / 16); larger head dims (no k_norm):
+  // one workgroup per (entry, kv head)
+  const int64_t lpa = head_dim / 16;
+  int lpr = 1;
+  while (lpr < lpa) lpr *= 2;
+  if (lpr <= 64) {
+    const dim3 grid(static_cast<unsigned>(num_entries));
+    const bool one = num_chunks < 64;
+#define BFA_RRE(DT, L)                                                                                 \
+  if (norm && one) hipLaunchKernelGGL((rerotate_entry_kernel<DT, true, L, true>), grid, dim3(256), 0, s, a);  \
+  else if (norm) hipLaunchKernelGGL((rerotate_entry_kernel<DT, true, L, false>), grid, dim3(256), 0, s, a);   \
+  else if (one) hipLaunchKernelGGL((rerotate_entry_kernel<DT, false, L, true>), grid, dim3(256), 0, s, a);    \
+  else hipLaunchKernelGGL((rerotate_entry_kernel<DT, false, L, false>), grid, dim3(256), 0, s, a);
+#define BFA_RRL(DT)                   \
+  switch (lpr) {                      \
+    case 1: BFA_RRE(DT, 1); break;    \
+    case 2: BFA_RRE(DT, 2); break;    \
+    case 4: BFA_RRE(DT, 4); break;    \
+    case 8: BFA_RRE(DT, 8); break;    \
+    case 16: BFA_RRE(DT, 16); break;  \
+    case 32: BFA_RRE(DT, 32); break;  \
+    default: BFA_RRE(DT, 64); break;  \
+  }
+    switch (dtype) {
+      case BFA_DTYPE_BF16: BFA_RRL(BFA_DTYPE_BF16); break;
+      case BFA_DTYPE_F16: BFA_RRL(BFA_DTYPE_F16); break;
+      default: BFA_RRL(BFA_DTYPE_F32); break;
+    }
+#undef BFA_RRL
+#undef BFA_RRE
+    return check_launch(what);
+  }
+  BFA_REQUIRE(!norm, "%s: the fused k_norm covers head_dim up to 1024 (got %lld)", what,
+              (long long)head_dim);
+  const dim3 grid(static_cast<unsigned>(num_entries), static_cast<unsigned>(num_kv_heads));
+#define BFA_RR(DT) hipLaunchKernelGGL((rerotate_kernel<DT, false>), grid, dim3(256), 0, s, a);
   switch (dtype) {
     case BFA_DTYPE_BF16: BFA_RR(BFA_DTYPE_BF16); break;
     case BFA_DTYPE_F16: BFA_RR(BFA_DTYPE_F16); break;

@@ -73,7 +73,9 @@ const char* bfa_last_error(void);
                                         flat form from 5 query rows */
 #define BFA_TUNE_CASCADE_FLAT_WG 9   /* BFA_CASCADE_FLAT_WG: flat-form workgroup target */
 #define BFA_TUNE_STREAM_STORES 10    /* BFA_STREAM_STORES: 0 = no nontemporal stores */
-#define BFA_TUNE_COUNT 11
+#define BFA_TUNE_QKV_PERSIST 11      /* BFA_QKV_PERSIST: prefill GEMM workgroups per CU that loop
+                                        over the tiles (0 = one workgroup per tile) */
+#define BFA_TUNE_COUNT 12
 int bfa_set_tuning(int key, int value);
 int bfa_get_tuning(int key);
 

@@ -306,8 +306,10 @@ def _paged(seed, pages, hkv, ps, d, chunk_pages, last_lens):
     return kv, perm[: int(indptr[-1])].to(torch.int32), indptr, torch.tensor(last_lens, dtype=torch.int32)
 
 
-@pytest.mark.parametrize("hkv,d", [(8, 128), (4, 64)])
+@pytest.mark.parametrize("hkv,d", [(8, 128), (4, 64), (2, 256), (4, 32), (1, 16), (2, 96), (1, 1024)])
 def test_rerotate_paged_k(hkv, d):
+    """Every row-group width of the one-workgroup-per-entry kernel (head_dim 16 ..
+    1024, 96 with idle lanes in each row group)."""
     maxp = 40960
     cache = R.cos_sin_cache(d, maxp, 1e6)
     kv, idx, indptr, last = _paged(113, 64, hkv, 16, d, [16, 1, 20, 7, 0, 4], [16, 9, 3, 16, 0, 1])
@@ -329,6 +331,40 @@ def test_rerotate_paged_k(hkv, d):
         n = int(last[c]) if e == int(indptr[c + 1]) - 1 else 16
         got = kvd[int(idx[e]), 0, :, :n].transpose(0, 1).cpu()
         assert torch.equal(bits(got), bits(ref[e, :n]))
+    braidinfer_amd.check_device_status()
+
+
+def test_rerotate_paged_k_wide_heads():
+    """head_dim above 1024 takes the per-(entry, kv head) kernel; the fused k_norm
+    is refused there."""
+    maxp, d = 4096, 2048
+    cache = R.cos_sin_cache(d, maxp, 1e4)
+    kv, idx, indptr, last = _paged(31, 6, 2, 4, d, [2, 3], [4, 2])
+    delta = torch.tensor([-17, 300], dtype=torch.int64)
+    args = [t.to(DEV) for t in (idx, indptr, delta, last)]
+    out = rerotate_paged_k(kv.to(DEV), *args, cache.to(DEV))
+    ref = R.rerotate_paged_k(kv, idx, indptr, delta, last, cache)
+    assert torch.equal(bits(out), bits(ref))
+    with pytest.raises(ValueError):
+        rerotate_paged_k(kv.to(DEV), *args, cache.to(DEV), k_norm_weight=torch.ones(d, device=DEV))
+    braidinfer_amd.check_device_status()
+
+
+def test_rerotate_paged_k_many_chunks():
+    """More than 64 chunks (the chunk search walks several 64-chunk blocks), empty
+    chunks among them, and a final chunk whose last page is partly filled."""
+    g = gen(21)
+    hkv, ps, d, maxp = 2, 16, 128, 40960
+    cache = R.cos_sin_cache(d, maxp, 1e6)
+    counts = [int(x) for x in torch.randint(0, 3, (150,), generator=g)]
+    pages = sum(counts) + 3
+    lasts = [int(x) for x in torch.randint(1, ps + 1, (150,), generator=g)]
+    kv, idx, indptr, last = _paged(22, pages, hkv, ps, d, counts, lasts)
+    delta = torch.randint(-4096, 4097, (150,), generator=g)
+    args = [t.to(DEV) for t in (idx, indptr, delta, last)]
+    out = rerotate_paged_k(kv.to(DEV), *args, cache.to(DEV))
+    ref = R.rerotate_paged_k(kv, idx, indptr, delta, last, cache)
+    assert torch.equal(bits(out), bits(ref))
     braidinfer_amd.check_device_status()
 
 
