@@ -1192,6 +1192,239 @@ __global__ __launch_bounds__(256) void cascade_decode_kernel(CasArgs a, int64_t 
   }
 }
 
+// ========================================= other head dims (multiple of 4, <= 256)
+// One wave per (query row, kv head, key split).  The wave walks its entries'
+// slots in blocks of 8 keys; lane l holds head-dim columns 2l, 2l + 1 and their
+// RoPE partners D/2 + 2l, D/2 + 2l + 1 (lanes past D/4 idle), so the rotation
+// needs no exchange, and the k_norm sum and each score are wave sums on DPP.
+// Lanes 0-7 fetch the block's slot metadata; the next block's metadata and its
+// K / V / cos-sin values are requested before the current block is processed.
+// Same rounding points as the head_dim 64 / 128 kernels; the split's (m, l,
+// acc) rows go to the partial layout, or with one split to the output.
+constexpr int CAS_GEN_DMAX = 256;
+
+template <bool BF16>
+__global__ __launch_bounds__(256) void cascade_generic_kernel(CasArgs a, int64_t D, int64_t ent_per_split) {
+  using E = Elem<BF16 ? BFA_DTYPE_BF16 : BFA_DTYPE_F16>;
+  constexpr int KB = 8;  // keys per block
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int64_t rows = a.tokens * a.group;
+  const int64_t r = static_cast<int64_t>(blockIdx.x) * 4 + wid;
+  if (r >= rows) return;  // whole waves
+  const int64_t g = blockIdx.y;
+  const int64_t e0 = static_cast<int64_t>(blockIdx.z) * ent_per_split;
+  const int64_t e1 = min(e0 + ent_per_split, a.num_entries);
+  const int64_t half = D / 2;
+  const bool act = 2 * lane < half;
+  const int64_t c0 = act ? 2 * lane : 0;  // idle lanes read column 0 and contribute nothing
+  const int64_t ps = a.page_size;
+  const int64_t t = r / a.group, hh = g * a.group + (r - t * a.group);
+  const float sl2 = a.scale * 1.4426950408889634f;  // scale x log2(e)
+  float q1[2], q2[2];
+  {
+    const uint16_t* qrow = a.q + t * a.q_st + hh * a.q_sh;
+    unpack_h<2, E>(ld16s<2, false>(qrow + c0), q1);
+    unpack_h<2, E>(ld16s<2, false>(qrow + half + c0), q2);
+    if (!act) q1[0] = q1[1] = q2[0] = q2[1] = 0.f;
+  }
+  const int64_t qp = a.qpos_i64 ? static_cast<const int64_t*>(a.qpos)[t] : static_cast<const int32_t*>(a.qpos)[t];
+  float kg1[2] = {1.f, 1.f}, kg2[2] = {1.f, 1.f};
+  if (a.knorm_w) {
+    ld_any_n<2>(a.knorm_w, a.knorm_dt, c0, kg1);
+    ld_any_n<2>(a.knorm_w, a.knorm_dt, half + c0, kg2);
+  }
+  // block b covers padded slots (e0 * ps + b * KB) .. +KB; lane u < KB fetches
+  // slot u's entry metadata (a slot past the range reads entry 0 and is masked)
+  struct Meta {
+    int32_t page, info;
+    int64_t kst, dpos, s;
+    bool in;
+  };
+  const int64_t nslots = (e1 > e0 ? e1 - e0 : 0) * ps;
+  auto load_meta = [&](int64_t b) {
+    Meta mt;
+    const int64_t j = b * KB + (lane & (KB - 1));
+    const int64_t e = e0 + j / ps;
+    mt.s = j - (j / ps) * ps;
+    mt.in = j < nslots;
+    const int64_t ec = mt.in ? e : 0;
+    mt.page = a.pages[ec];
+    mt.kst = a.kstart[ec];
+    mt.dpos = a.delta[ec];
+    mt.info = a.info[ec];
+    return mt;
+  };
+  struct Blk {
+    Half16<2> k1[KB], k2[KB], v1[KB], v2[KB];
+    float c[KB][2], sn[KB][2];
+    bool valid[KB], rot[KB];
+    int64_t kp[KB];
+  };
+  const uint16_t* zero = reinterpret_cast<const uint16_t*>(cas_zero_row);
+  auto rd64 = [](int64_t v, int u) {
+    const uint32_t lo = __builtin_amdgcn_readlane(static_cast<uint32_t>(v), u);
+    const uint32_t hi = __builtin_amdgcn_readlane(static_cast<uint32_t>(static_cast<uint64_t>(v) >> 32), u);
+    return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
+  };
+  auto issue = [&](const Meta& mt) {
+    Blk b;
+#pragma unroll
+    for (int u = 0; u < KB; ++u) {
+      const bool in = __builtin_amdgcn_readlane(static_cast<int>(mt.in), u) != 0;
+      int64_t page = __builtin_amdgcn_readlane(mt.page, u);
+      const int32_t info = __builtin_amdgcn_readlane(mt.info, u);
+      const int64_t sl = rd64(mt.s, u);
+      int64_t dpos = rd64(mt.dpos, u);
+      bool valid = in && sl < (info & 0xffff);
+      if (page < 0) page += a.num_pages;  // kv_cache[-1] is the last page
+      if (valid && (page < 0 || page >= a.num_pages)) {
+        if (lane == 0) flag_status(a.status, BFA_STATUS_INDEX_OOB);
+        valid = false;
+      }
+      bool rot = valid && a.cs != nullptr && ((info >> 16) & 1);
+      if (rot) {
+        if (dpos < 0) dpos += a.max_pos;
+        if (dpos < 0 || dpos >= a.max_pos) {
+          if (lane == 0) flag_status(a.status, BFA_STATUS_INDEX_OOB);
+          valid = rot = false;
+        }
+      }
+      b.valid[u] = valid;
+      b.rot[u] = rot;
+      b.kp[u] = rd64(mt.kst, u) + sl;
+      const uint16_t* krow = valid ? a.cache + page * a.c_sp + g * a.c_sh + sl * a.c_ss : zero;
+      const uint16_t* vrow = valid ? krow + a.c_skv : zero;
+      const int64_t cc = valid ? c0 : 0;  // the zeroed row is only CAS_DMAX floats long
+      b.k1[u] = ld16s<2, true>(krow + cc);
+      b.k2[u] = ld16s<2, true>(krow + (valid ? half : 0) + cc);
+      b.v1[u] = ld16s<2, true>(vrow + cc);
+      b.v2[u] = ld16s<2, true>(vrow + (valid ? half : 0) + cc);
+      const float* csrow = rot ? a.cs + dpos * D : cas_zero_row;
+      ldf<2>(csrow + (rot ? c0 : 0), b.c[u]);
+      ldf<2>(csrow + (rot ? half + c0 : 0), b.sn[u]);
+    }
+    return b;
+  };
+  float m = -INFINITY, l = 0.f, acc1[2] = {0.f, 0.f}, acc2[2] = {0.f, 0.f};
+  const int64_t nb = cdiv(nslots, KB);
+  if (nb > 0) {
+    Blk cur = issue(load_meta(0));
+    Meta mn = load_meta(1);
+    for (int64_t b = 0; b < nb; ++b) {
+      const Blk nxt = issue(mn);  // block b + 1's values fly while block b is processed
+      mn = load_meta(b + 2);
+#pragma unroll
+      for (int u = 0; u < KB; ++u) {
+        float x1[2], x2[2], v1[2], v2[2];
+        unpack_h<2, E>(cur.k1[u], x1);
+        unpack_h<2, E>(cur.k2[u], x2);
+        unpack_h<2, E>(cur.v1[u], v1);
+        unpack_h<2, E>(cur.v2[u], v2);
+        if (cur.rot[u]) {
+#pragma unroll
+          for (int i = 0; i < 2; ++i) {  // apply_rotary_emb: fp32, result in the cache dtype
+            const float p = x1[i], w = x2[i];
+            x1[i] = E::round(p * cur.c[u][i] - w * cur.sn[u][i]);
+            x2[i] = E::round(w * cur.c[u][i] + p * cur.sn[u][i]);
+          }
+        }
+        if (!act) x1[0] = x1[1] = x2[0] = x2[1] = 0.f;
+        if (a.knorm_w) {
+          const float ss = wave_sum_dpp(x1[0] * x1[0] + x1[1] * x1[1] + x2[0] * x2[0] + x2[1] * x2[1]);
+          const float rr = __builtin_amdgcn_rsqf(ss / static_cast<float>(D) + a.knorm_eps);
+#pragma unroll
+          for (int i = 0; i < 2; ++i) {
+            x1[i] = E::round(E::round(x1[i] * rr) * kg1[i]);
+            x2[i] = E::round(E::round(x2[i] * rr) * kg2[i]);
+          }
+        }
+        const float d = wave_sum_dpp(q1[0] * x1[0] + q1[1] * x1[1] + q2[0] * x2[0] + q2[1] * x2[1]);
+        const bool use = cur.valid[u] && (!a.causal || cur.kp[u] <= qp);
+        const float sc = use ? d * sl2 : -INFINITY;
+        const float m_new = fmaxf(m, sc);
+        const float mref = m_new == -INFINITY ? 0.f : m_new;  // nothing seen yet: stay at zero
+        const float alpha = __builtin_amdgcn_exp2f(m - mref);
+        const float pr = __builtin_amdgcn_exp2f(sc - mref);
+        l = l * alpha + pr;
+        m = m_new;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          acc1[i] = acc1[i] * alpha + pr * v1[i];
+          acc2[i] = acc2[i] * alpha + pr * v2[i];
+        }
+      }
+      cur = nxt;
+    }
+  }
+  if (gridDim.z == 1) {
+    if (act) {
+      const float inv = 1.0f / fmaxf(l, 1e-12f);
+      uint16_t* orow = static_cast<uint16_t*>(a.out) + t * a.out_st + hh * D;
+      const float o1[2] = {acc1[0] * inv, acc1[1] * inv}, o2[2] = {acc2[0] * inv, acc2[1] * inv};
+      st16s<2, BF16>(orow + c0, o1);
+      st16s<2, BF16>(orow + half + c0, o2);
+    }
+  } else {
+    float* pr = a.part + ((static_cast<int64_t>(blockIdx.z) * a.hkv + g) * rows + r) * (D + 2);
+    if (lane == 0) {
+      pr[0] = m;
+      pr[1] = l;
+    }
+    if (act) {
+      pr[2 + c0] = acc1[0];
+      pr[2 + c0 + 1] = acc1[1];
+      pr[2 + half + c0] = acc2[0];
+      pr[2 + half + c0 + 1] = acc2[1];
+    }
+  }
+}
+
+// Split combination for any head_dim: one wave per (kv head, row), the splits
+// walked in order (lanes over head-dim columns).
+template <bool BF16>
+__global__ __launch_bounds__(256) void cascade_merge_generic_kernel(CasArgs a, int64_t D, int64_t splits) {
+  using E = Elem<BF16 ? BFA_DTYPE_BF16 : BFA_DTYPE_F16>;
+  const int64_t rows = a.tokens * a.group;
+  const int64_t item = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (item >= a.hkv * rows) return;
+  const int64_t g = item / rows, r = item - g * rows;
+  const int lane = threadIdx.x & 63;
+  const int64_t zstride = a.hkv * rows * (D + 2);
+  const float* base = a.part + (g * rows + r) * (D + 2);
+  float mx = -INFINITY;
+  for (int64_t z = 0; z < splits; ++z) mx = fmaxf(mx, base[z * zstride]);
+  const float mref = mx == -INFINITY ? 0.f : mx;
+  float lsum = 0.f, oc[CAS_GEN_DMAX / 64] = {0.f, 0.f, 0.f, 0.f};
+  for (int64_t z = 0; z < splits; ++z) {
+    const float* pz = base + z * zstride;
+    const float w = __builtin_amdgcn_exp2f(pz[0] - mref);  // m in base 2; -inf -> 0
+    lsum += w * pz[1];
+#pragma unroll
+    for (int c = 0; c < CAS_GEN_DMAX / 64; ++c)
+      if (64 * c + lane < D) oc[c] += w * pz[2 + 64 * c + lane];
+  }
+  const float inv = 1.0f / fmaxf(lsum, 1e-12f);
+  const int64_t t = r / a.group, hh = g * a.group + (r - t * a.group);
+  uint16_t* orow = static_cast<uint16_t*>(a.out) + t * a.out_st + hh * D;
+#pragma unroll
+  for (int c = 0; c < CAS_GEN_DMAX / 64; ++c)
+    if (64 * c + lane < D) orow[64 * c + lane] = E::from_f32(oc[c] * inv);
+}
+
+// Split plan of the other head dims: about 4096 waves (16 per CU).
+struct GenericSplit {
+  int64_t per_split, splits;
+};
+static GenericSplit generic_split(int64_t rows, int64_t hkv, int64_t num_entries) {
+  GenericSplit gs{};
+  const int64_t want = std::max<int64_t>(1, std::min<int64_t>(num_entries, cdiv(4096, rows * hkv)));
+  gs.per_split = std::max<int64_t>(1, cdiv(num_entries, want));
+  gs.splits = num_entries > 0 ? cdiv(num_entries, gs.per_split) : 1;
+  return gs;
+}
+
+static bool mfma_head_dim(int64_t d) { return d == 64 || d == 128; }
+
 // Split plan of the decode form: items of (entry, 16-slot block), about 512
 // workgroups over the kv heads (Qwen3 decode over 4096 keys: 25 / 15.9 / 13.6 /
 // 15.1 / 20.5 us at 128 / 256 / 512 / 1024 / 2048 -- fewer leave SIMDs idle,
@@ -1347,6 +1580,10 @@ extern "C" int64_t bfa_cascade_attention_workspace_size(int64_t tokens, int64_t 
                                                         int64_t num_entries, int64_t page_size) {
   if (tokens <= 0 || num_kv_heads <= 0 || num_q_heads % num_kv_heads != 0 || page_size <= 0) return 0;
   const int64_t rows = tokens * (num_q_heads / num_kv_heads);
+  if (!mfma_head_dim(head_dim)) {
+    const GenericSplit gs = generic_split(rows, num_kv_heads, num_entries);
+    return gs.splits > 1 ? gs.splits * num_kv_heads * rows * (head_dim + 2) * 4 : 0;
+  }
   if (!decode_form(rows) && flat_form(rows, num_entries))
     return flat_plan(rows, num_kv_heads, num_entries, page_size, head_dim).total();
   const int64_t splits = decode_form(rows) ? decode_split(num_kv_heads, num_entries, page_size).splits
@@ -1367,8 +1604,8 @@ extern "C" int bfa_cascade_attention(
   const char* what = "bfa_cascade_attention";
   BFA_REQUIRE(dtype == BFA_DTYPE_BF16 || dtype == BFA_DTYPE_F16,
               "%s: query and cache must be bf16 or fp16", what);
-  BFA_REQUIRE(head_dim == 128 || head_dim == 64, "%s: head_dim %lld (the kernels cover 64 and 128)", what,
-              static_cast<long long>(head_dim));
+  BFA_REQUIRE(head_dim > 0 && head_dim % 4 == 0 && head_dim <= CAS_GEN_DMAX,
+              "%s: head_dim %lld (a multiple of 4 up to %d)", what, static_cast<long long>(head_dim), CAS_GEN_DMAX);
   BFA_REQUIRE(qpos_dtype == BFA_DTYPE_I32 || qpos_dtype == BFA_DTYPE_I64, "%s: bad positions dtype", what);
   BFA_REQUIRE(num_tokens >= 0 && num_kv_heads > 0 && num_q_heads % num_kv_heads == 0 && page_size > 0 &&
                   page_size < 65536 && num_entries >= 0 && num_pages >= 0,
@@ -1402,6 +1639,30 @@ extern "C" int bfa_cascade_attention(
   a.out = out; a.out_st = out_stride_token;
   a.status = status;
   const int64_t rows = num_tokens * a.group;
+  if (!mfma_head_dim(head_dim)) {
+    const GenericSplit gs = generic_split(rows, num_kv_heads, num_entries);
+    if (gs.splits > 1) {
+      BFA_REQUIRE(workspace && workspace_bytes >= gs.splits * num_kv_heads * rows * (head_dim + 2) * 4,
+                  "%s: workspace too small", what);
+      a.part = static_cast<float*>(workspace);
+    }
+    BFA_REQUIRE(cdiv(rows, 4) < (int64_t{1} << 31) && num_kv_heads < 65536 && gs.splits < 65536,
+                "%s: grid too large", what);
+    const dim3 grid(static_cast<unsigned>(cdiv(rows, 4)), static_cast<unsigned>(num_kv_heads),
+                    static_cast<unsigned>(gs.splits));
+    const dim3 mgrid(static_cast<unsigned>(cdiv(num_kv_heads * rows, 4)));
+    const hipStream_t s = as_stream(stream);
+    if (dtype == BFA_DTYPE_BF16) {
+      hipLaunchKernelGGL((cascade_generic_kernel<true>), grid, dim3(256), 0, s, a, head_dim, gs.per_split);
+      if (gs.splits > 1)
+        hipLaunchKernelGGL((cascade_merge_generic_kernel<true>), mgrid, dim3(256), 0, s, a, head_dim, gs.splits);
+    } else {
+      hipLaunchKernelGGL((cascade_generic_kernel<false>), grid, dim3(256), 0, s, a, head_dim, gs.per_split);
+      if (gs.splits > 1)
+        hipLaunchKernelGGL((cascade_merge_generic_kernel<false>), mgrid, dim3(256), 0, s, a, head_dim, gs.splits);
+    }
+    return check_launch(what);
+  }
   if (decode_form(rows)) {
     const DecodeSplit ds = decode_split(num_kv_heads, num_entries, page_size);
     if (ds.splits > 1) {

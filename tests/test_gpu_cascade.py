@@ -142,6 +142,24 @@ def test_cascade_attention_head_dim_64_flat_form(tuning, name, tokens, hq, hkv, 
     _check_case(name, tokens, hq, hkv, lengths, deltas, causal, knorm, d=64, base=1e4)
 
 
+# head dims other than 64 and 128 (a wave per query row walks the pages: the
+# same rounding points, scores on the VALU): decode, a prefill chunk and a
+# non-causal case, with k_norm, GQA 2 and 4, moved chunks
+CASES_OTHER_D = [
+    ("d32 decode k-norm", 32, 1, 8, 2, [200, 17, 1000], [0, -4096, 3000], True, True),
+    ("d96 decode", 96, 1, 16, 8, [100, 37, 516], [0, 4000, -77], True, False),
+    ("d96 prefill chunk k-norm", 96, 37, 16, 8, [48, 130, 64], [0, 77, -5], True, True),
+    ("d80 non-causal k-norm", 80, 9, 16, 4, [33, 16, 1], [0, 5, 0], False, True),
+    ("d256 decode batch", 256, 4, 8, 4, [64, 300, 5], [0, 0, 12], True, False),
+    ("d256 prefill k-norm", 256, 20, 8, 2, [128, 70, 30], [0, 2048, 0], True, True),
+]
+
+
+@pytest.mark.parametrize("name,d,tokens,hq,hkv,lengths,deltas,causal,knorm", CASES_OTHER_D)
+def test_cascade_attention_other_head_dims(name, d, tokens, hq, hkv, lengths, deltas, causal, knorm):
+    _check_case(name, tokens, hq, hkv, lengths, deltas, causal, knorm, d=d, base=1e4)
+
+
 def _check_case(name, tokens, hq, hkv, lengths, deltas, causal, knorm, d=128, base=1e6):
     seed = zlib.crc32(name.encode()) % 1000
     g = gen(seed)
