@@ -178,6 +178,7 @@ TUNING_KEYS = {
     "DECODE_KS": 0, "DECODE_WG": 1, "DECODE_SPLITS": 2, "QKV_TILE": 3, "EDT_RT": 4,
     "DECODE_PAIR": 5, "NO_OPERAND_FOLD": 6, "CASCADE_DECODE_WG": 7, "CASCADE_FLAT": 8,
     "CASCADE_FLAT_WG": 9, "STREAM_STORES": 10, "QKV_PERSIST": 11,
+    "DECODE_GEMV": 12,
 }
 
 

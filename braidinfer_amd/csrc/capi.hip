@@ -36,7 +36,8 @@ struct TuningFromEnv {
     static const char* const names[BFA_TUNE_COUNT] = {
         "BFA_DECODE_KS",      "BFA_DECODE_WG",         "BFA_DECODE_SPLITS", "BFA_QKV_TILE",
         "BFA_EDT_RT",         "BFA_DECODE_PAIR",       "BFA_NO_OPERAND_FOLD", "BFA_CASCADE_DECODE_WG",
-        "BFA_CASCADE_FLAT",   "BFA_CASCADE_FLAT_WG",   "BFA_STREAM_STORES", "BFA_QKV_PERSIST"};
+        "BFA_CASCADE_FLAT",   "BFA_CASCADE_FLAT_WG",   "BFA_STREAM_STORES", "BFA_QKV_PERSIST",
+        "BFA_DECODE_GEMV"};
     for (int k = 0; k < BFA_TUNE_COUNT; ++k) {
       const char* v = getenv(names[k]);
       g_tuning[k] = (v != nullptr && *v != '\0') ? atoi(v) : -1;

@@ -44,6 +44,7 @@
 #include "bfa_device.h"
 #include "bfa_host.h"
 #include "bfa_internal.h"
+#include "bfa_qkv.h"
 
 namespace bfa {
 
@@ -72,70 +73,6 @@ __device__ __forceinline__ f32x4_t mfma16(const uint4& a, const uint4& b, f32x4_
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a),
                                                   __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
   }
-}
-
-// ------------------------------------------------------------- epilogue spec
-struct QkvEpi {
-  const void* bias;
-  int bias_dtype;
-  int qkv_dt;   // rounding of the projection (BFA_DTYPE_F32 = none)
-  int norm_dt;  // dtype the q/k norm result is cast to
-  int out_dt;
-  int64_t n;        // columns (q|k|v)
-  int64_t hq, hkv;  // heads
-  int64_t hd;       // head_dim
-  const void* qn_w;
-  const void* kn_w;
-  int qk_w_dtype;
-  float qk_eps;
-  const void* positions;
-  int pos_is_i64;
-  const float* cs;  // cos|sin table [max_pos, hd] or nullptr (no RoPE)
-  int64_t max_pos;
-  void* out;
-  int64_t ldo;
-  int* status;
-  // EPI_LINEAR / EPI_SWIGLU: y = out_dt(mid_dt(qkv_dt(acc) + residual)) or
-  // out_dt(qkv_dt(silu(qkv_dt(gate))) * qkv_dt(up)); vec = 16-byte row access is
-  // allowed for out and residual (aligned bases, strides multiple of 8)
-  const void* res;
-  int res_dt;
-  int64_t ldr;
-  int mid_dt;
-  int vec;
-  // scale-after decode (the fp32 variants): stats[s * stat_rows + t] holds split
-  // s's sum of x^2 over its K slice for token t; the projection of x * gamma is
-  // multiplied by r = 1 / sqrt(sum / hidden + stat_eps) before the bias
-  const float* stats;
-  int64_t stat_rows;
-  int64_t hidden;
-  float stat_eps;
-  // Paged-KV append in the epilogue (bfa_fused_rmsnorm_qkv_append): the k and v
-  // heads of row t also go to cache + slot_off[t] + (V ? c_skv : 0) + (head -
-  // first head of its kind) * c_sh + column in the head, as cache_dt (from the
-  // value rounded to out_dt); slot_off[t] < 0 skips the row.  skip_kv_out = 1
-  // leaves the k/v columns of `out` unwritten.
-  void* cache;
-  int cache_dt;
-  int64_t c_skv, c_sh;
-  const int64_t* slot_off;
-  int skip_kv_out;
-  // app_in_kernel = 1: the prefill GEMM resolves its rows' cache slots itself
-  // (before the K loop, from `app`), and slot_off is not used
-  int app_in_kernel;
-  AppendArgs app;
-};
-
-__device__ __forceinline__ float round_to(float v, int dt) {
-  if (dt == BFA_DTYPE_BF16) return Elem<BFA_DTYPE_BF16>::round(v);
-  if (dt == BFA_DTYPE_F16) return Elem<BFA_DTYPE_F16>::round(v);
-  return v;
-}
-
-__device__ __forceinline__ void store_any(void* p, int dt, int64_t i, float v) {
-  if (dt == BFA_DTYPE_BF16) store1<BFA_DTYPE_BF16>(p, i, v);
-  else if (dt == BFA_DTYPE_F16) store1<BFA_DTYPE_F16>(p, i, v);
-  else store1<BFA_DTYPE_F32>(p, i, v);
 }
 
 // Stores 4 consecutive elements (8-byte / 16-byte vector store; the caller
@@ -238,31 +175,8 @@ __device__ __forceinline__ void store8_dt(void* p, int dt, int64_t i, const floa
   }
 }
 
-// 0 = q head, 1 = k head, 2 = v head
-__device__ __forceinline__ int head_kind(const QkvEpi& e, int64_t head) {
-  return head < e.hq ? 0 : (head < e.hq + e.hkv ? 1 : 2);
-}
 
-// Two elements of a small float vector of runtime dtype, with one dispatch.
-__device__ __forceinline__ void load2_any(const void* p, int dt, int64_t i1, int64_t i2, float& v1,
-                                          float& v2) {
-  if (dt == BFA_DTYPE_BF16) {
-    v1 = load1<BFA_DTYPE_BF16>(p, i1);
-    v2 = load1<BFA_DTYPE_BF16>(p, i2);
-  } else if (dt == BFA_DTYPE_F16) {
-    v1 = load1<BFA_DTYPE_F16>(p, i1);
-    v2 = load1<BFA_DTYPE_F16>(p, i2);
-  } else {
-    v1 = static_cast<const float*>(p)[i1];
-    v2 = static_cast<const float*>(p)[i2];
-  }
-}
 
-// Position p wrapped like a torch negative index; -1 when outside the table.
-__device__ __forceinline__ int32_t epi_pos_check(const QkvEpi& e, int64_t p) {
-  if (p < 0) p += e.max_pos;
-  return (p >= 0 && p < e.max_pos) ? static_cast<int32_t>(p) : -1;
-}
 
 __device__ __forceinline__ int64_t epi_position(const QkvEpi& e, int64_t row, bool& ok) {
   int64_t p = e.pos_is_i64 ? static_cast<const int64_t*>(e.positions)[row]
@@ -1085,26 +999,10 @@ struct OperandFold {
   float* stats;  // non-null: scale-after form of the deep-K kernel
 };
 
-template <int DT>
-__device__ __forceinline__ void unpack8(uint4 u, float (&v)[8]) {
-  const uint32_t w[4] = {u.x, u.y, u.z, u.w};
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    v[2 * i] = Elem<DT>::to_f32(static_cast<uint16_t>(w[i] & 0xffffu));
-    v[2 * i + 1] = Elem<DT>::to_f32(static_cast<uint16_t>(w[i] >> 16));
-  }
-}
 
 constexpr int KC_MAX = 512;  // deepest K slice per split (8 segments of 64)
 
-typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
 
-// 16-byte weight load returned through a plain vector value: loading straight
-// into the uint4 array member makes the compiler keep the whole array in scratch.
-__device__ __forceinline__ uint4 load16(const uint16_t* p) {
-  const u32x4_t t = *reinterpret_cast<const u32x4_t*>(p);
-  return make_uint4(t.x, t.y, t.z, t.w);
-}
 
 // staging slot of (row r, granule g) in a 32-row x 8-granule block: rows r and
 // r+8 share bank groups, so the granule is XORed with r/2 -- conflict-free for
@@ -2773,6 +2671,22 @@ static int qkv_projection_impl(const void* operand, int64_t lda, const OperandFo
   const hipStream_t st = as_stream(stream);
   const bool bf16 = w_dtype == BFA_DTYPE_BF16;
   float* part = static_cast<float*>(part_workspace);
+  // 1 to 8 tokens: one launch (no split-K partials); the fold's operand must be
+  // bf16 like the weight, and the scale-after form is not used
+  auto al4 = [](const void* q) { return (reinterpret_cast<uintptr_t>(q) & 3u) == 0; };
+  if (p.decode && !(fold && fold->stats) && al4(bias) && al4(q_norm_weight) && al4(k_norm_weight) &&
+      gemv_ok(tokens, hidden, hd, q_norm_weight || k_norm_weight, bf16, true, operand, lda)) {
+    GemvArgs d{};
+    d.a = static_cast<const uint16_t*>(operand);
+    d.w = static_cast<const uint16_t*>(qkv_weight);
+    d.m = tokens; d.k = hidden; d.lda = lda; d.ldw = w_stride;
+    if (fold) {
+      d.gamma = fold->gamma; d.gamma_dt = fold->gamma_dt; d.mixed = fold->mixed ? 1 : 0; d.eps = fold->eps;
+    }
+    e.stats = nullptr;
+    launch_qkv_gemv(d, fold != nullptr, e, st);
+    return check_launch(what);
+  }
   if (p.decode && pair_ok(p, qkv_dim, hd, hidden, q_norm_weight || k_norm_weight, bf16, lda, operand, tokens,
                          w_stride)) {
     DecodeArgs d{};
@@ -2877,9 +2791,15 @@ static int fused_impl(const void* x, int x_dtype, int64_t tokens, int64_t hidden
   const int fold_rows = (tokens <= 4 && hidden <= 4096) ? 1
                         : (tokens <= 8 && hidden <= 2048) ? 2
                         : (tokens <= 16 && hidden <= 1024) ? 4 : 0;
-  const bool fold = !no_fold && fold_rows > 0 && p.decode && p.stream && p.mt == 1 && x_dtype == w_dtype &&
-                    (w_dtype == BFA_DTYPE_BF16 || w_dtype == BFA_DTYPE_F16) && hidden % 8 == 0 &&
-                    x_stride % 8 == 0 && aligned16(x) && aligned16(norm_weight) && is_float_dtype(nw_dtype);
+  // 1 to 8 tokens in bf16 (the one-launch kernel, qkv_gemv.hip) always fold.
+  const bool gemv_fold = !no_fold && p.decode && x_dtype == BFA_DTYPE_BF16 && w_dtype == BFA_DTYPE_BF16 &&
+                         aligned16(norm_weight) && is_float_dtype(nw_dtype) &&
+                         gemv_ok(tokens, hidden, qkv_dim / heads, q_norm_weight || k_norm_weight, true, true, x,
+                                 x_stride);
+  const bool fold = gemv_fold ||
+                    (!no_fold && fold_rows > 0 && p.decode && p.stream && p.mt == 1 && x_dtype == w_dtype &&
+                     (w_dtype == BFA_DTYPE_BF16 || w_dtype == BFA_DTYPE_F16) && hidden % 8 == 0 &&
+                     x_stride % 8 == 0 && aligned16(x) && aligned16(norm_weight) && is_float_dtype(nw_dtype));
   // 17 to 64 decode tokens of the fp32 variants (operand (x / rms) * gamma): the
   // row scale 1 / rms comes out of the sum, so no operand pre-pass.  The
   // column-pair kernel projects x onto bf16(w * gamma) and sums the rows'
