@@ -74,7 +74,8 @@ const char* bfa_last_error(void);
 #define BFA_TUNE_CASCADE_FLAT_WG 9   /* BFA_CASCADE_FLAT_WG: flat-form workgroup target */
 #define BFA_TUNE_STREAM_STORES 10    /* BFA_STREAM_STORES: 0 = no nontemporal stores */
 #define BFA_TUNE_QKV_PERSIST 11      /* BFA_QKV_PERSIST: prefill GEMM workgroups per CU that loop
-                                        over the tiles (0 = one workgroup per tile) */
+                                        over the tiles (0 = one workgroup per tile; unset: 1 for
+                                        the 256x256 tile, 0 for the others) */
 #define BFA_TUNE_DECODE_GEMV 12      /* BFA_DECODE_GEMV: 0 = never the one-launch decode kernel
                                         (1-16 tokens without q/k norm) */
 #define BFA_TUNE_COUNT 13
