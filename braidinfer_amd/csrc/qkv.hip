@@ -682,17 +682,25 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, (WM * WN <= 8192 ? 2 : 
   uint4* const lds0 = lds;
   uint4* const lds1 = lds + (BM + BN) * 8;
 
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
-  const int wm = wid / NWN, wn = wid % NWN;
-
-  // A grid smaller than the tile count loops: workgroup b takes tiles b,
-  // b + gridDim.x, ... (the same XCD each time, since tile t and workgroup b
-  // agree modulo 8).  The barrier keeps the next tile's first copies out of
-  // the LDS that the previous tile's epilogue may still be reading.
+  // PERSIST (the 256x256 tile): a grid smaller than the tile count loops:
+  // workgroup b takes tiles b, b + gridDim.x, ... (the same XCD each time,
+  // since tile t and workgroup b agree modulo 8).  The barrier keeps the next
+  // tile's first copies out of the LDS that the previous tile's epilogue may
+  // still be reading.  The other tiles run one per workgroup.
+  constexpr bool PERSIST = BM == 256 && BN == 256;
   const int64_t ntiles = tile_count<EPI, BM, BN>(g);
   for (int64_t tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
   if (tile != blockIdx.x) __syncthreads();
+  // The thread id passes through an empty asm on every tile, so the values
+  // derived from it (LDS and DMA offsets, the epilogue's lane roles) are
+  // computed per tile, as in a one-tile workgroup, instead of once before the
+  // loop, where they would all stay live across the K loop and the epilogue
+  // and spill.
+  int tid = threadIdx.x;
+  if constexpr (PERSIST) asm volatile("" : "+v"(tid));
+  const int lane = tid & 63;
+  const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
+  const int wm = wid / NWN, wn = wid % NWN;
   int64_t m0, n0;
   tile_origin<EPI, BM, BN>(g, tile, m0, n0);
   const int64_t KT = cdiv(g.k, 64);
@@ -882,8 +890,13 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, (WM * WN <= 8192 ? 2 : 
     }
   }
 
-  gemm_epilogue<EPI, HD, MB, NB, WM, WN, NW, EDT, EARLY_POS, SLOT_U4>(acc, lds, g, e, m0, n0, wid, wm, wn,
-                                                                    lane, praw);
+  // (likewise into the epilogue, so that its lane roles are not computed
+  // before the K loop)
+  int lane_e = lane, wid_e = wid;
+  if constexpr (PERSIST) asm volatile("" : "+v"(lane_e), "+s"(wid_e));
+  gemm_epilogue<EPI, HD, MB, NB, WM, WN, NW, EDT, EARLY_POS, SLOT_U4>(acc, lds, g, e, m0, n0, wid_e, wid_e / NWN,
+                                                                    wid_e % NWN, lane_e, praw);
+  if constexpr (!PERSIST) break;  // one tile per workgroup: no loop, nothing hoisted out of one
   }
 }
 
@@ -2424,14 +2437,16 @@ static void launch_fused_edt(unsigned grid, dim3 block, int edt, const GemmArgs&
                      block, 0, st, g, e);
 }
 
-// Workgroups of a prefill GEMM launch: at most per_cu per CU, each looping over
-// tiles (per_cu = 0: one per tile).  The 256x256 tile (one workgroup per CU)
-// loops by default: the Llama-3-8B projection at 8192 tokens (768 tiles) took
-// 380.5 against 388.0 us on one box, with bit-identical output.  Planner
-// override BFA_TUNE_QKV_PERSIST = c sets per_cu to c.
-static unsigned persistent_grid(int64_t tiles, int per_cu) {
+// Workgroups of a prefill GEMM launch: one per tile, or for the 256x256 tile
+// (one workgroup per CU, the kernel's PERSIST form) one per CU, each looping
+// over tiles: the Llama-3-8B projection at 8192 tokens (768 tiles) took 380.5
+// against 388.0 us on one box, with bit-identical output.  Planner override
+// BFA_TUNE_QKV_PERSIST = c sets the workgroups per CU of the 256x256 tile
+// (0: one per tile).
+static unsigned persistent_grid(int64_t tiles, bool persist) {
+  int per_cu = persist ? 1 : 0;
   const int c = tuning(BFA_TUNE_QKV_PERSIST);
-  if (c >= 0) per_cu = c;
+  if (persist && c >= 0) per_cu = c;
   if (per_cu > 0) tiles = std::min<int64_t>(tiles, int64_t(256) * per_cu);
   return static_cast<unsigned>(tiles);
 }
@@ -2440,7 +2455,7 @@ static unsigned persistent_grid(int64_t tiles, int per_cu) {
 // BK-deep DMA stages (NS of them when BK = 32).
 template <int BM, int BN, int WM, int NS, int BK, bool BF16, bool DIRECT>
 static void launch_prefill_tile(const QkvPlan& p, const GemmArgs& g, const QkvEpi& e, hipStream_t st) {
-  const unsigned grid = persistent_grid(cdiv(g.m, BM) * cdiv(g.n, BN), BM == 256 && BN == 256 ? 1 : 0);
+  const unsigned grid = persistent_grid(cdiv(g.m, BM) * cdiv(g.n, BN), BM == 256 && BN == 256);
   const dim3 block((BM / WM) * (BN / 128) * 64);
   const int edt = fused_edt(e);
   if (!p.fused_epi) {
@@ -2459,7 +2474,7 @@ static void launch_prefill_tile(const QkvPlan& p, const GemmArgs& g, const QkvEp
 template <int BM, int BN, int WM, int NS, int BK, bool BF16, bool DIRECT>
 static void launch_linear_tile(const GemmArgs& g, const QkvEpi& e, bool swiglu, hipStream_t st) {
   const int64_t bno = swiglu ? BN / 2 : BN;
-  const unsigned grid = persistent_grid(cdiv(g.m, BM) * cdiv(g.n, bno), BM == 256 && BN == 256 ? 1 : 0);
+  const unsigned grid = persistent_grid(cdiv(g.m, BM) * cdiv(g.n, bno), BM == 256 && BN == 256);
   const dim3 block((BM / WM) * (BN / 128) * 64);
   if constexpr (BF16 && DIRECT) {
     if (linear_edt(e) == EDT_BF16) {
