@@ -107,11 +107,9 @@ __global__ __launch_bounds__(256) void qkv_gemv_kernel(GemvKArgs c) {
       xr[t][j] = load16(xrow + g * 8);
     }
   }
-  // ---- the first weight batch
-  uint4 wb[SB];
-#pragma unroll
-  for (int i = 0; i < SB; ++i) wb[i] = load16(wrow + static_cast<int64_t>(s0 + min(i, ns - 1)) * 32);
-  // ---- the fold's gamma granules (16 bytes, or 32 for fp32)
+  // ---- the fold's gamma granules (16 bytes, or 32 for fp32), requested ahead of
+  //      the weights: loads complete in order, so the fold then waits for the
+  //      operand rows and gamma alone and runs while the weight batch streams in
   if constexpr (FOLD) {
     const bool g32 = c.gamma_dt == BFA_DTYPE_F32;
 #pragma unroll
@@ -126,6 +124,10 @@ __global__ __launch_bounds__(256) void qkv_gemv_kernel(GemvKArgs c) {
   const uint32_t bw1 = ld_word(c.bias ? c.bias : own, bdt, c.bias ? ec1 : 0);
   const uint32_t bw2 = ld_word(c.bias ? c.bias : own, bdt, c.bias ? ec2 : 0);
   const int64_t so_raw = (app ? c.slot_off : reinterpret_cast<const int64_t*>(own))[app ? et : 0];
+  // ---- the first weight batch
+  uint4 wb[SB];
+#pragma unroll
+  for (int i = 0; i < SB; ++i) wb[i] = load16(wrow + static_cast<int64_t>(s0 + min(i, ns - 1)) * 32);
   // the cos/sin values (they wait for the position only)
   const int64_t praw = c.pos_is_i64 ? static_cast<int64_t>((static_cast<uint64_t>(static_cast<uint32_t>(phi)) << 32) |
                                                            static_cast<uint32_t>(plo))
@@ -199,9 +201,11 @@ __global__ __launch_bounds__(256) void qkv_gemv_kernel(GemvKArgs c) {
   __syncthreads();
 
   // ---- the projection: S / 4 steps per wave, weight batches of SB steps
-  gemv_f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+  // two accumulators, even and odd steps, so that consecutive MFMAs do not
+  // wait for each other's result; summed once at the end
+  gemv_f32x4_t acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
   const int arow = fr < TM ? fr : 0;  // A rows past TM read row 0 and are zeroed
-  auto step = [&](int s, const uint4& bfrag) {
+  auto step = [&](int s, const uint4& bfrag, gemv_f32x4_t& acc) {
     uint4 afrag = *reinterpret_cast<const uint4*>(xs + arow * XP + s * 32 + fq * 8);
     if (fr >= TM) afrag = make_uint4(0, 0, 0, 0);
     acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(gemv_bf16x8_t, afrag),
@@ -214,15 +218,33 @@ __global__ __launch_bounds__(256) void qkv_gemv_kernel(GemvKArgs c) {
 #pragma unroll
       for (int i = 0; i < SB; ++i) wn[i] = load16(wrow + static_cast<int64_t>(s0 + min(i0 + SB + i, ns - 1)) * 32);
     }
+    if (i0 + SB <= ns) {
+      // a whole batch: no per-step test, so the operand reads from LDS all go
+      // out ahead of the MFMAs instead of one round trip per step
+      uint4 af[SB];
 #pragma unroll
-    for (int i = 0; i < SB; ++i)
-      if (i0 + i < ns) step(s0 + i0 + i, wb[i]);
+      for (int i = 0; i < SB; ++i) {
+        af[i] = *reinterpret_cast<const uint4*>(xs + arow * XP + (s0 + i0 + i) * 32 + fq * 8);
+        if (fr >= TM) af[i] = make_uint4(0, 0, 0, 0);
+      }
+#pragma unroll
+      for (int i = 0; i < SB; ++i) {
+        gemv_f32x4_t& acc = (i & 1) ? acc1 : acc0;
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(gemv_bf16x8_t, af[i]),
+                                                      __builtin_bit_cast(gemv_bf16x8_t, wb[i]), acc, 0, 0, 0);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < SB; ++i)
+        if (i0 + i < ns) step(s0 + i0 + i, wb[i], (i & 1) ? acc1 : acc0);
+    }
     if (more) {
 #pragma unroll
       for (int i = 0; i < SB; ++i) wb[i] = wn[i];
     }
   }
   // D layout: lane l holds D[4 (l / 16) + i][l % 16] (token, group column)
+  const gemv_f32x4_t acc = acc0 + acc1;
 #pragma unroll
   for (int i = 0; i < 4; ++i) red[wid][4 * fq + i][fr] = acc[i];
   __syncthreads();
