@@ -81,6 +81,34 @@ __device__ __forceinline__ int head_kind(const QkvEpi& e, int64_t head) {
 }
 
 // Position p wrapped like a torch negative index; -1 when outside the table.
+// Element i of a vector of run-time dtype (fp32, bf16 or fp16) in two steps: the
+// 4-byte word holding it (ld_word), then its value (word_value).  The load has
+// no branch, so it issues with its neighbours; the conversion, which the
+// compiler may branch on, comes after every load is out.  A 16-bit element is
+// read as the aligned 4-byte word that contains it (whatever the vector's own
+// alignment), so the word never crosses an aligned 4-byte block of the vector.
+__device__ __forceinline__ uint32_t ld_word(const void* p, int dt, int64_t i) {
+  const uintptr_t a = reinterpret_cast<uintptr_t>(p) + static_cast<uintptr_t>(dt == BFA_DTYPE_F32 ? i * 4 : i * 2);
+  return *reinterpret_cast<const uint32_t*>(dt == BFA_DTYPE_F32 ? a : (a & ~uintptr_t(3)));
+}
+__device__ __forceinline__ float word_value(uint32_t w, int dt, const void* p, int64_t i) {
+  const bool hi = ((reinterpret_cast<uintptr_t>(p) >> 1) + static_cast<uintptr_t>(i)) & 1;
+  const uint32_t h = hi ? (w >> 16) : (w & 0xffffu);
+  return dt == BFA_DTYPE_F32 ? __uint_as_float(w) : (dt == BFA_DTYPE_BF16 ? bf16_bits_to_f32(h) : f16_bits_to_f32(h));
+}
+// The same for a vector whose base is 4-byte aligned (checked by the caller's
+// host side): the word offset comes from the index alone, which keeps the
+// address arithmetic to one select (the one-launch decode kernel's compiler
+// schedule depends on it: a wider select there cost it its early loads).
+__device__ __forceinline__ uint32_t ld_word_al4(const void* p, int dt, int64_t i) {
+  return *reinterpret_cast<const uint32_t*>(static_cast<const char*>(p) +
+                                            (dt == BFA_DTYPE_F32 ? i * 4 : (i * 2) & ~int64_t(3)));
+}
+__device__ __forceinline__ float word_value_al4(uint32_t w, int dt, int64_t i) {
+  const uint32_t h = (i & 1) ? (w >> 16) : (w & 0xffffu);
+  return dt == BFA_DTYPE_F32 ? __uint_as_float(w) : (dt == BFA_DTYPE_BF16 ? bf16_bits_to_f32(h) : f16_bits_to_f32(h));
+}
+
 __device__ __forceinline__ int32_t epi_pos_check(const QkvEpi& e, int64_t p) {
   if (p < 0) p += e.max_pos;
   return (p >= 0 && p < e.max_pos) ? static_cast<int32_t>(p) : -1;

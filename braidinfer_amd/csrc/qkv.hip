@@ -2103,87 +2103,124 @@ __global__ __launch_bounds__(256) void qkv_decode_pair_kernel(DecodeArgs d, QkvE
 // ============================================== reduction + row epilogue
 // One wave per (token, head).  v = sum over splits of part[s, t, col] (+bias),
 // then the same rounding / norm / RoPE chain as the in-register epilogue.
+// MAXP: RoPE pairs per lane (head_dim <= 128 MAXP).
+template <int MAXP>
 __device__ __forceinline__ void row_epilogue_item(const float* part, int64_t splits, int64_t m,
-                                                           const QkvEpi& e, int64_t t, int64_t h,
-                                                           int lane) {
-  constexpr int MAXP = 4;  // pairs per lane: head_dim <= 2*64*MAXP
+                                                  const QkvEpi& e, int64_t t, int64_t h, int lane) {
+  constexpr int SG = 8;    // splits whose partials are requested together
   const int64_t half = e.hd / 2;
   const int kd = head_kind(e, h);
   const int64_t base = h * e.hd;
-  float x1[MAXP], x2[MAXP];
-  int dt = e.qkv_dt;
-  float ss = 0.f;
-  // fused KV append: this token's cache slot
+  const void* nw = kd == 0 ? e.qn_w : (kd == 1 ? e.kn_w : nullptr);
+  const bool norm = kd != 2 && (e.qn_w || e.kn_w);
+  const bool rope = kd != 2 && e.cs;
   const bool app = e.cache != nullptr && kd != 0;
-  const int64_t so = app ? e.slot_off[t] : -1;
+  // Every load goes out before any value is used, unconditionally at clamped
+  // indices (absent inputs read a stand-in that is masked afterwards), so that
+  // each use waits for its own loads only: the position first (the cos/sin
+  // rows wait for it alone), then the cache slot, the bias and norm-weight
+  // words, and the first SG splits' partials.
+  const float* pr = part + t * e.n + base;
+  const int32_t* p32 = static_cast<const int32_t*>(rope ? e.positions : static_cast<const void*>(pr));
+  const int32_t plo = p32[!rope ? 0 : (e.pos_is_i64 ? 2 * t : t)];
+  const int32_t phi = p32[!rope ? 0 : (e.pos_is_i64 ? 2 * t + 1 : t)];
+  const int64_t so_raw = (app ? e.slot_off : reinterpret_cast<const int64_t*>(part))[app ? t : 0];
+  int64_t jj[MAXP];
+  bool jin[MAXP];
+  uint32_t bw1[MAXP], bw2[MAXP], nw1[MAXP], nw2[MAXP];
+  const int bdt = e.bias ? e.bias_dtype : BFA_DTYPE_F32;
+  const int ndt = nw ? e.qk_w_dtype : BFA_DTYPE_F32;
 #pragma unroll
   for (int p = 0; p < MAXP; ++p) {
-    const int64_t j = lane + 64 * p;
-    x1[p] = x2[p] = 0.f;
-    if (j < half) {
-      // issue the loads of all splits before summing (latency, not bandwidth, bound)
-      float s1 = 0.f, s2 = 0.f;
-      const float* pr = part + t * e.n + base;
-      const int64_t stride = m * e.n;
-      for (int64_t sp0 = 0; sp0 < splits; sp0 += 8) {
-        float v1[8], v2[8];
-#pragma unroll
-        for (int u = 0; u < 8; ++u) {
-          const bool in = sp0 + u < splits;
-          v1[u] = in ? pr[(sp0 + u) * stride + j] : 0.f;
-          v2[u] = in ? pr[(sp0 + u) * stride + half + j] : 0.f;
-        }
-#pragma unroll
-        for (int u = 0; u < 8; ++u) {
-          s1 += v1[u];
-          s2 += v2[u];
-        }
-      }
-      if (e.bias) {
-        s1 += load_any(e.bias, e.bias_dtype, base + j);
-        s2 += load_any(e.bias, e.bias_dtype, base + half + j);
-      }
-      x1[p] = round_to(s1, e.qkv_dt);
-      x2[p] = round_to(s2, e.qkv_dt);
-      ss += x1[p] * x1[p] + x2[p] * x2[p];
-    }
+    jin[p] = lane + 64 * p < half;
+    jj[p] = jin[p] ? lane + 64 * p : 0;
+    bw1[p] = ld_word(e.bias ? e.bias : static_cast<const void*>(pr), bdt, e.bias ? base + jj[p] : 0);
+    bw2[p] = ld_word(e.bias ? e.bias : static_cast<const void*>(pr), bdt, e.bias ? base + half + jj[p] : 0);
+    nw1[p] = ld_word(nw ? nw : static_cast<const void*>(pr), ndt, nw ? jj[p] : 0);
+    nw2[p] = ld_word(nw ? nw : static_cast<const void*>(pr), ndt, nw ? half + jj[p] : 0);
   }
-  const void* nw = kd == 0 ? e.qn_w : (kd == 1 ? e.kn_w : nullptr);
-  if (kd != 2 && (e.qn_w || e.kn_w)) {
+  const int64_t stride = m * e.n;
+  float s1[MAXP], s2[MAXP];
+#pragma unroll
+  for (int p = 0; p < MAXP; ++p) s1[p] = s2[p] = 0.f;
+  float v1[SG][MAXP], v2[SG][MAXP];
+  auto load_group = [&](int64_t sp0) {
+#pragma unroll
+    for (int u = 0; u < SG; ++u) {
+      const int64_t sp = min(sp0 + u, splits - 1);
+#pragma unroll
+      for (int p = 0; p < MAXP; ++p) {
+        v1[u][p] = pr[sp * stride + jj[p]];
+        v2[u][p] = pr[sp * stride + half + jj[p]];
+      }
+    }
+  };
+  load_group(0);
+  // the cos/sin values (they wait for the position only)
+  const int64_t praw = e.pos_is_i64 ? static_cast<int64_t>((static_cast<uint64_t>(static_cast<uint32_t>(phi)) << 32) |
+                                                           static_cast<uint32_t>(plo))
+                                    : static_cast<int64_t>(plo);
+  const int32_t pc = rope ? epi_pos_check(e, praw) : 0;
+  const float* csr = rope ? e.cs + static_cast<int64_t>(pc >= 0 ? pc : 0) * e.hd : pr;
+  float cv[MAXP], sv[MAXP];
+#pragma unroll
+  for (int p = 0; p < MAXP; ++p) {
+    cv[p] = csr[rope ? jj[p] : 0];
+    sv[p] = csr[rope ? half + jj[p] : 0];
+  }
+  // the split sums, in split order
+  for (int64_t sp0 = 0;;) {
+#pragma unroll
+    for (int u = 0; u < SG; ++u) {
+      const bool in = sp0 + u < splits;
+#pragma unroll
+      for (int p = 0; p < MAXP; ++p) {
+        s1[p] += in ? v1[u][p] : 0.f;
+        s2[p] += in ? v2[u][p] : 0.f;
+      }
+    }
+    sp0 += SG;
+    if (sp0 >= splits) break;
+    load_group(sp0);
+  }
+  int dt = e.qkv_dt;
+  float x1[MAXP], x2[MAXP], ss = 0.f;
+#pragma unroll
+  for (int p = 0; p < MAXP; ++p) {
+    const float b1 = e.bias ? word_value(bw1[p], bdt, e.bias, base + jj[p]) : 0.f;
+    const float b2 = e.bias ? word_value(bw2[p], bdt, e.bias, base + half + jj[p]) : 0.f;
+    x1[p] = jin[p] ? round_to(s1[p] + b1, e.qkv_dt) : 0.f;
+    x2[p] = jin[p] ? round_to(s2[p] + b2, e.qkv_dt) : 0.f;
+    ss += x1[p] * x1[p] + x2[p] * x2[p];
+  }
+  if (norm) {
     ss = wave_sum_dpp(ss);
     if (nw) {
       const float r = __builtin_amdgcn_rsqf(ss / static_cast<float>(e.hd) + e.qk_eps);
 #pragma unroll
       for (int p = 0; p < MAXP; ++p) {
-        const int64_t j = lane + 64 * p;
-        if (j < half) {
-          x1[p] = round_to((x1[p] * r) * load_any(nw, e.qk_w_dtype, j), e.norm_dt);
-          x2[p] = round_to((x2[p] * r) * load_any(nw, e.qk_w_dtype, half + j), e.norm_dt);
-        }
+        x1[p] = round_to((x1[p] * r) * word_value(nw1[p], ndt, nw, jj[p]), e.norm_dt);
+        x2[p] = round_to((x2[p] * r) * word_value(nw2[p], ndt, nw, half + jj[p]), e.norm_dt);
       }
       dt = e.norm_dt;
     }
   }
-  if (kd != 2 && e.cs) {
-    bool ok;
-    const int64_t pos = epi_position(e, t, ok);
+  if (rope) {
+    const bool ok = pc >= 0;
     if (!ok && h == 0 && lane == 0) flag_status(e.status, BFA_STATUS_INDEX_OOB);
 #pragma unroll
     for (int p = 0; p < MAXP; ++p) {
-      const int64_t j = lane + 64 * p;
-      if (j < half) {
-        const float c = e.cs[pos * e.hd + j], s = e.cs[pos * e.hd + half + j];
-        const float a = x1[p], b = x2[p];
-        x1[p] = ok ? round_to(a * c - b * s, dt) : 0.f;
-        x2[p] = ok ? round_to(b * c + a * s, dt) : 0.f;
-      }
+      const float a = x1[p], b = x2[p];
+      x1[p] = ok ? round_to(a * cv[p] - b * sv[p], dt) : 0.f;
+      x2[p] = ok ? round_to(b * cv[p] + a * sv[p], dt) : 0.f;
     }
   }
+  const int64_t so = app ? so_raw : -1;
   const int64_t cb = so + (kd == 2 ? e.c_skv : 0) + (h - e.hq - (kd == 2 ? e.hkv : 0)) * e.c_sh;
 #pragma unroll
   for (int p = 0; p < MAXP; ++p) {
-    const int64_t j = lane + 64 * p;
-    if (j < half) {
+    const int64_t j = jj[p];
+    if (jin[p]) {
       if (kd == 0 || !e.skip_kv_out) {
         store_any(e.out, e.out_dt, t * e.ldo + base + j, x1[p]);
         store_any(e.out, e.out_dt, t * e.ldo + base + half + j, x2[p]);
@@ -2196,13 +2233,17 @@ __device__ __forceinline__ void row_epilogue_item(const float* part, int64_t spl
   }
 }
 
+template <int MAXP>
 __global__ __launch_bounds__(256) void qkv_epilogue_kernel(const float* part, int64_t splits,
                                                            int64_t m, QkvEpi e) {
   const int64_t heads = e.hq + 2 * e.hkv;
-  const int64_t item = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  // wave-uniform (scalar) item, so the head kind and its flags are too: a
+  // divergent-looking test would let the compiler sink loads into it and wait
+  // for every load at its end
+  const int64_t item = static_cast<int64_t>(blockIdx.x) * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   if (item >= m * heads) return;
   const int64_t t = item / heads;
-  row_epilogue_item(part, splits, m, e, t, item - t * heads, threadIdx.x & 63);
+  row_epilogue_item<MAXP>(part, splits, m, e, t, item - t * heads, threadIdx.x & 63);
 }
 
 // ================================================================== host
@@ -2591,8 +2632,10 @@ static void launch_pair(const QkvPlan& p, const DecodeArgs& d, const QkvEpi& e, 
 static void launch_epilogue(const float* part, int64_t splits, int64_t m, const QkvEpi& e,
                             hipStream_t st) {
   const int64_t items = m * (e.hq + 2 * e.hkv);
-  hipLaunchKernelGGL(qkv_epilogue_kernel, dim3(static_cast<unsigned>(cdiv(items, 4))), dim3(256),
-                     0, st, part, splits, m, e);
+  const dim3 grid(static_cast<unsigned>(cdiv(items, 4)));
+  if (e.hd <= 128) hipLaunchKernelGGL(qkv_epilogue_kernel<1>, grid, dim3(256), 0, st, part, splits, m, e);
+  else if (e.hd <= 256) hipLaunchKernelGGL(qkv_epilogue_kernel<2>, grid, dim3(256), 0, st, part, splits, m, e);
+  else hipLaunchKernelGGL(qkv_epilogue_kernel<4>, grid, dim3(256), 0, st, part, splits, m, e);
 }
 
 }  // namespace bfa

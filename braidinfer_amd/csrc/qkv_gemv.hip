@@ -20,21 +20,6 @@
 
 namespace bfa {
 
-// Element i of a vector of run-time dtype (fp32, bf16 or fp16) in two steps: the
-// 4-byte word holding it (ld_word), then its value (word_value).  The load has
-// no branch, so it issues with its neighbours; the conversion, which the
-// compiler may branch on, comes after every load is out.  The base is 4-byte
-// aligned and a 16-bit vector has an even length, so the word never reaches
-// past the vector.
-__device__ __forceinline__ uint32_t ld_word(const void* p, int dt, int64_t i) {
-  return *reinterpret_cast<const uint32_t*>(static_cast<const char*>(p) +
-                                            (dt == BFA_DTYPE_F32 ? i * 4 : (i * 2) & ~int64_t(3)));
-}
-__device__ __forceinline__ float word_value(uint32_t w, int dt, int64_t i) {
-  const uint32_t h = (i & 1) ? (w >> 16) : (w & 0xffffu);
-  return dt == BFA_DTYPE_F32 ? __uint_as_float(w) : (dt == BFA_DTYPE_BF16 ? bf16_bits_to_f32(h) : f16_bits_to_f32(h));
-}
-
 typedef __attribute__((ext_vector_type(8))) __bf16 gemv_bf16x8_t;
 typedef __attribute__((ext_vector_type(4))) float gemv_f32x4_t;
 
@@ -121,8 +106,8 @@ __global__ __launch_bounds__(256) void qkv_gemv_kernel(GemvKArgs c) {
     }
   }
   const int bdt = c.bias ? c.bias_dt : BFA_DTYPE_BF16;
-  const uint32_t bw1 = ld_word(c.bias ? c.bias : own, bdt, c.bias ? ec1 : 0);
-  const uint32_t bw2 = ld_word(c.bias ? c.bias : own, bdt, c.bias ? ec2 : 0);
+  const uint32_t bw1 = ld_word_al4(c.bias ? c.bias : own, bdt, c.bias ? ec1 : 0);
+  const uint32_t bw2 = ld_word_al4(c.bias ? c.bias : own, bdt, c.bias ? ec2 : 0);
   const int64_t so_raw = (app ? c.slot_off : reinterpret_cast<const int64_t*>(own))[app ? et : 0];
   // ---- the first weight batch
   uint4 wb[SB];
@@ -137,7 +122,7 @@ __global__ __launch_bounds__(256) void qkv_gemv_kernel(GemvKArgs c) {
   const float* csr = rope ? c.cs + static_cast<int64_t>(pc >= 0 ? pc : 0) * hd : reinterpret_cast<const float*>(own);
   const float cv = csr[rope ? c0 + ep_p : 0];
   const float sv = csr[rope ? half + c0 + ep_p : 0];
-  const float b1 = c.bias ? word_value(bw1, bdt, ec1) : 0.f, b2 = c.bias ? word_value(bw2, bdt, ec2) : 0.f;
+  const float b1 = c.bias ? word_value_al4(bw1, bdt, ec1) : 0.f, b2 = c.bias ? word_value_al4(bw2, bdt, ec2) : 0.f;
   const int64_t so = app ? so_raw : -1;
 
   // ---- operand rows -> LDS (normalised by the fold: round(x / rms(x) * gamma),
