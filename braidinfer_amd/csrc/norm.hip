@@ -40,15 +40,27 @@ struct NormArgs {
   float eps;
 };
 
-__device__ __forceinline__ void load8_dyn(const void* p, int dt, int64_t i, float (&v)[8]) {
-  if (dt == BFA_DTYPE_BF16) {
-    load8<BFA_DTYPE_BF16>(static_cast<const uint16_t*>(p) + i, v);
-  } else if (dt == BFA_DTYPE_F16) {
-    load8<BFA_DTYPE_F16>(static_cast<const uint16_t*>(p) + i, v);
-  } else {
-    load8<BFA_DTYPE_F32>(static_cast<const float*>(p) + i, v);
+// Elements 8 g .. 8 g + 7 of a 16-byte aligned vector of run-time dtype in two
+// steps: the raw 16 (fp32: 32) bytes, requested without a branch on the dtype,
+// then their values.
+struct Raw8Dyn {
+  uint4 w0, w1;
+  __device__ __forceinline__ void load(const void* p, int dt, int64_t g) {
+    const bool f32 = dt == BFA_DTYPE_F32;
+    const char* q = static_cast<const char*>(p) + g * (f32 ? 32 : 16);
+    w0 = *reinterpret_cast<const uint4*>(q);
+    w1 = *reinterpret_cast<const uint4*>(f32 ? q + 16 : q);
   }
-}
+  __device__ __forceinline__ void to_f32(int dt, float (&v)[8]) const {
+    const uint32_t u[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const uint16_t h = static_cast<uint16_t>((i & 1) ? (u[i / 2] >> 16) : (u[i / 2] & 0xffffu));
+      v[i] = dt == BFA_DTYPE_F32 ? __uint_as_float(u[i])
+                                 : (dt == BFA_DTYPE_BF16 ? bf16_bits_to_f32(h) : f16_bits_to_f32(h));
+    }
+  }
+};
 
 // Applies the mode's normalisation to one value.  `inv` = 1 / sqrt(sum/H + eps)
 // for every mode: the torch chain multiplies by rsqrt(var + eps), and the
@@ -93,6 +105,11 @@ __global__ __launch_bounds__(256) void norm_vec_kernel(NormArgs a) {
 
   float v[MAXC][8];
   float ss = 0.f;
+  // the norm weight's granules go out with the row (raw, converted after the
+  // sum): requested after the reduction they were a second memory round trip
+  Raw8Dyn gw[MAXC];
+#pragma unroll
+  for (int c = 0; c < MAXC; ++c) gw[c].load(a.w, a.w_dtype, min(lane + c * L, nchunks - 1));
 #pragma unroll
   for (int c = 0; c < MAXC; ++c) {
     const int ch = lane + c * L;
@@ -125,7 +142,7 @@ __global__ __launch_bounds__(256) void norm_vec_kernel(NormArgs a) {
     const int ch = lane + c * L;
     if (ch < nchunks) {
       float g[8], o[8];
-      load8_dyn(a.w, a.w_dtype, static_cast<int64_t>(ch) * 8, g);
+      gw[c].to_f32(a.w_dtype, g);
 #pragma unroll
       for (int i = 0; i < 8; ++i) o[i] = norm_apply<DT_IN, MODE>(v[c][i], inv, g[i]);
       store8<DT_OUT>(yp + ch * 8, o);
