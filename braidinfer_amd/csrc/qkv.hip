@@ -478,16 +478,19 @@ __device__ __forceinline__ void gemm_epilogue(f32x16_t (&acc)[MB][NB], uint4* ld
     }
   } else {
     static_assert(HD == 32 || HD == 64 || HD == 128, "fused epilogue covers head_dim 32/64/128");
-    static_assert(WN == 128, "the row epilogue maps 16 lanes x 8 columns onto 128 columns");
+    static_assert(WN == 128 || (WN == 64 && HD <= 64), "a wave tile holds whole heads");
     // Each 32-row accumulator block is staged through this wave's slice of the
-    // (now idle) LDS, then processed row by row: 16 lanes per row, each lane
+    // (now idle) LDS, then processed row by row: WN / 8 lanes per row, each lane
     // owning 4 RoPE pairs (columns j..j+3 and j+D/2..j+D/2+3 of one head), so
     // the q/k norm is a butterfly over the D/8 lanes of a head and every store
     // is a contiguous 4-element vector.
-    constexpr int LH = HD / 8;  // lanes per head
+    constexpr int LH = HD / 8;      // lanes per head
+    constexpr int LPR = WN / 8;     // lanes per row (16 or 8)
+    constexpr int RPP = 64 / LPR;   // rows per pass (4 or 8)
+    constexpr int NP = 32 / RPP;    // passes per 32-row block (8 or 4)
     float* et = reinterpret_cast<float*>(lds) + wid * (32 * LDR);
-    const int l16 = lane & 15, rg = lane >> 4;
-    const int hloc = l16 / LH, q = l16 % LH;
+    const int lr = lane % LPR, rg = lane / LPR;
+    const int hloc = lr / LH, q = lr % LH;
     const int c1 = hloc * HD + q * 4, c2 = c1 + HD / 2;  // columns inside the wave tile
     const int64_t gc1 = wcol0 + c1, gc2 = wcol0 + c2;
     const bool colok = gc1 < e.n;
@@ -517,25 +520,25 @@ __device__ __forceinline__ void gemm_epilogue(f32x16_t (&acc)[MB][NB], uint4* ld
     // batch of independent loads) so that each row iteration has a single
     // dependent load level (its cos/sin) instead of two; -1 marks a position
     // outside the table.
-    int32_t posv[MB][8];
+    int32_t posv[MB][NP];
     if constexpr (EARLY_POS) {
       if (rope) {
 #pragma unroll
-        for (int it = 0; it < 8; ++it) posv[0][it] = epi_pos_check(e, praw[it]);
+        for (int it = 0; it < NP; ++it) posv[0][it] = epi_pos_check(e, praw[it]);
       }
     } else if (rope) {
       if (e.pos_is_i64) {
 #pragma unroll
         for (int i = 0; i < MB; ++i)
 #pragma unroll
-          for (int it = 0; it < 8; ++it)
-            posv[i][it] = epi_pos_check(e, static_cast<const int64_t*>(e.positions)[min(wrow0 + i * 32 + rg + 4 * it, g.m - 1)]);
+          for (int it = 0; it < NP; ++it)
+            posv[i][it] = epi_pos_check(e, static_cast<const int64_t*>(e.positions)[min(wrow0 + i * 32 + rg + RPP * it, g.m - 1)]);
       } else {
 #pragma unroll
         for (int i = 0; i < MB; ++i)
 #pragma unroll
-          for (int it = 0; it < 8; ++it)
-            posv[i][it] = epi_pos_check(e, static_cast<const int32_t*>(e.positions)[min(wrow0 + i * 32 + rg + 4 * it, g.m - 1)]);
+          for (int it = 0; it < NP; ++it)
+            posv[i][it] = epi_pos_check(e, static_cast<const int32_t*>(e.positions)[min(wrow0 + i * 32 + rg + RPP * it, g.m - 1)]);
       }
     }
     __syncthreads();
@@ -551,10 +554,10 @@ __device__ __forceinline__ void gemm_epilogue(f32x16_t (&acc)[MB][NB], uint4* ld
     // accumulators are staged (their registers are free) and before block i's
     // stores: requested after them, their wait would also wait for every store
     // of block i, which all CUs issue at once.
-    float4 cvv[2][8], svv[2][8];
-    auto load_cs = [&](int i, float4 (&cv)[8], float4 (&sv)[8]) {
+    float4 cvv[2][NP], svv[2][NP];
+    auto load_cs = [&](int i, float4 (&cv)[NP], float4 (&sv)[NP]) {
 #pragma unroll
-      for (int it = 0; it < 8; ++it) {
+      for (int it = 0; it < NP; ++it) {
         const int64_t p = posv[i][it] >= 0 ? posv[i][it] : 0;
         cv[it] = *reinterpret_cast<const float4*>(e.cs + p * HD + q * 4);
         sv[it] = *reinterpret_cast<const float4*>(e.cs + p * HD + HD / 2 + q * 4);
@@ -563,8 +566,8 @@ __device__ __forceinline__ void gemm_epilogue(f32x16_t (&acc)[MB][NB], uint4* ld
     if (rope) load_cs(0, cvv[0], svv[0]);
 #pragma unroll
     for (int i = 0; i < MB; ++i) {
-      float4 (&cvv_i)[8] = cvv[i & 1];
-      float4 (&svv_i)[8] = svv[i & 1];
+      float4 (&cvv_i)[NP] = cvv[i & 1];
+      float4 (&svv_i)[NP] = svv[i & 1];
 #pragma unroll
       for (int j = 0; j < NB; ++j)
 #pragma unroll
@@ -578,8 +581,8 @@ __device__ __forceinline__ void gemm_epilogue(f32x16_t (&acc)[MB][NB], uint4* ld
       if (rope && i + 1 < MB) load_cs(i + 1, cvv[(i + 1) & 1], svv[(i + 1) & 1]);
       bool bad = false;
 #pragma unroll
-      for (int it = 0; it < 8; ++it) {
-        const int rl = rg + 4 * it;
+      for (int it = 0; it < NP; ++it) {
+        const int rl = rg + RPP * it;
         const int64_t row = wrow0 + i * 32 + rl;
         const float4 a1 = *reinterpret_cast<const float4*>(et + rl * LDR + c1);
         const float4 a2 = *reinterpret_cast<const float4*>(et + rl * LDR + c2);
@@ -728,16 +731,17 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, (WM * WN <= 8192 ? 2 : 
   // requested here, before the K loop (16 registers), so that the epilogue's
   // cos/sin loads do not wait a memory round trip for them.
   constexpr bool EARLY_POS = EPI == EPI_FUSED && MB == 1;
-  int64_t praw[EARLY_POS ? 8 : 1];
+  constexpr int ERPP = 64 / (WN / 8), ENP = 32 / ERPP;  // the epilogue's rows per pass and passes
+  int64_t praw[EARLY_POS ? ENP : 1];
   if constexpr (EARLY_POS) {
-    const int64_t r0 = m0 + wm * WM + (lane >> 4);
+    const int64_t r0 = m0 + wm * WM + lane / (WN / 8);
     if (e.cs != nullptr) {
       if (e.pos_is_i64) {
 #pragma unroll
-        for (int it = 0; it < 8; ++it) praw[it] = static_cast<const int64_t*>(e.positions)[min(r0 + 4 * it, g.m - 1)];
+        for (int it = 0; it < ENP; ++it) praw[it] = static_cast<const int64_t*>(e.positions)[min(r0 + ERPP * it, g.m - 1)];
       } else {
 #pragma unroll
-        for (int it = 0; it < 8; ++it) praw[it] = static_cast<const int32_t*>(e.positions)[min(r0 + 4 * it, g.m - 1)];
+        for (int it = 0; it < ENP; ++it) praw[it] = static_cast<const int32_t*>(e.positions)[min(r0 + ERPP * it, g.m - 1)];
       }
     }
   }
@@ -2254,7 +2258,7 @@ struct QkvPlan {
   int64_t splits;
   int64_t kchunk;
   bool fused_epi;  // prefill: in-register epilogue
-  int tile;        // prefill: 2 (256x256, 8 waves), 3 (128x256, 8 waves), 1 (128x256, 4 waves), 128
+  int tile;        // prefill: 2 (256x256, 8 waves), 3 (128x256, 8 waves), 1 (128x256, 4 waves), 128, 64 (128x64)
   bool stream;     // decode: weight-streaming kernel (k % 64 == 0)
   int ks;          // decode stream: 64-deep K segments per split
   int nch;         // decode stream: 256-deep chunks per split of the deep-K form (0: not used)
@@ -2340,9 +2344,14 @@ static QkvPlan make_plan(int64_t m, int64_t n, int64_t k, int64_t hd) {
     if (cdiv(m, 256) * cdiv(n, 256) >= 256) p.tile = 2;
     else if (cdiv(m, 128) * cdiv(n, 256) >= 192) p.tile = 3;
     else p.tile = 128;
+    // Under 128 tiles of 128x128 most CUs would idle, and each busy one is
+    // bound by its LDS traffic: for heads of up to 64 columns 128x64 tiles put
+    // twice the CUs on the product (TinyLlama, 512 tokens: 80 -> 160 tiles).
+    const bool narrow_ok = p.fused_epi && hd <= 64;
+    if (p.tile == 128 && narrow_ok && cdiv(m, 128) * cdiv(n, 128) < 128) p.tile = 64;
     {
       const int v = tuning(BFA_TUNE_QKV_TILE);
-      if ((v >= 1 && v <= 3) || v == 128) p.tile = v;
+      if ((v >= 1 && v <= 3) || v == 128 || (v == 64 && narrow_ok)) p.tile = v;
     }
     p.splits = 1;
     p.part_bytes = p.fused_epi ? 0 : align256(m * n * 4);
@@ -2511,6 +2520,27 @@ static void launch_prefill_tile(const QkvPlan& p, const GemmArgs& g, const QkvEp
   }
 }
 
+// 128x64 tile: four waves of 32x64, a ring of four 32-deep DMA stages, the
+// fused epilogue with 8 lanes per row (head_dim 32 or 64).
+template <bool BF16, int HD>
+static void launch_prefill_narrow_hd(const GemmArgs& g, const QkvEpi& e, hipStream_t st) {
+  const dim3 grid(static_cast<unsigned>(cdiv(g.m, 128) * cdiv(g.n, 64))), block(256);
+  const int edt = fused_edt(e);
+  if constexpr (BF16) {
+    if (edt == EDT_F32_BF16) {
+      hipLaunchKernelGGL((qkv_gemm_kernel<128, 64, 32, 64, BF16, EPI_FUSED, HD, true, 4, 32, EDT_F32_BF16>), grid,
+                         block, 0, st, g, e);
+      return;
+    }
+    if (edt == EDT_BF16) {
+      hipLaunchKernelGGL((qkv_gemm_kernel<128, 64, 32, 64, BF16, EPI_FUSED, HD, true, 4, 32, EDT_BF16>), grid,
+                         block, 0, st, g, e);
+      return;
+    }
+  }
+  hipLaunchKernelGGL((qkv_gemm_kernel<128, 64, 32, 64, BF16, EPI_FUSED, HD, true, 4, 32>), grid, block, 0, st, g, e);
+}
+
 // The linear fusions: same tiles, EPI_LINEAR or EPI_SWIGLU epilogue.
 template <int BM, int BN, int WM, int NS, int BK, bool BF16, bool DIRECT>
 static void launch_linear_tile(const GemmArgs& g, const QkvEpi& e, bool swiglu, hipStream_t st) {
@@ -2562,6 +2592,10 @@ static void launch_prefill_t(const QkvPlan& p, const GemmArgs& g, const QkvEpi& 
       case 2: launch_prefill_tile<256, 256, 64, 2, 64, BF16, true>(p, g, e, st); break;
       case 3: launch_prefill_tile<128, 256, 32, 2, 64, BF16, true>(p, g, e, st); break;
       case 1: launch_prefill_tile<128, 256, 64, 3, 32, BF16, true>(p, g, e, st); break;
+      case 64:
+        if (e.hd == 64) launch_prefill_narrow_hd<BF16, 64>(g, e, st);
+        else launch_prefill_narrow_hd<BF16, 32>(g, e, st);
+        break;
       default: launch_prefill_tile<128, 128, 32, 4, 32, BF16, true>(p, g, e, st); break;
     }
   } else {

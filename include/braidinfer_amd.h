@@ -63,7 +63,7 @@ const char* bfa_last_error(void);
 #define BFA_TUNE_DECODE_KS 0         /* BFA_DECODE_KS: 64-deep K segments per decode split (1..8) */
 #define BFA_TUNE_DECODE_WG 1         /* BFA_DECODE_WG: workgroup target of the deep-K decode form */
 #define BFA_TUNE_DECODE_SPLITS 2     /* BFA_DECODE_SPLITS: split count of the deep-K decode form */
-#define BFA_TUNE_QKV_TILE 3          /* BFA_QKV_TILE: prefill tile, 1 2 3 or 128 */
+#define BFA_TUNE_QKV_TILE 3          /* BFA_QKV_TILE: prefill tile, 1 2 3 64 or 128 (64: head_dim <= 64) */
 #define BFA_TUNE_EDT_RT 4            /* BFA_EDT_RT: non-zero = run-time epilogue dtypes only */
 #define BFA_TUNE_DECODE_PAIR 5       /* BFA_DECODE_PAIR: 0 = never the column-pair decode
                                         kernel, 1 = at any shape it supports */

@@ -345,3 +345,36 @@ def test_prefill_8192_sampled_rows(chain):
     for got, exp, name, sl in zip((q, k, v), ref, "qkv", slack):
         assert_close(got[rd], exp, what=f"{chain} 8192 {name}",
                      slack=None if sl is None else sl.reshape(exp.shape))
+
+
+@pytest.mark.parametrize("tile", [None, 128, 64])
+@pytest.mark.parametrize("t,h,hq,hkv,d", [
+    (512, 2048, 32, 4, 64),   # TinyLlama prefill: the planner takes 128x64 (160 tiles)
+    (300, 512, 8, 2, 32),     # head_dim 32 (two heads per 64-column wave), ragged rows
+    (1100, 1024, 8, 4, 64),   # nine row tiles, the last one ragged
+])
+def test_prefill_narrow_tile(tuning, tile, t, h, hq, hkv, d):
+    """The 128x64 tile (head_dim <= 64 under 128 tiles of 128x128; 8 lanes per
+    row in the fused epilogue) and the 128x128 form it replaces, each against
+    the oracle: the Llama chain, a q/k-norm chain with extreme k_norm weights
+    (rope_flip_slack as in test_qwen3_chain) and the mixed variant with bias."""
+    tuning("QKV_TILE", tile)
+    g, x, ln, w, b = make(230 + d, t, h, hq, hkv, d)
+    pos = torch.randint(0, 4096, (t,), generator=g)
+    cache = R.cos_sin_cache(d, 4096, 1e4)
+    q, k, v = llama_attention_input(x.to(DEV), ln.to(DEV), w.to(DEV), hq, hkv, 1e-5, pos.to(DEV), cache.to(DEV))
+    for got, exp, name in zip((q, k, v), R.llama_attention_input(x, ln, w, hq, hkv, 1e-5, pos, cache), "qkv"):
+        assert_close(got, exp, what=f"narrow llama {name} t={t} tile={tile}")
+    qn = randn(g, d, mean=1.0, std=0.1)
+    kn = torch.exp(torch.empty(d).uniform_(math.log(0.05), math.log(100), generator=g)).to(torch.bfloat16)
+    q, k, v = qwen3_attention_input(x.to(DEV), ln.to(DEV), w.to(DEV), None, hq, hkv, 1e-6, pos.to(DEV),
+                                    cache.to(DEV), qn.to(DEV), kn.to(DEV))
+    ref = R.qwen3_attention_input(x, ln, w, None, hq, hkv, 1e-6, pos, cache, qn, kn)
+    pq, pk = _qwen3_rope_inputs(x, ln, w, qn, kn, hq, hkv)
+    assert_close(q, ref[0], what=f"narrow q/k-norm q t={t}", slack=rope_flip_slack(pq).reshape(ref[0].shape))
+    assert_close(k, ref[1], what=f"narrow q/k-norm k t={t}", slack=rope_flip_slack(pk).reshape(ref[1].shape))
+    assert_close(v, ref[2], what=f"narrow q/k-norm v t={t}")
+    got = FusedRMSNormQKVMixedPrecision.forward(x.to(DEV), ln.to(DEV), w.to(DEV), b.to(DEV), hq, hkv, eps=1e-6)
+    for g_, exp, name in zip(got, R.split_qkv(R.qkv_mixed_precision(x, ln, w, b, 1e-6), hq, hkv), "qkv"):
+        assert_close(g_, exp, what=f"narrow mixed+bias {name} t={t}")
+    braidinfer_amd.check_device_status()
