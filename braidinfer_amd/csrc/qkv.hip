@@ -1664,6 +1664,17 @@ __global__ __launch_bounds__(256) void linear_decode_epilogue_kernel(const float
   const int64_t id = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   if (id >= cdiv(m, 4) * g.n) return;
   const int64_t tg = id / g.n, c = id - tg * g.n;
+  // the residual and bias words go out with the partials (converted after the
+  // sums): requested after them they were a second dependent memory round trip
+  uint32_t rw[4] = {0u, 0u, 0u, 0u}, bw = 0u;
+  const int rdt = e.res ? e.res_dt : BFA_DTYPE_F32, bdt = e.bias ? e.bias_dtype : BFA_DTYPE_F32;
+  if constexpr (!SWIGLU) {
+#pragma unroll
+    for (int v = 0; v < 4; ++v)
+      rw[v] = ld_word(e.res ? e.res : static_cast<const void*>(part), rdt,
+                      e.res ? min(tg * 4 + v, m - 1) * e.ldr + c : 0);
+    bw = ld_word(e.bias ? e.bias : static_cast<const void*>(part), bdt, e.bias ? c : 0);
+  }
   float acc[2][4];
 #pragma unroll
   for (int f = 0; f < 2; ++f)
@@ -1720,8 +1731,8 @@ __global__ __launch_bounds__(256) void linear_decode_epilogue_kernel(const float
       const float gt = round_to(acc[0][v], e.qkv_dt), ut = round_to(acc[1][v], e.qkv_dt);
       y = round_to(silu_fast(gt), e.qkv_dt) * ut;
     } else {
-      const float r = e.res ? load_any(e.res, e.res_dt, t * e.ldr + c) : 0.f;
-      const float b = e.bias ? load_any(e.bias, e.bias_dtype, c) : 0.f;
+      const float r = e.res ? word_value(rw[v], rdt, e.res, t * e.ldr + c) : 0.f;
+      const float b = e.bias ? word_value(bw, bdt, e.bias, c) : 0.f;
       y = round_to(round_to(acc[0][v] + b, e.qkv_dt) + r, e.mid_dt);
     }
     store_any(e.out, e.out_dt, t * e.ldo + c, y);
