@@ -2778,7 +2778,7 @@ static int qkv_projection_impl(const void* operand, int64_t lda, const OperandFo
   const hipStream_t st = as_stream(stream);
   const bool bf16 = w_dtype == BFA_DTYPE_BF16;
   float* part = static_cast<float*>(part_workspace);
-  // 1 to 8 tokens: one launch (no split-K partials); the fold's operand must be
+  // 1 to 16 tokens: one launch (no split-K partials); the fold's operand must be
   // bf16 like the weight, and the scale-after form is not used
   auto al4 = [](const void* q) { return (reinterpret_cast<uintptr_t>(q) & 3u) == 0; };
   if (p.decode && !(fold && fold->stats) && al4(bias) && al4(q_norm_weight) && al4(k_norm_weight) &&
@@ -2898,7 +2898,8 @@ static int fused_impl(const void* x, int x_dtype, int64_t tokens, int64_t hidden
   const int fold_rows = (tokens <= 4 && hidden <= 4096) ? 1
                         : (tokens <= 8 && hidden <= 2048) ? 2
                         : (tokens <= 16 && hidden <= 1024) ? 4 : 0;
-  // 1 to 8 tokens in bf16 (the one-launch kernel, qkv_gemv.hip) always fold.
+  // 1 to 16 tokens in bf16 without q/k norm (the one-launch kernel,
+  // qkv_gemv.hip) always fold: it normalises the rows into LDS itself.
   const bool gemv_fold = !no_fold && p.decode && x_dtype == BFA_DTYPE_BF16 && w_dtype == BFA_DTYPE_BF16 &&
                          aligned16(norm_weight) && is_float_dtype(nw_dtype) &&
                          gemv_ok(tokens, hidden, qkv_dim / heads, q_norm_weight || k_norm_weight, true, true, x,
