@@ -180,11 +180,12 @@ struct GemvKArgs {
   uint8_t gamma_dt, mixed, bias_dt, qkv_dt, out_dt, cache_dt, pos_is_i64, skip_kv_out;
 };
 
-// Whether the one-launch kernel takes the call: 1 to 16 tokens without q/k
-// norm, bf16 operand and weight, hidden a multiple of 128 up to 4096, head_dim
-// a multiple of 16 (planner override BFA_TUNE_DECODE_GEMV = 0: never).
-bool gemv_ok(int64_t tokens, int64_t k, int64_t hd, bool qk_norm, bool bf16_w, bool bf16_x, const void* a,
-             int64_t lda);
+// Whether the one-launch kernel takes the call: up to 4 tokens (8 when the
+// grid, n / 16 workgroups, is at most 192) without q/k norm, bf16 operand and
+// weight, hidden a multiple of 128 up to 4096, head_dim a multiple of 16, a
+// 4-byte-aligned bias (planner override BFA_TUNE_DECODE_GEMV = 0: never).
+bool gemv_ok(int64_t tokens, int64_t k, int64_t n, int64_t hd, bool qk_norm, const void* bias, bool bf16_w,
+             bool bf16_x, const void* a, int64_t lda);
 // Launches it (fold: `a` holds the raw rows and the kernel normalises them).
 void launch_qkv_gemv(GemvArgs d, bool fold, const QkvEpi& e, hipStream_t s);
 

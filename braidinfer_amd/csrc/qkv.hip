@@ -2778,11 +2778,10 @@ static int qkv_projection_impl(const void* operand, int64_t lda, const OperandFo
   const hipStream_t st = as_stream(stream);
   const bool bf16 = w_dtype == BFA_DTYPE_BF16;
   float* part = static_cast<float*>(part_workspace);
-  // 1 to 16 tokens: one launch (no split-K partials); the fold's operand must be
+  // 1 to 8 tokens: one launch (no split-K partials); the fold's operand must be
   // bf16 like the weight, and the scale-after form is not used
-  auto al4 = [](const void* q) { return (reinterpret_cast<uintptr_t>(q) & 3u) == 0; };
-  if (p.decode && !(fold && fold->stats) && al4(bias) && al4(q_norm_weight) && al4(k_norm_weight) &&
-      gemv_ok(tokens, hidden, hd, q_norm_weight || k_norm_weight, bf16, true, operand, lda)) {
+  if (p.decode && !(fold && fold->stats) &&
+      gemv_ok(tokens, hidden, qkv_dim, hd, q_norm_weight || k_norm_weight, bias, bf16, true, operand, lda)) {
     GemvArgs d{};
     d.a = static_cast<const uint16_t*>(operand);
     d.w = static_cast<const uint16_t*>(qkv_weight);
@@ -2898,12 +2897,12 @@ static int fused_impl(const void* x, int x_dtype, int64_t tokens, int64_t hidden
   const int fold_rows = (tokens <= 4 && hidden <= 4096) ? 1
                         : (tokens <= 8 && hidden <= 2048) ? 2
                         : (tokens <= 16 && hidden <= 1024) ? 4 : 0;
-  // 1 to 16 tokens in bf16 without q/k norm (the one-launch kernel,
+  // 1 to 8 tokens in bf16 without q/k norm (the one-launch kernel,
   // qkv_gemv.hip) always fold: it normalises the rows into LDS itself.
   const bool gemv_fold = !no_fold && p.decode && x_dtype == BFA_DTYPE_BF16 && w_dtype == BFA_DTYPE_BF16 &&
                          aligned16(norm_weight) && is_float_dtype(nw_dtype) &&
-                         gemv_ok(tokens, hidden, qkv_dim / heads, q_norm_weight || k_norm_weight, true, true, x,
-                                 x_stride);
+                         gemv_ok(tokens, hidden, qkv_dim, qkv_dim / heads, q_norm_weight || k_norm_weight, bias,
+                                 true, true, x, x_stride);
   const bool fold = gemv_fold ||
                     (!no_fold && fold_rows > 0 && p.decode && p.stream && p.mt == 1 && x_dtype == w_dtype &&
                      (w_dtype == BFA_DTYPE_BF16 || w_dtype == BFA_DTYPE_F16) && hidden % 8 == 0 &&

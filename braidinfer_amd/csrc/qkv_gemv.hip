@@ -1,5 +1,5 @@
 // One-launch fused RMSNorm + QKV projection (+ bias, RoPE, KV append) for 1 to
-// 16 decode tokens without q/k norm, on gfx950.
+// 8 decode tokens without q/k norm, on gfx950.
 //
 // Same reference semantics as qkv.hip (kernels/fused_rmsnorm_qkv_*.py and the
 // RoPE of layers/rotary_embedding.py:49-65, models/llama.py:169-205).  At a few
@@ -10,9 +10,7 @@
 // the fused op: round(x / rms(x) * gamma), the operand pre-pass's rounding
 // points), the weight rows stream straight into MFMA B fragments, the four
 // waves' partial tiles meet in LDS, and one thread per (token, pair) finishes.
-// Heads with q/k norm stay on the split-K path: the norm needs a head's whole
-// 128 columns, which would leave one workgroup per head streaming 256 KiB
-// (Qwen3-0.6B, one token: 12.4 us that way against 7.3 us).
+// Heads with q/k norm stay on the split-K path (gemv_ok below).
 #include "bfa_device.h"
 #include "bfa_host.h"
 #include "bfa_internal.h"
@@ -23,7 +21,7 @@ namespace bfa {
 typedef __attribute__((ext_vector_type(8))) __bf16 gemv_bf16x8_t;
 typedef __attribute__((ext_vector_type(4))) float gemv_f32x4_t;
 
-// TM: token capacity (1, 2, 4, 8 or 16; tokens <= TM).  A workgroup owns PG
+// TM: token capacity (1, 2, 4 or 8; tokens <= TM).  A workgroup owns PG
 // RoPE pairs of one head, c0 .. c0+PG-1, and their partners D/2 on: 2 PG output
 // columns (PG = 8 from the launcher; with PG = 4 the MFMA's columns 8-15 would
 // repeat 0-7 and be dropped).
@@ -260,16 +258,30 @@ __global__ __launch_bounds__(256) void qkv_gemv_kernel(GemvKArgs c) {
   }
 }
 
-// The planner takes it for 1 to 16 tokens without q/k norm (a q/k-norm head
-// would need its whole 128 columns in one workgroup: at Qwen3-0.6B shape 24
-// workgroups each streaming 256 KiB, latency-bound).  Planner override
+// The planner takes it where it beats the split-K kernels and their reduction
+// (fused op, graph-replayed, one box; gemv / split-K in us):
+//   tokens              2            4            6-8          10-16
+//   TinyLlama        5.5 / 7.5    6.2 / 7.9    7.8 / 8.6-8.9  13.0 / 9.8-10.5
+//   Qwen3 geometry   5.3 / 6.3    6.0 / 6.5    7.6 / 6.9-7.1  12.8 / 8.0-8.7
+//   Llama-3-8B      12.6 / 13.8  13.9 / 14.2  21.4 / 16.9-17.2 38.6 / 17.2-17.7
+// (Qwen3 geometry without its q/k norm).  So: up to 4 tokens, and up to 8 when
+// the grid is at most 192 workgroups (TinyLlama's 160): each workgroup reads
+// and normalises every operand row into LDS, which from 5 tokens costs more
+// than the second launch unless the grid is small (at 8 rows and K = 4096 the
+// rows alone fill 64 KiB of LDS).  A q/k-norm head needs all of its columns for
+// the norm, and its workgroups hold 16 each; handing them to one finisher
+// through device-coherent memory cost 3-8 us (one token: 7.9 us against 6.3 us
+// split-K), so those calls stay on the split-K path.  Planner override
 // BFA_TUNE_DECODE_GEMV = 0 never takes it.
-bool gemv_ok(int64_t tokens, int64_t k, int64_t hd, bool qk_norm, bool bf16_w, bool bf16_x, const void* a,
-             int64_t lda) {
+bool gemv_ok(int64_t tokens, int64_t k, int64_t n, int64_t hd, bool qk_norm, const void* bias, bool bf16_w,
+             bool bf16_x, const void* a, int64_t lda) {
   if (tuning(BFA_TUNE_DECODE_GEMV) == 0) return false;
-  if (tokens < 1 || tokens > 16 || qk_norm || !bf16_w || !bf16_x) return false;
-  return k % 32 == 0 && k <= 4096 && k / 32 >= 4 && (k / 32) % 4 == 0 && hd % 16 == 0 && hd <= 1024 &&
-         aligned16(a) && lda % 8 == 0 && lda < (int64_t{1} << 31);
+  if (tokens < 1 || tokens > 8 || qk_norm || !bf16_w || !bf16_x || hd % 16 != 0) return false;
+  if (tokens > 4 && n / 16 > 192) return false;
+  // the bias words are read at 4-byte-aligned addresses from the index alone
+  if ((reinterpret_cast<uintptr_t>(bias) & 3u) != 0) return false;
+  return k % 32 == 0 && k <= 4096 && k / 32 >= 4 && (k / 32) % 4 == 0 && hd <= 1024 && aligned16(a) &&
+         lda % 8 == 0 && lda < (int64_t{1} << 31);
 }
 
 template <int TM>
@@ -303,8 +315,7 @@ void launch_qkv_gemv(GemvArgs d, bool fold, const QkvEpi& e, hipStream_t s) {
   if (d.m <= 1) launch_gemv_t<1>(fold, grid, c, s);
   else if (d.m <= 2) launch_gemv_t<2>(fold, grid, c, s);
   else if (d.m <= 4) launch_gemv_t<4>(fold, grid, c, s);
-  else if (d.m <= 8) launch_gemv_t<8>(fold, grid, c, s);
-  else launch_gemv_t<16>(fold, grid, c, s);
+  else launch_gemv_t<8>(fold, grid, c, s);
 }
 
 }  // namespace bfa

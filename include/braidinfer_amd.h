@@ -77,7 +77,7 @@ const char* bfa_last_error(void);
                                         over the tiles (0 = one workgroup per tile; unset: 1 for
                                         the 256x256 tile, 0 for the others) */
 #define BFA_TUNE_DECODE_GEMV 12      /* BFA_DECODE_GEMV: 0 = never the one-launch decode kernel
-                                        (1-16 tokens without q/k norm) */
+                                        (1-8 tokens without q/k norm) */
 #define BFA_TUNE_COUNT 13
 int bfa_set_tuning(int key, int value);
 int bfa_get_tuning(int key);

@@ -1,13 +1,13 @@
 """GPU parity of the one-launch decode kernel (qkv_gemv.hip): the fused
-RMSNorm+QKV(+bias, RoPE, KV append) of 1-16 tokens without q/k norm, in one
+RMSNorm+QKV(+bias, RoPE, KV append) of 1-8 tokens without q/k norm, in one
 launch (a workgroup per 16 output columns, the whole of K), against the
 oracle's restatement of each reference variant (kernels/fused_rmsnorm_qkv_*.py,
 models/llama.py:169-205).
 
-The planner takes the kernel from 1 to 16 tokens without q/k norm; the
-DECODE_GEMV override = 0 keeps the split-K kernels and their reduction.  Every
-case runs both ways, each against the oracle within |d| <= 2e-2 + 1e-2 |r|
-(tests/helpers.py)."""
+The planner takes the kernel up to 4 tokens, and up to 8 when the grid is at
+most 192 workgroups, without q/k norm; the DECODE_GEMV override = 0 keeps the
+split-K kernels and their reduction.  Every case runs both ways, each against
+the oracle within |d| <= 2e-2 + 1e-2 |r| (tests/helpers.py)."""
 from __future__ import annotations
 
 import pytest
@@ -29,7 +29,8 @@ SHAPES = [
     (2, 2048, 32, 4, 64),     # two tokens
     (3, 2048, 32, 4, 64),     # three (4-token capacity, a padded row)
     (8, 2048, 32, 4, 64),     # TinyLlama decode batch 8
-    (16, 1024, 16, 8, 128),   # sixteen, Qwen3-0.6B geometry without q/k norm
+    (4, 1024, 16, 8, 128),    # four, Qwen3-0.6B geometry without q/k norm
+    (6, 1024, 8, 4, 128),     # six (8-token capacity, 128 workgroups)
     (1, 4096, 32, 8, 128),    # Llama-3-8B, one token (two weight batches per wave)
     (5, 512, 4, 2, 96),       # head_dim 96 (six column groups per head), hidden 512
 ]

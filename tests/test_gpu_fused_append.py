@@ -11,7 +11,8 @@ Each case runs the fused call and checks
   * the whole cache against the oracle's append (oracle/torch_ref.py) of the
     k and v heads that output holds: bit for bit.
 The token counts reach every epilogue that writes the cache: 1-16 tokens (the
-row epilogue after the weight-streaming kernel), 17-64 (the split-K decode
+one-launch kernel's epilogue where the planner takes it, without q/k norm;
+else the row epilogue after the weight-streaming kernel), 17-64 (the split-K decode
 epilogue), more (the prefill GEMM's fused epilogue, every tile form), and
 head_dim 80 (the raw projection + row epilogue)."""
 from __future__ import annotations
