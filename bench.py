@@ -117,9 +117,14 @@ class Chain:
 
 
 class QkvStages:
-    """Calls the two stages of the fused QKV op directly through the C ABI, so
-    each kernel can be timed on its own: the RMSNorm operand pre-pass and the
-    MFMA projection with the fused RoPE epilogue."""
+    """Calls the stages of the fused QKV op directly through the C ABI, so each
+    kernel can be timed on its own: the row statistic (the first stage of the
+    Llama chain's fused op, whose projection reads x with the norm weight folded
+    into W), the RMSNorm operand pre-pass (the first stage of the mixed-rounding
+    variants) and the MFMA projection with the fused RoPE epilogue, the same
+    kernel as the fused op's, timed on the pre-pass operand (filled here once,
+    so that it multiplies real data: on an operand of zeros the power-limited
+    kernel runs much faster)."""
 
     def __init__(self, c: Chain, dev):
         self.c = c
@@ -127,12 +132,19 @@ class QkvStages:
         ws = _lib.call("bfa_fused_rmsnorm_qkv_workspace_size", c.t, H, N, D)
         self.op_bytes = (c.t * H * 2 + 255) // 256 * 256
         self.ws = torch.empty(max(ws, 16), dtype=torch.uint8, device=dev)
+        self.rs = torch.empty(c.t, dtype=torch.float32, device=dev)
         self.status = _lib.status_word(dev)
+        self.operand()
 
     def operand(self):
         c = self.c
         _lib.call("bfa_rmsnorm_qkv_operand", _lib.ptr(c.hidden), _lib.BF16, c.t, H, H,
                   _lib.ptr(c.ln_w), _lib.BF16, 0, _lib.ptr(self.ws), _lib.BF16, EPS,
+                  _lib.stream_of(self.dev))
+
+    def row_statistic(self):
+        c = self.c
+        _lib.call("bfa_rmsnorm_row_scale", _lib.ptr(c.hidden), _lib.BF16, c.t, H, H, _lib.ptr(self.rs), EPS,
                   _lib.stream_of(self.dev))
 
     def projection(self):
@@ -172,18 +184,20 @@ class Row:
 
 
 def chain_rows(c: Chain, dev, stages: bool) -> list:
-    """The chain's kernels at c.t tokens; `stages` adds the two stages of the
-    fused QKV op (operand pre-pass, projection) as rows of their own."""
+    """The chain's kernels at c.t tokens; `stages` adds the stages of the fused
+    QKV op (row statistic, projection) as rows of their own."""
     t = c.t
     rows = [Row("add_rms_norm", lambda: c.norm(c.x, c.residual)[0], 4 * t * H * 2 + H * 2,
                 ref=lambda: _oracle().add_rms_forward(c.cpu["x"], c.cpu["residual"], c.cpu["norm_w"], EPS)[0],
                 ref32=lambda: _oracle32().add_rms_forward(c.cpu["x"], c.cpu["residual"], c.cpu["norm_w"], EPS)[0])]
     if stages:
         st = QkvStages(c, dev)
-        rows += [Row("qkv_operand_prepass", st.operand, 2 * t * H * 2 + H * 2, note="stage of the fused op"),
+        rows += [Row("qkv_row_statistic", st.row_statistic, t * H * 2 + t * 4,
+                     note="stage of the fused op (1 / rms per row)"),
                  Row("qkv_projection_rope", st.projection,
                      t * H * 2 + N * H * 2 + t * N * 2 + t * 8 + t * D * 4, 2.0 * t * H * N,
-                     note="stage of the fused op (operand from the pre-pass)")]
+                     note="the fused op's projection kernel, timed on the pre-pass operand (in the fused "
+                          "op it reads x, with the norm weight folded into W and a scale per row)")]
 
     def llama_ref(o=_oracle):
         q, k, v = o().llama_attention_input(c.cpu["hidden"], c.cpu["ln_w"], c.cpu["w_qkv"], HQ, HKV, EPS,
@@ -803,7 +817,8 @@ def profile_one(kernel: str, tokens: int, steps: int, dev) -> int:
         ms = time_fn(lambda: torch.mm(c.hidden, wt, out=out), steps)
         print(json.dumps({"kernel": kernel, "tokens": tokens, "calls": steps, "us": round(ms * 1e3, 3)}))
         return 0
-    fn = {"qkv_projection": st.projection, "qkv_operand": st.operand, "fused_qkv": c.qkv,
+    fn = {"qkv_projection": st.projection, "qkv_operand": st.operand, "qkv_row_statistic": st.row_statistic,
+          "fused_qkv": c.qkv,
           "add_rms_norm": lambda: c.norm(c.x, c.residual), "silu_and_mul": lambda: c.silu(c.gate_up),
           "embedding": lambda: embedding(c.ids, table)}[kernel]
     ms = time_fn(fn, steps)
@@ -821,7 +836,7 @@ def main(argv=None) -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-cold", action="store_true", help="skip the cold-cache timings")
     ap.add_argument("--kernel", help="only run this kernel --steps times at --tokens (for "
-                    "profilers): qkv_projection, qkv_operand, fused_qkv (the whole fused "
+                    "profilers): qkv_projection, qkv_operand, qkv_row_statistic, fused_qkv (the whole fused "
                     "RMSNorm+QKV+RoPE op), add_rms_norm, silu_and_mul, "
                     "embedding, copy, library_gemm (the projection's product through torch.mm), or "
                     "case:<name> for a case of the configuration table")

@@ -69,6 +69,14 @@ _SIGNATURES = {
                                               c_float, c_int, _P, c_int, c_int64, c_int64, _P, c_int,
                                               c_int64, c_int64, c_int, _P, _P, c_int, c_float, c_int,
                                               _P, c_int, _P, c_int64, _P, c_int, c_int64, _P, _P]),
+    "bfa_fold_rmsnorm_weight": (c_int, [_P, c_int, c_int64, c_int64, c_int64, _P, c_int, _P, c_int64, _P]),
+    "bfa_rmsnorm_row_scale": (c_int, [_P, c_int, c_int64, c_int64, c_int64, _P, c_float, _P]),
+    "bfa_fused_rmsnorm_qkv_folded": (c_int, [_P, c_int, c_int64, c_int64, c_int64, c_float, _P, c_int,
+                                             c_int64, c_int64, _P, c_int, c_int64, c_int64, c_int,
+                                             _P, c_int, _P, c_int64, _P, c_int, c_int64, _P, c_int64,
+                                             _P, c_int, c_int64, c_int64, c_int64, c_int64, c_int64,
+                                             c_int64, _P, c_int, c_int64, _P, _P, c_int, c_int64,
+                                             _P, c_int, c_int64, c_int, _P, _P]),
     "bfa_rmsnorm_qkv_operand": (c_int, [_P, c_int, c_int64, c_int64, c_int64, _P, c_int,
                                         c_int, _P, c_int, c_float, _P]),
     "bfa_qkv_projection": (c_int, [_P, c_int64, c_int64, _P, c_int, c_int64, c_int64, _P,

@@ -15,6 +15,11 @@ int launch_qkv_operand(const void* x, int x_dtype, int64_t rows, int64_t hidden,
                        const void* w, int w_dtype, bool mixed, void* out, int out_dtype,
                        float eps, hipStream_t s);
 
+// The row statistic alone (norm.hip): out[r] = 1 / sqrt(sum(x[r]^2)/hidden + eps),
+// fp32, the same value the operand pre-pass multiplies by.
+int launch_row_scale(const void* x, int x_dtype, int64_t rows, int64_t hidden, int64_t x_stride,
+                     float* out, float eps, hipStream_t s);
+
 // Paged-KV append addressing (kv_append.hip): checks the cache, page-table and
 // position arguments of bfa_append_paged_kv (dtypes, page size, geometry; not
 // the pointers, which the callers check once they know there is work) and fills

@@ -60,6 +60,9 @@ struct QkvEpi {
   // (before the K loop, from `app`), and slot_off is not used
   int app_in_kernel;
   AppendArgs app;
+  // prefill with the norm weight folded into W (the fp32 variants): the
+  // projection of row t is multiplied by row_scale[t] (1 / rms) before the bias
+  const float* row_scale;
 };
 
 __device__ __forceinline__ float round_to(float v, int dt) {

@@ -11,6 +11,9 @@
 //   kOperandProd  normalised QKV operand, fused_rmsnorm_qkv_production.py:61-116
 //                 (also the f32 variants minimal_f32.py:59-107, with_bias.py, whose
 //                 fp32 operand is rounded once to the MFMA input type)
+//   kRowScale     the row statistic alone, 1 / rms per row (fp32), for the f32
+//                 variants' prefill with the norm weight folded into the QKV weight
+//                 (the projection of x multiplied by it per row; minimal_f32.py:59-107)
 //
 // Design: a row is owned by a group of L lanes (L = 16, 64 or 256).  Each lane
 // keeps up to MAXC chunks of 8 elements in registers, loaded with 16-byte
@@ -24,7 +27,7 @@
 
 namespace bfa {
 
-enum NormMode { kRms = 0, kAddRms = 1, kF32 = 2, kOperandMixed = 3, kOperandProd = 4 };
+enum NormMode { kRms = 0, kAddRms = 1, kF32 = 2, kOperandMixed = 3, kOperandProd = 4, kRowScale = 5 };
 
 struct NormArgs {
   const void* x;
@@ -108,13 +111,18 @@ __global__ __launch_bounds__(256) void norm_vec_kernel(NormArgs a) {
   // the norm weight's granules go out with the row (raw, converted after the
   // sum): requested after the reduction they were a second memory round trip
   Raw8Dyn gw[MAXC];
+  if constexpr (MODE != kRowScale) {
 #pragma unroll
-  for (int c = 0; c < MAXC; ++c) gw[c].load(a.w, a.w_dtype, min(lane + c * L, nchunks - 1));
+    for (int c = 0; c < MAXC; ++c) gw[c].load(a.w, a.w_dtype, min(lane + c * L, nchunks - 1));
+  }
 #pragma unroll
   for (int c = 0; c < MAXC; ++c) {
     const int ch = lane + c * L;
     if (ch < nchunks) {
-      load8_nt<DT_IN>(xp + ch * 8, v[c]);
+      // kRowScale: plain loads, so that x stays in the caches for the projection
+      // that reads it next (the other modes read their input once)
+      if constexpr (MODE == kRowScale) load8<DT_IN>(xp + ch * 8, v[c]);
+      else load8_nt<DT_IN>(xp + ch * 8, v[c]);
       if constexpr (MODE == kAddRms) {
         float r[8];
         load8_nt<DT_IN>(static_cast<const TIN*>(a.res) + row * a.r_s + ch * 8, r);
@@ -136,6 +144,10 @@ __global__ __launch_bounds__(256) void norm_vec_kernel(NormArgs a) {
     for (int w = 0; w < L / kWave; ++w) ss += red[w];
   }
   const float inv = norm_inv(ss, a.hidden, a.eps);
+  if constexpr (MODE == kRowScale) {
+    if (lane == 0) static_cast<float*>(a.y)[row] = inv;
+    return;
+  }
 
 #pragma unroll
   for (int c = 0; c < MAXC; ++c) {
@@ -174,6 +186,10 @@ __global__ __launch_bounds__(256) void norm_scalar_kernel(NormArgs a) {
 #pragma unroll
   for (int w = 0; w < 256 / kWave; ++w) ss += red[w];
   const float inv = norm_inv(ss, a.hidden, a.eps);
+  if constexpr (MODE == kRowScale) {
+    if (tid == 0) static_cast<float*>(a.y)[row] = inv;
+    return;
+  }
 
   for (int64_t i = tid; i < a.hidden; i += 256) {
     float v = load1<DT_IN>(a.x, xoff + i * a.x_sc);
@@ -283,9 +299,82 @@ int launch_qkv_operand(const void* x, int x_dtype, int64_t rows, int64_t hidden,
                : launch_norm_out<BFA_DTYPE_F16, kOperandProd>(x_dtype, a, vec_ok, s, what);
 }
 
+int launch_row_scale(const void* x, int x_dtype, int64_t rows, int64_t hidden, int64_t x_stride,
+                     float* out, float eps, hipStream_t s) {
+  const char* what = "rmsnorm row scale";
+  BFA_REQUIRE(is_float_dtype(x_dtype), "%s: bad dtype", what);
+  NormArgs a{};
+  a.x = x; a.y = out;
+  a.rows = rows; a.rows_inner = 1; a.hidden = hidden;
+  a.x_so = x_stride; a.x_si = 0; a.x_sc = 1;
+  a.y_so = 1; a.y_si = 0; a.y_sc = 1;
+  a.eps = eps;
+  const bool vec_ok = mult8(hidden) && mult8(x_stride) && aligned16(x);
+  return launch_norm_out<BFA_DTYPE_F32, kRowScale>(x_dtype, a, vec_ok, s, what);
+}
+
+// folded[n, k] = W[n, k] * gamma[k], the product in fp32 rounded once to W's
+// dtype: 8 elements per thread, 16-byte rows (k % 8 == 0, aligned bases).
+template <int DT_W>
+__global__ __launch_bounds__(256) void fold_weight_kernel(const uint16_t* w, int64_t ldw, const void* g, int g_dt,
+                                                          uint16_t* out, int64_t ldo, int64_t n, int64_t k8) {
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (idx >= n * k8) return;
+  const int64_t row = idx / k8, c = idx - row * k8;
+  Raw8Dyn gr;
+  gr.load(g, g_dt, c);
+  const uint4 wr = *reinterpret_cast<const uint4*>(w + row * ldw + c * 8);
+  float wv[8], gv[8];
+  const uint32_t u[4] = {wr.x, wr.y, wr.z, wr.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    wv[2 * i] = Elem<DT_W>::to_f32(static_cast<uint16_t>(u[i] & 0xffffu));
+    wv[2 * i + 1] = Elem<DT_W>::to_f32(static_cast<uint16_t>(u[i] >> 16));
+  }
+  gr.to_f32(g_dt, gv);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) wv[i] = wv[i] * gv[i];
+  store8<DT_W>(out + row * ldo + c * 8, wv);
+}
+
+int launch_fold_weight(const void* w, int w_dtype, int64_t n, int64_t k, int64_t ldw, const void* g,
+                       int g_dtype, void* out, int64_t ldo, hipStream_t s) {
+  const char* what = "bfa_fold_rmsnorm_weight";
+  BFA_REQUIRE(w_dtype == BFA_DTYPE_BF16 || w_dtype == BFA_DTYPE_F16, "%s: weight must be bf16/fp16", what);
+  BFA_REQUIRE(is_float_dtype(g_dtype), "%s: bad norm weight dtype", what);
+  BFA_REQUIRE(n >= 0 && k >= 0 && ldw >= k && ldo >= k, "%s: bad geometry", what);
+  BFA_REQUIRE(mult8(k) && mult8(ldw) && mult8(ldo) && aligned16(w) && aligned16(g) && aligned16(out),
+              "%s: rows must be 16-byte aligned with hidden a multiple of 8", what);
+  const int64_t total = n * (k / 8);
+  if (total == 0) return BFA_OK;
+  const unsigned grid = static_cast<unsigned>(cdiv(total, 256));
+  if (w_dtype == BFA_DTYPE_BF16)
+    hipLaunchKernelGGL((fold_weight_kernel<BFA_DTYPE_BF16>), dim3(grid), dim3(256), 0, s,
+                       static_cast<const uint16_t*>(w), ldw, g, g_dtype, static_cast<uint16_t*>(out), ldo, n, k / 8);
+  else
+    hipLaunchKernelGGL((fold_weight_kernel<BFA_DTYPE_F16>), dim3(grid), dim3(256), 0, s,
+                       static_cast<const uint16_t*>(w), ldw, g, g_dtype, static_cast<uint16_t*>(out), ldo, n, k / 8);
+  return check_launch(what);
+}
+
 }  // namespace bfa
 
 using namespace bfa;
+
+extern "C" int bfa_rmsnorm_row_scale(const void* x, int x_dtype, int64_t rows, int64_t hidden, int64_t x_stride,
+                                     float* out, float eps, void* stream) {
+  BFA_REQUIRE(x && out, "bfa_rmsnorm_row_scale: null pointer");
+  BFA_REQUIRE(rows >= 0 && hidden > 0 && x_stride >= hidden, "bfa_rmsnorm_row_scale: bad geometry");
+  return launch_row_scale(x, x_dtype, rows, hidden, x_stride, out, eps, as_stream(stream));
+}
+
+extern "C" int bfa_fold_rmsnorm_weight(const void* qkv_weight, int w_dtype, int64_t qkv_dim, int64_t hidden,
+                                       int64_t w_stride, const void* norm_weight, int nw_dtype, void* folded,
+                                       int64_t folded_stride, void* stream) {
+  BFA_REQUIRE(qkv_weight && norm_weight && folded, "bfa_fold_rmsnorm_weight: null pointer");
+  return launch_fold_weight(qkv_weight, w_dtype, qkv_dim, hidden, w_stride, norm_weight, nw_dtype, folded,
+                            folded_stride, as_stream(stream));
+}
 
 extern "C" int bfa_rms_norm(const void* x, void* y, const void* weight, int x_dtype, int w_dtype,
                             int64_t rows, int64_t rows_inner, int64_t hidden,

@@ -374,7 +374,8 @@ __device__ __forceinline__ void tile_origin(const GemmArgs& g, int64_t tile, int
 // floats, free for the wave-private staging slices (the caller's barrier-free
 // LDS use must be over).  praw: the rows' raw positions when EARLY (one block
 // per wave, requested before the K loop).  SLOT_U4: uint4 offset in lds of the
-// fused KV append's slot table (MB x 32 int64 per wave).
+// fused KV append's slot table (MB x 32 int64 per wave), followed by the row
+// scales' table (MB x 32 floats per wave).
 template <int EPI, int HD, int MB, int NB, int WM, int WN, int NW, int EDT, bool EARLY, int SLOT_U4>
 __device__ __forceinline__ void gemm_epilogue(f32x16_t (&acc)[MB][NB], uint4* lds, const GemmArgs& g,
                                               const QkvEpi& e, int64_t m0, int64_t n0, int wid, int wm,
@@ -547,6 +548,15 @@ __device__ __forceinline__ void gemm_epilogue(f32x16_t (&acc)[MB][NB], uint4* ld
       for (int r = lane; r < MB * 32; r += 64) stab[r] = e.slot_off[min(wrow0 + r, g.m - 1)];
       __asm__ volatile("" ::: "memory");  // the wave's own LDS writes precede its reads below
     }
+    // Row scales (the norm weight folded into W): this wave's rows go to a
+    // wave-private LDS table after the slot tables, read once per row below
+    // (held in registers a block ahead, they had made the epilogue spill).
+    const bool rsc = e.row_scale != nullptr;
+    float* const rtab = reinterpret_cast<float*>(lds + SLOT_U4 + NW * MB * 32 / 2) + wid * (MB * 32);
+    if (rsc) {
+      for (int r = lane; r < MB * 32; r += 64) rtab[r] = e.row_scale[min(wrow0 + r, g.m - 1)];
+      __asm__ volatile("" ::: "memory");
+    }
     // The cos/sin rows of a block's 8 rows are all requested before its row
     // loop: there each load would sit behind the previous row's stores (the
     // table and the output may alias as far as the compiler knows), paying the
@@ -564,6 +574,7 @@ __device__ __forceinline__ void gemm_epilogue(f32x16_t (&acc)[MB][NB], uint4* ld
       }
     };
     if (rope) load_cs(0, cvv[0], svv[0]);
+
 #pragma unroll
     for (int i = 0; i < MB; ++i) {
       float4 (&cvv_i)[NP] = cvv[i & 1];
@@ -587,6 +598,14 @@ __device__ __forceinline__ void gemm_epilogue(f32x16_t (&acc)[MB][NB], uint4* ld
         const float4 a1 = *reinterpret_cast<const float4*>(et + rl * LDR + c1);
         const float4 a2 = *reinterpret_cast<const float4*>(et + rl * LDR + c2);
         float x1[4] = {a1.x, a1.y, a1.z, a1.w}, x2[4] = {a2.x, a2.y, a2.z, a2.w};
+        if (rsc) {
+          const float r = rtab[i * 32 + rl];
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            x1[t] = x1[t] * r;
+            x2[t] = x2[t] * r;
+          }
+        }
         if (has_bias) {
 #pragma unroll
           for (int t = 0; t < 4; ++t) {
@@ -680,7 +699,8 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, (WM * WN <= 8192 ? 2 : 
   // K loop's buffers and the epilogue's staging slices: it is filled before the
   // K loop and read in the epilogue
   constexpr int SLOT_U4 = MAIN_U4 > EPI_U4 ? MAIN_U4 : EPI_U4;
-  constexpr int LDS_U4 = SLOT_U4 + (EPI == EPI_FUSED ? NW * MB * 32 / 2 : 0);
+  // and after it the fused epilogue's row-scale table (MB x 32 floats per wave)
+  constexpr int LDS_U4 = SLOT_U4 + (EPI == EPI_FUSED ? NW * MB * 32 / 2 + NW * MB * 32 / 4 : 0);
   __shared__ uint4 lds[LDS_U4];
   uint4* const lds0 = lds;
   uint4* const lds1 = lds + (BM + BN) * 8;
@@ -2718,7 +2738,7 @@ static int qkv_projection_impl(const void* operand, int64_t lda, const OperandFo
                                   const float* cos_sin_cache, int64_t max_position, void* out,
                                   int out_dtype, int64_t out_stride, void* part_workspace,
                                   int64_t part_workspace_bytes, int32_t* status, void* stream,
-                                  const CacheEpi* ce = nullptr) {
+                                  const CacheEpi* ce = nullptr, const float* row_scale = nullptr) {
   const char* what = fold ? "bfa_fused_rmsnorm_qkv" : "bfa_qkv_projection";
   BFA_REQUIRE(w_dtype == BFA_DTYPE_BF16 || w_dtype == BFA_DTYPE_F16, "%s: weight must be bf16/fp16", what);
   BFA_REQUIRE(is_float_dtype(qkv_dtype) && is_float_dtype(out_dtype) && is_float_dtype(qk_norm_out_dtype),
@@ -2747,6 +2767,8 @@ static int qkv_projection_impl(const void* operand, int64_t lda, const OperandFo
   const QkvPlan p = make_plan(tokens, qkv_dim, hidden, hd);
   BFA_REQUIRE(p.decode || !p.fused_epi || (out_stride % 4 == 0 && aligned16(out)),
               "%s: output rows must be 16-byte aligned", what);
+  BFA_REQUIRE(row_scale == nullptr || (!p.decode && p.fused_epi), "%s: row scales need the prefill epilogue",
+              what);
   BFA_REQUIRE(part_workspace_bytes >= p.part_bytes && (p.part_bytes == 0 || part_workspace),
               "%s: workspace too small (%lld < %lld bytes)", what, (long long)part_workspace_bytes,
               (long long)p.part_bytes);
@@ -2761,6 +2783,7 @@ static int qkv_projection_impl(const void* operand, int64_t lda, const OperandFo
   e.positions = positions; e.pos_is_i64 = positions_dtype == BFA_DTYPE_I64;
   e.cs = cos_sin_cache; e.max_pos = max_position;
   e.out = out; e.ldo = out_stride; e.status = status;
+  e.row_scale = row_scale;
   if (fold && fold->stats) {
     e.stats = fold->stats; e.stat_rows = 16 * p.mt; e.hidden = hidden; e.stat_eps = fold->eps;
   }
@@ -2842,7 +2865,7 @@ static int qkv_projection_impl(const void* operand, int64_t lda, const OperandFo
   GemmArgs g{};
   g.a = static_cast<const uint16_t*>(operand);
   g.w = static_cast<const uint16_t*>(qkv_weight);
-  g.m = tokens; g.n = qkv_dim; g.k = hidden; g.lda = hidden; g.ldw = w_stride;
+  g.m = tokens; g.n = qkv_dim; g.k = hidden; g.lda = lda; g.ldw = w_stride;
   g.raw = part;
   if (bf16) launch_prefill<true>(p, g, e, st); else launch_prefill<false>(p, g, e, st);
   int rc = check_launch(what);
@@ -2977,6 +3000,29 @@ extern "C" int64_t bfa_fused_rmsnorm_qkv_append_workspace_size(int64_t tokens, i
   return bfa_fused_rmsnorm_qkv_workspace_size(tokens, hidden, qkv_dim, head_dim) + align256(tokens * 8);
 }
 
+// The cache arguments of the fused append, checked and gathered into `a`.
+static int append_setup(const char* what, void* layer_cache, int cache_dtype, int64_t num_pages,
+                        int64_t cache_page_slots, int64_t stride_page, int64_t stride_kv, int64_t stride_head,
+                        int64_t stride_slot, const void* kv_indices, int kv_indices_dtype, int64_t num_indices,
+                        const int32_t* kv_indptr, const void* batch_indices, int batch_indices_dtype,
+                        int64_t num_seqs, const void* cache_positions, int cache_positions_dtype,
+                        int64_t page_size, int64_t tokens, int32_t* status, AppendArgs* a) {
+  int rc = fill_append_args(what, layer_cache, cache_dtype, num_pages, cache_page_slots, stride_page,
+                            stride_kv, stride_head, stride_slot, kv_indices, kv_indices_dtype, num_indices,
+                            kv_indptr, batch_indices, batch_indices_dtype, num_seqs, cache_positions,
+                            cache_positions_dtype, page_size, status, a);
+  if (rc != BFA_OK) return rc;
+  BFA_REQUIRE(tokens >= 0 && tokens < (int64_t{1} << 31), "%s: bad token count", what);
+  if (tokens == 0) return BFA_OK;
+  BFA_REQUIRE(layer_cache && cache_positions, "%s: null cache or positions", what);
+  BFA_REQUIRE(num_indices == 0 || kv_indices, "%s: null kv_indices", what);
+  // the prefill epilogue writes 4 consecutive elements per store
+  BFA_REQUIRE(stride_page % 4 == 0 && stride_kv % 4 == 0 && stride_head % 4 == 0 && stride_slot % 4 == 0 &&
+                  aligned16(layer_cache),
+              "%s: cache strides must be multiples of 4 elements and the cache 16-byte aligned", what);
+  return BFA_OK;
+}
+
 extern "C" int bfa_fused_rmsnorm_qkv_append(
     const void* x, int x_dtype, int64_t tokens, int64_t hidden, int64_t x_stride, const void* norm_weight,
     int nw_dtype, float eps, int mixed_rounding, const void* qkv_weight, int w_dtype, int64_t qkv_dim,
@@ -2992,19 +3038,11 @@ extern "C" int bfa_fused_rmsnorm_qkv_append(
     int32_t* status, void* stream) {
   const char* what = "bfa_fused_rmsnorm_qkv_append";
   AppendArgs a{};
-  int rc = fill_append_args(what, layer_cache, cache_dtype, num_pages, cache_page_slots, stride_page,
-                            stride_kv, stride_head, stride_slot, kv_indices, kv_indices_dtype, num_indices,
-                            kv_indptr, batch_indices, batch_indices_dtype, num_seqs, cache_positions,
-                            cache_positions_dtype, page_size, status, &a);
-  if (rc != BFA_OK) return rc;
-  BFA_REQUIRE(tokens >= 0 && tokens < (int64_t{1} << 31), "%s: bad token count", what);
-  if (tokens == 0) return BFA_OK;
-  BFA_REQUIRE(layer_cache && cache_positions, "%s: null cache or positions", what);
-  BFA_REQUIRE(num_indices == 0 || kv_indices, "%s: null kv_indices", what);
-  // the prefill epilogue writes 4 consecutive elements per store
-  BFA_REQUIRE(stride_page % 4 == 0 && stride_kv % 4 == 0 && stride_head % 4 == 0 && stride_slot % 4 == 0 &&
-                  aligned16(layer_cache),
-              "%s: cache strides must be multiples of 4 elements and the cache 16-byte aligned", what);
+  int rc = append_setup(what, layer_cache, cache_dtype, num_pages, cache_page_slots, stride_page, stride_kv,
+                        stride_head, stride_slot, kv_indices, kv_indices_dtype, num_indices, kv_indptr,
+                        batch_indices, batch_indices_dtype, num_seqs, cache_positions, cache_positions_dtype,
+                        page_size, tokens, status, &a);
+  if (rc != BFA_OK || tokens == 0) return rc;
   const int64_t heads = num_q_heads + 2 * num_kv_heads;
   BFA_REQUIRE(heads > 0 && qkv_dim % heads == 0, "%s: bad head geometry", what);
   const int64_t fsize = bfa_fused_rmsnorm_qkv_workspace_size(tokens, hidden, qkv_dim, qkv_dim / heads);
@@ -3027,6 +3065,56 @@ extern "C" int bfa_fused_rmsnorm_qkv_append(
                     qkv_dtype, q_norm_weight, k_norm_weight, qk_norm_dtype, qk_eps, qk_norm_out_dtype,
                     positions, positions_dtype, cos_sin_cache, max_position, out, out_dtype, out_stride,
                     workspace, fsize, status, stream, &ce);
+}
+
+// The fp32 variants' prefill with the norm weight folded into the QKV weight
+// (bfa_fold_rmsnorm_weight): the row statistic 1 / rms goes to the workspace,
+// then x itself is projected onto bf16(W * gamma) and each row's projection is
+// multiplied by its statistic before the bias; the rest of the epilogue, and
+// with a cache the append, are bfa_fused_rmsnorm_qkv(_append)'s.  No
+// normalised operand is written.  layer_cache = NULL: no append (the other
+// cache arguments are not read).
+extern "C" int bfa_fused_rmsnorm_qkv_folded(
+    const void* x, int x_dtype, int64_t tokens, int64_t hidden, int64_t x_stride, float eps,
+    const void* folded_weight, int w_dtype, int64_t qkv_dim, int64_t w_stride, const void* bias, int bias_dtype,
+    int64_t num_q_heads, int64_t num_kv_heads, int qkv_dtype, const void* positions, int positions_dtype,
+    const float* cos_sin_cache, int64_t max_position, void* out, int out_dtype, int64_t out_stride,
+    void* workspace, int64_t workspace_bytes, void* layer_cache, int cache_dtype, int64_t num_pages,
+    int64_t cache_page_slots, int64_t stride_page, int64_t stride_kv, int64_t stride_head, int64_t stride_slot,
+    const void* kv_indices, int kv_indices_dtype, int64_t num_indices, const int32_t* kv_indptr,
+    const void* batch_indices, int batch_indices_dtype, int64_t num_seqs, const void* cache_positions,
+    int cache_positions_dtype, int64_t page_size, int write_kv_out, int32_t* status, void* stream) {
+  const char* what = "bfa_fused_rmsnorm_qkv_folded";
+  BFA_REQUIRE(x && folded_weight, "%s: null pointer", what);
+  AppendArgs a{};
+  if (layer_cache) {
+    const int rc = append_setup(what, layer_cache, cache_dtype, num_pages, cache_page_slots, stride_page,
+                                stride_kv, stride_head, stride_slot, kv_indices, kv_indices_dtype, num_indices,
+                                kv_indptr, batch_indices, batch_indices_dtype, num_seqs, cache_positions,
+                                cache_positions_dtype, page_size, tokens, status, &a);
+    if (rc != BFA_OK) return rc;
+  }
+  if (tokens == 0) return BFA_OK;
+  BFA_REQUIRE(x_dtype == w_dtype, "%s: x must have the weight's dtype", what);
+  BFA_REQUIRE(x_stride >= hidden && x_stride % 8 == 0, "%s: x rows must be 16-byte aligned", what);
+  const int64_t heads = num_q_heads + 2 * num_kv_heads;
+  BFA_REQUIRE(heads > 0 && qkv_dim % heads == 0, "%s: bad head geometry", what);
+  const QkvPlan p = make_plan(tokens, qkv_dim, hidden, qkv_dim / heads);
+  BFA_REQUIRE(!p.decode && p.fused_epi, "%s: prefill (more than 64 tokens, head_dim 32, 64 or 128) only", what);
+  BFA_REQUIRE(workspace && workspace_bytes >= p.operand_bytes + p.part_bytes && aligned16(workspace),
+              "%s: workspace too small (%lld < %lld bytes)", what, (long long)workspace_bytes,
+              (long long)(p.operand_bytes + p.part_bytes));
+  float* rs = static_cast<float*>(workspace);
+  const int64_t rs_bytes = align256(tokens * 4);
+  int rc = launch_row_scale(x, x_dtype, tokens, hidden, x_stride, rs, eps, as_stream(stream));
+  if (rc != BFA_OK) return rc;
+  // the prefill GEMM's fused epilogue resolves the cache slots itself
+  const CacheEpi ce{layer_cache, cache_dtype, stride_kv, stride_head, nullptr, write_kv_out ? 0 : 1, &a};
+  return qkv_projection_impl(x, x_stride, nullptr, tokens, hidden, folded_weight, w_dtype, qkv_dim, w_stride,
+                             bias, bias_dtype, num_q_heads, num_kv_heads, qkv_dtype, nullptr, nullptr, 0, 0.f,
+                             BFA_DTYPE_BF16, positions, positions_dtype, cos_sin_cache, max_position, out,
+                             out_dtype, out_stride, static_cast<char*>(workspace) + rs_bytes,
+                             workspace_bytes - rs_bytes, status, stream, layer_cache ? &ce : nullptr, rs);
 }
 
 // ------------------------------------------------ allocation-free variant

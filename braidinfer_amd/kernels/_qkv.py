@@ -9,6 +9,8 @@ models/llama.py:169-205).
 """
 from __future__ import annotations
 
+import weakref
+
 import torch
 
 from .. import _lib
@@ -19,6 +21,54 @@ _OPERAND_DTYPES = (torch.bfloat16, torch.float16)
 def head_dim_of(qkv_dim: int, num_q_heads: int, num_kv_heads: int) -> int:
     """head_dim = qkv_dim // (Hq + 2*Hkv), as every reference variant derives it."""
     return qkv_dim // (num_q_heads + 2 * num_kv_heads)
+
+
+# Without the mixed rounding (the production and fp32 variants) the prefill
+# projects x onto W * gamma (bfa_fold_rmsnorm_weight) and scales each row by
+# 1 / rms, so no normalised operand is written.  The
+# folded weight is made once per (weight, norm weight) pair and kept while both
+# tensor objects are alive, with the same storage and version counter (an
+# in-place update of either, or a new `.data`, makes the next call fold again).
+# A write that bypasses torch's version counter (a raw-pointer kernel writing
+# into the weight) needs clear_folded_weights().
+_folded: dict = {}
+_FOLD_MIN_TOKENS = 65  # the prefill projection's fused epilogue
+
+
+def _drop_folded(key, ref) -> None:
+    ent = _folded.get(key)
+    if ent is not None and (ent[0] is ref or ent[1] is ref):
+        del _folded[key]
+
+
+def folded_weight(w: torch.Tensor, norm_weight: torch.Tensor) -> torch.Tensor | None:
+    """bf16(W * gamma) for (w, norm_weight), from the cache or folded now; None
+    under graph capture when no folded copy exists yet (the caller then runs the
+    unfolded path: a fold captured into a graph would be redone on every replay)."""
+    key = (id(w), id(norm_weight))
+    state = (w.data_ptr(), w._version, tuple(w.shape), w.stride(0), w.dtype,
+             norm_weight.data_ptr(), norm_weight._version, norm_weight.dtype)
+    ent = _folded.get(key)
+    if ent is not None and ent[0]() is w and ent[1]() is norm_weight and ent[2] == state:
+        return ent[3]
+    if torch.cuda.is_current_stream_capturing():
+        return None
+    n, k = w.shape
+    wf = torch.empty((n, k), dtype=w.dtype, device=w.device)
+    _lib.call("bfa_fold_rmsnorm_weight", w.data_ptr(), _lib.dtype_code(w), n, k, w.stride(0),
+              norm_weight.data_ptr(), _lib.dtype_code(norm_weight), wf.data_ptr(), wf.stride(0),
+              _lib.stream_of(w.device))
+    wr = weakref.ref(w, lambda r, key=key: _drop_folded(key, r))
+    nr = weakref.ref(norm_weight, lambda r, key=key: _drop_folded(key, r))
+    _folded[key] = (wr, nr, state, wf)
+    return wf
+
+
+def clear_folded_weights() -> int:
+    """Drops every cached folded weight; returns how many there were."""
+    n = len(_folded)
+    _folded.clear()
+    return n
 
 
 def _matrix_weight(w: torch.Tensor) -> torch.Tensor:
@@ -62,6 +112,7 @@ def fused_rmsnorm_qkv(
     qkv_dim = qkv_weight.shape[0]
     if input.stride(-1) != 1 or input.data_ptr() % 16 != 0:
         input = input.contiguous()
+    orig_norm_weight = norm_weight
     if not norm_weight.is_contiguous():
         norm_weight = norm_weight.contiguous()
     w = _matrix_weight(qkv_weight)
@@ -98,6 +149,33 @@ def fused_rmsnorm_qkv(
         out = torch.empty((tokens, qkv_dim), dtype=out_dtype, device=dev)
     if paged_kv is not None:
         cache_args = paged_kv.c_args(tokens, num_kv_heads, hd)
+    # the variants without the mixed rounding, at prefill: x projected onto the
+    # folded weight (the unconverted weight and norm weight only, so that the
+    # cache key is the caller's own tensors)
+    if (not mixed_rounding and tokens >= _FOLD_MIN_TOKENS
+            and q_norm_weight is None and k_norm_weight is None and hd in (32, 64, 128)
+            and w is qkv_weight and norm_weight is orig_norm_weight and input.dtype == w.dtype
+            and hidden % 8 == 0 and input.stride(0) % 8 == 0 and norm_weight.data_ptr() % 16 == 0
+            and out.stride(-1) == 1 and out.stride(0) % 4 == 0 and out.data_ptr() % 16 == 0):
+        wf = folded_weight(w, norm_weight)
+        if wf is not None:
+            ws_bytes = _lib.workspace_size("bfa_fused_rmsnorm_qkv_workspace_size", tokens, hidden, qkv_dim, hd)
+            workspace = _lib.workspace(dev, ws_bytes)
+            no_cache = (None, 0, 0, 0, 0, 0, 0, 0, None, 0, 0, None, None, 0, 0, None, 0, 0, 0)
+            _lib.call(
+                "bfa_fused_rmsnorm_qkv_folded",
+                input.data_ptr(), _lib.dtype_code(input), tokens, hidden, input.stride(0), float(eps),
+                wf.data_ptr(), _lib.dtype_code(wf), qkv_dim, wf.stride(0),
+                _lib.ptr(qkv_bias), _lib.dtype_code(qkv_bias) if qkv_bias is not None else 0,
+                num_q_heads, num_kv_heads, _lib.dtype_code(qkv_dtype),
+                _lib.ptr(positions), _lib.dtype_code(positions) if positions is not None else 0,
+                _lib.ptr(cos_sin_cache), cos_sin_cache.shape[0] if cos_sin_cache is not None else 0,
+                out.data_ptr(), _lib.dtype_code(out), out.stride(0),
+                workspace.data_ptr(), workspace.numel(),
+                *(cache_args if paged_kv is not None else no_cache),
+                _lib.status_word(dev).data_ptr(), _lib.stream_of(dev),
+            )
+            return out
     if tokens == 0:
         return out
     if paged_kv is not None:

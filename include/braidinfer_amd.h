@@ -258,6 +258,43 @@ int bfa_fused_rmsnorm_qkv_noalloc(const void* x, int x_dtype, int64_t tokens, in
                                   const float* cos_sin_cache, int64_t max_position, void* out,
                                   int out_dtype, int64_t out_stride, int32_t* status, void* stream);
 
+/* The variants without the mixed rounding (FusedRMSNormQKV,
+ * kernels/fused_rmsnorm_qkv_production.py:13-229; FusedRMSNormQKVMinimalF32,
+ * kernels/fused_rmsnorm_qkv_minimal_f32.py:14-214; FusedRMSNormQKVWithBias,
+ * kernels/fused_rmsnorm_qkv_with_bias.py:13-228; the Llama attention input,
+ * models/llama.py:169-205) at prefill, with the norm weight folded
+ * into the QKV weight.  (x / rms) * gamma projected onto W equals the projection of x
+ * onto W * gamma, scaled by 1 / rms per row, so the normalised operand is never
+ * written: one pass computes the row statistic, the projection reads x itself.
+ * bfa_fold_rmsnorm_weight: folded[n, k] = W[n, k] * norm_weight[k], the product in
+ * fp32 rounded once to W's dtype (hidden a multiple of 8, 16-byte aligned rows); the
+ * caller computes it once per (W, norm weight) pair and keeps it while both are
+ * unchanged.
+ * bfa_fused_rmsnorm_qkv_folded: as bfa_fused_rmsnorm_qkv with mixed_rounding = 0 and
+ * no q/k norm, on the folded weight, and with layer_cache != NULL as
+ * bfa_fused_rmsnorm_qkv_append (same cache arguments; NULL: no append, the other
+ * cache arguments unread); more than 64 tokens and head_dim 32, 64 or 128 (the
+ * prefill projection's fused epilogue), x in W's dtype.  Against the oracle the
+ * bf16 rounding moves from the operand to the weight, within the same tolerance.
+ * workspace: bfa_fused_rmsnorm_qkv_workspace_size() bytes. */
+int bfa_fold_rmsnorm_weight(const void* qkv_weight, int w_dtype, int64_t qkv_dim, int64_t hidden,
+                            int64_t w_stride, const void* norm_weight, int nw_dtype, void* folded,
+                            int64_t folded_stride, void* stream);
+/* The folded form's first stage on its own: out[r] = 1 / sqrt(sum(x[r]^2)/hidden + eps)
+ * (fp32), the factor the operand pre-pass multiplies by (minimal_f32.py:59-107). */
+int bfa_rmsnorm_row_scale(const void* x, int x_dtype, int64_t rows, int64_t hidden, int64_t x_stride,
+                          float* out, float eps, void* stream);
+int bfa_fused_rmsnorm_qkv_folded(
+    const void* x, int x_dtype, int64_t tokens, int64_t hidden, int64_t x_stride, float eps,
+    const void* folded_weight, int w_dtype, int64_t qkv_dim, int64_t w_stride, const void* bias, int bias_dtype,
+    int64_t num_q_heads, int64_t num_kv_heads, int qkv_dtype, const void* positions, int positions_dtype,
+    const float* cos_sin_cache, int64_t max_position, void* out, int out_dtype, int64_t out_stride,
+    void* workspace, int64_t workspace_bytes, void* layer_cache, int cache_dtype, int64_t num_pages,
+    int64_t cache_page_slots, int64_t stride_page, int64_t stride_kv, int64_t stride_head, int64_t stride_slot,
+    const void* kv_indices, int kv_indices_dtype, int64_t num_indices, const int32_t* kv_indptr,
+    const void* batch_indices, int batch_indices_dtype, int64_t num_seqs, const void* cache_positions,
+    int cache_positions_dtype, int64_t page_size, int write_kv_out, int32_t* status, void* stream);
+
 /* The two stages of bfa_fused_rmsnorm_qkv, exposed separately.
  * Stage 1 (the RMSNorm prologue of every variant): operand[rows, hidden] =
  *   mixed_rounding ? to(op)( to(bf16)(x / rms) * w ) : to(op)( (x / rms) * w ),

@@ -143,7 +143,8 @@ def test_decode_scale_after(t, heads, h, gdtype):
 ])
 def test_prefill_fp32_variants(t, h, hq, hkv, d, strided, gdtype, sample):
     """FusedRMSNormQKVMinimalF32 and FusedRMSNormQKVWithBias over the prefill
-    tile forms (operand pre-pass, then the GEMM with the fp32 epilogue): within
+    tile forms (the row statistic, then the GEMM of x on the weight with the norm
+    weight folded in, and the fp32 epilogue scaling each row): within
     the tolerance of the oracle's (x / rms) * gamma operand in fp32, with
     strided and ragged inputs; every `sample`-th row is checked at the large
     sizes (rows of a GEMM are independent)."""
