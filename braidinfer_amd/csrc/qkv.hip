@@ -1821,15 +1821,18 @@ __device__ __forceinline__ void wait_vm_dyn(int n) {
   }
 }
 
-template <int MT, bool SA, int EDT>
+// GIN (with SA): gamma goes onto the weight fragments in the kernel; without,
+// the weight already holds bf16(w * gamma) (bfa_fold_rmsnorm_weight).
+template <int MT, bool SA, int EDT, bool GIN = true>
 __global__ __launch_bounds__(256) void qkv_decode_pair_kernel(DecodeArgs d, QkvEpi e, int nch) {
   using DT = EpiDt<EDT>;
+  constexpr bool G = SA && GIN;         // gamma applied here
   constexpr int RX = PairRing<MT>::RX, RW = PairRing<MT>::RW;
   constexpr int ROWS = MT * 16;
   constexpr int XN = ROWS / 8;          // operand DMAs per wave per chunk (8 rows x 128 B)
-  constexpr int WN = 4 + (SA ? 1 : 0);  // weight DMAs (+ gamma)
+  constexpr int WN = 4 + (G ? 1 : 0);   // weight DMAs (+ gamma)
   constexpr int XS = ROWS * 8;          // uint4 per operand slot
-  constexpr int WS = 32 * 8 + (SA ? 8 : 0);  // uint4 per weight slot: 32 rows, then 64 gamma values
+  constexpr int WS = 32 * 8 + (G ? 8 : 0);  // uint4 per weight slot: 32 rows, then 64 gamma values
   constexpr int WAVE_U4 = RX * XS + RW * WS;
   // requests issued after the later of a chunk's operand and weight requests
   constexpr int YMAX = RX < RW ? WN + (RX - 1) * (XN + WN) : (RW - 1) * (XN + WN);
@@ -1889,7 +1892,7 @@ __global__ __launch_bounds__(256) void qkv_decode_pair_kernel(DecodeArgs d, QkvE
     const uint16_t* wb = d.w + kc * 256;
 #pragma unroll
     for (int j = 0; j < 4; ++j) dma16(wb, woff[j], ls + j * 1024);
-    if constexpr (SA) {
+    if constexpr (G) {
       // lanes 0-7: the segment's 64 gamma values
       if (lane < 8) dma16(static_cast<const uint16_t*>(d.gamma) + kc * 256, goff, ls + 256 * 16);
     }
@@ -1985,7 +1988,7 @@ __global__ __launch_bounds__(256) void qkv_decode_pair_kernel(DecodeArgs d, QkvE
 #pragma unroll
       for (int h = 0; h < 2; ++h) wf[j][h] = wsl[wslot(j * 16 + lr, h * 4 + lq)];
     uint4 gw[2] = {};
-    if constexpr (SA) {
+    if constexpr (G) {
       gw[0] = wsl[256 + lq];
       gw[1] = wsl[256 + 4 + lq];
     }
@@ -2024,17 +2027,21 @@ __global__ __launch_bounds__(256) void qkv_decode_pair_kernel(DecodeArgs d, QkvE
       for (int i = 0; i < MT; ++i)
 #pragma unroll
         for (int h = 0; h < 2; ++h) gacc[i] = mfma16<true>(af[i][h], af[i][h], gacc[i]);
-      convert(0);
-      interleave();
-      __builtin_amdgcn_sched_barrier(0);
+      if constexpr (G) {
+        convert(0);
+        interleave();
+        __builtin_amdgcn_sched_barrier(0);
+      }
 #pragma unroll
       for (int i = 0; i < MT; ++i) {
         acc[i][0] = mfma16<true>(af[i][0], wf[0][0], acc[i][0]);
         acc[i][1] = mfma16<true>(af[i][0], wf[1][0], acc[i][1]);
       }
-      convert(1);
-      interleave();
-      __builtin_amdgcn_sched_barrier(0);
+      if constexpr (G) {
+        convert(1);
+        interleave();
+        __builtin_amdgcn_sched_barrier(0);
+      }
 #pragma unroll
       for (int i = 0; i < MT; ++i) {
         acc[i][0] = mfma16<true>(af[i][1], wf[0][1], acc[i][0]);
@@ -2669,10 +2676,15 @@ template <int MT>
 static void launch_pair_mt(bool sa, int edt, dim3 grid, const DecodeArgs& d, const QkvEpi& e, int nch,
                            hipStream_t st) {
   if (sa) {
-    if (edt == EDT_F32_BF16)
-      hipLaunchKernelGGL((qkv_decode_pair_kernel<MT, true, EDT_F32_BF16>), grid, dim3(256), 0, st, d, e, nch);
-    else
-      hipLaunchKernelGGL((qkv_decode_pair_kernel<MT, true, EDT_RT>), grid, dim3(256), 0, st, d, e, nch);
+    // no gamma: the weight has it folded in
+    const bool gin = d.gamma != nullptr;
+    if (edt == EDT_F32_BF16) {
+      if (gin) hipLaunchKernelGGL((qkv_decode_pair_kernel<MT, true, EDT_F32_BF16>), grid, dim3(256), 0, st, d, e, nch);
+      else hipLaunchKernelGGL((qkv_decode_pair_kernel<MT, true, EDT_F32_BF16, false>), grid, dim3(256), 0, st, d, e, nch);
+    } else {
+      if (gin) hipLaunchKernelGGL((qkv_decode_pair_kernel<MT, true, EDT_RT>), grid, dim3(256), 0, st, d, e, nch);
+      else hipLaunchKernelGGL((qkv_decode_pair_kernel<MT, true, EDT_RT, false>), grid, dim3(256), 0, st, d, e, nch);
+    }
     return;
   }
   if (edt == EDT_F32_BF16)
@@ -2824,7 +2836,8 @@ static int qkv_projection_impl(const void* operand, int64_t lda, const OperandFo
     d.m = tokens; d.n = qkv_dim; d.k = hidden; d.lda = lda; d.ldw = w_stride;
     const bool sa = fold && fold->stats;
     if (sa) {
-      BFA_REQUIRE(fold->gamma_dt == BFA_DTYPE_BF16 && aligned16(fold->gamma),
+      // a null gamma: folded into the weight already
+      BFA_REQUIRE(!fold->gamma || (fold->gamma_dt == BFA_DTYPE_BF16 && aligned16(fold->gamma)),
                   "%s: scale-after needs a 16-byte aligned bf16 norm weight", what);
       d.gamma = fold->gamma; d.gamma_dt = fold->gamma_dt; d.eps = fold->eps;
     }
@@ -2832,8 +2845,10 @@ static int qkv_projection_impl(const void* operand, int64_t lda, const OperandFo
     launch_pair(p, d, e, sa, st);
     return check_launch(what);
   }
-  // the scale-after fold outside the pair kernel is the deep-K kernel's
-  BFA_REQUIRE(!(fold && fold->stats) || (p.decode && p.nch > 0), "%s: scale-after fold without a kernel", what);
+  // the scale-after fold outside the pair kernel is the deep-K kernel's (with
+  // its gamma: a folded weight has only the pair kernel)
+  BFA_REQUIRE(!(fold && fold->stats) || (p.decode && p.nch > 0 && fold->gamma),
+              "%s: scale-after fold without a kernel", what);
   if (p.decode) {
     SplitArgs s{};
     s.a = static_cast<const uint16_t*>(operand);
@@ -3099,11 +3114,37 @@ extern "C" int bfa_fused_rmsnorm_qkv_folded(
   BFA_REQUIRE(x_stride >= hidden && x_stride % 8 == 0, "%s: x rows must be 16-byte aligned", what);
   const int64_t heads = num_q_heads + 2 * num_kv_heads;
   BFA_REQUIRE(heads > 0 && qkv_dim % heads == 0, "%s: bad head geometry", what);
-  const QkvPlan p = make_plan(tokens, qkv_dim, hidden, qkv_dim / heads);
-  BFA_REQUIRE(!p.decode && p.fused_epi, "%s: prefill (more than 64 tokens, head_dim 32, 64 or 128) only", what);
-  BFA_REQUIRE(workspace && workspace_bytes >= p.operand_bytes + p.part_bytes && aligned16(workspace),
-              "%s: workspace too small (%lld < %lld bytes)", what, (long long)workspace_bytes,
-              (long long)(p.operand_bytes + p.part_bytes));
+  const int64_t hd = qkv_dim / heads;
+  const QkvPlan p = make_plan(tokens, qkv_dim, hidden, hd);
+  // decode: the column-pair kernel on x, its row statistic from the Gram
+  // diagonal (the scale-after form without the gamma conversion)
+  const bool pair = p.decode && x_dtype == BFA_DTYPE_BF16 && aligned16(x) &&
+                    pair_ok(p, qkv_dim, hd, hidden, false, true, x_stride, x, tokens, w_stride);
+  if (!pair && (p.decode || !p.fused_epi))
+    return set_error(BFA_ERR_UNSUPPORTED,
+                     "%s: the prefill epilogue (more than 64 tokens, head_dim 32, 64 or 128) or the "
+                     "column-pair decode shapes (17-64 bf16 tokens) only", what);
+  const int64_t fsize = p.operand_bytes + p.part_bytes;
+  const int64_t need = fsize + (layer_cache && p.decode ? align256(tokens * 8) : 0);
+  BFA_REQUIRE(workspace && workspace_bytes >= need && aligned16(workspace),
+              "%s: workspace too small (%lld < %lld bytes)", what, (long long)workspace_bytes, (long long)need);
+  char* ws = static_cast<char*>(workspace);
+  if (pair) {
+    int64_t* slot_off = nullptr;
+    if (layer_cache) {
+      slot_off = reinterpret_cast<int64_t*>(ws + fsize);
+      launch_kv_slots(a, tokens, slot_off, as_stream(stream));
+      const int rc = check_launch(what);
+      if (rc != BFA_OK) return rc;
+    }
+    const CacheEpi ce{layer_cache, cache_dtype, stride_kv, stride_head, slot_off, write_kv_out ? 0 : 1, &a};
+    const OperandFold f{nullptr, BFA_DTYPE_BF16, false, eps, 0, reinterpret_cast<float*>(ws)};
+    return qkv_projection_impl(x, x_stride, &f, tokens, hidden, folded_weight, w_dtype, qkv_dim, w_stride, bias,
+                               bias_dtype, num_q_heads, num_kv_heads, qkv_dtype, nullptr, nullptr, 0, 0.f,
+                               BFA_DTYPE_BF16, positions, positions_dtype, cos_sin_cache, max_position, out,
+                               out_dtype, out_stride, ws + p.operand_bytes, fsize - p.operand_bytes, status,
+                               stream, layer_cache ? &ce : nullptr);
+  }
   float* rs = static_cast<float*>(workspace);
   const int64_t rs_bytes = align256(tokens * 4);
   int rc = launch_row_scale(x, x_dtype, tokens, hidden, x_stride, rs, eps, as_stream(stream));

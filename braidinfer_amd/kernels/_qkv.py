@@ -32,7 +32,11 @@ def head_dim_of(qkv_dim: int, num_q_heads: int, num_kv_heads: int) -> int:
 # A write that bypasses torch's version counter (a raw-pointer kernel writing
 # into the weight) needs clear_folded_weights().
 _folded: dict = {}
-_FOLD_MIN_TOKENS = 65  # the prefill projection's fused epilogue
+# From 17 tokens: the column-pair decode kernel (17-64, shapes it takes) and the
+# prefill projection's fused epilogue; fewer tokens fold the norm into their
+# one decode launch already.
+_FOLD_MIN_TOKENS = 17
+_ERR_UNSUPPORTED = -2  # BFA_ERR_UNSUPPORTED: the folded entry does not take the shape
 
 
 def _drop_folded(key, ref) -> None:
@@ -152,18 +156,26 @@ def fused_rmsnorm_qkv(
     # the variants without the mixed rounding, at prefill: x projected onto the
     # folded weight (the unconverted weight and norm weight only, so that the
     # cache key is the caller's own tensors)
+    # (decode counts: the column-pair kernel's shapes, bf16, at least 128 column
+    # pairs; the C side has the last word and answers BFA_ERR_UNSUPPORTED otherwise)
+    decode_ok = (_FOLD_MIN_TOKENS <= tokens <= 64 and not mixed_rounding and input.dtype == torch.bfloat16
+                 and hd % 32 == 0 and hidden % 256 == 0
+                 and (qkv_dim // 32 >= 128 or _lib.get_tuning("DECODE_PAIR") == 1)
+                 and _lib.get_tuning("DECODE_PAIR") != 0)
     if (not mixed_rounding and tokens >= _FOLD_MIN_TOKENS
-            and q_norm_weight is None and k_norm_weight is None and hd in (32, 64, 128)
+            and q_norm_weight is None and k_norm_weight is None
+            and (decode_ok or (tokens > 64 and hd in (32, 64, 128)))
             and w is qkv_weight and norm_weight is orig_norm_weight and input.dtype == w.dtype
             and hidden % 8 == 0 and input.stride(0) % 8 == 0 and norm_weight.data_ptr() % 16 == 0
             and out.stride(-1) == 1 and out.stride(0) % 4 == 0 and out.data_ptr() % 16 == 0):
         wf = folded_weight(w, norm_weight)
         if wf is not None:
-            ws_bytes = _lib.workspace_size("bfa_fused_rmsnorm_qkv_workspace_size", tokens, hidden, qkv_dim, hd)
+            size_fn = ("bfa_fused_rmsnorm_qkv_append_workspace_size" if paged_kv is not None
+                       else "bfa_fused_rmsnorm_qkv_workspace_size")
+            ws_bytes = _lib.workspace_size(size_fn, tokens, hidden, qkv_dim, hd)
             workspace = _lib.workspace(dev, ws_bytes)
             no_cache = (None, 0, 0, 0, 0, 0, 0, 0, None, 0, 0, None, None, 0, 0, None, 0, 0, 0)
-            _lib.call(
-                "bfa_fused_rmsnorm_qkv_folded",
+            rc = _FOLDED()(
                 input.data_ptr(), _lib.dtype_code(input), tokens, hidden, input.stride(0), float(eps),
                 wf.data_ptr(), _lib.dtype_code(wf), qkv_dim, wf.stride(0),
                 _lib.ptr(qkv_bias), _lib.dtype_code(qkv_bias) if qkv_bias is not None else 0,
@@ -175,7 +187,10 @@ def fused_rmsnorm_qkv(
                 *(cache_args if paged_kv is not None else no_cache),
                 _lib.status_word(dev).data_ptr(), _lib.stream_of(dev),
             )
-            return out
+            if rc == 0:
+                return out
+            if rc != _ERR_UNSUPPORTED:
+                _lib.raise_error(rc)
     if tokens == 0:
         return out
     if paged_kv is not None:
@@ -229,6 +244,16 @@ def _FUSED():
     if _fused_fn is None:
         _fused_fn = _lib.entry("bfa_fused_rmsnorm_qkv")
     return _fused_fn
+
+
+_folded_fn = None
+
+
+def _FOLDED():
+    global _folded_fn
+    if _folded_fn is None:
+        _folded_fn = _lib.entry("bfa_fused_rmsnorm_qkv_folded")
+    return _folded_fn
 
 
 def split_heads(output: torch.Tensor, num_q_heads: int, num_kv_heads: int):

@@ -273,10 +273,15 @@ int bfa_fused_rmsnorm_qkv_noalloc(const void* x, int x_dtype, int64_t tokens, in
  * bfa_fused_rmsnorm_qkv_folded: as bfa_fused_rmsnorm_qkv with mixed_rounding = 0 and
  * no q/k norm, on the folded weight, and with layer_cache != NULL as
  * bfa_fused_rmsnorm_qkv_append (same cache arguments; NULL: no append, the other
- * cache arguments unread); more than 64 tokens and head_dim 32, 64 or 128 (the
- * prefill projection's fused epilogue), x in W's dtype.  Against the oracle the
- * bf16 rounding moves from the operand to the weight, within the same tolerance.
- * workspace: bfa_fused_rmsnorm_qkv_workspace_size() bytes. */
+ * cache arguments unread).  It takes the prefill projection's fused epilogue
+ * (more than 64 tokens, head_dim 32, 64 or 128) and the column-pair decode
+ * kernel's shapes (17-64 bf16 tokens, head_dim a multiple of 32, hidden a
+ * multiple of 256, at least 128 column pairs: the row statistic then comes from
+ * the kernel's own Gram diagonal), x in W's dtype; other shapes return
+ * BFA_ERR_UNSUPPORTED before any launch.  Against the oracle the bf16 rounding
+ * moves from the operand to the weight, within the same tolerance.
+ * workspace: bfa_fused_rmsnorm_qkv_workspace_size() bytes, and with an append at
+ * decode counts bfa_fused_rmsnorm_qkv_append_workspace_size(). */
 int bfa_fold_rmsnorm_weight(const void* qkv_weight, int w_dtype, int64_t qkv_dim, int64_t hidden,
                             int64_t w_stride, const void* norm_weight, int nw_dtype, void* folded,
                             int64_t folded_stride, void* stream);

@@ -6,9 +6,11 @@ models/llama.py:169-205) project x onto bf16(W * gamma) and scale each row by
 
 Checked here: the folded weight against its definition (bit for bit), the
 folded path against the oracle and against the pre-pass path at the same
-tolerance, the cache of folded weights (an in-place change of either weight, or
-a new tensor, folds again; clear_folded_weights drops them), graph capture with
-and without a folded copy, and the entry point's refusal of decode token counts.
+tolerance, at prefill and at the 17-64-token decode shapes of the column-pair
+kernel (with and without the paged append), the cache of folded weights (an
+in-place change of either weight, or a new tensor, folds again;
+clear_folded_weights drops them), graph capture with and without a folded copy,
+and the entry point's refusal of the other decode shapes.
 The parity tests of the variants themselves (test_gpu_qkv.py,
 test_gpu_fused_append.py, test_gpu_fp32_mode.py) run through this path at
 prefill token counts."""
@@ -145,8 +147,10 @@ def test_folded_graph_capture(warm):
     _qkv.clear_folded_weights()
 
 
-def test_folded_entry_refuses_decode_counts():
-    """The folded entry point takes the prefill epilogue only: 64 tokens is an error."""
+def test_folded_entry_refuses_other_decode_shapes():
+    """Below 65 tokens the folded entry point takes the column-pair kernel's shapes
+    only: 64 tokens on 48 column pairs is BFA_ERR_UNSUPPORTED (and the Python
+    layer runs the unfolded path for them)."""
     t, h, hq, hkv, d = 64, 1024, 8, 2, 128
     x, ln, w, _ = make(505, t, h, hq, hkv, d)
     xd, wd = x.to(DEV), w.to(DEV)
@@ -155,8 +159,49 @@ def test_folded_entry_refuses_decode_counts():
     ws = torch.empty(_lib.workspace_size("bfa_fused_rmsnorm_qkv_workspace_size", t, h, n, d), dtype=torch.uint8,
                      device=DEV)
     no_cache = (None, 0, 0, 0, 0, 0, 0, 0, None, 0, 0, None, None, 0, 0, None, 0, 0, 0)
-    with pytest.raises(ValueError, match="prefill"):
+    with pytest.raises(_lib.BraidinferAMDError, match="column-pair"):
         _lib.call("bfa_fused_rmsnorm_qkv_folded", xd.data_ptr(), _lib.BF16, t, h, h, 1e-5, wd.data_ptr(),
                   _lib.BF16, n, h, None, 0, hq, hkv, _lib.F32, None, 0, None, 0, out.data_ptr(), _lib.F32, n,
                   ws.data_ptr(), ws.numel(), *no_cache, _lib.status_word(torch.device(DEV)).data_ptr(),
                   _lib.stream_of(torch.device(DEV)))
+
+
+@pytest.mark.parametrize("t", [17, 40, 64])
+def test_folded_decode_pair(monkeypatch, t):
+    """Llama-3-8B decode batches of 17-64 tokens: the column-pair kernel on x and
+    the folded weight, against the oracle and against the in-kernel gamma form;
+    with the paged append, the cache holds the output's k/v bit for bit."""
+    h, hq, hkv, d = 4096, 32, 8, 128
+    x, ln, w, g = make(506, t, h, hq, hkv, d)
+    cache = R.cos_sin_cache(d, 8192, 5e5)
+    pos = torch.randint(0, 8192, (t,), generator=g)
+    args = (x.to(DEV), ln.to(DEV), w.to(DEV))
+    _qkv.clear_folded_weights()
+    ref = R.llama_attention_input(x, ln, w, hq, hkv, 1e-5, pos, cache)
+    folded = llama_attention_input(*args, hq, hkv, 1e-5, pos.to(DEV), cache.to(DEV))
+    assert len(_qkv._folded) == 1, "the decode batch did not take the folded path"
+    for g_, e_, name in zip(folded, ref, "qkv"):
+        assert_close(g_, e_, what=f"folded decode {name} t={t}")
+    monkeypatch.setattr(_qkv, "_FOLD_MIN_TOKENS", 1 << 40)  # gamma on the weight fragments in the kernel
+    unfolded = llama_attention_input(*args, hq, hkv, 1e-5, pos.to(DEV), cache.to(DEV))
+    monkeypatch.undo()
+    for a, b, name in zip(folded, unfolded, "qkv"):
+        assert_close(a, b, what=f"folded against in-kernel gamma {name} t={t}")
+    # with the paged append (HND cache, 16-slot pages, shuffled page list)
+    from braidinfer_amd.kernels import PagedKVAppend
+    ps, start = 16, 5
+    need = (start + t + ps - 1) // ps
+    kv_indices = torch.randperm(need + 3, generator=g)[:need].to(torch.int32)
+    layer = torch.zeros(need + 3, 2, hkv, ps, d, dtype=torch.bfloat16, device=DEV)
+    cpos = torch.arange(start, start + t, dtype=torch.int64)
+    pkv = PagedKVAppend(layer, kv_indices.to(DEV), cpos.to(DEV), ps, "HND")
+    q2, k2, v2 = llama_attention_input(*args, hq, hkv, 1e-5, pos.to(DEV), cache.to(DEV), paged_kv=pkv)
+    torch.cuda.synchronize()
+    for a, b in zip((q2, k2, v2), folded):
+        assert torch.equal(bits(a.cpu()), bits(b.cpu())), "the append call's output differs from the plain call's"
+    exp, skipped = R.append_to_paged_kv_cache(k2.cpu().reshape(t, hkv, d), v2.cpu().reshape(t, hkv, d),
+                                              torch.zeros(need + 3, 2, hkv, ps, d, dtype=torch.bfloat16),
+                                              kv_indices, cpos, ps, "HND")
+    assert skipped == [] and torch.equal(bits(layer.cpu()), bits(exp))
+    braidinfer_amd.check_device_status()
+    _qkv.clear_folded_weights()
