@@ -62,6 +62,8 @@ def folded_weight(w: torch.Tensor, norm_weight: torch.Tensor) -> torch.Tensor | 
     _lib.call("bfa_fold_rmsnorm_weight", w.data_ptr(), _lib.dtype_code(w), n, k, w.stride(0),
               norm_weight.data_ptr(), _lib.dtype_code(norm_weight), wf.data_ptr(), wf.stride(0),
               _lib.stream_of(w.device))
+    # once per pair: the fold is finished before any stream can read the copy
+    torch.cuda.current_stream(w.device).synchronize()
     wr = weakref.ref(w, lambda r, key=key: _drop_folded(key, r))
     nr = weakref.ref(norm_weight, lambda r, key=key: _drop_folded(key, r))
     _folded[key] = (wr, nr, state, wf)
