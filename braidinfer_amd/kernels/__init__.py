@@ -1,4 +1,5 @@
 """MI355X kernels under the module and class names of braidinfer/kernels."""
+from ._qkv import clear_folded_weights
 from .fused_attention_output import FusedAttentionOutput, attention_output, attention_output_gemv
 from .fused_rmsnorm_qkv_minimal_f32 import FusedRMSNormQKVMinimalF32
 from .fused_rmsnorm_qkv_mixed_precision import FusedRMSNormQKVMixedPrecision
@@ -22,5 +23,6 @@ __all__ = [
     "attention_output_gemv",
     "append_to_paged_kv_cache_custom",
     "build_paged_kv_indices",
+    "clear_folded_weights",
     "online_softmax_update",
 ]
