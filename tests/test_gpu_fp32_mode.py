@@ -10,7 +10,7 @@ that bound.  So every case asserts:
 
 * where the reference's rounding keeps every element inside the bound (the
   norms, SiLU*mul, the Llama chains, the v heads, the linear fusions), the GPU
-  path keeps every element inside it too -- the north-star bound, outright;
+  path keeps every element inside it too -- the bound itself, outright;
 * elsewhere (the Qwen3 q/k heads after the extreme k_norm weights), that the
   GPU path is no further from the fp32 reference than the reference's rounding
   is: at most 1e-4 of the elements more outside the bound (the count is
