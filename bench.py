@@ -660,6 +660,11 @@ def chain_graph_rotating_us(c: Chain, steps: int, warmup: int, nw: int = 4) -> f
         turn[0] += 1
         c.step()
     try:
+        # one eager step per copy first, as a model's warm-up forward would: each
+        # weight gets its folded copy before the capture (a fold is never captured)
+        for _ in range(nw):
+            step()
+        torch.cuda.synchronize()
         return chain_graph_us(c, -(-steps // nw) * nw, warmup, step)
     finally:
         c.w_qkv = ws[0]
