@@ -190,15 +190,23 @@ TUNING_KEYS = {
 }
 
 
+_tuning_seen: dict = {}  # the values this module has read or set (the library changes them only through set_tuning)
+
+
 def set_tuning(name: str, value: int | None) -> None:
     """Sets planner override `name` (a TUNING_KEYS key); None or -1 unsets it."""
     call("bfa_set_tuning", TUNING_KEYS[name], -1 if value is None else int(value))
+    _tuning_seen.pop(name, None)
 
 
 def get_tuning(name: str) -> int | None:
-    """Current value of planner override `name`, None when unset."""
+    """Current value of planner override `name`, None when unset (read from the
+    library once, then remembered until set_tuning changes it)."""
+    if name in _tuning_seen:
+        return _tuning_seen[name]
     v = load().bfa_get_tuning(TUNING_KEYS[name])
-    return None if v < 0 else v
+    _tuning_seen[name] = None if v < 0 else v
+    return _tuning_seen[name]
 
 
 _workspaces: dict = {}

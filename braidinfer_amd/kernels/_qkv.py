@@ -50,8 +50,9 @@ def folded_weight(w: torch.Tensor, norm_weight: torch.Tensor) -> torch.Tensor | 
     under graph capture when no folded copy exists yet (the caller then runs the
     unfolded path: a fold captured into a graph would be redone on every replay)."""
     key = (id(w), id(norm_weight))
-    state = (w.data_ptr(), w._version, tuple(w.shape), w.stride(0), w.dtype,
-             norm_weight.data_ptr(), norm_weight._version, norm_weight.dtype)
+    # storage, version counter and shape: a new `.data` or an in-place change
+    # moves one of them
+    state = (w.data_ptr(), w._version, w.shape, norm_weight.data_ptr(), norm_weight._version)
     ent = _folded.get(key)
     if ent is not None and ent[0]() is w and ent[1]() is norm_weight and ent[2] == state:
         return ent[3]
@@ -160,10 +161,11 @@ def fused_rmsnorm_qkv(
     # cache key is the caller's own tensors)
     # (decode counts: the column-pair kernel's shapes, bf16, at least 128 column
     # pairs; the C side has the last word and answers BFA_ERR_UNSUPPORTED otherwise)
-    decode_ok = (_FOLD_MIN_TOKENS <= tokens <= 64 and not mixed_rounding and input.dtype == torch.bfloat16
-                 and hd % 32 == 0 and hidden % 256 == 0
-                 and (qkv_dim // 32 >= 128 or _lib.get_tuning("DECODE_PAIR") == 1)
-                 and _lib.get_tuning("DECODE_PAIR") != 0)
+    decode_ok = False
+    if _FOLD_MIN_TOKENS <= tokens <= 64 and not mixed_rounding and input.dtype == torch.bfloat16 \
+            and hd % 32 == 0 and hidden % 256 == 0:
+        pair_mode = _lib.get_tuning("DECODE_PAIR")
+        decode_ok = pair_mode != 0 and (qkv_dim // 32 >= 128 or pair_mode == 1)
     if (not mixed_rounding and tokens >= _FOLD_MIN_TOKENS
             and q_norm_weight is None and k_norm_weight is None
             and (decode_ok or (tokens > 64 and hd in (32, 64, 128)))
