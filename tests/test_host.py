@@ -144,3 +144,80 @@ def test_cascade_query_shape_is_checked_before_launch():
     for bad in (torch.zeros(3, 2, 128), torch.zeros(3, 4, 64), torch.zeros(3, 4 * 128 - 8)):
         with pytest.raises(ValueError):
             att.forward(bad.bfloat16(), pos, cache, [], 0)
+
+
+class _FoldSpy:
+    """Stands in for the library and torch.cuda in the folded-weight cache: the
+    fold call is counted, not run (no GPU here)."""
+
+    def __init__(self, monkeypatch, capturing=False):
+        from braidinfer_amd import _lib
+        from braidinfer_amd.kernels import _qkv
+        self.folds = 0
+        self.capturing = capturing
+
+        def call(name, *args):
+            assert name == "bfa_fold_rmsnorm_weight"
+            self.folds += 1
+            return 0
+
+        class _Stream:
+            def synchronize(self):
+                pass
+        monkeypatch.setattr(_lib, "call", call)
+        monkeypatch.setattr(_lib, "stream_of", lambda dev: 0)
+        monkeypatch.setattr(_qkv.torch.cuda, "current_stream", lambda dev=None: _Stream())
+        monkeypatch.setattr(_qkv.torch.cuda, "is_current_stream_capturing", lambda: self.capturing)
+        _qkv.clear_folded_weights()
+
+
+def test_folded_weight_cache_rules(monkeypatch):
+    """The folded copy of (W, norm weight) is made once and reused while both
+    tensors are the same objects with the same storage, version counter and
+    shape; an in-place change, a new `.data`, a new tensor, or a dropped tensor
+    changes that; under graph capture nothing is folded."""
+    import gc
+
+    from braidinfer_amd.kernels import _qkv
+    spy = _FoldSpy(monkeypatch)
+    w = torch.zeros(64, 32, dtype=torch.bfloat16)
+    ln = torch.ones(32, dtype=torch.bfloat16)
+    a = _qkv.folded_weight(w, ln)
+    assert spy.folds == 1 and a.shape == w.shape and a.dtype == w.dtype
+    assert _qkv.folded_weight(w, ln) is a and spy.folds == 1           # reused
+    ln.mul_(2)                                                          # in place: version moves
+    b = _qkv.folded_weight(w, ln)
+    assert spy.folds == 2 and b is not a
+    w[0].fill_(1)                                                       # in place through a view
+    _qkv.folded_weight(w, ln)
+    assert spy.folds == 3
+    w.data = torch.zeros(64, 32, dtype=torch.bfloat16)                  # new storage
+    _qkv.folded_weight(w, ln)
+    assert spy.folds == 4 and len(_qkv._folded) == 1
+    w2 = w.clone()                                                      # another tensor: its own entry
+    _qkv.folded_weight(w2, ln)
+    assert spy.folds == 5 and len(_qkv._folded) == 2
+    del w2
+    gc.collect()
+    assert len(_qkv._folded) == 1                                       # dropped with its tensor
+    spy.capturing = True
+    assert _qkv.folded_weight(w.clone(), ln) is None and spy.folds == 5  # no fold under capture
+    assert _qkv.folded_weight(w, ln) is not None and spy.folds == 5      # an existing copy is used
+    assert _qkv.clear_folded_weights() == 1 and not _qkv._folded
+
+
+def test_fold_algebra_in_float64():
+    """The identity the folded path rests on, in float64 on the oracle's own
+    operand: ((x / rms) * gamma) @ W^T == (x @ (W * gamma)^T) / rms, gamma along
+    the hidden (K) axis of W.  Folding gamma along the other axis fails it."""
+    g = torch.Generator().manual_seed(7)
+    t, h = 5, 64
+    x = torch.randn(t, h, generator=g, dtype=torch.float64)
+    w = torch.randn(h, h, generator=g, dtype=torch.float64)  # square, so either axis fits
+    gamma = torch.rand(h, generator=g, dtype=torch.float64) + 0.5
+    inv = 1.0 / torch.sqrt((x * x).mean(-1, keepdim=True) + 1e-5)
+    ref = ((x * inv) * gamma) @ w.t()
+    folded = (x @ (w * gamma[None, :]).t()) * inv
+    assert torch.allclose(folded, ref, rtol=1e-12, atol=1e-12)
+    wrong_axis = (x @ (w * gamma[:, None]).t()) * inv
+    assert not torch.allclose(wrong_axis, ref, rtol=1e-3, atol=1e-3)
