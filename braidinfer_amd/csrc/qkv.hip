@@ -246,6 +246,33 @@ __device__ __forceinline__ void mfma_block(f32x16_t (&acc)[MB][NB], const uint4 
     for (int j = 0; j < NB; ++j) acc[i][j] = mfma32<BF16>(af[i], bf[j], acc[i][j]);
 }
 
+// 16x16x32 fragments of a 64-deep tile (the 64-deep DMA path): sub-step ks (0
+// or 1) is 32 deep, and lane l reads row l % 16 of each 16-row block at granule
+// 4 ks + l / 16.  A 16-lane phase still reads one granule of 16 consecutive
+// rows, so swz() keeps the reads on 16 distinct bank groups.
+template <int MB16, int BM, int WM>
+__device__ __forceinline__ void load_a16(const uint4* buf, int ks, int wm, int lane, uint4 (&af)[MB16]) {
+  const int r = lane & 15, gsel = ks * 4 + (lane >> 4);
+#pragma unroll
+  for (int i = 0; i < MB16; ++i) af[i] = buf[swz(wm * WM + i * 16 + r, gsel)];
+}
+
+// half h (0 or 1) of the wave's 16-column weight blocks
+template <int NH, int BM, int WN>
+__device__ __forceinline__ void load_b16(const uint4* buf, int ks, int h, int wn, int lane, uint4 (&bf)[NH]) {
+  const int r = lane & 15, gsel = ks * 4 + (lane >> 4);
+#pragma unroll
+  for (int j = 0; j < NH; ++j) bf[j] = buf[BM * 8 + swz(wn * WN + (h * NH + j) * 16 + r, gsel)];
+}
+
+template <int MB16, int NB16, int NH, bool BF16>
+__device__ __forceinline__ void mfma_half16(f32x4_t (&acc)[MB16][NB16], const uint4 (&af)[MB16],
+                                            const uint4 (&bf)[NH], int h) {
+#pragma unroll
+  for (int i = 0; i < MB16; ++i)
+#pragma unroll
+    for (int j = 0; j < NH; ++j) acc[i][h * NH + j] = mfma16<BF16>(af[i], bf[j], acc[i][h * NH + j]);
+}
 
 // s_waitcnt vmcnt(N) for a compile-time N, other counters untouched
 // (gfx9 encoding: vmcnt[3:0], expcnt[6:4], lgkmcnt[11:8], vmcnt[5:4] in [15:14]).
@@ -367,26 +394,43 @@ __device__ __forceinline__ void tile_origin(const GemmArgs& g, int64_t tile, int
 }
 
 // ------------------------------------------------------------ GEMM epilogue
-// Shared by the GEMM kernels.  32x32 accumulator layout: lane holds column
-// (lane & 31) and rows 8*(v/4) + 4*(lane/32) + (v%4), v = 0..15, of each of the
-// wave's MB x NB 32x32 blocks; the wave tile starts at row m0 + wm * WM and
-// column n0 + wn * WN (n0 in output columns).  lds: at least NW x 32 x LDR
+// Shared by the GEMM kernels.  acc is either f32x16_t [MB][NB], the 32x32
+// layout (lane holds column (lane & 31) and rows 8*(v/4) + 4*(lane/32) + (v%4),
+// v = 0..15, of each of the wave's MB x NB 32x32 blocks), or f32x4_t
+// [2 MB][2 NB], the 16x16 layout (lane holds column (lane & 15) and rows
+// 4*(lane/16) + v, v = 0..3, of each 16x16 block); the wave tile starts at row
+// m0 + wm * WM and column n0 + wn * WN (n0 in output columns).  lds: at least NW x 32 x LDR
 // floats, free for the wave-private staging slices (the caller's barrier-free
 // LDS use must be over).  praw: the rows' raw positions when EARLY (one block
 // per wave, requested before the K loop).  SLOT_U4: uint4 offset in lds of the
 // fused KV append's slot table (MB x 32 int64 per wave), followed by the row
 // scales' table (MB x 32 floats per wave).
-template <int EPI, int HD, int MB, int NB, int WM, int WN, int NW, int EDT, bool EARLY, int SLOT_U4>
-__device__ __forceinline__ void gemm_epilogue(f32x16_t (&acc)[MB][NB], uint4* lds, const GemmArgs& g,
-                                              const QkvEpi& e, int64_t m0, int64_t n0, int wid, int wm,
-                                              int wn, int lane, const int64_t* praw) {
+template <int EPI, int HD, int MB, int NB, int WM, int WN, int NW, int EDT, bool EARLY, int SLOT_U4, typename ACC>
+__device__ __forceinline__ void gemm_epilogue(ACC& acc, uint4* lds, const GemmArgs& g, const QkvEpi& e,
+                                              int64_t m0, int64_t n0, int wid, int wm, int wn, int lane,
+                                              const int64_t* praw) {
   using DT = EpiDt<EDT>;
+  constexpr bool A16 = sizeof(acc[0][0]) == sizeof(f32x4_t);  // 16x16 accumulator blocks
   constexpr int LDR = 136;
   constexpr bool EARLY_POS = EARLY;
   const int frow = lane & 31, fhalf = lane >> 5;
   const int64_t wcol0 = n0 + wn * WN;
   const int64_t wrow0 = m0 + wm * WM;
-  if constexpr (EPI == EPI_RAW) {
+  if constexpr (EPI == EPI_RAW && A16) {
+#pragma unroll
+    for (int i = 0; i < 2 * MB; ++i)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int64_t row = wrow0 + i * 16 + 4 * (lane >> 4) + v;
+        if (row >= g.m) continue;
+#pragma unroll
+        for (int j = 0; j < 2 * NB; ++j) {
+          const int64_t col = wcol0 + j * 16 + (lane & 15);
+          if (col < g.n) g.raw[row * g.n + col] = acc[i][j][v];
+        }
+      }
+    return;
+  } else if constexpr (EPI == EPI_RAW) {
 #pragma unroll
     for (int i = 0; i < MB; ++i)
 #pragma unroll
@@ -412,11 +456,21 @@ __device__ __forceinline__ void gemm_epilogue(f32x16_t (&acc)[MB][NB], uint4* ld
     __syncthreads();  // the K loop's last LDS reads are done before the slices are reused
 #pragma unroll
     for (int i = 0; i < MB; ++i) {
+      if constexpr (A16) {
 #pragma unroll
-      for (int j = 0; j < NB; ++j)
+        for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
-        for (int v = 0; v < 16; ++v)
-          et[(8 * (v / 4) + 4 * fhalf + (v % 4)) * LDR + j * 32 + frow] = acc[i][j][v];
+          for (int cb = 0; cb < 2 * NB; ++cb)
+#pragma unroll
+            for (int v = 0; v < 4; ++v)
+              et[(rb * 16 + 4 * (lane >> 4) + v) * LDR + cb * 16 + (lane & 15)] = acc[2 * i + rb][cb][v];
+      } else {
+#pragma unroll
+        for (int j = 0; j < NB; ++j)
+#pragma unroll
+          for (int v = 0; v < 16; ++v)
+            et[(8 * (v / 4) + 4 * fhalf + (v % 4)) * LDR + j * 32 + frow] = acc[i][j][v];
+      }
       __asm__ volatile("" ::: "memory");  // wave-private slice, LDS keeps a wave's order
       // Kept rolled: unrolled over the 4 row groups the residual / store paths
       // grew the kernel past the instruction cache, and the K loop of the other
@@ -579,11 +633,21 @@ __device__ __forceinline__ void gemm_epilogue(f32x16_t (&acc)[MB][NB], uint4* ld
     for (int i = 0; i < MB; ++i) {
       float4 (&cvv_i)[NP] = cvv[i & 1];
       float4 (&svv_i)[NP] = svv[i & 1];
+      if constexpr (A16) {
 #pragma unroll
-      for (int j = 0; j < NB; ++j)
+        for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
-        for (int v = 0; v < 16; ++v)
-          et[(8 * (v / 4) + 4 * fhalf + (v % 4)) * LDR + j * 32 + frow] = acc[i][j][v];
+          for (int cb = 0; cb < 2 * NB; ++cb)
+#pragma unroll
+            for (int v = 0; v < 4; ++v)
+              et[(rb * 16 + 4 * (lane >> 4) + v) * LDR + cb * 16 + (lane & 15)] = acc[2 * i + rb][cb][v];
+      } else {
+#pragma unroll
+        for (int j = 0; j < NB; ++j)
+#pragma unroll
+          for (int v = 0; v < 16; ++v)
+            et[(8 * (v / 4) + 4 * fhalf + (v % 4)) * LDR + j * 32 + frow] = acc[i][j][v];
+      }
       // The slice is private to this wave and LDS executes one wave's accesses
       // in issue order, so the row reads below see these writes (and the next
       // block's writes follow this block's reads) without a barrier; only the
@@ -766,11 +830,30 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, (WM * WN <= 8192 ? 2 : 
     }
   }
 
-  f32x16_t acc[MB][NB];
+  // The QKV projection's 64-deep DMA path multiplies with v_mfma_f32_16x16x32
+  // into 16x16 blocks (acc4); every other path with v_mfma_f32_32x32x16 into
+  // 32x32 blocks (acc).  Same product and the same fragment bytes per wave tile,
+  // but a 16x16x32 MFMA reads and writes a quarter of the accumulators for half
+  // the work, and the chip is power limited under this loop: at 8192 tokens the
+  // Llama-3-8B projection took 313-325 against 323-334 us and the fused op
+  // 329-334 against 344-347 us, same box, interleaved processes.  The linear
+  // fusions keep the 32x32 form: with 16x16 blocks gate_up+SiLU*mul took 1629-
+  // 1633 against 1601-1608 us and down_proj+residual 827-831 against 810-815 us
+  // (o_proj+residual 219-224 against 227-228 us), same box, ABBA order.
+  constexpr bool M16 = DIRECT && BK == 64 && (EPI == EPI_FUSED || EPI == EPI_RAW);
+  f32x16_t acc[M16 ? 1 : MB][M16 ? 1 : NB];
+  f32x4_t acc4[M16 ? 2 * MB : 1][M16 ? 2 * NB : 1];
+  if constexpr (M16) {
 #pragma unroll
-  for (int i = 0; i < MB; ++i)
+    for (int i = 0; i < 2 * MB; ++i)
 #pragma unroll
-    for (int j = 0; j < NB; ++j) acc[i][j] = f32x16_t{};
+      for (int j = 0; j < 2 * NB; ++j) acc4[i][j] = f32x4_t{};
+  } else {
+#pragma unroll
+    for (int i = 0; i < MB; ++i)
+#pragma unroll
+      for (int j = 0; j < NB; ++j) acc[i][j] = f32x16_t{};
+  }
 
   // global -> register -> LDS (any K that is a multiple of 8).  The next
   // tile's loads are issued before this tile's MFMAs and stored to the other
@@ -842,6 +925,52 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, (WM * WN <= 8192 ? 2 : 
     for (int i = 0; i < BDPW; ++i)
       boff[i] = static_cast<uint32_t>((weight_row<EPI>(g, n0, (i * NW + wid) * 8 + lrow) * g.ldw + lgran * 8) * 2);
     const uint32_t l0 = lds_addr(lds0) + wid * 1024, l1 = lds_addr(lds1) + wid * 1024;
+    if constexpr (M16) {
+    // A stage is two 32-deep sub-steps, each in two halves of the wave's 16-column
+    // blocks: four quarters of M2 x NH MFMAs, each quarter's fragment reads issued
+    // under the previous quarter's MFMAs.  Two operand and two half-weight
+    // fragment sets (64 VGPRs; double-buffering whole sub-steps took 96 and
+    // spilled inside the loop).
+    constexpr int M2 = M16 ? 2 * MB : 1, N2 = M16 ? 2 * NB : 1, NH = M16 ? NB : 1;
+    uint4 fa0[M2], fa1[M2], fbA[NH], fbB[NH];
+    auto stage = [&](const uint4* cur) {
+      load_b16<NH, BM, WN>(cur, 0, 1, wn, lane, fbB);
+      mfma_half16<M2, N2, NH, BF16>(acc4, fa0, fbA, 0);
+      load_a16<M2, BM, WM>(cur, 1, wm, lane, fa1);
+      load_b16<NH, BM, WN>(cur, 1, 0, wn, lane, fbA);
+      mfma_half16<M2, N2, NH, BF16>(acc4, fa0, fbB, 1);
+      load_b16<NH, BM, WN>(cur, 1, 1, wn, lane, fbB);
+      mfma_half16<M2, N2, NH, BF16>(acc4, fa1, fbA, 0);
+      mfma_half16<M2, N2, NH, BF16>(acc4, fa1, fbB, 1);
+    };
+    issue_stage<ADPW, BDPW, BM, 64, NW>(g.a, g.w, 0, aoff, boff, l0);
+    resolve_slots();
+    wait_vmem();
+    __syncthreads();
+    load_a16<M2, BM, WM>(lds0, 0, wm, lane, fa0);  // the first quarter's fragments
+    load_b16<NH, BM, WN>(lds0, 0, 0, wn, lane, fbA);
+    int64_t kt = 0;
+    for (; kt + 2 <= KT; kt += 2) {
+      issue_stage<ADPW, BDPW, BM, 64, NW>(g.a, g.w, kt + 1, aoff, boff, l1);
+      stage(lds0);
+      wait_vmem();
+      __syncthreads();
+      load_a16<M2, BM, WM>(lds1, 0, wm, lane, fa0);
+      load_b16<NH, BM, WN>(lds1, 0, 0, wn, lane, fbA);
+      if (kt + 2 < KT) issue_stage<ADPW, BDPW, BM, 64, NW>(g.a, g.w, kt + 2, aoff, boff, l0);
+      stage(lds1);
+      wait_vmem();
+      __syncthreads();
+      if (kt + 2 < KT) {
+        load_a16<M2, BM, WM>(lds0, 0, wm, lane, fa0);
+        load_b16<NH, BM, WN>(lds0, 0, 0, wn, lane, fbA);
+      }
+    }
+    if (kt < KT) {  // odd tile count: the last tile is in lds0
+      stage(lds0);
+      __syncthreads();
+    }
+    } else {
     uint4 fa0[MB], fb0[NB], fa1[MB], fb1[NB];
     issue_stage<ADPW, BDPW, BM, 64, NW>(g.a, g.w, 0, aoff, boff, l0);
     resolve_slots();
@@ -867,6 +996,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, (WM * WN <= 8192 ? 2 : 
       compute3<MB, NB, BM, WM, WN, BF16>(lds0, wm, wn, frow, fhalf, acc, fa0, fb0, fa1, fb1);
       mfma_block<MB, NB, BF16>(acc, fa1, fb1);
       __syncthreads();
+    }
     }
   } else {
     const int gg = tid & 7, gr = tid >> 3;
@@ -918,8 +1048,12 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, (WM * WN <= 8192 ? 2 : 
   // before the K loop)
   int lane_e = lane, wid_e = wid;
   if constexpr (PERSIST) asm volatile("" : "+v"(lane_e), "+s"(wid_e));
-  gemm_epilogue<EPI, HD, MB, NB, WM, WN, NW, EDT, EARLY_POS, SLOT_U4>(acc, lds, g, e, m0, n0, wid_e, wid_e / NWN,
-                                                                    wid_e % NWN, lane_e, praw);
+  if constexpr (M16)
+    gemm_epilogue<EPI, HD, MB, NB, WM, WN, NW, EDT, EARLY_POS, SLOT_U4>(acc4, lds, g, e, m0, n0, wid_e,
+                                                                      wid_e / NWN, wid_e % NWN, lane_e, praw);
+  else
+    gemm_epilogue<EPI, HD, MB, NB, WM, WN, NW, EDT, EARLY_POS, SLOT_U4>(acc, lds, g, e, m0, n0, wid_e,
+                                                                      wid_e / NWN, wid_e % NWN, lane_e, praw);
   if constexpr (!PERSIST) break;  // one tile per workgroup: no loop, nothing hoisted out of one
   }
 }
