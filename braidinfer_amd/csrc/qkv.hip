@@ -273,6 +273,15 @@ __device__ __forceinline__ void mfma_half16(f32x4_t (&acc)[MB16][NB16], const ui
 #pragma unroll
     for (int j = 0; j < NH; ++j) acc[i][h * NH + j] = mfma16<BF16>(af[i], bf[j], acc[i][h * NH + j]);
 }
+// An empty statement that takes the accumulators in and out: every MFMA before
+// it in program order is issued before it, and none after it moves above it.
+template <int R, int C>
+__device__ __forceinline__ void pin_acc(f32x4_t (&acc)[R][C]) {
+#pragma unroll
+  for (int i = 0; i < R; ++i)
+#pragma unroll
+    for (int j = 0; j < C; ++j) asm volatile("" : "+v"(acc[i][j]));
+}
 
 // s_waitcnt vmcnt(N) for a compile-time N, other counters untouched
 // (gfx9 encoding: vmcnt[3:0], expcnt[6:4], lgkmcnt[11:8], vmcnt[5:4] in [15:14]).
@@ -930,7 +939,11 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, (WM * WN <= 8192 ? 2 : 
     // blocks: four quarters of M2 x NH MFMAs, each quarter's fragment reads issued
     // under the previous quarter's MFMAs.  Two operand and two half-weight
     // fragment sets (64 VGPRs; double-buffering whole sub-steps took 96 and
-    // spilled inside the loop).
+    // spilled inside the loop).  pin_acc keeps every MFMA of a stage above the
+    // stage's barrier: left alone, the compiler sank about half of them below it,
+    // ahead of the next stage's DMAs, which then went out a quarter of a stage
+    // late (8192 tokens, same box: the layer chain 514-515 against 496 us, and
+    // 543-544 against 513-515 us with the QKV weight rotating over four copies).
     constexpr int M2 = M16 ? 2 * MB : 1, N2 = M16 ? 2 * NB : 1, NH = M16 ? NB : 1;
     uint4 fa0[M2], fa1[M2], fbA[NH], fbB[NH];
     auto stage = [&](const uint4* cur) {
@@ -953,12 +966,14 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, (WM * WN <= 8192 ? 2 : 
     for (; kt + 2 <= KT; kt += 2) {
       issue_stage<ADPW, BDPW, BM, 64, NW>(g.a, g.w, kt + 1, aoff, boff, l1);
       stage(lds0);
+      pin_acc(acc4);
       wait_vmem();
       __syncthreads();
       load_a16<M2, BM, WM>(lds1, 0, wm, lane, fa0);
       load_b16<NH, BM, WN>(lds1, 0, 0, wn, lane, fbA);
       if (kt + 2 < KT) issue_stage<ADPW, BDPW, BM, 64, NW>(g.a, g.w, kt + 2, aoff, boff, l0);
       stage(lds1);
+      pin_acc(acc4);
       wait_vmem();
       __syncthreads();
       if (kt + 2 < KT) {
