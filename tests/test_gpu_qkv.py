@@ -316,6 +316,30 @@ def test_prefill_raw_epilogue_256_tiles():
         assert_close(got[rd], exp, what=f"raw 256-tile {name}")
 
 
+@pytest.mark.parametrize("tile", [2, 3])
+@pytest.mark.parametrize("h", [64, 192, 320, 448])
+@pytest.mark.parametrize("d,hq,hkv", [(128, 4, 2), (80, 6, 2)])
+def test_prefill_16x16_stage_counts(tuning, tile, h, d, hq, hkv):
+    """The 64-deep DMA loop of the 256x256 (tile 2) and 128x256 8-wave (tile 3)
+    tiles, which multiplies 16x16x32 blocks: 1, 3, 5 and 7 stages (the odd tail
+    after the two-stage loop), ragged rows and column tiles, through the fused
+    epilogue (head_dim 128, with RoPE) and the raw fp32 store plus the row
+    epilogue (head_dim 80), each against the oracle."""
+    tuning("QKV_TILE", tile)
+    t = 300
+    g, x, ln, w, _ = make(260 + h + d, t, h, hq, hkv, d)
+    q, k, v = FusedRMSNormQKV.forward(x.to(DEV), ln.to(DEV), w.to(DEV), hq, hkv, eps=1e-6)
+    for got, exp, name in zip((q, k, v), R.split_qkv(R.qkv_production(x, ln, w, 1e-6), hq, hkv), "qkv"):
+        assert_close(got, exp, what=f"16x16 production {name} tile={tile} h={h} d={d}")
+    if d == 128:
+        pos = torch.randint(0, 4096, (t,), generator=g)
+        cache = R.cos_sin_cache(d, 4096, 1e4)
+        q, k, v = llama_attention_input(x.to(DEV), ln.to(DEV), w.to(DEV), hq, hkv, 1e-5, pos.to(DEV),
+                                        cache.to(DEV))
+        for got, exp, name in zip((q, k, v), R.llama_attention_input(x, ln, w, hq, hkv, 1e-5, pos, cache), "qkv"):
+            assert_close(got, exp, what=f"16x16 llama {name} tile={tile} h={h}")
+
+
 @pytest.mark.parametrize("chain", ["llama", "qwen3"])
 def test_prefill_8192_sampled_rows(chain):
     """Llama-3-8B / Qwen3 prefill shapes at full size; the oracle checks a row sample."""
