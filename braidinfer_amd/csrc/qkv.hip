@@ -15,8 +15,9 @@
 //
 // Kernels
 //  * qkv_gemm_kernel   prefill.  BMxBN tile per workgroup of 4 or 8 waves, each
-//    wave WMx128 with v_mfma_f32_32x32x16_{bf16,f16}; 256x256 with 8 waves (two
-//    per SIMD) for large token counts.  Operand and weight K-slices move HBM ->
+//    wave WMx128: v_mfma_f32_16x16x32_{bf16,f16} on the QKV projection's 64-deep
+//    DMA path, v_mfma_f32_32x32x16 elsewhere; 256x256 with 8 waves (two per SIMD)
+//    for large token counts.  Operand and weight K-slices move HBM ->
 //    LDS by LDS DMA (global_load_lds_dwordx4) into XOR-swizzled buffers, so the
 //    MFMA fragment reads spread over the banks; unaligned or odd K goes through a
 //    register-staged path with masking.  The epilogue stages each wave's
