@@ -283,6 +283,13 @@ __device__ __forceinline__ void pin_acc(f32x4_t (&acc)[R][C]) {
 #pragma unroll
     for (int j = 0; j < C; ++j) asm volatile("" : "+v"(acc[i][j]));
 }
+template <int R, int C>
+__device__ __forceinline__ void pin_acc(f32x16_t (&acc)[R][C]) {
+#pragma unroll
+  for (int i = 0; i < R; ++i)
+#pragma unroll
+    for (int j = 0; j < C; ++j) asm volatile("" : "+v"(acc[i][j]));
+}
 
 // s_waitcnt vmcnt(N) for a compile-time N, other counters untouched
 // (gfx9 encoding: vmcnt[3:0], expcnt[6:4], lgkmcnt[11:8], vmcnt[5:4] in [15:14]).
@@ -987,6 +994,12 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, (WM * WN <= 8192 ? 2 : 
       __syncthreads();
     }
     } else {
+    // The linear fusions' 32x32x16 loop, its MFMAs pinned above each barrier as
+    // above: 8192 tokens, same box, ABBA order, gate_up+SiLU*mul 1652-1655 ->
+    // 1628-1634 us and down_proj+residual 826-830 -> 804-806 us, but
+    // o_proj+residual 241-243 -> 247-248 us (its operands fit the Infinity
+    // Cache, so the earlier copies buy little there and the MFMA pipe idles at
+    // the barrier instead).
     uint4 fa0[MB], fb0[NB], fa1[MB], fb1[NB];
     issue_stage<ADPW, BDPW, BM, 64, NW>(g.a, g.w, 0, aoff, boff, l0);
     resolve_slots();
@@ -998,12 +1011,14 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, (WM * WN <= 8192 ? 2 : 
       issue_stage<ADPW, BDPW, BM, 64, NW>(g.a, g.w, kt + 1, aoff, boff, l1);
       compute3<MB, NB, BM, WM, WN, BF16>(lds0, wm, wn, frow, fhalf, acc, fa0, fb0, fa1, fb1);
       mfma_block<MB, NB, BF16>(acc, fa1, fb1);
+      pin_acc(acc);
       wait_vmem();
       __syncthreads();
       load_frags<MB, NB, BM, WM, WN>(lds1, 0, wm, wn, frow, fhalf, fa0, fb0);
       if (kt + 2 < KT) issue_stage<ADPW, BDPW, BM, 64, NW>(g.a, g.w, kt + 2, aoff, boff, l0);
       compute3<MB, NB, BM, WM, WN, BF16>(lds1, wm, wn, frow, fhalf, acc, fa0, fb0, fa1, fb1);
       mfma_block<MB, NB, BF16>(acc, fa1, fb1);
+      pin_acc(acc);
       wait_vmem();
       __syncthreads();
       if (kt + 2 < KT) load_frags<MB, NB, BM, WM, WN>(lds0, 0, wm, wn, frow, fhalf, fa0, fb0);
