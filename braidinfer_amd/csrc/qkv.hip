@@ -758,8 +758,9 @@ __device__ __forceinline__ void gemm_epilogue(ACC& acc, uint4* lds, const GemmAr
 // 4-wave workgroups, or one 8-wave workgroup, per CU.  BK is the depth of a DMA
 // stage: 32 (ring of NS stages, 16 rows x 64 bytes per copy) or 64 (two
 // buffers, 8 rows x 128 bytes per copy, full cache lines).
+// PIN (the linear fusions' 64-deep loop): a stage's MFMAs stay above its barrier.
 template <int BM, int BN, int WM, int WN, bool BF16, int EPI, int HD, bool DIRECT, int NS, int BK,
-          int EDT = EDT_RT>
+          int EDT = EDT_RT, bool PIN = true>
 __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, (WM * WN <= 8192 ? 2 : 1)) void qkv_gemm_kernel(
     GemmArgs g, QkvEpi e) {
   constexpr int NWN = BN / WN;
@@ -994,12 +995,12 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, (WM * WN <= 8192 ? 2 : 
       __syncthreads();
     }
     } else {
-    // The linear fusions' 32x32x16 loop, its MFMAs pinned above each barrier as
-    // above: 8192 tokens, same box, ABBA order, gate_up+SiLU*mul 1652-1655 ->
+    // The linear fusions' 32x32x16 loop.  PIN keeps its MFMAs above each barrier
+    // as above: 8192 tokens, same box, ABBA order, gate_up+SiLU*mul 1652-1655 ->
     // 1628-1634 us and down_proj+residual 826-830 -> 804-806 us, but
-    // o_proj+residual 241-243 -> 247-248 us (its operands fit the Infinity
+    // o_proj+residual 241-243 -> 247-248 us: its operands fit the Infinity
     // Cache, so the earlier copies buy little there and the MFMA pipe idles at
-    // the barrier instead).
+    // the barrier instead (the launcher leaves such products unpinned).
     uint4 fa0[MB], fb0[NB], fa1[MB], fb1[NB];
     issue_stage<ADPW, BDPW, BM, 64, NW>(g.a, g.w, 0, aoff, boff, l0);
     resolve_slots();
@@ -1011,14 +1012,14 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, (WM * WN <= 8192 ? 2 : 
       issue_stage<ADPW, BDPW, BM, 64, NW>(g.a, g.w, kt + 1, aoff, boff, l1);
       compute3<MB, NB, BM, WM, WN, BF16>(lds0, wm, wn, frow, fhalf, acc, fa0, fb0, fa1, fb1);
       mfma_block<MB, NB, BF16>(acc, fa1, fb1);
-      pin_acc(acc);
+      if constexpr (PIN) pin_acc(acc);
       wait_vmem();
       __syncthreads();
       load_frags<MB, NB, BM, WM, WN>(lds1, 0, wm, wn, frow, fhalf, fa0, fb0);
       if (kt + 2 < KT) issue_stage<ADPW, BDPW, BM, 64, NW>(g.a, g.w, kt + 2, aoff, boff, l0);
       compute3<MB, NB, BM, WM, WN, BF16>(lds1, wm, wn, frow, fhalf, acc, fa0, fb0, fa1, fb1);
       mfma_block<MB, NB, BF16>(acc, fa1, fb1);
-      pin_acc(acc);
+      if constexpr (PIN) pin_acc(acc);
       wait_vmem();
       __syncthreads();
       if (kt + 2 < KT) load_frags<MB, NB, BM, WM, WN>(lds0, 0, wm, wn, frow, fhalf, fa0, fb0);
@@ -2752,6 +2753,21 @@ static void launch_linear_tile(const GemmArgs& g, const QkvEpi& e, bool swiglu, 
   const dim3 block((BM / WM) * (BN / 128) * 64);
   if constexpr (BF16 && DIRECT) {
     if (linear_edt(e) == EDT_BF16) {
+      // A product whose operand and weight fit in 128 MiB (well inside the 256 MB
+      // Infinity Cache) runs the 64-deep loop unpinned (o_proj at 8192 tokens:
+      // 96 MiB, 230.5-231.6 against 237.5-239.9 us pinned).
+      const int64_t bytes = (g.m + (swiglu ? 2 : 1) * g.n) * g.k * 2;
+      if (BK == 64 && bytes <= (int64_t(128) << 20)) {
+        if (swiglu)
+          hipLaunchKernelGGL(
+              (qkv_gemm_kernel<BM, BN, WM, 128, BF16, EPI_SWIGLU, 128, DIRECT, NS, BK, EDT_BF16, false>),
+              dim3(grid), block, 0, st, g, e);
+        else
+          hipLaunchKernelGGL(
+              (qkv_gemm_kernel<BM, BN, WM, 128, BF16, EPI_LINEAR, 128, DIRECT, NS, BK, EDT_BF16, false>),
+              dim3(grid), block, 0, st, g, e);
+        return;
+      }
       if (swiglu)
         hipLaunchKernelGGL((qkv_gemm_kernel<BM, BN, WM, 128, BF16, EPI_SWIGLU, 128, DIRECT, NS, BK, EDT_BF16>),
                            dim3(grid), block, 0, st, g, e);
