@@ -15,9 +15,9 @@
 //
 // Kernels
 //  * qkv_gemm_kernel   prefill.  BMxBN tile per workgroup of 4 or 8 waves, each
-//    wave WMx128: v_mfma_f32_16x16x32_{bf16,f16} on the QKV projection's 64-deep
-//    DMA path, v_mfma_f32_32x32x16 elsewhere; 256x256 with 8 waves (two per SIMD)
-//    for large token counts.  Operand and weight K-slices move HBM ->
+//    wave WMx128: v_mfma_f32_16x16x32_{bf16,f16} on the 64-deep DMA path,
+//    v_mfma_f32_32x32x16 on the 32-deep rings and the register-staged path;
+//    256x256 with 8 waves (two per SIMD) for large token counts.  Operand and weight K-slices move HBM ->
 //    LDS by LDS DMA (global_load_lds_dwordx4) into XOR-swizzled buffers, so the
 //    MFMA fragment reads spread over the banks; unaligned or odd K goes through a
 //    register-staged path with masking.  The epilogue stages each wave's
@@ -278,13 +278,6 @@ __device__ __forceinline__ void mfma_half16(f32x4_t (&acc)[MB16][NB16], const ui
 // it in program order is issued before it, and none after it moves above it.
 template <int R, int C>
 __device__ __forceinline__ void pin_acc(f32x4_t (&acc)[R][C]) {
-#pragma unroll
-  for (int i = 0; i < R; ++i)
-#pragma unroll
-    for (int j = 0; j < C; ++j) asm volatile("" : "+v"(acc[i][j]));
-}
-template <int R, int C>
-__device__ __forceinline__ void pin_acc(f32x16_t (&acc)[R][C]) {
 #pragma unroll
   for (int i = 0; i < R; ++i)
 #pragma unroll
@@ -758,9 +751,8 @@ __device__ __forceinline__ void gemm_epilogue(ACC& acc, uint4* lds, const GemmAr
 // 4-wave workgroups, or one 8-wave workgroup, per CU.  BK is the depth of a DMA
 // stage: 32 (ring of NS stages, 16 rows x 64 bytes per copy) or 64 (two
 // buffers, 8 rows x 128 bytes per copy, full cache lines).
-// PIN (the linear fusions' 64-deep loop): a stage's MFMAs stay above its barrier.
 template <int BM, int BN, int WM, int WN, bool BF16, int EPI, int HD, bool DIRECT, int NS, int BK,
-          int EDT = EDT_RT, bool PIN = true>
+          int EDT = EDT_RT>
 __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, (WM * WN <= 8192 ? 2 : 1)) void qkv_gemm_kernel(
     GemmArgs g, QkvEpi e) {
   constexpr int NWN = BN / WN;
@@ -848,17 +840,17 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, (WM * WN <= 8192 ? 2 : 
     }
   }
 
-  // The QKV projection's 64-deep DMA path multiplies with v_mfma_f32_16x16x32
-  // into 16x16 blocks (acc4); every other path with v_mfma_f32_32x32x16 into
-  // 32x32 blocks (acc).  Same product and the same fragment bytes per wave tile,
-  // but a 16x16x32 MFMA reads and writes a quarter of the accumulators for half
-  // the work, and the chip is power limited under this loop: at 8192 tokens the
-  // Llama-3-8B projection took 313-325 against 323-334 us and the fused op
-  // 329-334 against 344-347 us, same box, interleaved processes.  The linear
-  // fusions keep the 32x32 form: with 16x16 blocks gate_up+SiLU*mul took 1629-
-  // 1633 against 1601-1608 us and down_proj+residual 827-831 against 810-815 us
-  // (o_proj+residual 219-224 against 227-228 us), same box, ABBA order.
-  constexpr bool M16 = DIRECT && BK == 64 && (EPI == EPI_FUSED || EPI == EPI_RAW);
+  // The 64-deep DMA path multiplies with v_mfma_f32_16x16x32 into 16x16 blocks
+  // (acc4); the 32-deep rings and the register-staged path with
+  // v_mfma_f32_32x32x16 into 32x32 blocks (acc).  Same product and the same
+  // fragment bytes per wave tile, but a 16x16x32 MFMA reads and writes a quarter
+  // of the accumulators for half the work, and the chip is power limited under
+  // this loop: at 8192 tokens the Llama-3-8B projection took 313-325 against
+  // 323-334 us and the fused op 329-334 against 344-347 us, same box,
+  // interleaved processes; with the pinned loop below, gate_up+SiLU*mul
+  // 1560-1568 against 1605-1613 us, down_proj+residual 777-778 against 810-812
+  // us and o_proj+residual 230-232 against 233 us (the 32x32x16 loop pinned).
+  constexpr bool M16 = DIRECT && BK == 64;
   f32x16_t acc[M16 ? 1 : MB][M16 ? 1 : NB];
   f32x4_t acc4[M16 ? 2 * MB : 1][M16 ? 2 * NB : 1];
   if constexpr (M16) {
@@ -943,7 +935,6 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, (WM * WN <= 8192 ? 2 : 
     for (int i = 0; i < BDPW; ++i)
       boff[i] = static_cast<uint32_t>((weight_row<EPI>(g, n0, (i * NW + wid) * 8 + lrow) * g.ldw + lgran * 8) * 2);
     const uint32_t l0 = lds_addr(lds0) + wid * 1024, l1 = lds_addr(lds1) + wid * 1024;
-    if constexpr (M16) {
     // A stage is two 32-deep sub-steps, each in two halves of the wave's 16-column
     // blocks: four quarters of M2 x NH MFMAs, each quarter's fragment reads issued
     // under the previous quarter's MFMAs.  Two operand and two half-weight
@@ -993,42 +984,6 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, (WM * WN <= 8192 ? 2 : 
     if (kt < KT) {  // odd tile count: the last tile is in lds0
       stage(lds0);
       __syncthreads();
-    }
-    } else {
-    // The linear fusions' 32x32x16 loop.  PIN keeps its MFMAs above each barrier
-    // as above: 8192 tokens, same box, ABBA order, gate_up+SiLU*mul 1652-1655 ->
-    // 1628-1634 us and down_proj+residual 826-830 -> 804-806 us, but
-    // o_proj+residual 241-243 -> 247-248 us: its operands fit the Infinity
-    // Cache, so the earlier copies buy little there and the MFMA pipe idles at
-    // the barrier instead (the launcher leaves such products unpinned).
-    uint4 fa0[MB], fb0[NB], fa1[MB], fb1[NB];
-    issue_stage<ADPW, BDPW, BM, 64, NW>(g.a, g.w, 0, aoff, boff, l0);
-    resolve_slots();
-    wait_vmem();
-    __syncthreads();
-    load_frags<MB, NB, BM, WM, WN>(lds0, 0, wm, wn, frow, fhalf, fa0, fb0);
-    int64_t kt = 0;
-    for (; kt + 2 <= KT; kt += 2) {
-      issue_stage<ADPW, BDPW, BM, 64, NW>(g.a, g.w, kt + 1, aoff, boff, l1);
-      compute3<MB, NB, BM, WM, WN, BF16>(lds0, wm, wn, frow, fhalf, acc, fa0, fb0, fa1, fb1);
-      mfma_block<MB, NB, BF16>(acc, fa1, fb1);
-      if constexpr (PIN) pin_acc(acc);
-      wait_vmem();
-      __syncthreads();
-      load_frags<MB, NB, BM, WM, WN>(lds1, 0, wm, wn, frow, fhalf, fa0, fb0);
-      if (kt + 2 < KT) issue_stage<ADPW, BDPW, BM, 64, NW>(g.a, g.w, kt + 2, aoff, boff, l0);
-      compute3<MB, NB, BM, WM, WN, BF16>(lds1, wm, wn, frow, fhalf, acc, fa0, fb0, fa1, fb1);
-      mfma_block<MB, NB, BF16>(acc, fa1, fb1);
-      if constexpr (PIN) pin_acc(acc);
-      wait_vmem();
-      __syncthreads();
-      if (kt + 2 < KT) load_frags<MB, NB, BM, WM, WN>(lds0, 0, wm, wn, frow, fhalf, fa0, fb0);
-    }
-    if (kt < KT) {  // odd tile count: the last tile is in lds0
-      compute3<MB, NB, BM, WM, WN, BF16>(lds0, wm, wn, frow, fhalf, acc, fa0, fb0, fa1, fb1);
-      mfma_block<MB, NB, BF16>(acc, fa1, fb1);
-      __syncthreads();
-    }
     }
   } else {
     const int gg = tid & 7, gr = tid >> 3;
@@ -2753,21 +2708,6 @@ static void launch_linear_tile(const GemmArgs& g, const QkvEpi& e, bool swiglu, 
   const dim3 block((BM / WM) * (BN / 128) * 64);
   if constexpr (BF16 && DIRECT) {
     if (linear_edt(e) == EDT_BF16) {
-      // A product whose operand and weight fit in 128 MiB (well inside the 256 MB
-      // Infinity Cache) runs the 64-deep loop unpinned (o_proj at 8192 tokens:
-      // 96 MiB, 230.5-231.6 against 237.5-239.9 us pinned).
-      const int64_t bytes = (g.m + (swiglu ? 2 : 1) * g.n) * g.k * 2;
-      if (BK == 64 && bytes <= (int64_t(128) << 20)) {
-        if (swiglu)
-          hipLaunchKernelGGL(
-              (qkv_gemm_kernel<BM, BN, WM, 128, BF16, EPI_SWIGLU, 128, DIRECT, NS, BK, EDT_BF16, false>),
-              dim3(grid), block, 0, st, g, e);
-        else
-          hipLaunchKernelGGL(
-              (qkv_gemm_kernel<BM, BN, WM, 128, BF16, EPI_LINEAR, 128, DIRECT, NS, BK, EDT_BF16, false>),
-              dim3(grid), block, 0, st, g, e);
-        return;
-      }
       if (swiglu)
         hipLaunchKernelGGL((qkv_gemm_kernel<BM, BN, WM, 128, BF16, EPI_SWIGLU, 128, DIRECT, NS, BK, EDT_BF16>),
                            dim3(grid), block, 0, st, g, e);
